@@ -1,0 +1,140 @@
+/*
+ * gdn.h -- C ABI of libgdn.so, the MI355X (gfx950) Gated DeltaNet token-mixing path.
+ *
+ * Plain C: device pointers, int64 sizes, dtype codes and a stream handle (a hipStream_t passed as
+ * void*; NULL is the legacy default stream). No entry point allocates device memory; outputs and
+ * any workspace are owned by the caller. Every entry point returns GDN_OK or a non-zero status,
+ * and gdn_last_error() returns a message for the calling thread's last failure.
+ *
+ * Layouts (row-major, contiguous, last axis fastest):
+ *   q, k        [B, T, H,  K]      v, o  [B, T, HV, V]       g, beta [B, T, HV]
+ *   states      [N, HV, K, V] fp32 (V fastest)
+ *   cu_seqlens  [N + 1] int32 or int64 on the device, 0 = cu[0] < ... < cu[N] = T, with B == 1.
+ *   Without cu_seqlens, N == B and every batch row is one sequence.
+ * HV must be a multiple of H: value head i reads q/k head i / (HV / H).
+ */
+#ifndef SORERNN_AMD_GDN_H
+#define SORERNN_AMD_GDN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GDN_ABI_VERSION 1
+
+#if defined(__GNUC__) || defined(__clang__)
+#define GDN_API __attribute__((visibility("default")))
+#else
+#define GDN_API
+#endif
+
+/* status codes */
+#define GDN_OK 0
+#define GDN_ERR_INVALID 1 /* an argument violates the contract (shape, dtype, pointer) */
+#define GDN_ERR_UNSUPPORTED 2 /* a legal combination this build does not implement */
+#define GDN_ERR_HIP 3 /* the HIP runtime reported an error */
+
+/* dtype codes */
+#define GDN_DTYPE_F32 0
+#define GDN_DTYPE_BF16 1
+#define GDN_DTYPE_F16 2
+
+/* flags for the delta-rule entry points */
+#define GDN_FLAG_QK_L2NORM 0x1u /* L2-normalise q and k per (token, head) in the kernel */
+#define GDN_FLAG_BETA_SIGMOID 0x2u /* beta holds logits: use sigmoid(beta) */
+#define GDN_FLAG_GATE_IN_KERNEL 0x4u /* g holds a: use g = -exp(A_log[h]) * softplus(a + dt_bias[h]) */
+#define GDN_FLAG_CU_INT32 0x8u /* cu_seqlens is int32 (default int64) */
+
+/* activation codes for the conv and the gated norm */
+#define GDN_ACT_NONE 0
+#define GDN_ACT_SILU 1
+
+/* ABI version of the loaded library (GDN_ABI_VERSION at build time). */
+GDN_API int gdn_abi_version(void);
+
+/* Message for the calling thread's last failed call ("" if none). */
+GDN_API const char* gdn_last_error(void);
+
+/*
+ * Chunked gated delta rule forward (prefill), C = 64 tokens per chunk.
+ * Replaces FLA 0.5.2 chunk_gated_delta_rule(q, k, v, g, beta, scale, initial_state,
+ * output_final_state, use_qk_l2norm_in_kernel, use_beta_sigmoid_in_kernel, ..., cu_seqlens,
+ * cu_seqlens_cpu) as called at sore/model/gdn.py:166-169 (signature:
+ * docs/superpowers/plans/2026-10-23-sorernn-v2-core.md:141; gate kwargs gdn.py:157-162).
+ * q/k/v/o share qkv_dtype (bf16 or f32); g and beta have their own dtypes. initial_state may be
+ * NULL (zero state); final_state may be NULL (not written). A_log/dt_bias [HV] fp32 are read only
+ * with GDN_FLAG_GATE_IN_KERNEL. K and V must each be 64 or 128.
+ */
+GDN_API int gdn_chunk_fwd(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                  const float* initial_state, void* o, float* final_state, const void* cu_seqlens,
+                  int64_t B, int64_t T, int64_t H, int64_t HV, int64_t K, int64_t V, int64_t N,
+                  int qkv_dtype, int g_dtype, int beta_dtype, float scale, unsigned flags,
+                  const float* A_log, const float* dt_bias, void* stream);
+
+/*
+ * Recurrent gated delta rule forward: tokens in order, the state held on chip for the whole
+ * sequence (one read and one write of each state). With T == 1 this is the decode step.
+ * Replaces FLA fused_recurrent_gated_delta_rule (named by the profiler rule at
+ * sore/train/profiling.py:35; no call site in the reference). final_state may equal
+ * initial_state (in-place update). Same layouts, dtypes and flags as gdn_chunk_fwd.
+ */
+GDN_API int gdn_recurrent_fwd(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                      const float* initial_state, void* o, float* final_state, const void* cu_seqlens,
+                      int64_t B, int64_t T, int64_t H, int64_t HV, int64_t K, int64_t V, int64_t N,
+                      int qkv_dtype, int g_dtype, int beta_dtype, float scale, unsigned flags,
+                      const float* A_log, const float* dt_bias, void* stream);
+
+/*
+ * Fused decode step for one token per sequence: conv-cache update + conv + SiLU on the packed
+ * pre-conv projection x_qkv [B, 2*H*D + HV*D] (q | k | v channels), then the gated delta rule
+ * step on the updated state. conv_state [B, C, W] (newest input last, updated in place),
+ * conv_weight [C, W] fp32 (weight[:, W-1] multiplies the current token), state [B, HV, D, D]
+ * fp32 updated in place, o [B, 1, HV, D]. g/beta [B, HV] as in gdn_chunk_fwd (flags apply).
+ * No counterpart call in the reference (it has no decode path); composes the conv of
+ * sore/model/conv.py:6-23 + SiLU (gdn.py:209), the L2 norm (gdn.py:177) and one step of
+ * sore/model/gdn_ref.py:17-21.
+ */
+GDN_API int gdn_decode_step(const void* x_qkv, void* conv_state, const float* conv_weight, const void* g,
+                    const void* beta, float* state, void* o, int64_t B, int64_t H, int64_t HV,
+                    int64_t D, int64_t W, int x_dtype, int conv_state_dtype, int g_dtype, int beta_dtype,
+                    float scale, unsigned flags, const float* A_log, const float* dt_bias, void* stream);
+
+/*
+ * Depthwise causal conv1d (+ optional SiLU) with per-document reset.
+ * Replaces FLA causal_conv1d(x, weight, activation="silu", cu_seqlens, cu_seqlens_cpu)
+ * (sore/model/gdn.py:199-207) and the torch path causal_conv1d_varlen + F.silu
+ * (sore/model/conv.py:6-23, gdn.py:208-209). x, y [B, T, C] (x_dtype); weight [C, W] fp32;
+ * bias [C] fp32 or NULL. initial_state [N, C, W] (x_dtype) or NULL supplies the inputs before
+ * each sequence; final_state [N, C, W] (x_dtype) or NULL receives the last W inputs of each
+ * sequence (zero-padded). Math in fp32, one rounding to x_dtype.
+ */
+GDN_API int gdn_causal_conv1d_fwd(const void* x, const float* weight, const float* bias, void* y,
+                          const void* initial_state, void* final_state, const void* cu_seqlens,
+                          int64_t B, int64_t T, int64_t C, int64_t W, int64_t N, int x_dtype,
+                          int activation, unsigned flags, void* stream);
+
+/*
+ * Row-wise L2 normalisation y = x / max(||x||_2, eps) over the last axis of length D.
+ * Replaces F.normalize(q/k, dim=-1) (sore/model/gdn.py:177) and FLA's l2norm_fwd_kernel
+ * (tests/train/test_profiling.py:30). Math in fp32, one rounding.
+ */
+GDN_API int gdn_l2norm_fwd(const void* x, void* y, int64_t rows, int64_t D, int dtype, float eps, void* stream);
+
+/*
+ * Gated RMSNorm: y = x * rsqrt(mean(x^2) + eps) * weight (+ bias) * act(gate), per row of D.
+ * Replaces FLA rms_norm_gated(o, gate, weight, None, activation="swish", eps) at
+ * sore/model/gdn.py:182-186 and o_norm(o) * F.silu(gate) at gdn.py:188 (RMSNorm:
+ * sore/model/layers.py:7-18). gate may be NULL (plain RMSNorm). weight [D] fp32 or NULL (ones).
+ * Math in fp32, one rounding to dtype.
+ */
+GDN_API int gdn_rms_norm_gated_fwd(const void* x, const void* gate, const float* weight, const float* bias, void* y,
+                           int64_t rows, int64_t D, int dtype, float eps, int activation, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SORERNN_AMD_GDN_H */

@@ -1,0 +1,16 @@
+"""MI355X-native (gfx950) Gated DeltaNet token-mixing path for soreRNN.
+
+A drop-in for FLA's ``chunk_gated_delta_rule`` / ``fused_recurrent_gated_delta_rule`` and the conv
+and gated-norm modules used by ``sore/model/gdn.py``: Python host code calls the C ABI of
+``libgdn.so`` (``include/gdn.h``), which launches hand-written HIP kernels built for gfx950.
+"""
+from sorernn_amd.ops import (  # noqa: F401
+    causal_conv1d,
+    chunk_gated_delta_rule,
+    fused_recurrent_gated_delta_rule,
+    gated_delta_decode_step,
+    l2norm,
+    rms_norm_gated,
+)
+
+__version__ = "0.1.0"

@@ -1,0 +1,84 @@
+"""Build ``libgdn.so`` in-tree from ``sorernn_amd/csrc/*.hip`` with hipcc for gfx950.
+
+Usage: ``python -m sorernn_amd.build`` (or ``__graft_entry__.build()``). Every source is compiled
+to an object in parallel and linked into ``sorernn_amd/libgdn.so``; the previous library is replaced
+atomically, so a failed build never leaves a half-written file behind.
+"""
+from __future__ import annotations
+
+import concurrent.futures
+import os
+import shutil
+import subprocess
+import sys
+import tempfile
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+INCLUDE = os.path.join(ROOT, "include")
+LIB_PATH = os.path.join(HERE, "libgdn.so")
+ARCH = "gfx950"
+
+# Packed fp32 VALU ops are disabled for all device code (some forms are unreliable on these boxes).
+DEVICE_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-fvisibility=hidden",
+    "-ffp-contract=fast",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    f"-I{INCLUDE}",
+]
+
+
+def _hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found (ROCm toolchain required to build libgdn.so)")
+
+
+def sources() -> list[str]:
+    return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
+
+
+def _run(cmd: list[str]) -> None:
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"command failed ({res.returncode}): {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
+    # hipcc's host pass warns about the device-only target feature; anything else is worth showing
+    noise = "is not a recognized feature for this target"
+    lines = [ln for ln in (res.stderr or "").splitlines() if ln.strip() and noise not in ln]
+    if lines:
+        print("\n".join(lines), file=sys.stderr)
+
+
+def build(verbose: bool = False, jobs: int | None = None) -> str:
+    hipcc = _hipcc()
+    srcs = sources()
+    if not srcs:
+        raise RuntimeError(f"no .hip sources under {CSRC}")
+    with tempfile.TemporaryDirectory(prefix="gdn_build_") as tmp:
+        objs = [os.path.join(tmp, os.path.basename(s) + ".o") for s in srcs]
+        cmds = [[hipcc, *DEVICE_FLAGS, "-c", s, "-o", o] for s, o in zip(srcs, objs)]
+        if verbose:
+            for c in cmds:
+                print(" ".join(c))
+        workers = jobs or min(len(cmds), max(1, (os.cpu_count() or 2) // 2), 8)
+        with concurrent.futures.ThreadPoolExecutor(workers) as pool:
+            list(pool.map(_run, cmds))
+        tmp_lib = os.path.join(tmp, "libgdn.so")
+        link = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp_lib, *objs]
+        if verbose:
+            print(" ".join(link))
+        _run(link)
+        staged = LIB_PATH + ".tmp"
+        shutil.copyfile(tmp_lib, staged)
+        os.replace(staged, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

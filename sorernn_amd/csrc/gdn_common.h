@@ -1,0 +1,67 @@
+// Shared device helpers for the gfx950 Gated DeltaNet kernels: element types, conversions,
+// wave-level reductions, the MFMA fragment types and the library's error channel.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/gdn.h"
+
+namespace gdn {
+
+typedef __bf16 bf16;
+typedef _Float16 f16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------- element access by runtime dtype
+__device__ __forceinline__ float load_as_f32(const void* p, int dtype, int64_t i) {
+  switch (dtype) {
+    case GDN_DTYPE_BF16: return static_cast<float>(static_cast<const bf16*>(p)[i]);
+    case GDN_DTYPE_F16: return static_cast<float>(static_cast<const f16*>(p)[i]);
+    default: return static_cast<const float*>(p)[i];
+  }
+}
+
+__device__ __forceinline__ void store_from_f32(void* p, int dtype, int64_t i, float x) {
+  switch (dtype) {
+    case GDN_DTYPE_BF16: static_cast<bf16*>(p)[i] = static_cast<bf16>(x); break;
+    case GDN_DTYPE_F16: static_cast<f16*>(p)[i] = static_cast<f16>(x); break;
+    default: static_cast<float*>(p)[i] = x; break;
+  }
+}
+
+// Round an fp32 value to the storage dtype and back (the value a store followed by a load sees).
+__device__ __forceinline__ float round_to(int dtype, float x) {
+  switch (dtype) {
+    case GDN_DTYPE_BF16: return static_cast<float>(static_cast<bf16>(x));
+    case GDN_DTYPE_F16: return static_cast<float>(static_cast<f16>(x));
+    default: return x;
+  }
+}
+
+__device__ __forceinline__ int64_t load_index(const void* p, int is_i32, int64_t i) {
+  return is_i32 ? static_cast<int64_t>(static_cast<const int32_t*>(p)[i]) : static_cast<const int64_t*>(p)[i];
+}
+
+// ---------------------------------------------------------------- scalar math
+// softplus with torch's default threshold (beta=1, threshold=20): x for x > 20, else log1p(exp(x)).
+__device__ __forceinline__ float softplus_f32(float x) { return x > 20.f ? x : log1pf(expf(x)); }
+__device__ __forceinline__ float sigmoid_f32(float x) { return 1.f / (1.f + expf(-x)); }
+__device__ __forceinline__ float silu_f32(float x) { return x / (1.f + expf(-x)); }
+
+// ---------------------------------------------------------------- wave reductions
+__device__ __forceinline__ float wave_xor_sum(float x, int from_stride) {
+  for (int s = from_stride; s < kWave; s <<= 1) x += __shfl_xor(x, s, kWave);
+  return x;
+}
+
+}  // namespace gdn
+
+// Error channel shared by every entry point (defined in gdn_api.hip).
+extern "C" void gdn_internal_set_error(const char* fmt, ...) __attribute__((visibility("hidden")));
+extern "C" int gdn_internal_check_launch(const char* what) __attribute__((visibility("hidden")));

@@ -1,0 +1,399 @@
+"""Host-side drop-ins for FLA's GDN operators, launching the gfx950 kernels of ``libgdn.so``.
+
+Each function keeps the signature and argument meaning of the FLA 0.5.2 call it replaces, as used
+by soreRNN's ``sore/model/gdn.py`` (the reference's only caller), so the model code changes only
+its imports:
+
+- ``chunk_gated_delta_rule``            <- ``fla.ops.gated_delta_rule.chunk_gated_delta_rule`` (gdn.py:151,166-169)
+- ``fused_recurrent_gated_delta_rule``  <- ``fla.ops.gated_delta_rule.fused_recurrent_gated_delta_rule``
+- ``causal_conv1d``                     <- ``fla.modules.conv.causal_conv1d`` (gdn.py:200-207)
+- ``rms_norm_gated``                    <- ``fla.modules.fused_norm_gate.rms_norm_gated`` (gdn.py:182-186)
+- ``l2norm``                            <- ``F.normalize(x, dim=-1)`` / FLA ``l2norm`` (gdn.py:177)
+- ``gated_delta_decode_step``           (no reference counterpart: the fused decode step)
+
+Outputs are allocated here from torch's caching allocator; the C ABI never allocates. Everything
+is forward-only: a call that would need a backward raises ``NotImplementedError`` instead of
+silently detaching. Contract violations raise ``ValueError`` with the reference's wording
+("B == 1", "cu_seqlens"; ``sore/model/gdn_ref.py:42-43,54-55``).
+"""
+from __future__ import annotations
+
+import torch
+from torch import Tensor
+
+from sorernn_amd import _lib
+
+__all__ = [
+    "causal_conv1d",
+    "chunk_gated_delta_rule",
+    "fused_recurrent_gated_delta_rule",
+    "gated_delta_decode_step",
+    "l2norm",
+    "rms_norm_gated",
+]
+
+
+def _no_grad_check(name: str, *tensors) -> None:
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in tensors):
+        raise NotImplementedError(
+            f"{name}: only the forward pass is implemented on gfx950 (inputs require grad); "
+            "run under torch.no_grad() or detach the inputs"
+        )
+
+
+def _check_cuda(name: str, *tensors) -> torch.device:
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise ValueError(f"{name}: every tensor must be on the GPU (got {t.device})")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"{name}: tensors on different devices ({dev} vs {t.device})")
+    return dev
+
+
+def _cu_info(name: str, cu_seqlens: Tensor | None, cu_seqlens_cpu: Tensor | None, batch: int, t: int):
+    """Validate ``cu_seqlens`` and return (number of sequences, flags bits).
+
+    The bounds are checked on ``cu_seqlens_cpu`` when given (no device sync); otherwise the device
+    tensor is copied to the host once, as FLA does when it builds its chunk indices.
+    """
+    if cu_seqlens is None:
+        return batch, 0
+    if batch != 1:
+        raise ValueError(f"{name}: cu_seqlens requires B == 1, got B = {batch}")
+    if cu_seqlens.dim() != 1 or cu_seqlens.numel() < 2:
+        raise ValueError(f"{name}: cu_seqlens must be 1-D with at least 2 entries")
+    if cu_seqlens.dtype not in (torch.int32, torch.int64):
+        raise ValueError(f"{name}: cu_seqlens must be int32 or int64, got {cu_seqlens.dtype}")
+    host = cu_seqlens_cpu if cu_seqlens_cpu is not None else cu_seqlens.detach().cpu()
+    if host.numel() != cu_seqlens.numel():
+        raise ValueError(f"{name}: cu_seqlens_cpu has {host.numel()} entries, cu_seqlens {cu_seqlens.numel()}")
+    b = host.tolist()
+    if b[0] != 0 or b[-1] != t:
+        raise ValueError(f"{name}: cu_seqlens must go from 0 to T = {t}, got {b[0]}..{b[-1]}")
+    if any(y <= x for x, y in zip(b[:-1], b[1:])):
+        raise ValueError(f"{name}: cu_seqlens must be strictly increasing")
+    return len(b) - 1, (_lib.FLAG_CU_INT32 if cu_seqlens.dtype == torch.int32 else 0)
+
+
+def _delta_rule_args(name, q, k, v, g, beta, scale, initial_state, cu_seqlens, cu_seqlens_cpu,
+                     use_qk_l2norm_in_kernel, use_beta_sigmoid_in_kernel, use_gate_in_kernel, A_log, dt_bias):
+    if q.dim() != 4 or k.shape != q.shape or v.dim() != 4 or v.shape[:2] != q.shape[:2]:
+        raise ValueError(f"{name}: expected q,k [B,T,H,K] and v [B,T,HV,V], got {tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
+    b, t, h, kd = q.shape
+    hv, vd = v.shape[2], v.shape[3]
+    if hv % h:
+        raise ValueError(f"{name}: value heads ({hv}) must be a multiple of q/k heads ({h})")
+    if q.dtype != k.dtype or q.dtype != v.dtype:
+        raise ValueError(f"{name}: q, k, v must share a dtype ({q.dtype}, {k.dtype}, {v.dtype})")
+    for nm, x in (("g", g), ("beta", beta)):
+        if tuple(x.shape) != (b, t, hv):
+            raise ValueError(f"{name}: {nm} must be [B,T,HV] = {(b, t, hv)}, got {tuple(x.shape)}")
+    n, flags = _cu_info(name, cu_seqlens, cu_seqlens_cpu, b, t)
+    if initial_state is not None and tuple(initial_state.shape) != (n, hv, kd, vd):
+        raise ValueError(f"{name}: initial_state must be [N,HV,K,V] = {(n, hv, kd, vd)}, got {tuple(initial_state.shape)}")
+    if use_qk_l2norm_in_kernel:
+        flags |= _lib.FLAG_QK_L2NORM
+    if use_beta_sigmoid_in_kernel:
+        flags |= _lib.FLAG_BETA_SIGMOID
+    if use_gate_in_kernel:
+        if A_log is None or dt_bias is None:
+            raise ValueError(f"{name}: use_gate_in_kernel needs A_log and dt_bias")
+        if A_log.numel() != hv or dt_bias.numel() != hv:
+            raise ValueError(f"{name}: A_log and dt_bias must have HV = {hv} entries")
+        flags |= _lib.FLAG_GATE_IN_KERNEL
+        A_log = A_log.detach().float().contiguous()
+        dt_bias = dt_bias.detach().float().contiguous()
+    else:
+        A_log = dt_bias = None
+    if scale is None:
+        scale = kd**-0.5
+    return b, t, h, kd, hv, vd, n, flags, float(scale), A_log, dt_bias
+
+
+def _gdn_call(entry, name, q, k, v, g, beta, scale, initial_state, output_final_state, cu_seqlens, cu_seqlens_cpu,
+              use_qk_l2norm_in_kernel, use_beta_sigmoid_in_kernel, use_gate_in_kernel, A_log, dt_bias,
+              inplace_final_state=False):
+    _check_cuda(name, q, k, v, g, beta, initial_state, cu_seqlens, A_log, dt_bias)
+    _no_grad_check(name, q, k, v, g, beta, initial_state, A_log, dt_bias)
+    b, t, h, kd, hv, vd, n, flags, scale, A_log, dt_bias = _delta_rule_args(
+        name, q, k, v, g, beta, scale, initial_state, cu_seqlens, cu_seqlens_cpu,
+        use_qk_l2norm_in_kernel, use_beta_sigmoid_in_kernel, use_gate_in_kernel, A_log, dt_bias)
+    out_dtype = v.dtype
+    if out_dtype == torch.float16 and entry == "gdn_chunk_fwd":
+        # the chunk kernel stages bf16 or fp32 operands; fp16 runs on the fp32 (split-bf16) path
+        q, k, v = q.float(), k.float(), v.float()
+    q, k, v, g, beta = (x.contiguous() for x in (q, k, v, g, beta))
+    h0 = None
+    if initial_state is not None:
+        h0 = initial_state if (initial_state.dtype == torch.float32 and initial_state.is_contiguous()) else initial_state.float().contiguous()
+    if inplace_final_state:
+        if initial_state is None or h0.data_ptr() != initial_state.data_ptr():
+            raise ValueError(f"{name}: inplace_final_state needs a contiguous fp32 initial_state")
+        final = h0
+    elif output_final_state:
+        final = torch.empty(n, hv, kd, vd, device=q.device, dtype=torch.float32)
+    else:
+        final = None
+    o = torch.empty(b, t, hv, vd, device=q.device, dtype=q.dtype)
+    if t > 0 or final is not None:
+        cu = cu_seqlens.contiguous() if cu_seqlens is not None else None
+        _lib.call(entry, _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.ptr(beta), _lib.ptr(h0),
+                  _lib.ptr(o), _lib.ptr(final), _lib.ptr(cu), b, t, h, hv, kd, vd, n,
+                  _lib.dtype_code(q.dtype), _lib.dtype_code(g.dtype), _lib.dtype_code(beta.dtype),
+                  scale, flags, _lib.ptr(A_log), _lib.ptr(dt_bias), _lib.stream_of(q))
+    if o.dtype != out_dtype:
+        o = o.to(out_dtype)
+    return o, final
+
+
+def chunk_gated_delta_rule(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    g: Tensor,
+    beta: Tensor,
+    scale: float | None = None,
+    initial_state: Tensor | None = None,
+    output_final_state: bool = False,
+    use_qk_l2norm_in_kernel: bool = False,
+    use_beta_sigmoid_in_kernel: bool = False,
+    allow_neg_eigval: bool = False,
+    state_v_first: bool = False,
+    cu_seqlens: Tensor | None = None,
+    cu_seqlens_cpu: Tensor | None = None,
+    cp_context=None,
+    use_gate_in_kernel: bool = False,
+    A_log: Tensor | None = None,
+    dt_bias: Tensor | None = None,
+):
+    """Chunked gated delta rule forward on gfx950 (fused MFMA prefill, 64-token chunks).
+
+    FLA 0.5.2 signature (``docs/superpowers/plans/2026-10-23-sorernn-v2-core.md:141``) plus the
+    gate kwargs soreRNN passes (``sore/model/gdn.py:157-162``). ``q,k [B,T,H,K]``, ``v [B,T,HV,V]``,
+    ``g,beta [B,T,HV]``; returns ``(o [B,T,HV,V] in v.dtype, final_state [N,HV,K,V] fp32 or None)``.
+    With ``cu_seqlens`` (``[N+1]``, needs ``B == 1``) the state and the chunking restart at every
+    document. ``cu_seqlens_cpu`` only serves to validate the bounds without a device sync; the
+    kernel's grid depends on ``N`` alone.
+    """
+    if allow_neg_eigval or state_v_first or cp_context is not None:
+        raise NotImplementedError("chunk_gated_delta_rule: allow_neg_eigval, state_v_first and cp_context are not supported")
+    return _gdn_call("gdn_chunk_fwd", "chunk_gated_delta_rule", q, k, v, g, beta, scale, initial_state,
+                     output_final_state, cu_seqlens, cu_seqlens_cpu, use_qk_l2norm_in_kernel,
+                     use_beta_sigmoid_in_kernel, use_gate_in_kernel, A_log, dt_bias)
+
+
+def fused_recurrent_gated_delta_rule(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    g: Tensor | None = None,
+    beta: Tensor | None = None,
+    scale: float | None = None,
+    initial_state: Tensor | None = None,
+    output_final_state: bool = False,
+    inplace_final_state: bool = False,
+    cu_seqlens: Tensor | None = None,
+    cu_seqlens_cpu: Tensor | None = None,
+    use_qk_l2norm_in_kernel: bool = False,
+    use_beta_sigmoid_in_kernel: bool = False,
+    use_gate_in_kernel: bool = False,
+    A_log: Tensor | None = None,
+    dt_bias: Tensor | None = None,
+):
+    """Token-by-token gated delta rule with the state on chip (the decode step at ``T == 1``).
+
+    Same layouts as ``chunk_gated_delta_rule``. ``g=None`` means no decay and ``beta=None`` means
+    ``beta = 1`` (FLA's defaults). With ``inplace_final_state=True`` the final state overwrites
+    ``initial_state`` (which must be contiguous fp32) and is returned.
+    """
+    b, t = q.shape[:2]
+    hv = v.shape[2]
+    if g is None:
+        g = torch.zeros(b, t, hv, device=q.device, dtype=torch.float32)
+    if beta is None:
+        beta = torch.ones(b, t, hv, device=q.device, dtype=torch.float32)
+    return _gdn_call("gdn_recurrent_fwd", "fused_recurrent_gated_delta_rule", q, k, v, g, beta, scale, initial_state,
+                     output_final_state or inplace_final_state, cu_seqlens, cu_seqlens_cpu, use_qk_l2norm_in_kernel,
+                     use_beta_sigmoid_in_kernel, use_gate_in_kernel, A_log, dt_bias,
+                     inplace_final_state=inplace_final_state)
+
+
+def gated_delta_decode_step(
+    x_qkv: Tensor,
+    conv_state: Tensor,
+    conv_weight: Tensor,
+    g: Tensor,
+    beta: Tensor,
+    state: Tensor,
+    num_qk_heads: int,
+    num_v_heads: int,
+    head_dim: int,
+    scale: float | None = None,
+    use_qk_l2norm_in_kernel: bool = True,
+    use_beta_sigmoid_in_kernel: bool = False,
+    use_gate_in_kernel: bool = False,
+    A_log: Tensor | None = None,
+    dt_bias: Tensor | None = None,
+    out: Tensor | None = None,
+) -> Tensor:
+    """One fused decode token per sequence; updates ``conv_state`` and ``state`` in place.
+
+    ``x_qkv [B, C]`` (or ``[B,1,C]``) is the pre-conv q|k|v projection with
+    ``C = 2*num_qk_heads*head_dim + num_v_heads*head_dim``; ``conv_state [B,C,W]`` (newest input
+    last); ``conv_weight [C,W]`` fp32; ``g,beta [B,HV]`` (or ``[B,1,HV]``); ``state [B,HV,D,D]``
+    fp32. Returns ``o [B,1,HV,D]`` in ``x_qkv.dtype`` (written into ``out`` when given).
+    """
+    name = "gated_delta_decode_step"
+    _check_cuda(name, x_qkv, conv_state, conv_weight, g, beta, state, A_log, dt_bias, out)
+    _no_grad_check(name, x_qkv, conv_state, conv_weight, g, beta, state)
+    b = x_qkv.shape[0]
+    x2 = x_qkv.reshape(b, -1)
+    c = x2.shape[1]
+    h, hv, d = num_qk_heads, num_v_heads, head_dim
+    if c != (2 * h + hv) * d:
+        raise ValueError(f"{name}: x_qkv has {c} channels, expected {(2 * h + hv) * d}")
+    if conv_state.dim() != 3 or tuple(conv_state.shape[:2]) != (b, c) or not conv_state.is_contiguous():
+        raise ValueError(f"{name}: conv_state must be a contiguous [B,C,W] = [{b},{c},W] tensor")
+    w = conv_state.shape[2]
+    if tuple(conv_weight.shape) != (c, w):
+        raise ValueError(f"{name}: conv_weight must be [C,W] = {(c, w)}")
+    if tuple(state.shape) != (b, hv, d, d) or state.dtype != torch.float32 or not state.is_contiguous():
+        raise ValueError(f"{name}: state must be a contiguous fp32 [B,HV,D,D] = {(b, hv, d, d)} tensor")
+    g2, b2 = g.reshape(b, -1).contiguous(), beta.reshape(b, -1).contiguous()
+    if g2.shape[1] != hv or b2.shape[1] != hv:
+        raise ValueError(f"{name}: g and beta must be [B,HV] = {(b, hv)}")
+    flags = 0
+    if use_qk_l2norm_in_kernel:
+        flags |= _lib.FLAG_QK_L2NORM
+    if use_beta_sigmoid_in_kernel:
+        flags |= _lib.FLAG_BETA_SIGMOID
+    if use_gate_in_kernel:
+        if A_log is None or dt_bias is None:
+            raise ValueError(f"{name}: use_gate_in_kernel needs A_log and dt_bias")
+        flags |= _lib.FLAG_GATE_IN_KERNEL
+        A_log = A_log.detach().float().contiguous()
+        dt_bias = dt_bias.detach().float().contiguous()
+    else:
+        A_log = dt_bias = None
+    wgt = conv_weight.detach().float().contiguous()
+    x2 = x2.contiguous()
+    if out is None:
+        out = torch.empty(b, 1, hv, d, device=x_qkv.device, dtype=x_qkv.dtype)
+    elif tuple(out.shape) != (b, 1, hv, d) or out.dtype != x_qkv.dtype or not out.is_contiguous():
+        raise ValueError(f"{name}: out must be a contiguous [B,1,HV,D] tensor of x_qkv's dtype")
+    _lib.call("gdn_decode_step", _lib.ptr(x2), _lib.ptr(conv_state), _lib.ptr(wgt), _lib.ptr(g2), _lib.ptr(b2),
+              _lib.ptr(state), _lib.ptr(out), b, h, hv, d, w, _lib.dtype_code(x2.dtype),
+              _lib.dtype_code(conv_state.dtype), _lib.dtype_code(g2.dtype), _lib.dtype_code(b2.dtype),
+              float(d**-0.5 if scale is None else scale), flags, _lib.ptr(A_log), _lib.ptr(dt_bias),
+              _lib.stream_of(x2))
+    return out
+
+
+def causal_conv1d(
+    x: Tensor,
+    weight: Tensor | None = None,
+    bias: Tensor | None = None,
+    residual: Tensor | None = None,
+    initial_state: Tensor | None = None,
+    output_final_state: bool = False,
+    activation: str | None = None,
+    cu_seqlens: Tensor | None = None,
+    cu_seqlens_cpu: Tensor | None = None,
+):
+    """Depthwise causal conv1d (+ SiLU) with per-document reset; returns ``(y, final_state | None)``.
+
+    ``x [B,T,C]``, ``weight [C,W]`` (``weight[:, W-1]`` multiplies the current token, as
+    ``sore/model/conv.py:7``), ``bias [C]``. ``initial_state``/``final_state`` are conv caches
+    ``[N,C,W]`` (newest input last). ``activation`` is None, "silu" or "swish".
+    """
+    name = "causal_conv1d"
+    if weight is None:
+        raise ValueError(f"{name}: weight is required")
+    if residual is not None:
+        raise NotImplementedError(f"{name}: residual is not supported")
+    _check_cuda(name, x, weight, bias, initial_state, cu_seqlens)
+    _no_grad_check(name, x, weight, bias, initial_state)
+    if x.dim() != 3 or weight.dim() != 2 or weight.shape[0] != x.shape[2]:
+        raise ValueError(f"{name}: expected x [B,T,C] and weight [C,W], got {tuple(x.shape)}, {tuple(weight.shape)}")
+    b, t, c = x.shape
+    w = weight.shape[1]
+    n, flags = _cu_info(name, cu_seqlens, cu_seqlens_cpu, b, t)
+    if activation in ("silu", "swish"):
+        act = _lib.ACT_SILU
+    elif activation is None:
+        act = _lib.ACT_NONE
+    else:
+        raise NotImplementedError(f"{name}: activation {activation!r} is not supported")
+    x = x.contiguous()
+    if initial_state is not None:
+        if tuple(initial_state.shape) != (n, c, w):
+            raise ValueError(f"{name}: initial_state must be [N,C,W] = {(n, c, w)}")
+        initial_state = initial_state.to(x.dtype).contiguous()
+    wgt = weight.detach().float().contiguous()
+    bs = None if bias is None else bias.detach().float().contiguous()
+    y = torch.empty_like(x)
+    fin = torch.empty(n, c, w, device=x.device, dtype=x.dtype) if output_final_state else None
+    cu = cu_seqlens.contiguous() if cu_seqlens is not None else None
+    _lib.call("gdn_causal_conv1d_fwd", _lib.ptr(x), _lib.ptr(wgt), _lib.ptr(bs), _lib.ptr(y), _lib.ptr(initial_state),
+              _lib.ptr(fin), _lib.ptr(cu), b, t, c, w, n, _lib.dtype_code(x.dtype), act, flags, _lib.stream_of(x))
+    return y, fin
+
+
+def l2norm(x: Tensor, eps: float = 1e-12) -> Tensor:
+    """``x / max(||x||_2, eps)`` over the last axis (``F.normalize`` semantics, fp32 math, one rounding)."""
+    _check_cuda("l2norm", x)
+    _no_grad_check("l2norm", x)
+    xc = x.contiguous()
+    y = torch.empty_like(xc)
+    d = xc.shape[-1]
+    _lib.call("gdn_l2norm_fwd", _lib.ptr(xc), _lib.ptr(y), xc.numel() // max(d, 1), d, _lib.dtype_code(xc.dtype),
+              float(eps), _lib.stream_of(xc))
+    return y
+
+
+def rms_norm_gated(
+    x: Tensor,
+    g: Tensor | None,
+    weight: Tensor | None,
+    bias: Tensor | None = None,
+    activation: str = "swish",
+    residual: Tensor | None = None,
+    prenorm: bool = False,
+    residual_in_fp32: bool = False,
+    eps: float = 1e-6,
+) -> Tensor:
+    """``x * rsqrt(mean(x^2) + eps) * weight (+ bias) * act(g)`` per row, fp32 math, one rounding.
+
+    ``activation`` is "swish"/"silu" (``sore/model/gdn.py:186``) or None (gate used as is).
+    """
+    name = "rms_norm_gated"
+    if residual is not None or prenorm:
+        raise NotImplementedError(f"{name}: residual/prenorm are not supported")
+    if activation in ("swish", "silu"):
+        act = _lib.ACT_SILU
+    elif activation is None:
+        act = _lib.ACT_NONE
+    else:
+        raise NotImplementedError(f"{name}: activation {activation!r} is not supported")
+    _check_cuda(name, x, g, weight, bias)
+    _no_grad_check(name, x, g, weight, bias)
+    xc = x.contiguous()
+    d = xc.shape[-1]
+    gc = None
+    if g is not None:
+        if g.shape != x.shape:
+            raise ValueError(f"{name}: gate shape {tuple(g.shape)} != x shape {tuple(x.shape)}")
+        gc = g.to(xc.dtype).contiguous()
+    wc = None if weight is None else weight.detach().float().contiguous()
+    bc = None if bias is None else bias.detach().float().contiguous()
+    if (wc is not None and wc.numel() != d) or (bc is not None and bc.numel() != d):
+        raise ValueError(f"{name}: weight/bias must have {d} entries")
+    y = torch.empty_like(xc)
+    _lib.call("gdn_rms_norm_gated_fwd", _lib.ptr(xc), _lib.ptr(gc), _lib.ptr(wc), _lib.ptr(bc), _lib.ptr(y),
+              xc.numel() // max(d, 1), d, _lib.dtype_code(xc.dtype), float(eps), act, _lib.stream_of(xc))
+    return y

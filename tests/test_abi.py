@@ -1,0 +1,51 @@
+"""CPU checks of the C ABI: libgdn.so loads, exports every entry point of include/gdn.h with the
+parameter counts the ctypes binding declares, and the host layer rejects bad calls before any launch.
+"""
+import os
+import re
+
+import pytest
+import torch
+
+from sorernn_amd import _lib
+from sorernn_amd import chunk_gated_delta_rule, fused_recurrent_gated_delta_rule
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "gdn.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for m in re.finditer(r"GDN_API\s+[\w\s\*]+?\b(gdn_\w+)\s*\(([^)]*)\)\s*;", text):
+        params = [p.strip() for p in m.group(2).split(",") if p.strip() and p.strip() != "void"]
+        out[m.group(1)] = len(params)
+    return out
+
+
+def test_header_declares_the_entry_points():
+    decl = _declared()
+    assert set(decl) == set(_lib.SIGNATURES), f"header {sorted(decl)} vs binding {sorted(_lib.SIGNATURES)}"
+
+
+def test_library_exports_every_declared_symbol_with_matching_arity():
+    lib = _lib.load()
+    for name, nparams in _declared().items():
+        assert hasattr(lib, name), f"{name} not exported by libgdn.so"
+        assert len(_lib.SIGNATURES[name]) == nparams, f"{name}: binding has {len(_lib.SIGNATURES[name])} params, header {nparams}"
+    assert lib.gdn_abi_version() == _lib.ABI_VERSION
+
+
+def test_no_cpu_path():
+    q = torch.randn(1, 4, 1, 64)
+    with pytest.raises(ValueError, match="GPU"):
+        chunk_gated_delta_rule(q, q, q, torch.zeros(1, 4, 1), torch.ones(1, 4, 1))
+    with pytest.raises(ValueError, match="GPU"):
+        fused_recurrent_gated_delta_rule(q, q, q, torch.zeros(1, 4, 1), torch.ones(1, 4, 1))
+
+
+def test_unsupported_options_raise():
+    q = torch.randn(1, 4, 1, 64)
+    with pytest.raises(NotImplementedError):
+        chunk_gated_delta_rule(q, q, q, torch.zeros(1, 4, 1), torch.ones(1, 4, 1), allow_neg_eigval=True)

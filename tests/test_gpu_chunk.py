@@ -1,0 +1,154 @@
+"""GPU parity of the fused chunked prefill kernel (``chunk_gated_delta_rule``) vs the CPU oracle.
+
+Small shapes compare against the oracle directly; the BASELINE config-1 size is compared against
+the oracle on a slice (one batch row, two heads, all 4096 tokens) and, in full, against the GPU
+recurrent kernel (exact fp32 token-by-token path), plus split invariance at full length.
+Tolerances: max-abs 2e-2 on bf16 outputs, relative L2 1e-3 on fp32 final states.
+"""
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import recurrent_gated_delta_rule
+from sorernn_amd import chunk_gated_delta_rule, fused_recurrent_gated_delta_rule
+from sorernn_amd.synthetic import config_inputs, gdn_inputs, varlen_cu_seqlens
+from tests.parity import assert_output_close, assert_state_close
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _chunk(inp, **kw):
+    d = inp.to(DEV)
+    o, st = chunk_gated_delta_rule(d.q, d.k, d.v, d.g, d.beta, scale=inp.scale, initial_state=d.h0,
+                                   output_final_state=True, cu_seqlens=d.cu_seqlens,
+                                   cu_seqlens_cpu=inp.cu_seqlens, **kw)
+    torch.cuda.synchronize()
+    return o, st
+
+
+def _oracle(inp):
+    cu = None if inp.cu_seqlens is None else inp.cu_seqlens.long()
+    return recurrent_gated_delta_rule(inp.q, inp.k, inp.v, inp.g, inp.beta, inp.scale, inp.h0, True, cu_seqlens=cu)
+
+
+@pytest.mark.parametrize("t", [256, 200, 65, 64, 1], ids=lambda t: f"T{t}")
+@pytest.mark.parametrize("h0", [False, True], ids=["zero_h0", "h0"])
+def test_chunk_small_matches_oracle(t, h0):
+    print(f"chunk T={t} h0={h0}", flush=True)
+    inp = gdn_inputs(1, t, 4, 64, dtype=torch.bfloat16, seed=1000, h0=h0)
+    o, st = _chunk(inp)
+    o_ref, st_ref = _oracle(inp)
+    assert_output_close(o.cpu(), o_ref)
+    assert_state_close(st.cpu(), st_ref)
+
+
+@pytest.mark.parametrize("kv", [(128, 128), (64, 64), (128, 64), (64, 128)], ids=lambda x: f"K{x[0]}V{x[1]}")
+def test_chunk_head_dims(kv):
+    kd, vd = kv
+    print(f"chunk K={kd} V={vd}", flush=True)
+    inp = gdn_inputs(2, 300, 3, kd, V=vd, dtype=torch.bfloat16, seed=7, h0=True)
+    o, st = _chunk(inp)
+    o_ref, st_ref = _oracle(inp)
+    assert_output_close(o.cpu(), o_ref)
+    assert_state_close(st.cpu(), st_ref)
+
+
+@pytest.mark.parametrize("cu", [[0, 1, 3, 4, 70, 200, 512], [0, 512], [0, 63, 64, 65, 129, 300]],
+                         ids=["short_docs", "one_doc", "chunk_edges"])
+@pytest.mark.parametrize("rep", [1, 2], ids=["no_gva", "gva2x"])
+def test_chunk_varlen_matches_oracle(cu, rep):
+    print(f"chunk varlen cu={cu} rep={rep}", flush=True)
+    cu_t = torch.tensor(cu, dtype=torch.long)
+    inp = gdn_inputs(1, cu[-1], 2, 128, HV=2 * rep, dtype=torch.bfloat16, seed=3, h0=True, cu_seqlens=cu_t)
+    o, st = _chunk(inp)
+    o_ref, st_ref = _oracle(inp)
+    assert_output_close(o.cpu(), o_ref)
+    assert_state_close(st.cpu(), st_ref)
+
+
+def test_chunk_kernel_options_match_oracle():
+    # raw inputs as sore/model/gdn.py passes them with gdn_kernel_gate: unnormalised q/k, a, b logits
+    gen = torch.Generator().manual_seed(31)
+    t, h, hv, d = 200, 2, 4, 128
+    q = (torch.randn(1, t, h, d, generator=gen) * 2).to(torch.bfloat16)
+    k = (torch.randn(1, t, h, d, generator=gen) * 2).to(torch.bfloat16)
+    v = torch.randn(1, t, hv, d, generator=gen).to(torch.bfloat16)
+    a = torch.randn(1, t, hv, generator=gen).to(torch.bfloat16)
+    b = torch.randn(1, t, hv, generator=gen).to(torch.bfloat16)
+    A_log = torch.empty(hv).uniform_(1, 16, generator=gen).log()
+    dt_bias = torch.randn(hv, generator=gen) * 0.3
+    cu = torch.tensor([0, 5, 77, 200])
+    dev = lambda x: x.to(DEV)  # noqa: E731
+    o, st = chunk_gated_delta_rule(dev(q), dev(k), dev(v), dev(a), dev(b), initial_state=None, output_final_state=True,
+                                   use_qk_l2norm_in_kernel=True, use_beta_sigmoid_in_kernel=True,
+                                   use_gate_in_kernel=True, A_log=dev(A_log), dt_bias=dev(dt_bias),
+                                   cu_seqlens=dev(cu), cu_seqlens_cpu=cu)
+    g_ref = -A_log.exp() * F.softplus(a.float() + dt_bias)
+    qn = F.normalize(q.float(), dim=-1).to(torch.bfloat16)
+    kn = F.normalize(k.float(), dim=-1).to(torch.bfloat16)
+    o_ref, st_ref = recurrent_gated_delta_rule(qn, kn, v, g_ref, b.float().sigmoid(), d**-0.5, None, True, cu_seqlens=cu)
+    assert_output_close(o.cpu(), o_ref)
+    assert_state_close(st.cpu(), st_ref)
+
+
+def test_chunk_matches_recurrent_kernel_config1_full_size():
+    inp = config_inputs(1)
+    print("config1 full size", flush=True)
+    o, st = _chunk(inp)
+    d = inp.to(DEV)
+    o_r, st_r = fused_recurrent_gated_delta_rule(d.q, d.k, d.v, d.g, d.beta, scale=inp.scale, initial_state=d.h0,
+                                                 output_final_state=True)
+    torch.cuda.synchronize()
+    assert_output_close(o, o_r.float())
+    assert_state_close(st, st_r)
+    # the oracle on a slice: batch row 1, heads 5 and 11, all 4096 tokens
+    sl = lambda x: x[1:2, :, [5, 11]]  # noqa: E731
+    o_ref, st_ref = recurrent_gated_delta_rule(sl(inp.q), sl(inp.k), sl(inp.v), sl(inp.g), sl(inp.beta), inp.scale,
+                                               inp.h0[1:2, [5, 11]], True)
+    assert_output_close(o[1:2, :, [5, 11]].cpu(), o_ref)
+    assert_state_close(st[1:2, [5, 11]].cpu(), st_ref)
+
+
+def test_chunk_split_invariance_config1():
+    inp = config_inputs(1).to(DEV)
+    kw = dict(scale=inp.scale, output_final_state=True)
+    o, st = chunk_gated_delta_rule(inp.q, inp.k, inp.v, inp.g, inp.beta, initial_state=inp.h0, **kw)
+    t1 = 1000  # not a multiple of 64: the second call's chunks are shifted
+    o1, s1 = chunk_gated_delta_rule(inp.q[:, :t1], inp.k[:, :t1], inp.v[:, :t1], inp.g[:, :t1], inp.beta[:, :t1],
+                                    initial_state=inp.h0, **kw)
+    o2, s2 = chunk_gated_delta_rule(inp.q[:, t1:], inp.k[:, t1:], inp.v[:, t1:], inp.g[:, t1:], inp.beta[:, t1:],
+                                    initial_state=s1, **kw)
+    assert_output_close(torch.cat([o1, o2], 1), o.float())
+    assert_state_close(s2, st)
+
+
+def test_chunk_varlen_config3_matches_recurrent_kernel():
+    inp = config_inputs(3)
+    print("config3 varlen", inp.cu_seqlens.tolist(), flush=True)
+    o, st = _chunk(inp)
+    d = inp.to(DEV)
+    o_r, st_r = fused_recurrent_gated_delta_rule(d.q, d.k, d.v, d.g, d.beta, scale=inp.scale, initial_state=d.h0,
+                                                 output_final_state=True, cu_seqlens=d.cu_seqlens,
+                                                 cu_seqlens_cpu=inp.cu_seqlens)
+    torch.cuda.synchronize()
+    assert st.shape == (8, 16, 128, 128)
+    assert_output_close(o, o_r.float())
+    assert_state_close(st, st_r)
+
+
+def test_varlen_generator_sums_exactly():
+    cu = varlen_cu_seqlens(8, 32768, 512, 8192, 1003)
+    assert cu[0] == 0 and cu[-1] == 32768 and (cu[1:] > cu[:-1]).all()
+
+
+def test_chunk_extreme_inputs_stay_finite():
+    # x100 inputs (reference test_gdn.py:60-71): large |g| drives exp(gam) to 0; nothing may be NaN
+    inp = gdn_inputs(1, 130, 2, 64, dtype=torch.bfloat16, seed=5, h0=True)
+    inp.g = inp.g * 100
+    inp.v = (inp.v.float() * 100).to(torch.bfloat16)
+    o, st = _chunk(inp)
+    assert torch.isfinite(o).all() and torch.isfinite(st).all()
+    o_ref, st_ref = _oracle(inp)
+    assert_output_close(o.cpu(), o_ref, tol=2e-2 * float(o_ref.abs().max()))
+    assert_state_close(st.cpu(), st_ref)

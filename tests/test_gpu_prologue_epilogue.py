@@ -1,0 +1,83 @@
+"""GPU parity: causal conv1d (+SiLU, caches, varlen), L2 norm and gated RMSNorm vs the CPU oracle."""
+import pytest
+import torch
+
+from oracle import (
+    causal_conv1d_silu,
+    causal_conv1d_varlen,
+    conv_state_from_sequence,
+    doc_ids_from_cu_seqlens,
+    l2norm as l2norm_ref,
+    rms_norm_gated as rms_norm_gated_ref,
+)
+from sorernn_amd import causal_conv1d, l2norm, rms_norm_gated
+from tests.parity import assert_output_close
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("cu", [None, [0, 1, 3, 4, 70, 200, 300]], ids=["rows", "varlen"])
+def test_conv_matches_oracle(dtype, cu):
+    gen = torch.Generator().manual_seed(1)
+    b = 2 if cu is None else 1
+    x = torch.randn(b, 300, 384, generator=gen).to(dtype)
+    w = torch.randn(384, 4, generator=gen) * 0.5
+    cu_t = None if cu is None else torch.tensor(cu)
+    y, fin = causal_conv1d(x.to(DEV), w.to(DEV), activation="silu", output_final_state=True,
+                           cu_seqlens=None if cu_t is None else cu_t.to(DEV), cu_seqlens_cpu=cu_t)
+    y_ref = causal_conv1d_silu(x, w, cu_t)
+    assert_output_close(y.cpu(), y_ref, tol=1e-2 if dtype == torch.bfloat16 else 1e-5)
+    assert torch.equal(fin.cpu(), conv_state_from_sequence(x, 4, cu_t))
+
+
+def test_conv_tap_order_and_no_activation():
+    x = torch.zeros(1, 5, 64)
+    x[0, 2, :] = 1.0
+    w = torch.zeros(64, 3)
+    w[:, 0], w[:, 1], w[:, 2] = 1.0, 10.0, 100.0
+    y, _ = causal_conv1d(x.to(DEV), w.to(DEV), activation=None)
+    assert y[0, :, 0].cpu().tolist() == [0.0, 0.0, 100.0, 10.0, 1.0]
+
+
+def test_conv_initial_state_continues_sequence():
+    gen = torch.Generator().manual_seed(2)
+    x = torch.randn(1, 50, 128, generator=gen)
+    w = torch.randn(128, 4, generator=gen)
+    full, _ = causal_conv1d(x.to(DEV), w.to(DEV), activation="silu")
+    _, cache = causal_conv1d(x[:, :20].to(DEV), w.to(DEV), activation="silu", output_final_state=True)
+    tail, _ = causal_conv1d(x[:, 20:].to(DEV), w.to(DEV), activation="silu", initial_state=cache)
+    assert_output_close(tail.cpu(), full[:, 20:].cpu(), tol=1e-5)
+
+
+def test_conv_nan_does_not_leak_across_documents():
+    cu = torch.tensor([0, 4, 9])
+    x = torch.randn(1, 9, 64)
+    x[:, 3] = float("nan")
+    y, _ = causal_conv1d(x.to(DEV), torch.randn(64, 4).to(DEV), cu_seqlens=cu.to(DEV), cu_seqlens_cpu=cu)
+    y = y.cpu()
+    assert torch.isfinite(y[:, 4:]).all() and torch.isnan(y[:, 3]).all()
+    ids = doc_ids_from_cu_seqlens(cu, 9)
+    ref = causal_conv1d_varlen(x.double(), torch.zeros(64, 4, dtype=torch.float64), ids)
+    assert ref.shape == y.shape
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_l2norm_matches_oracle(dtype):
+    x = (torch.randn(37, 3, 128) * 4).to(dtype)
+    x[0, 0] = 0
+    y = l2norm(x.to(DEV)).cpu()
+    assert_output_close(y, l2norm_ref(x), tol=1e-2 if dtype == torch.bfloat16 else 1e-6)
+    assert (y[0, 0] == 0).all()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("d", [64, 128])
+def test_rms_norm_gated_matches_oracle(dtype, d):
+    gen = torch.Generator().manual_seed(3)
+    x = torch.randn(4, 33, 16, d, generator=gen).to(dtype)
+    gate = torch.randn(4, 33, 16, d, generator=gen).to(dtype)
+    w = torch.randn(d, generator=gen)
+    y = rms_norm_gated(x.to(DEV), gate.to(DEV), w.to(DEV), None, activation="swish", eps=1e-6).cpu()
+    assert_output_close(y, rms_norm_gated_ref(x, gate, w, 1e-6), tol=2e-2 if dtype == torch.bfloat16 else 1e-5)
