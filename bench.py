@@ -1,0 +1,267 @@
+#!/usr/bin/env python3
+"""Benchmark of the GDN token-mixing path on one MI355X (BASELINE.json metric).
+
+``python bench.py [--gpus 1] [--steps K] [--warmup W]`` prints ONE JSON line. A step is one
+``chunk_gated_delta_rule`` call over BASELINE config 1 (B=4, T=4096, H=16, d_k=d_v=128, bf16 q/k/v,
+fp32 g/beta/h0, final state out), inputs already resident in HBM; ``value`` is prefill tokens/s.
+
+The same line carries
+- ``roofline``: the fused chunk kernel against bf16 dense MFMA peak, from HIP events around each
+  launch on the stream it runs on; algorithmic FLOPs per launch = (10 C^2 d + 6 C d^2) per
+  (chunk, head) x 4096 chunk-heads = 47,244,640,256 (C = 64, d = 128, solve excluded);
+  ``traffic`` (HBM bytes per launch) comes from the committed rocprofv3 PMC summary when present;
+- ``decode``: config 2, 1000 back-to-back fused decode steps (conv cache + SiLU + L2 norm + state
+  update, state updated in place) with HBM bytes/step = 141,664,256, plus a run rotating over
+  5 state copies (335 MB > the 256 MB Infinity Cache) that forces DRAM traffic;
+- ``varlen``: config 3 (8 packed documents, 32768 tokens);
+- ``cpu_baseline``: the CPU oracle (``oracle/``, torch fp32 recurrence) on the GPU box's host
+  cores over the full config-1 input, plus 100 decode steps of config 2.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+BF16_PEAK_TFLOPS = 2516.6  # MI355X dense bf16 MFMA
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+C = 64
+
+
+def chunk_flops(lengths, heads: int, d: int) -> int:
+    """Algorithmic forward FLOPs: sum over chunks of (10 c^2 d + 6 c d^2) x heads, c = real chunk length."""
+    total = 0
+    for L in lengths:
+        full, rem = divmod(L, C)
+        total += full * (10 * C * C * d + 6 * C * d * d)
+        if rem:
+            total += 10 * rem * rem * d + 6 * rem * d * d
+    return total * heads
+
+
+def decode_bytes(B=64, H=16, HV=16, D=128, W=4) -> int:
+    state = B * HV * D * D * 4 * 2  # read + write
+    ch = (2 * H + HV) * D
+    qkv = B * ch * 2  # pre-conv q|k|v bf16
+    out = B * HV * D * 2
+    gates = B * HV * 4 * 2
+    conv = B * ch * W * 2 * 2 + ch * W * 4  # cache read + write, fp32 weight
+    return state + qkv + out + gates + conv
+
+
+def time_launches(torch, fn, steps: int) -> tuple[float, float]:
+    """(mean ms per step from one event pair over all steps, mean ms per launch from per-launch event pairs)."""
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for i in range(steps):
+        starts[i].record(stream)
+        fn()
+        ends[i].record(stream)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    per_launch = sum(s.elapsed_time(e) for s, e in zip(starts, ends)) / steps
+    return e0.elapsed_time(e1) / steps, per_launch
+
+
+def load_traffic(name: str):
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get(name)
+
+
+def cpu_baseline(torch, decode_steps: int = 100):
+    """The CPU oracle timed on this host: config-1 prefill (full input) and config-2 decode steps."""
+    from oracle import decode_step_ref, recurrent_gated_delta_rule
+    from sorernn_amd.synthetic import config_inputs, decode_inputs
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    inp = config_inputs(1)
+    times = []
+    for _ in range(2):
+        t0 = time.perf_counter()
+        recurrent_gated_delta_rule(inp.q, inp.k, inp.v, inp.g, inp.beta, inp.scale, inp.h0, True)
+        times.append(time.perf_counter() - t0)
+    best = min(times)
+    tokens = inp.q.shape[0] * inp.q.shape[1]
+    di = decode_inputs()
+    conv, st = di.conv_state.clone(), di.state.clone()
+    t0 = time.perf_counter()
+    for _ in range(decode_steps):
+        _, conv, st = decode_step_ref(di.x_qkv, conv, di.conv_weight, di.g, di.beta, st, di.H, di.HV, di.D)
+    dec_us = (time.perf_counter() - t0) / decode_steps * 1e6
+    cpu = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            cpu = next(ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name"))
+    except Exception:
+        pass
+    return {
+        "value": round(tokens / best, 1),
+        "unit": "tokens/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"full config 1 (B=4,T=4096,H=16,d=128) through the oracle's torch fp32 recurrence, best of {len(times)} "
+                  f"({', '.join(f'{t:.2f}' for t in times)} s); decode: {decode_steps} config-2 steps incl. conv cache",
+        "decode_us_per_step": round(dec_us, 1),
+        "cpu_model": cpu,
+        "torch": torch.__version__,
+        "host": platform.node(),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--decode-steps", type=int, default=1000)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(f"bench.py: this build runs one GPU only (the GDN op needs no collective: every (sequence, head) "
+              f"chain is independent); got --gpus {args.gpus}. Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 1
+    from sorernn_amd import chunk_gated_delta_rule, gated_delta_decode_step
+    from sorernn_amd.synthetic import config_inputs, decode_inputs
+
+    dev = "cuda"
+    # ------------------------------------------------------------------ config 1: prefill
+    inp = config_inputs(1).to(dev)
+    B, T, H, K = inp.q.shape
+
+    def step():
+        return chunk_gated_delta_rule(inp.q, inp.k, inp.v, inp.g, inp.beta, scale=inp.scale, initial_state=inp.h0,
+                                      output_final_state=True)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ms_step, ms_launch = time_launches(torch, step, args.steps)
+    wall = (time.perf_counter() - t0) / args.steps * 1e3
+    flops = chunk_flops([T] * B, H, K)
+    achieved = flops / (ms_launch * 1e-3) / 1e12
+    tok_s = B * T / (ms_step * 1e-3)
+    min_bytes = 4 * inp.q.numel() * 2 + 2 * inp.g.numel() * 4 + 2 * inp.h0.numel() * 4
+    traffic = load_traffic("gated_delta_chunk_kernel")
+
+    # ------------------------------------------------------------------ config 2: decode
+    di = decode_inputs()
+    x, cs, cw, g, b, st = (t.to(dev) for t in (di.x_qkv, di.conv_state, di.conv_weight, di.g, di.beta, di.state))
+    out = torch.empty(di.x_qkv.shape[0], 1, di.HV, di.D, device=dev, dtype=di.x_qkv.dtype)
+
+    def dstep(state=st, conv=cs):
+        gated_delta_decode_step(x, conv, cw, g, b, state, di.H, di.HV, di.D, out=out)
+
+    for _ in range(10):
+        dstep()
+    dec_ms, dec_launch = time_launches(torch, dstep, args.decode_steps)
+    nrot = 5
+    states = [st.clone() for _ in range(nrot)]
+    convs = [cs.clone() for _ in range(nrot)]
+    it = [0]
+
+    def dstep_rot():
+        i = it[0] % nrot
+        it[0] += 1
+        dstep(states[i], convs[i])
+
+    for _ in range(nrot):
+        dstep_rot()
+    rot_ms, rot_launch = time_launches(torch, dstep_rot, args.decode_steps)
+    dbytes = decode_bytes()
+    del states, convs
+
+    # ------------------------------------------------------------------ config 3: varlen
+    v3 = config_inputs(3)
+    cu_cpu = v3.cu_seqlens
+    v3 = v3.to(dev)
+
+    def vstep():
+        return chunk_gated_delta_rule(v3.q, v3.k, v3.v, v3.g, v3.beta, scale=v3.scale, initial_state=v3.h0,
+                                      output_final_state=True, cu_seqlens=v3.cu_seqlens, cu_seqlens_cpu=cu_cpu)
+
+    for _ in range(3):
+        vstep()
+    v_ms, v_launch = time_launches(torch, vstep, max(5, args.steps // 5))
+    lens = (cu_cpu[1:] - cu_cpu[:-1]).tolist()
+    v_flops = chunk_flops(lens, 16, 128)
+
+    result = {
+        "metric": "GDN prefill tokens/s & decode-step µs (H=16,d=128); % of MI355X roofline",
+        "value": round(tok_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "wall_ms_per_step": round(wall, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded CPU generator, BASELINE config 1 distributions)",
+        "config": {"workload": "config1 chunked GDN prefill: B=4, T=4096, H=HV=16, d_k=d_v=128, chunk=64, "
+                               "bf16 q/k/v, fp32 g/beta/h0, output_final_state",
+                   "global_batch": B, "seq_len": T, "parallelism": "single GPU"},
+        "roofline": {
+            "bound": "mfma",
+            "kernel": "gated_delta_chunk_kernel",
+            "achieved": round(achieved, 2),
+            "peak": BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
+            "traffic": traffic,
+            "flops_per_launch": flops,
+            "min_hbm_bytes_per_launch": min_bytes,
+            "hbm_frac_at_min_bytes": round(min_bytes / (ms_launch * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "ms_per_launch": round(ms_launch, 4),
+        },
+        "decode": {
+            "workload": "config2: B=64, H=HV=16, D=128, conv cache [64,6144,4] bf16, fp32 state in place",
+            "us_per_step": round(dec_ms * 1e3, 3),
+            "us_per_launch": round(dec_launch * 1e3, 3),
+            "bytes_per_step": dbytes,
+            "achieved_GBs": round(dbytes / (dec_launch * 1e-3) / 1e9, 1),
+            "frac_hbm_peak": round(dbytes / (dec_launch * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "rotating_5_states_us_per_launch": round(rot_launch * 1e3, 3),
+            "rotating_achieved_GBs": round(dbytes / (rot_launch * 1e-3) / 1e9, 1),
+            "rotating_frac_hbm_peak": round(dbytes / (rot_launch * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "steps": args.decode_steps,
+        },
+        "varlen": {
+            "workload": "config3: 8 packed docs, 32768 tokens, H=16, d=128, per-doc h0 and final states",
+            "doc_lengths": lens,
+            "tokens_per_s": round(32768 / (v_ms * 1e-3), 1),
+            "ms_per_launch": round(v_launch, 4),
+            "tflops": round(v_flops / (v_launch * 1e-3) / 1e12, 2),
+            "frac_mfma_peak": round(v_flops / (v_launch * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+        },
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(torch)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,27 +1,36 @@
 // Fused chunked gated delta rule forward (prefill) for gfx950: bf16 MFMA, 64-token chunks, the fp32
 // state held in MFMA accumulators across the whole sequence.
 //
-// Work split: one workgroup (4 waves) per (sequence, value head, 32-column slice of V). The state
-// columns evolve independently, so the slice's state S_b [K x 32] never leaves the workgroup; the
-// K-side of a chunk (k.k and k.q Gram tiles, the triangular solve) is recomputed by each of the
-// V/32 slices. Workgroups of one (sequence, head) are placed on the same XCD so the q/k tiles they
+// Work split: one workgroup (8 waves, two per SIMD) per (sequence, value head, 32-column slice of V).
+// The state columns evolve independently, so the slice's state S_b [K x 32] never leaves the
+// workgroup; the K-side of a chunk (Gram tiles and the triangular solve) is recomputed by each of the
+// V/32 slices. The slices of one (sequence, head) are placed on the same XCD, so the q/k tiles they
 // all read come from one L2.
 //
 // Per chunk of c <= 64 tokens with gam = in-chunk cumsum of g (sore/model/gdn_ref.py:17-21 in
-// chunk form, the algebra restated in oracle/gdn_oracle.py::_chunk_segment):
+// chunk form; the algebra is restated in oracle/gdn_oracle.py::_chunk_segment):
 //   A_tj  = beta_t exp(gam_t - gam_j) k_t.k_j   (j < t)          T = (I + A)^-1
 //   X     = diag(beta) V - diag(beta exp(gam)) K S              Delta = T X = X + (T - I) X
 //   O     = scale (diag(exp(gam)) Q S + P Delta),  P_tj = exp(gam_t - gam_j) q_t.k_j  (j <= t)
 //   S'    = exp(gam_c) S + K^T diag(exp(gam_c - gam)) Delta
-// Precision: q/k/v are bf16 already, so the Gram tiles are exact products with fp32 accumulation.
-// S, X and Delta enter MFMA as single bf16; the state update's right operand is split into bf16
-// hi + lo (two MFMAs), which keeps the fp32 final state within 1e-3 relative L2 over 64 chunks.
-// T is built in fp32: the four 16x16 diagonal blocks by forward substitution, then two merge levels
-// (16 -> 32 -> 64) with fp32 MFMA.
+//
+// Two-stage software pipeline: iteration i runs the state-dependent work of chunk i (S-side) and
+// the state-independent work of chunk i+1 (K-side: A, the diagonal 16x16 inverses, the 16->32->64
+// merges of T), so the solve's latency overlaps the state chain. Phases (one barrier each):
+//   A: S: Y = K S, Z = Q S, X, P.        K: Gram k.k tiles -> A; diagonal inverses of T.
+//   B: S: Delta = X + (T - I) X.         K: 16 -> 32 merges of T.
+//   C: S: O, S' = e^{gam_c} S + K^T Delta~.   K: 32 -> 64 merge of T.
+//   stage: write the prefetched tiles of the chunk after next (global loads issued in phase A).
+//
+// Precision: q/k/v are bf16, so Gram tiles are exact products with fp32 accumulation. S, X and
+// Delta enter MFMA as single bf16; the state update's right operand is split into bf16 hi + lo (two
+// MFMAs), which keeps the fp32 final state within 1e-3 relative L2 over 64 chunks. T is built in
+// fp32: diagonal blocks by forward substitution, merges with three-term bf16 products
+// (hi*hi + hi*lo + lo*hi, about 2^-16 relative), and rounded to bf16 once as an MFMA operand.
 //
 // LDS operand layouts (bf16 rows padded by 8 elements):
-//   Kc, Qc [token][key]  natural tiles: A/B operands with the key dim contiguous; K^T for the state
-//                        update is read with ds_read_b64_tr_b16 (token-contiguous fragments).
+//   Kc, Qc [token][key]  natural tiles (two chunk buffers): A/B operands with the key dim contiguous;
+//                        K^T for the state update is read with ds_read_b64_tr_b16.
 //   Sb [v][key], Xb/Db/DtH/DtL [v][token], Tb/Pb [t][j]: written from accumulators with 8-byte stores.
 
 #include "gdn_common.h"
@@ -42,24 +51,27 @@ struct ChunkParams {
   const float *A_log, *dt_bias;
 };
 
-constexpr int kC = 64;       // chunk length
-constexpr int kVB = 32;      // value columns per workgroup
-constexpr int kNT = 256;     // threads per workgroup (4 waves)
-constexpr int kCP = kC + 8;  // bf16 pitch of [*][64] operand tiles (144 B rows)
-constexpr int kFP = kC + 4;  // fp32 pitch of 64x64 matrices (272 B rows)
+constexpr int kC = 64;        // chunk length
+constexpr int kVB = 32;       // value columns per workgroup
+constexpr int kNT = 512;      // threads per workgroup (8 waves)
+constexpr int kCP = kC + 8;   // bf16 pitch of [*][64] operand tiles (144 B rows)
 constexpr int kVP = kVB + 8;  // bf16 pitch of the V slice (80 B rows)
+constexpr int kAdP = 20;      // fp32 pitch of the transposed diagonal A blocks
+constexpr int kAoP = 52;      // fp32 pitch of the off-diagonal A rows 16..63 x cols 0..47
+constexpr int kTfP = 36;      // fp32 pitch of the two 32x32 T blocks and the merge scratch
 
 typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+typedef short i16x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ bf16x8 ld8(const bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
 __device__ __forceinline__ f32x4 mma(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
-__device__ __forceinline__ f32x4 mma_f32(float a, float b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+__device__ __forceinline__ f32x4 mma16(bf16x4 a, bf16x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, a), __builtin_bit_cast(i16x4, b), c, 0, 0, 0);
 }
 
-// Transposed A/B fragment from a row-major bf16 LDS tile M (pitch in elements): lane (g = lane/16,
+// Transposed fragment from a row-major bf16 LDS tile M (pitch in elements): lane (g = lane/16,
 // i = lane%16) receives M[j0 + 8g + m][c0 + i] for m = 0..7, i.e. the fragment of M^T with rows
 // c0.. and the contraction index j0.. contiguous. Each ds_read_b64_tr_b16 covers 4 rows: inside a
 // group of 16 lanes, lane 4m+q reads row m at columns c0+4q..+3 and the instruction hands lane i
@@ -77,27 +89,51 @@ __device__ __forceinline__ bf16x4 to_bf16x4(float a, float b, float c, float d) 
   return bf16x4{static_cast<bf16>(a), static_cast<bf16>(b), static_cast<bf16>(c), static_cast<bf16>(d)};
 }
 
+// fp32 x4 -> bf16 hi and lo parts (x ~= hi + lo to about 2^-16 relative)
+__device__ __forceinline__ void split4(float a, float b, float c, float d, bf16x4& hi, bf16x4& lo) {
+  hi = to_bf16x4(a, b, c, d);
+  lo = to_bf16x4(a - (float)hi[0], b - (float)hi[1], c - (float)hi[2], d - (float)hi[3]);
+}
+
+// Three-term bf16 product step for a 16x16x16 fp32 tile: acc += A(4 k) * B(4 k).
+__device__ __forceinline__ f32x4 mma16x3(const float (&a)[4], const float (&b)[4], f32x4 acc) {
+  bf16x4 ah, al, bh, bl;
+  split4(a[0], a[1], a[2], a[3], ah, al);
+  split4(b[0], b[1], b[2], b[3], bh, bl);
+  acc = mma16(ah, bh, acc);
+  acc = mma16(ah, bl, acc);
+  acc = mma16(al, bh, acc);
+  return acc;
+}
+
+struct ChunkSmem {
+  float gam[2][kC], egam[2][kC], bet[2][kC], begam[2][kC], dlast[2][kC];
+};
+
 template <int KD, int VD>
 __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p) {
   constexpr int NVB = VD / kVB;
   constexpr int KP = KD + 8;       // bf16 pitch of the q/k tiles
   constexpr int KS = KD / 32;      // MFMA k-steps over the key dim
-  constexpr int SMT = KD / 64;     // 16-row state tiles per wave
   constexpr int KCH = KD / 8;      // 16-byte chunks per q/k row
+  constexpr int QKPT = kC * KCH / kNT;  // q/k 16-byte chunks per thread per matrix
+  constexpr int STW = KD / 64;     // state tiles (16 x 16) per wave
 
-  __shared__ __align__(16) bf16 Kc[kC * KP];
-  __shared__ __align__(16) bf16 Qc[kC * KP];
+  __shared__ __align__(16) bf16 Kc[2][kC * KP];
+  __shared__ __align__(16) bf16 Qc[2][kC * KP];
   __shared__ __align__(16) bf16 Vc[kC * kVP];
   __shared__ __align__(16) bf16 Sb[kVB * KP];
-  __shared__ __align__(16) float Af[kC * kFP];
-  __shared__ __align__(16) float Tf[kC * kFP];
-  __shared__ __align__(16) bf16 Tb[kC * kCP];
+  __shared__ __align__(16) float Ad[4][16 * kAdP];       // diagonal A blocks, transposed: Ad[b][m][r] = A[16b+r][16b+m]
+  __shared__ __align__(16) float Ao[48 * kAoP];          // A rows 16..63 x cols 0..47 (off-diagonal lower blocks)
+  __shared__ __align__(16) float Tf[2][32 * kTfP];       // T[0:32][0:32] and T[32:64][32:64] in fp32
+  __shared__ __align__(16) float Wsc[32 * kTfP];         // merge scratch
+  __shared__ __align__(16) bf16 Tb[2][kC * kCP];         // T - I in bf16, A operand [t][j], per chunk parity
   __shared__ __align__(16) bf16 Pb[kC * kCP];
   __shared__ __align__(16) bf16 Xb[kVB * kCP];
   __shared__ __align__(16) bf16 Db[kVB * kCP];
   __shared__ __align__(16) bf16 DtH[kVB * kCP];
   __shared__ __align__(16) bf16 DtL[kVB * kCP];
-  __shared__ float gam[kC], egam[kC], bet[kC], begam[kC], dlast[kC];
+  __shared__ ChunkSmem gv;
 
   const int t = threadIdx.x, lane = t & 63, w = t >> 6, g4 = lane >> 4, li = lane & 15;
 
@@ -121,44 +157,54 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
     bos = n * p.T;
     eos = bos + p.T;
   }
+  const int nc = (int)((eos - bos + kC - 1) / kC);
   const bool l2 = p.flags & GDN_FLAG_QK_L2NORM;
   const bf16* __restrict__ qg = static_cast<const bf16*>(p.q);
   const bf16* __restrict__ kg = static_cast<const bf16*>(p.k);
   const bf16* __restrict__ vg = static_cast<const bf16*>(p.v);
   bf16* __restrict__ og = static_cast<bf16*>(p.o);
 
-  // T - I and P are strictly/causally lower: their upper blocks stay zero for the whole run
-  for (int e = t; e < kC * kCP / 8; e += kNT) {
-    reinterpret_cast<bf16x8*>(Tb)[e] = bf16x8{};
-    reinterpret_cast<bf16x8*>(Pb)[e] = bf16x8{};
-  }
-
-  // state slice: wave w owns key rows [16*SMT*w, 16*SMT*(w+1)) x 32 columns as 2*SMT accumulators
-  f32x4 sacc[SMT][2];
-  const int64_t sbase = (n * p.HV + hv) * (int64_t)KD * VD + vb * kVB;
-#pragma unroll
-  for (int mt = 0; mt < SMT; ++mt) {
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      const int kd0 = 16 * (w * SMT + mt) + 4 * g4, vv = 16 * nt + li;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) sacc[mt][nt][i] = p.h0 ? p.h0[sbase + (int64_t)(kd0 + i) * VD + vv] : 0.f;
-      *reinterpret_cast<bf16x4*>(Sb + vv * KP + kd0) =
-          to_bf16x4(sacc[mt][nt][0], sacc[mt][nt][1], sacc[mt][nt][2], sacc[mt][nt][3]);
-    }
-  }
-
-  for (int64_t c0 = bos; c0 < eos; c0 += kC) {
+  // ------------------------------------------------------------------ prefetch registers
+  bf16x8 pk[QKPT], pq[QKPT], pv{};
+  float pgv = 0.f, pbv = 0.f;
+  // K/Q/gates of chunk c (into registers)
+  auto fetch_kq = [&](int c) {
+    const int64_t c0 = bos + (int64_t)c * kC;
     const int len = (int)((eos - c0) < kC ? (eos - c0) : kC);
-    // ---------------------------------------------------------------- stage the chunk
-    for (int e = t; e < kC * KCH; e += kNT) {
-      const int row = e / KCH, c8 = e % KCH;
-      bf16x8 kv{}, qv{};
-      if (row < len) {
+#pragma unroll
+    for (int u = 0; u < QKPT; ++u) {
+      const int e = t + u * kNT, row = e / KCH, c8 = e % KCH;
+      pk[u] = bf16x8{};
+      pq[u] = bf16x8{};
+      if (c < nc && row < len) {
         const int64_t base = ((c0 + row) * p.H + h) * KD + c8 * 8;
-        kv = *reinterpret_cast<const bf16x8*>(kg + base);
-        qv = *reinterpret_cast<const bf16x8*>(qg + base);
+        pk[u] = *reinterpret_cast<const bf16x8*>(kg + base);
+        pq[u] = *reinterpret_cast<const bf16x8*>(qg + base);
       }
+    }
+    pgv = 0.f;
+    pbv = 0.f;
+    if (w == 0 && c < nc && lane < len) {
+      const int64_t gi = (c0 + lane) * p.HV + hv;
+      pgv = load_as_f32(p.g, p.dg, gi);
+      pbv = load_as_f32(p.beta, p.db, gi);
+    }
+  };
+  auto fetch_v = [&](int c) {
+    const int64_t c0 = bos + (int64_t)c * kC;
+    const int len = (int)((eos - c0) < kC ? (eos - c0) : kC);
+    pv = bf16x8{};
+    if (t < kC * 4 && c < nc) {
+      const int row = t >> 2, c8 = t & 3;
+      if (row < len) pv = *reinterpret_cast<const bf16x8*>(vg + ((c0 + row) * p.HV + hv) * VD + vb * kVB + c8 * 8);
+    }
+  };
+  // registers -> LDS buffer `buf` (K/Q/gates) and the V slice
+  auto stage_kq = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < QKPT; ++u) {
+      const int e = t + u * kNT, row = e / KCH, c8 = e % KCH;
+      bf16x8 kv = pk[u], qv = pq[u];
       if (l2) {  // F.normalize over the row: KCH consecutive lanes hold one row
         float sk = 0.f, sq = 0.f;
 #pragma unroll
@@ -178,242 +224,357 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
           qv[i] = static_cast<bf16>((float)qv[i] * iq);
         }
       }
-      *reinterpret_cast<bf16x8*>(Kc + row * KP + c8 * 8) = kv;
-      *reinterpret_cast<bf16x8*>(Qc + row * KP + c8 * 8) = qv;
-    }
-    {
-      const int row = t >> 2, c8 = t & 3;  // 64 rows x 4 chunks of 8 = 256 threads
-      bf16x8 vv{};
-      if (row < len) vv = *reinterpret_cast<const bf16x8*>(vg + ((c0 + row) * p.HV + hv) * VD + vb * kVB + c8 * 8);
-      *reinterpret_cast<bf16x8*>(Vc + row * kVP + c8 * 8) = vv;
+      *reinterpret_cast<bf16x8*>(&Kc[buf][row * KP + c8 * 8]) = kv;
+      *reinterpret_cast<bf16x8*>(&Qc[buf][row * KP + c8 * 8]) = qv;
     }
     if (w == 0) {  // gates and the in-chunk cumsum of g (padding rows: g = 0, beta = 0)
-      float gv = 0.f, bv = 0.f;
-      if (lane < len) {
-        const int64_t gi = (c0 + lane) * p.HV + hv;
-        gv = load_as_f32(p.g, p.dg, gi);
-        if (p.flags & GDN_FLAG_GATE_IN_KERNEL) gv = -expf(p.A_log[hv]) * softplus_f32(gv + p.dt_bias[hv]);
-        bv = load_as_f32(p.beta, p.db, gi);
-        if (p.flags & GDN_FLAG_BETA_SIGMOID) bv = sigmoid_f32(bv);
-      }
-      float cs = gv;
+      const float bval = pbv;
+      float cs = pgv;
 #pragma unroll
       for (int off = 1; off < kWave; off <<= 1) {
         const float y = __shfl_up(cs, off, kWave);
         if (lane >= off) cs += y;
       }
       const float last = __shfl(cs, kWave - 1, kWave);
-      const float e = expf(cs);
-      gam[lane] = cs;
-      egam[lane] = e;
-      bet[lane] = bv;
-      begam[lane] = bv * e;
-      dlast[lane] = expf(last - cs);
+      const float e = __expf(cs);
+      gv.gam[buf][lane] = cs;
+      gv.egam[buf][lane] = e;
+      gv.bet[buf][lane] = bval;
+      gv.begam[buf][lane] = bval * e;
+      gv.dlast[buf][lane] = __expf(last - cs);
     }
-    __syncthreads();
+  };
+  auto stage_v = [&]() {
+    if (t < kC * 4) *reinterpret_cast<bf16x8*>(Vc + (t >> 2) * kVP + (t & 3) * 8) = pv;
+  };
+  // gate transforms applied at fetch time (they need the token index, which fetch knows)
+  auto gate_fix = [&](int c) {
+    const int64_t c0 = bos + (int64_t)c * kC;
+    const int len = (int)((eos - c0) < kC ? (eos - c0) : kC);
+    if (w == 0 && c < nc && lane < len) {
+      if (p.flags & GDN_FLAG_GATE_IN_KERNEL) pgv = -__expf(p.A_log[hv]) * softplus_f32(pgv + p.dt_bias[hv]);
+      if (p.flags & GDN_FLAG_BETA_SIGMOID) pbv = sigmoid_f32(pbv);
+    }
+  };
 
-    // ---------------------------------------------------------------- Gram tiles, K S and Q S
-    // 20 jobs: upper tiles (rb <= cb) of K K^T (-> A) and of K Q^T (-> P); element (r, c) of tile
-    // (rb, cb) is row j = r, column t = c, so the accumulator writes 4 consecutive j of row t.
-#pragma unroll
-    for (int jj = 0; jj < 5; ++jj) {
-      const int job = w + 4 * jj;
-      const bool isq = job >= 10;
-      const int tj = isq ? job - 10 : job;
-      const int rb = tj < 4 ? 0 : tj < 7 ? 1 : tj < 9 ? 2 : 3;
-      const int cb = tj < 4 ? tj : tj < 7 ? tj - 3 : tj < 9 ? tj - 5 : 3;
-      const bf16* bsrc = isq ? Qc : Kc;
-      f32x4 acc{};
-#pragma unroll
-      for (int s = 0; s < KS; ++s)
-        acc = mma(ld8(Kc + (16 * rb + li) * KP + 32 * s + 8 * g4), ld8(bsrc + (16 * cb + li) * KP + 32 * s + 8 * g4), acc);
-      const int tt = 16 * cb + li, j0 = 16 * rb + 4 * g4;
-      const float gt = gam[tt];
-      float val[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int j = j0 + i;
-        const bool keep = isq ? (j <= tt) : (j < tt);
-        val[i] = keep ? expf(gt - gam[j]) * acc[i] : 0.f;
-      }
-      if (isq) {
-        *reinterpret_cast<bf16x4*>(Pb + tt * kCP + j0) = to_bf16x4(val[0], val[1], val[2], val[3]);
-      } else {
-        const float bt = bet[tt];
-        *reinterpret_cast<float4*>(Af + tt * kFP + j0) = make_float4(bt * val[0], bt * val[1], bt * val[2], bt * val[3]);
-      }
-    }
-    f32x4 yacc[2] = {}, zacc[2] = {};
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      const bf16x8 ak = ld8(Kc + (16 * w + li) * KP + 32 * s + 8 * g4);
-      const bf16x8 aq = ld8(Qc + (16 * w + li) * KP + 32 * s + 8 * g4);
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        const bf16x8 b = ld8(Sb + (16 * nt + li) * KP + 32 * s + 8 * g4);
-        yacc[nt] = mma(ak, b, yacc[nt]);
-        zacc[nt] = mma(aq, b, zacc[nt]);
-      }
-    }
-    // X = beta V - beta e^gam (K S), rows j = 16w + 4g + i; kept in fp32 for the identity part of T
-    f32x4 xacc[2];
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      const int vv = 16 * nt + li;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int j = 16 * w + 4 * g4 + i;
-        xacc[nt][i] = bet[j] * (float)Vc[j * kVP + vv] - begam[j] * yacc[nt][i];
-      }
-      *reinterpret_cast<bf16x4*>(Xb + vv * kCP + 16 * w + 4 * g4) = to_bf16x4(xacc[nt][0], xacc[nt][1], xacc[nt][2], xacc[nt][3]);
-    }
-    __syncthreads();
+  // T - I and P are strictly/causally lower: their upper blocks stay zero for the whole run
+  for (int e = t; e < kC * kCP / 8; e += kNT) {
+    reinterpret_cast<bf16x8*>(Tb[0])[e] = bf16x8{};
+    reinterpret_cast<bf16x8*>(Tb[1])[e] = bf16x8{};
+    reinterpret_cast<bf16x8*>(Pb)[e] = bf16x8{};
+  }
 
-    // ---------------------------------------------------------------- T = (I + A)^-1
-    if (w == 0) {  // diagonal 16x16 blocks: lane (b, c) solves column c of block b
-      const int b = g4, c = li;
-      const float* ab = Af + 16 * b * kFP + 16 * b;
-      float x[16];
+  // state slice: 16x16 tiles ti = STW*w + u, row tile ti/2, column tile ti%2
+  f32x4 sacc[STW];
+  const int64_t sbase = (n * p.HV + hv) * (int64_t)KD * VD + vb * kVB;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) x[r] = (r == c) ? 1.f : 0.f;
+  for (int u = 0; u < STW; ++u) {
+    const int ti = STW * w + u, kd0 = 16 * (ti >> 1) + 4 * g4, vv = 16 * (ti & 1) + li;
 #pragma unroll
-      for (int m = 0; m < 16; ++m) {
-        const float xm = x[m];
-#pragma unroll
-        for (int r = m + 1; r < 16; ++r) x[r] -= ab[r * kFP + m] * xm;
-      }
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        Tf[(16 * b + r) * kFP + 16 * b + c] = x[r];
-        Tb[(16 * b + r) * kCP + 16 * b + c] = static_cast<bf16>(r == c ? 0.f : x[r]);
-      }
-    }
-    __syncthreads();
-    if (w < 2) {  // 16 -> 32: W = A_{2q+1,2q} T_{2q,2q} into the unused upper block (2q, 2q+1)
-      const int R = 16 * (2 * w + 1), Cc = 16 * (2 * w);
-      f32x4 acc{};
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-        acc = mma_f32(Af[(R + li) * kFP + Cc + 4 * s + g4], Tf[(Cc + 4 * s + g4) * kFP + Cc + li], acc);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) Tf[(Cc + 4 * g4 + i) * kFP + R + li] = acc[i];
-    }
-    __syncthreads();
-    if (w < 2) {  // T_{2q+1,2q} = -T_{2q+1,2q+1} W
-      const int R = 16 * (2 * w + 1), Cc = 16 * (2 * w);
-      f32x4 acc{};
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-        acc = mma_f32(Tf[(R + li) * kFP + R + 4 * s + g4], Tf[(Cc + 4 * s + g4) * kFP + R + li], acc);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        Tf[(R + 4 * g4 + i) * kFP + Cc + li] = -acc[i];
-        Tb[(R + 4 * g4 + i) * kCP + Cc + li] = static_cast<bf16>(-acc[i]);
-      }
-    }
-    __syncthreads();
-    {  // 32 -> 64: W' = A[32:64][0:32] T[0:32][0:32] into the unused upper block [0:32][32:64]
-      const int rt = w >> 1, ct = w & 1;
-      f32x4 acc{};
-#pragma unroll
-      for (int s = 4 * ct; s < 8; ++s)
-        acc = mma_f32(Af[(32 + 16 * rt + li) * kFP + 4 * s + g4], Tf[(4 * s + g4) * kFP + 16 * ct + li], acc);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) Tf[(16 * rt + 4 * g4 + i) * kFP + 32 + 16 * ct + li] = acc[i];
-    }
-    __syncthreads();
-    {  // T[32:64][0:32] = -T[32:64][32:64] W'
-      const int rt = w >> 1, ct = w & 1;
-      f32x4 acc{};
-      for (int s = 0; s < 4 * rt + 4; ++s)
-        acc = mma_f32(Tf[(32 + 16 * rt + li) * kFP + 32 + 4 * s + g4], Tf[(4 * s + g4) * kFP + 32 + 16 * ct + li], acc);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) Tb[(32 + 16 * rt + 4 * g4 + i) * kCP + 16 * ct + li] = static_cast<bf16>(-acc[i]);
-    }
-    __syncthreads();
+    for (int i = 0; i < 4; ++i) sacc[u][i] = p.h0 ? p.h0[sbase + (int64_t)(kd0 + i) * VD + vv] : 0.f;
+    *reinterpret_cast<bf16x4*>(Sb + vv * KP + kd0) = to_bf16x4(sacc[u][0], sacc[u][1], sacc[u][2], sacc[u][3]);
+  }
 
-    // ---------------------------------------------------------------- Delta = X + (T - I) X
-    f32x4 dacc[2] = {xacc[0], xacc[1]};
-    const int ksteps = (w >= 2) ? 2 : 1;  // (T - I) and P vanish for j > t
-    for (int s = 0; s < ksteps; ++s) {
-      const bf16x8 a = ld8(Tb + (16 * w + li) * kCP + 32 * s + 8 * g4);
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt) dacc[nt] = mma(a, ld8(Xb + (16 * nt + li) * kCP + 32 * s + 8 * g4), dacc[nt]);
-    }
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      const int vv = 16 * nt + li, tb = 16 * w + 4 * g4;
-      *reinterpret_cast<bf16x4*>(Db + vv * kCP + tb) = to_bf16x4(dacc[nt][0], dacc[nt][1], dacc[nt][2], dacc[nt][3]);
-      float hi[4], lo[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float d = dlast[tb + i] * dacc[nt][i];
-        hi[i] = (float)static_cast<bf16>(d);
-        lo[i] = d - hi[i];
-      }
-      *reinterpret_cast<bf16x4*>(DtH + vv * kCP + tb) = to_bf16x4(hi[0], hi[1], hi[2], hi[3]);
-      *reinterpret_cast<bf16x4*>(DtL + vv * kCP + tb) = to_bf16x4(lo[0], lo[1], lo[2], lo[3]);
-    }
-    __syncthreads();
+  if (nc > 0) {
+    fetch_kq(0);
+    gate_fix(0);
+    stage_kq(0);
+  }
+  __syncthreads();
 
-    // ---------------------------------------------------------------- O = scale (e^gam Q S + P Delta)
-    {
-      f32x4 oacc[2] = {};
-      for (int s = 0; s < ksteps; ++s) {
-        const bf16x8 a = ld8(Pb + (16 * w + li) * kCP + 32 * s + 8 * g4);
+  f32x4 xacc[2], zacc[2];
+  for (int i = -1; i < nc; ++i) {
+    const bool s_on = i >= 0, k_on = i + 1 < nc;
+    const int b0 = (i + 2) & 1, b1 = (i + 1) & 1;  // buffer of chunk i and of chunk i+1
+    const int64_t c0 = bos + (int64_t)i * kC;
+    const int len = s_on ? (int)((eos - c0) < kC ? (eos - c0) : kC) : 0;
+    // prefetch: K/Q/gates of chunk i+2, V of chunk i+1 (held in registers until the stage step)
+    fetch_kq(i + 2);
+    fetch_v(i + 1);
+
+    // ================================================================ phase A
+    if (w < 4) {
+      if (k_on) {  // diagonal Gram tile (w, w) of chunk i+1 -> A block (transposed) -> its inverse
+        const bf16* kb = Kc[b1];
+        f32x4 acc{};
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) oacc[nt] = mma(a, ld8(Db + (16 * nt + li) * kCP + 32 * s + 8 * g4), oacc[nt]);
-      }
+        for (int s = 0; s < KS; ++s)
+          acc = mma(ld8(kb + (16 * w + li) * KP + 32 * s + 8 * g4), ld8(kb + (16 * w + li) * KP + 32 * s + 8 * g4), acc);
+        // element (j = 16w + 4g + i, t = 16w + li); A[t][j] for j < t
+        const float gt = gv.gam[b1][16 * w + li], bt = gv.bet[b1][16 * w + li];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int tt = 16 * w + 4 * g4 + i;
-        if (tt < len) {
-          bf16* orow = og + ((c0 + tt) * p.HV + hv) * VD + vb * kVB + li;
-          const float eg = egam[tt];
-#pragma unroll
-          for (int nt = 0; nt < 2; ++nt) orow[16 * nt] = static_cast<bf16>(p.scale * (eg * zacc[nt][i] + oacc[nt][i]));
+        for (int ii = 0; ii < 4; ++ii) {
+          const int jl = 4 * g4 + ii;
+          const float val = (jl < li) ? bt * __expf(gt - gv.gam[b1][16 * w + jl]) * acc[ii] : 0.f;
+          Ad[w][jl * kAdP + li] = val;  // Ad[m = j_local][r = t_local]
         }
-      }
-    }
-    // ---------------------------------------------------------------- S' = e^{gam_c} S + K^T Delta~
-    {
-      const float ec = expf(gam[kC - 1]);
+        if (lane < 16) {  // column c = lane of (I + A_ww)^-1 by right-looking substitution
+          const int c = lane;
+          float x[16];
 #pragma unroll
-      for (int mt = 0; mt < SMT; ++mt)
+          for (int r = 0; r < 16; ++r) x[r] = (r == c) ? 1.f : 0.f;
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) sacc[mt][nt] *= ec;
+          for (int m = 0; m < 15; ++m) {
+            const float* col = &Ad[w][m * kAdP];
+            float a[16];
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
+            for (int q4 = 0; q4 < 4; ++q4) {
+              const float4 v4 = *reinterpret_cast<const float4*>(col + 4 * q4);
+              a[4 * q4] = v4.x; a[4 * q4 + 1] = v4.y; a[4 * q4 + 2] = v4.z; a[4 * q4 + 3] = v4.w;
+            }
+            const float xm = x[m];
 #pragma unroll
-        for (int mt = 0; mt < SMT; ++mt) {
-          const bf16x8 a = ld8_tr(Kc, KP, 32 * s, 16 * (w * SMT + mt), lane);
+            for (int r = m + 1; r < 16; ++r) x[r] -= a[r] * xm;
+          }
+          float* tf = &Tf[w >> 1][(16 * (w & 1)) * kTfP + 16 * (w & 1) + c];
+          bf16* tb = &Tb[b1][(16 * w) * kCP + 16 * w + c];
 #pragma unroll
-          for (int nt = 0; nt < 2; ++nt) {
-            const int off = (16 * nt + li) * kCP + 32 * s + 8 * g4;
-            sacc[mt][nt] = mma(a, ld8(DtH + off), sacc[mt][nt]);
-            sacc[mt][nt] = mma(a, ld8(DtL + off), sacc[mt][nt]);
+          for (int r = 0; r < 16; ++r) {
+            tf[r * kTfP] = x[r];
+            tb[r * kCP] = static_cast<bf16>(r == c ? 0.f : x[r]);
           }
         }
       }
+      if (s_on) {  // Y = K S for row tile w, then X -> Xb
+        const bf16* kb = Kc[b0];
+        f32x4 yacc[2] = {};
 #pragma unroll
-      for (int mt = 0; mt < SMT; ++mt)
+        for (int s = 0; s < KS; ++s) {
+          const bf16x8 a = ld8(kb + (16 * w + li) * KP + 32 * s + 8 * g4);
+          const bf16x8 s0 = ld8(Sb + li * KP + 32 * s + 8 * g4);
+          const bf16x8 s1 = ld8(Sb + (16 + li) * KP + 32 * s + 8 * g4);
+          yacc[0] = mma(a, s0, yacc[0]);
+          yacc[1] = mma(a, s1, yacc[1]);
+        }
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
-          *reinterpret_cast<bf16x4*>(Sb + (16 * nt + li) * KP + 16 * (w * SMT + mt) + 4 * g4) =
-              to_bf16x4(sacc[mt][nt][0], sacc[mt][nt][1], sacc[mt][nt][2], sacc[mt][nt][3]);
+        for (int nt = 0; nt < 2; ++nt) {
+          const int vv = 16 * nt + li;
+#pragma unroll
+          for (int ii = 0; ii < 4; ++ii) {
+            const int j = 16 * w + 4 * g4 + ii;
+            xacc[nt][ii] = gv.bet[b0][j] * (float)Vc[j * kVP + vv] - gv.begam[b0][j] * yacc[nt][ii];
+          }
+          *reinterpret_cast<bf16x4*>(Xb + vv * kCP + 16 * w + 4 * g4) =
+              to_bf16x4(xacc[nt][0], xacc[nt][1], xacc[nt][2], xacc[nt][3]);
+        }
+      }
+    } else {
+      const int wz = w - 4;
+      // 16 jobs: 6 off-diagonal k.k tiles of chunk i+1 (-> Ao) and 10 k.q tiles of chunk i (-> P)
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const int job = wz + 4 * jj;
+        const bool isq = job >= 6;
+        if (isq ? !s_on : !k_on) continue;
+        int rb, cb;
+        if (!isq) {  // (rb < cb) pairs: (0,1),(0,2),(0,3),(1,2),(1,3),(2,3)
+          rb = job < 3 ? 0 : job < 5 ? 1 : 2;
+          cb = job < 3 ? job + 1 : job < 5 ? job - 1 : 3;
+        } else {  // (rb <= cb) pairs
+          const int tj = job - 6;
+          rb = tj < 4 ? 0 : tj < 7 ? 1 : tj < 9 ? 2 : 3;
+          cb = tj < 4 ? tj : tj < 7 ? tj - 3 : tj < 9 ? tj - 5 : 3;
+        }
+        const int bb = isq ? b0 : b1;
+        const bf16* ka = Kc[bb];
+        const bf16* bsrc = isq ? Qc[bb] : Kc[bb];
+        bf16x8 fa[KS], fb[KS];
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          fa[s] = ld8(ka + (16 * rb + li) * KP + 32 * s + 8 * g4);
+          fb[s] = ld8(bsrc + (16 * cb + li) * KP + 32 * s + 8 * g4);
+        }
+        f32x4 acc{};
+#pragma unroll
+        for (int s = 0; s < KS; ++s) acc = mma(fa[s], fb[s], acc);
+        // element (r, c) -> row t = 16cb + li, column j = 16rb + 4g + i
+        const int tt = 16 * cb + li, j0 = 16 * rb + 4 * g4;
+        const float gt = gv.gam[bb][tt];
+        float val[4];
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) {
+          const int j = j0 + ii;
+          const float d = __expf(gt - gv.gam[bb][j]);
+          val[ii] = (isq ? (j <= tt) : true) ? d * acc[ii] : 0.f;
+        }
+        if (isq) {
+          *reinterpret_cast<bf16x4*>(Pb + tt * kCP + j0) = to_bf16x4(val[0], val[1], val[2], val[3]);
+        } else {
+          const float bt = gv.bet[bb][tt];
+          *reinterpret_cast<float4*>(&Ao[(tt - 16) * kAoP + j0]) = make_float4(bt * val[0], bt * val[1], bt * val[2], bt * val[3]);
+        }
+      }
+      if (s_on) {  // Z = Q S for row tile wz
+        const bf16* qb = Qc[b0];
+        zacc[0] = f32x4{};
+        zacc[1] = f32x4{};
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          const bf16x8 a = ld8(qb + (16 * wz + li) * KP + 32 * s + 8 * g4);
+          const bf16x8 s0 = ld8(Sb + li * KP + 32 * s + 8 * g4);
+          const bf16x8 s1 = ld8(Sb + (16 + li) * KP + 32 * s + 8 * g4);
+          zacc[0] = mma(a, s0, zacc[0]);
+          zacc[1] = mma(a, s1, zacc[1]);
+        }
+      }
     }
+    __syncthreads();
+
+    // ================================================================ phase B
+    if (w < 4) {
+      if (s_on) {  // Delta = X + (T - I) X for row tile w -> Db, Delta~ hi/lo
+        f32x4 dacc[2] = {xacc[0], xacc[1]};
+        const bf16* tb = Tb[b0];
+        const int ksteps = (w >= 2) ? 2 : 1;  // (T - I) vanishes for j >= t
+        for (int s = 0; s < ksteps; ++s) {
+          const bf16x8 a = ld8(tb + (16 * w + li) * kCP + 32 * s + 8 * g4);
+          const bf16x8 x0 = ld8(Xb + li * kCP + 32 * s + 8 * g4);
+          const bf16x8 x1 = ld8(Xb + (16 + li) * kCP + 32 * s + 8 * g4);
+          dacc[0] = mma(a, x0, dacc[0]);
+          dacc[1] = mma(a, x1, dacc[1]);
+        }
+        const int tb0 = 16 * w + 4 * g4;
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+          const int vv = 16 * nt + li;
+          *reinterpret_cast<bf16x4*>(Db + vv * kCP + tb0) = to_bf16x4(dacc[nt][0], dacc[nt][1], dacc[nt][2], dacc[nt][3]);
+          bf16x4 hi, lo;
+          const float* dl = &gv.dlast[b0][tb0];
+          split4(dl[0] * dacc[nt][0], dl[1] * dacc[nt][1], dl[2] * dacc[nt][2], dl[3] * dacc[nt][3], hi, lo);
+          *reinterpret_cast<bf16x4*>(DtH + vv * kCP + tb0) = hi;
+          *reinterpret_cast<bf16x4*>(DtL + vv * kCP + tb0) = lo;
+        }
+      }
+    } else if (w < 6 && k_on) {  // T 16 -> 32 merges: T_{2q+1,2q} = -T_{2q+1,2q+1} (A_{2q+1,2q} T_{2q,2q})
+      const int q = w - 4;
+      const float* tq = Tf[q];
+      float* wsc = &Wsc[16 * q];  // 16x16 scratch in columns 16q..16q+15
+      f32x4 acc{};
+      {
+        float a[4], b[4];
+        const float* ar = &Ao[(16 * (2 * q + 1) + li - 16) * kAoP + 32 * q + 4 * g4];
+        a[0] = ar[0]; a[1] = ar[1]; a[2] = ar[2]; a[3] = ar[3];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) b[m] = tq[(4 * g4 + m) * kTfP + li];
+        acc = mma16x3(a, b, acc);
+      }
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) wsc[(4 * g4 + ii) * kTfP + li] = acc[ii];
+      f32x4 acc2{};
+      {
+        float a[4], b[4];
+        const float* ar = &tq[(16 + li) * kTfP + 16 + 4 * g4];
+        a[0] = ar[0]; a[1] = ar[1]; a[2] = ar[2]; a[3] = ar[3];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) b[m] = wsc[(4 * g4 + m) * kTfP + li];
+        acc2 = mma16x3(a, b, acc2);
+      }
+      float* tw = &Tf[q][16 * kTfP];
+      bf16* tbw = &Tb[b1][(32 * q + 16) * kCP + 32 * q];
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) {
+        tw[(4 * g4 + ii) * kTfP + li] = -acc2[ii];
+        tbw[(4 * g4 + ii) * kCP + li] = static_cast<bf16>(-acc2[ii]);
+      }
+    }
+    __syncthreads();
+
+    // ================================================================ phase C
+    if (s_on) {
+      if (w >= 4) {  // O = scale (e^gam Z + P Delta) for row tile wz
+        const int wz = w - 4;
+        f32x4 oacc[2] = {};
+        const int ksteps = (wz >= 2) ? 2 : 1;
+        for (int s = 0; s < ksteps; ++s) {
+          const bf16x8 a = ld8(Pb + (16 * wz + li) * kCP + 32 * s + 8 * g4);
+          oacc[0] = mma(a, ld8(Db + li * kCP + 32 * s + 8 * g4), oacc[0]);
+          oacc[1] = mma(a, ld8(Db + (16 + li) * kCP + 32 * s + 8 * g4), oacc[1]);
+        }
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) {
+          const int tt = 16 * wz + 4 * g4 + ii;
+          if (tt < len) {
+            bf16* orow = og + ((c0 + tt) * p.HV + hv) * VD + vb * kVB + li;
+            const float eg = gv.egam[b0][tt];
+            orow[0] = static_cast<bf16>(p.scale * (eg * zacc[0][ii] + oacc[0][ii]));
+            orow[16] = static_cast<bf16>(p.scale * (eg * zacc[1][ii] + oacc[1][ii]));
+          }
+        }
+      }
+      // S' = e^{gam_c} S + K^T Delta~ (hi + lo)
+      const float ec = __expf(gv.gam[b0][kC - 1]);
+      const bf16* kb = Kc[b0];
+#pragma unroll
+      for (int u = 0; u < STW; ++u) {
+        const int ti = STW * w + u, rt = ti >> 1, nt = ti & 1;
+        sacc[u] *= ec;
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          const bf16x8 a = ld8_tr(kb, KP, 32 * s, 16 * rt, lane);
+          const int off = (16 * nt + li) * kCP + 32 * s + 8 * g4;
+          sacc[u] = mma(a, ld8(DtH + off), sacc[u]);
+          sacc[u] = mma(a, ld8(DtL + off), sacc[u]);
+        }
+      }
+    }
+    if (w < 2 && k_on) {  // T 32 -> 64: W' = A[32:64][0:32] T[0:32][0:32]; T[32:64][0:32] = -T[32:64][32:64] W'
+      const int ct = w;
+      float* wsc = &Wsc[16 * ct];
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        f32x4 acc{};
+#pragma unroll
+        for (int ks = ct; ks < 2; ++ks) {  // T[k][c] vanishes for k < c
+          float a[4], b[4];
+          const float* ar = &Ao[(16 + 16 * rt + li) * kAoP + 16 * ks + 4 * g4];
+          a[0] = ar[0]; a[1] = ar[1]; a[2] = ar[2]; a[3] = ar[3];
+#pragma unroll
+          for (int m = 0; m < 4; ++m) b[m] = Tf[0][(16 * ks + 4 * g4 + m) * kTfP + 16 * ct + li];
+          acc = mma16x3(a, b, acc);
+        }
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) wsc[(16 * rt + 4 * g4 + ii) * kTfP + li] = acc[ii];
+      }
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        f32x4 acc{};
+#pragma unroll
+        for (int ks = 0; ks <= rt; ++ks) {  // T[32+r][32+k] vanishes for k > r
+          float a[4], b[4];
+          const float* ar = &Tf[1][(16 * rt + li) * kTfP + 16 * ks + 4 * g4];
+          a[0] = ar[0]; a[1] = ar[1]; a[2] = ar[2]; a[3] = ar[3];
+#pragma unroll
+          for (int m = 0; m < 4; ++m) b[m] = wsc[(16 * ks + 4 * g4 + m) * kTfP + li];
+          acc = mma16x3(a, b, acc);
+        }
+        bf16* tbw = &Tb[b1][(32 + 16 * rt) * kCP + 16 * ct];
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) tbw[(4 * g4 + ii) * kCP + li] = static_cast<bf16>(-acc[ii]);
+      }
+    }
+    if (s_on) {
+#pragma unroll
+      for (int u = 0; u < STW; ++u) {
+        const int ti = STW * w + u, kd0 = 16 * (ti >> 1) + 4 * g4, vv = 16 * (ti & 1) + li;
+        *reinterpret_cast<bf16x4*>(Sb + vv * KP + kd0) = to_bf16x4(sacc[u][0], sacc[u][1], sacc[u][2], sacc[u][3]);
+      }
+    }
+    __syncthreads();
+
+    // ================================================================ stage chunk i+2 (K/Q/gates), i+1 (V)
+    gate_fix(i + 2);
+    if (i + 2 < nc) stage_kq(b0);
+    stage_v();
     __syncthreads();
   }
 
   if (p.ht) {
 #pragma unroll
-    for (int mt = 0; mt < SMT; ++mt)
+    for (int u = 0; u < STW; ++u) {
+      const int ti = STW * w + u, kd0 = 16 * (ti >> 1) + 4 * g4, vv = 16 * (ti & 1) + li;
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        const int kd0 = 16 * (w * SMT + mt) + 4 * g4, vv = 16 * nt + li;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) p.ht[sbase + (int64_t)(kd0 + i) * VD + vv] = sacc[mt][nt][i];
-      }
+      for (int ii = 0; ii < 4; ++ii) p.ht[sbase + (int64_t)(kd0 + ii) * VD + vv] = sacc[u][ii];
+    }
   }
 }
 
