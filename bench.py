@@ -122,6 +122,29 @@ def cpu_baseline(torch, decode_steps: int = 100):
     }
 
 
+def run_only(torch, args) -> int:
+    """One workload for --steps launches (profiler runs: PMC counters per dispatch)."""
+    from sorernn_amd import chunk_gated_delta_rule, gated_delta_decode_step
+    from sorernn_amd.synthetic import config_inputs, decode_inputs
+
+    if args.only in ("prefill", "varlen"):
+        idx = 1 if args.only == "prefill" else 3
+        inp = config_inputs(idx)
+        cu_cpu = inp.cu_seqlens
+        d = inp.to("cuda")
+        for _ in range(args.warmup + args.steps):
+            chunk_gated_delta_rule(d.q, d.k, d.v, d.g, d.beta, scale=d.scale, initial_state=d.h0,
+                                   output_final_state=True, cu_seqlens=d.cu_seqlens, cu_seqlens_cpu=cu_cpu)
+    else:
+        di = decode_inputs()
+        x, cs, cw, g, b, st = (t.to("cuda") for t in (di.x_qkv, di.conv_state, di.conv_weight, di.g, di.beta, di.state))
+        for _ in range(args.warmup + args.steps):
+            gated_delta_decode_step(x, cs, cw, g, b, st, di.H, di.HV, di.D)
+    torch.cuda.synchronize()
+    print(f"ran {args.only}: {args.warmup + args.steps} launches", flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -129,6 +152,10 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--decode-steps", type=int, default=1000)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain 256 MiB device copy (the reference kernel for PMC byte counters)")
+    ap.add_argument("--only", choices=["prefill", "decode", "varlen"], default=None,
+                    help="run one workload only (for profiler runs); prints no JSON line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(f"bench.py: this build runs one GPU only (the GDN op needs no collective: every (sequence, head) "
@@ -144,6 +171,17 @@ def main() -> int:
     from sorernn_amd.synthetic import config_inputs, decode_inputs
 
     dev = "cuda"
+    if args.calibrate_copy:
+        # 256 MiB read + 256 MiB written per launch: divides FETCH_SIZE / WRITE_SIZE into a scale factor
+        src = torch.empty(64 * 1024 * 1024, device=dev, dtype=torch.float32).fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_each_way": src.numel() * 4, "launches": args.steps}))
+        return 0
+    if args.only:
+        return run_only(torch, args)
     # ------------------------------------------------------------------ config 1: prefill
     inp = config_inputs(1).to(dev)
     B, T, H, K = inp.q.shape

@@ -56,7 +56,7 @@ constexpr int kVB = 32;       // value columns per workgroup
 constexpr int kNT = 512;      // threads per workgroup (8 waves)
 constexpr int kCP = kC + 8;   // bf16 pitch of [*][64] operand tiles (144 B rows)
 constexpr int kVP = kVB + 8;  // bf16 pitch of the V slice (80 B rows)
-constexpr int kAdP = 20;      // fp32 pitch of the transposed diagonal A blocks
+constexpr int kAdP = 20;      // fp32 pitch of the diagonal A blocks
 constexpr int kAoP = 52;      // fp32 pitch of the off-diagonal A rows 16..63 x cols 0..47
 constexpr int kTfP = 36;      // fp32 pitch of the two 32x32 T blocks and the merge scratch
 
@@ -83,6 +83,17 @@ __device__ __forceinline__ bf16x8 ld8_tr(const bf16* tile, int pitch, int j0, in
   const bf16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p0));
   const bf16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p1));
   return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
+// Value of lane (quad base + q) broadcast to the 4 lanes of each quad (DPP quad_perm q,q,q,q).
+__device__ __forceinline__ float quad_bcast(float x, int q) {
+  const int v = __float_as_int(x);
+  switch (q) {
+    case 0: return __int_as_float(__builtin_amdgcn_mov_dpp(v, 0x00, 0xf, 0xf, false));
+    case 1: return __int_as_float(__builtin_amdgcn_mov_dpp(v, 0x55, 0xf, 0xf, false));
+    case 2: return __int_as_float(__builtin_amdgcn_mov_dpp(v, 0xaa, 0xf, 0xf, false));
+    default: return __int_as_float(__builtin_amdgcn_mov_dpp(v, 0xff, 0xf, 0xf, false));
+  }
 }
 
 __device__ __forceinline__ bf16x4 to_bf16x4(float a, float b, float c, float d) {
@@ -123,7 +134,7 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
   __shared__ __align__(16) bf16 Qc[2][kC * KP];
   __shared__ __align__(16) bf16 Vc[kC * kVP];
   __shared__ __align__(16) bf16 Sb[kVB * KP];
-  __shared__ __align__(16) float Ad[4][16 * kAdP];       // diagonal A blocks, transposed: Ad[b][m][r] = A[16b+r][16b+m]
+  __shared__ __align__(16) float Ad[4][16 * kAdP];       // diagonal A blocks, row-major: Ad[b][r][m] = A[16b+r][16b+m]
   __shared__ __align__(16) float Ao[48 * kAoP];          // A rows 16..63 x cols 0..47 (off-diagonal lower blocks)
   __shared__ __align__(16) float Tf[2][32 * kTfP];       // T[0:32][0:32] and T[32:64][32:64] in fp32
   __shared__ __align__(16) float Wsc[32 * kTfP];         // merge scratch
@@ -166,7 +177,7 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
 
   // ------------------------------------------------------------------ prefetch registers
   bf16x8 pk[QKPT], pq[QKPT], pv{};
-  float pgv = 0.f, pbv = 0.f;
+  uint32_t pgraw = 0, pbraw = 0;  // gate bits as loaded (converted at the stage step)
   // K/Q/gates of chunk c (into registers)
   auto fetch_kq = [&](int c) {
     const int64_t c0 = bos + (int64_t)c * kC;
@@ -182,12 +193,12 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
         pq[u] = *reinterpret_cast<const bf16x8*>(qg + base);
       }
     }
-    pgv = 0.f;
-    pbv = 0.f;
+    pgraw = 0;
+    pbraw = 0;
     if (w == 0 && c < nc && lane < len) {
       const int64_t gi = (c0 + lane) * p.HV + hv;
-      pgv = load_as_f32(p.g, p.dg, gi);
-      pbv = load_as_f32(p.beta, p.db, gi);
+      pgraw = load_raw32(p.g, p.dg, gi);
+      pbraw = load_raw32(p.beta, p.db, gi);
     }
   };
   auto fetch_v = [&](int c) {
@@ -200,7 +211,7 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
     }
   };
   // registers -> LDS buffer `buf` (K/Q/gates) and the V slice
-  auto stage_kq = [&](int buf) {
+  auto stage_kq = [&](int buf, int valid_rows) {
 #pragma unroll
     for (int u = 0; u < QKPT; ++u) {
       const int e = t + u * kNT, row = e / KCH, c8 = e % KCH;
@@ -228,8 +239,12 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
       *reinterpret_cast<bf16x8*>(&Qc[buf][row * KP + c8 * 8]) = qv;
     }
     if (w == 0) {  // gates and the in-chunk cumsum of g (padding rows: g = 0, beta = 0)
-      const float bval = pbv;
-      float cs = pgv;
+      float gval = raw32_to_f32(pgraw, p.dg), bval = raw32_to_f32(pbraw, p.db);
+      if (lane < valid_rows) {
+        if (p.flags & GDN_FLAG_GATE_IN_KERNEL) gval = -__expf(p.A_log[hv]) * softplus_f32(gval + p.dt_bias[hv]);
+        if (p.flags & GDN_FLAG_BETA_SIGMOID) bval = sigmoid_f32(bval);
+      }
+      float cs = gval;
 #pragma unroll
       for (int off = 1; off < kWave; off <<= 1) {
         const float y = __shfl_up(cs, off, kWave);
@@ -246,15 +261,6 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
   };
   auto stage_v = [&]() {
     if (t < kC * 4) *reinterpret_cast<bf16x8*>(Vc + (t >> 2) * kVP + (t & 3) * 8) = pv;
-  };
-  // gate transforms applied at fetch time (they need the token index, which fetch knows)
-  auto gate_fix = [&](int c) {
-    const int64_t c0 = bos + (int64_t)c * kC;
-    const int len = (int)((eos - c0) < kC ? (eos - c0) : kC);
-    if (w == 0 && c < nc && lane < len) {
-      if (p.flags & GDN_FLAG_GATE_IN_KERNEL) pgv = -__expf(p.A_log[hv]) * softplus_f32(pgv + p.dt_bias[hv]);
-      if (p.flags & GDN_FLAG_BETA_SIGMOID) pbv = sigmoid_f32(pbv);
-    }
   };
 
   // T - I and P are strictly/causally lower: their upper blocks stay zero for the whole run
@@ -275,11 +281,8 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
     *reinterpret_cast<bf16x4*>(Sb + vv * KP + kd0) = to_bf16x4(sacc[u][0], sacc[u][1], sacc[u][2], sacc[u][3]);
   }
 
-  if (nc > 0) {
-    fetch_kq(0);
-    gate_fix(0);
-    stage_kq(0);
-  }
+  fetch_kq(0);
+  stage_kq(0, nc > 0 ? (int)((eos - bos) < kC ? (eos - bos) : kC) : 0);
   __syncthreads();
 
   f32x4 xacc[2], zacc[2];
@@ -294,50 +297,9 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
 
     // ================================================================ phase A
     if (w < 4) {
-      if (k_on) {  // diagonal Gram tile (w, w) of chunk i+1 -> A block (transposed) -> its inverse
-        const bf16* kb = Kc[b1];
-        f32x4 acc{};
-#pragma unroll
-        for (int s = 0; s < KS; ++s)
-          acc = mma(ld8(kb + (16 * w + li) * KP + 32 * s + 8 * g4), ld8(kb + (16 * w + li) * KP + 32 * s + 8 * g4), acc);
-        // element (j = 16w + 4g + i, t = 16w + li); A[t][j] for j < t
-        const float gt = gv.gam[b1][16 * w + li], bt = gv.bet[b1][16 * w + li];
-#pragma unroll
-        for (int ii = 0; ii < 4; ++ii) {
-          const int jl = 4 * g4 + ii;
-          const float val = (jl < li) ? bt * __expf(gt - gv.gam[b1][16 * w + jl]) * acc[ii] : 0.f;
-          Ad[w][jl * kAdP + li] = val;  // Ad[m = j_local][r = t_local]
-        }
-        if (lane < 16) {  // column c = lane of (I + A_ww)^-1 by right-looking substitution
-          const int c = lane;
-          float x[16];
-#pragma unroll
-          for (int r = 0; r < 16; ++r) x[r] = (r == c) ? 1.f : 0.f;
-#pragma unroll
-          for (int m = 0; m < 15; ++m) {
-            const float* col = &Ad[w][m * kAdP];
-            float a[16];
-#pragma unroll
-            for (int q4 = 0; q4 < 4; ++q4) {
-              const float4 v4 = *reinterpret_cast<const float4*>(col + 4 * q4);
-              a[4 * q4] = v4.x; a[4 * q4 + 1] = v4.y; a[4 * q4 + 2] = v4.z; a[4 * q4 + 3] = v4.w;
-            }
-            const float xm = x[m];
-#pragma unroll
-            for (int r = m + 1; r < 16; ++r) x[r] -= a[r] * xm;
-          }
-          float* tf = &Tf[w >> 1][(16 * (w & 1)) * kTfP + 16 * (w & 1) + c];
-          bf16* tb = &Tb[b1][(16 * w) * kCP + 16 * w + c];
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            tf[r * kTfP] = x[r];
-            tb[r * kCP] = static_cast<bf16>(r == c ? 0.f : x[r]);
-          }
-        }
-      }
-      if (s_on) {  // Y = K S for row tile w, then X -> Xb
+      f32x4 yacc[2] = {};
+      if (s_on) {  // Y = K S for row tile w (MFMAs issued first; the solve below overlaps them)
         const bf16* kb = Kc[b0];
-        f32x4 yacc[2] = {};
 #pragma unroll
         for (int s = 0; s < KS; ++s) {
           const bf16x8 a = ld8(kb + (16 * w + li) * KP + 32 * s + 8 * g4);
@@ -346,6 +308,56 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
           yacc[0] = mma(a, s0, yacc[0]);
           yacc[1] = mma(a, s1, yacc[1]);
         }
+      }
+      if (k_on) {  // diagonal Gram tile (w, w) of chunk i+1 -> A block -> (I + A_ww)^-1
+        const bf16* kb = Kc[b1];
+        f32x4 acc{};
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          const bf16x8 f = ld8(kb + (16 * w + li) * KP + 32 * s + 8 * g4);
+          acc = mma(f, f, acc);
+        }
+        // k.k is symmetric: acc[i] = k_t.k_j with t = 16w + li, j = 16w + 4g + i; A[t][j] for j < t
+        const float gt = gv.gam[b1][16 * w + li], bt = gv.bet[b1][16 * w + li];
+        float av[4];
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) {
+          const int jl = 4 * g4 + ii;
+          av[ii] = (jl < li) ? bt * __expf(gt - gv.gam[b1][16 * w + jl]) * acc[ii] : 0.f;
+        }
+        float* ad = Ad[w];  // row-major 16 x 16 block, pitch kAdP
+        *reinterpret_cast<float4*>(ad + li * kAdP + 4 * g4) = make_float4(av[0], av[1], av[2], av[3]);
+        // Forward substitution on 64 lanes: lane (c = lane/4, k = lane%4) holds rows 4q+k of column c of
+        // T_ww; x_m is broadcast inside each quad with DPP. A is strictly lower (zeros on and above the
+        // diagonal), so the update needs no row mask.
+        const int c = lane >> 2, kq = lane & 3;
+        float ar[4][16];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int m4 = 0; m4 < 4; ++m4) {
+            const float4 v4 = *reinterpret_cast<const float4*>(ad + (4 * q + kq) * kAdP + 4 * m4);
+            ar[q][4 * m4] = v4.x; ar[q][4 * m4 + 1] = v4.y; ar[q][4 * m4 + 2] = v4.z; ar[q][4 * m4 + 3] = v4.w;
+          }
+        float x[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) x[q] = (4 * q + kq == c) ? 1.f : 0.f;
+#pragma unroll
+        for (int m = 0; m < 15; ++m) {
+          const float xm = quad_bcast(x[m >> 2], m & 3);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) x[q] -= ar[q][m] * xm;
+        }
+        float* tf = &Tf[w >> 1][(16 * (w & 1)) * kTfP + 16 * (w & 1) + c];
+        bf16* tb = &Tb[b1][(16 * w) * kCP + 16 * w + c];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int r = 4 * q + kq;
+          tf[r * kTfP] = x[q];
+          tb[r * kCP] = static_cast<bf16>(r == c ? 0.f : x[q]);
+        }
+      }
+      if (s_on) {  // X = beta V - beta e^gam (K S) -> Xb; kept in fp32 for the identity part of T
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) {
           const int vv = 16 * nt + li;
@@ -517,8 +529,8 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
         }
       }
     }
-    if (w < 2 && k_on) {  // T 32 -> 64: W' = A[32:64][0:32] T[0:32][0:32]; T[32:64][0:32] = -T[32:64][32:64] W'
-      const int ct = w;
+    if ((w == 2 || w == 3) && k_on) {  // T 32 -> 64: W' = A[32:64][0:32] T[0:32][0:32]; T[32:64][0:32] = -T[32:64][32:64] W'
+      const int ct = w - 2;
       float* wsc = &Wsc[16 * ct];
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt) {
@@ -562,8 +574,10 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
     __syncthreads();
 
     // ================================================================ stage chunk i+2 (K/Q/gates), i+1 (V)
-    gate_fix(i + 2);
-    if (i + 2 < nc) stage_kq(b0);
+    {  // always consume the prefetch registers (zeros past the last chunk) so no load stays pending
+      const int64_t cn = bos + (int64_t)(i + 2) * kC;
+      stage_kq(b0, i + 2 < nc ? (int)((eos - cn) < kC ? (eos - cn) : kC) : 0);
+    }
     stage_v();
     __syncthreads();
   }

@@ -44,6 +44,21 @@ __device__ __forceinline__ float round_to(int dtype, float x) {
   }
 }
 
+// Raw bits of element i (fp32 as is, 16-bit types zero-extended): a load with no conversion, so the
+// wait for it can be deferred to the first use.
+__device__ __forceinline__ uint32_t load_raw32(const void* p, int dtype, int64_t i) {
+  if (dtype == GDN_DTYPE_F32) return static_cast<const uint32_t*>(p)[i];
+  return static_cast<uint32_t>(static_cast<const uint16_t*>(p)[i]);
+}
+
+__device__ __forceinline__ float raw32_to_f32(uint32_t bits, int dtype) {
+  switch (dtype) {
+    case GDN_DTYPE_BF16: return __uint_as_float(bits << 16);
+    case GDN_DTYPE_F16: return static_cast<float>(__builtin_bit_cast(f16, static_cast<uint16_t>(bits)));
+    default: return __uint_as_float(bits);
+  }
+}
+
 __device__ __forceinline__ int64_t load_index(const void* p, int is_i32, int64_t i) {
   return is_i32 ? static_cast<int64_t>(static_cast<const int32_t*>(p)[i]) : static_cast<const int64_t*>(p)[i];
 }
