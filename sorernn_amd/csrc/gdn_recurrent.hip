@@ -250,6 +250,100 @@ __global__ __launch_bounds__(256) void gated_delta_decode_kernel(DecodeParams p)
   }
 }
 
+
+template <class T>
+__device__ __forceinline__ float elem_to_f32(T x) { return static_cast<float>(x); }
+template <class T>
+__device__ __forceinline__ T f32_to_elem(float x) { return static_cast<T>(x); }
+
+// Width-W conv cache of one channel as one vector access (W * sizeof(T) bytes).
+template <int W, class T>
+struct alignas(W * sizeof(T) >= 16 ? 16 : W * sizeof(T)) ConvWindow {
+  T v[W];
+};
+
+// Fast decode step for width-4 conv caches whose dtype equals the activation dtype T. Every
+// global load of the step is issued before the first dependent use: the first value head's state
+// (64 KB per workgroup at D = 128), the conv caches, inputs and weights of the q/k channels and of
+// that head's v channels, and the gates; the conv math then overlaps the state's arrival.
+template <int D, class T>
+__global__ __launch_bounds__(256) void gated_delta_decode_w4_kernel(DecodeParams p) {
+  constexpr int W = 4;
+  using L = RecLayout<D, D>;
+  using Win = ConvWindow<W, T>;
+  __shared__ float qk[2 * D];
+  __shared__ float vs[2][D];
+  __shared__ float red[2][L::NW * L::CG * 12];
+  const int h = blockIdx.x;
+  const int64_t b = blockIdx.y;
+  const int rep = (int)(p.HV / p.H);
+  const int64_t C = (2 * p.H + p.HV) * D;
+  const int t = threadIdx.x;
+  const T* __restrict__ xg = static_cast<const T*>(p.x);
+  Win* __restrict__ cs = static_cast<Win*>(p.conv_state);
+  const float4* __restrict__ wg = reinterpret_cast<const float4*>(p.conv_w);
+  const bool l2 = p.flags & GDN_FLAG_QK_L2NORM;
+
+  // channel handled by this thread: q/k channel e = t (t < 2D) and v channel e = t (t < D)
+  const bool has_qk = t < 2 * D, has_v = t < D;
+  const int64_t ch_qk = (t < D) ? (int64_t)h * D + t : p.H * D + (int64_t)h * D + (t - D);
+
+  for (int r = 0; r < rep; ++r) {
+    const int hv = h * rep + r;
+    const int par = r & 1;
+    const int64_t sbase = (b * p.HV + hv) * (int64_t)D * D;
+    StateRegs<D, D> s;
+    load_state<D, D>(s, p.state + sbase);
+    const int64_t ch_v = 2 * p.H * D + (int64_t)hv * D + t;
+    Win wq{}, wv{};
+    T xq{}, xv{};
+    float4 kq{}, kv{};
+    const bool do_qk = has_qk && r == 0;
+    if (do_qk) {
+      wq = cs[b * C + ch_qk];
+      xq = xg[b * C + ch_qk];
+      kq = wg[ch_qk];
+    }
+    if (has_v) {
+      wv = cs[b * C + ch_v];
+      xv = xg[b * C + ch_v];
+      kv = wg[ch_v];
+    }
+    const uint32_t graw = load_raw32(p.g, p.dg, b * p.HV + hv);
+    const uint32_t braw = load_raw32(p.beta, p.db, b * p.HV + hv);
+    // conv: window = (cache[1..3], x); y = sum_i w[i] window[i]; the new cache is the window
+    if (do_qk) {
+      const float y = kq.x * elem_to_f32(wq.v[1]) + kq.y * elem_to_f32(wq.v[2]) + kq.z * elem_to_f32(wq.v[3]) +
+                      kq.w * elem_to_f32(xq);
+      Win nw;
+      nw.v[0] = wq.v[1]; nw.v[1] = wq.v[2]; nw.v[2] = wq.v[3]; nw.v[3] = xq;
+      cs[b * C + ch_qk] = nw;
+      qk[t] = elem_to_f32(f32_to_elem<T>(silu_f32(y)));
+    }
+    if (has_v) {
+      const float y = kv.x * elem_to_f32(wv.v[1]) + kv.y * elem_to_f32(wv.v[2]) + kv.z * elem_to_f32(wv.v[3]) +
+                      kv.w * elem_to_f32(xv);
+      Win nw;
+      nw.v[0] = wv.v[1]; nw.v[1] = wv.v[2]; nw.v[2] = wv.v[3]; nw.v[3] = xv;
+      cs[b * C + ch_v] = nw;
+      vs[par][t] = elem_to_f32(f32_to_elem<T>(silu_f32(y)));
+    }
+    float gv = raw32_to_f32(graw, p.dg), bv = raw32_to_f32(braw, p.db);
+    if (p.flags & GDN_FLAG_GATE_IN_KERNEL) gv = -expf(p.A_log[hv]) * softplus_f32(gv + p.dt_bias[hv]);
+    if (p.flags & GDN_FLAG_BETA_SIGMOID) bv = sigmoid_f32(bv);
+    const float a = expf(gv);
+    __syncthreads();
+    float o4[4];
+    rec_token<D, D>(s, qk, qk + D, vs[par], a, bv, l2, p.scale, red[par], o4);
+    if (t < L::CG) {
+      T* og = static_cast<T*>(p.o) + (b * p.HV + hv) * D + 4 * t;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) og[c] = f32_to_elem<T>(o4[c]);
+    }
+    store_state<D, D>(s, p.state + sbase);
+  }
+}
+
 }  // namespace gdn
 
 using namespace gdn;
@@ -329,6 +423,14 @@ extern "C" int gdn_decode_step(const void* x_qkv, void* conv_state, const float*
                  g_dtype, beta_dtype, scale, flags, A_log, dt_bias};
   dim3 grid((unsigned)H, (unsigned)B), block(256);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (W == 4 && conv_state_dtype == x_dtype) {  // vectorised width-4 path
+#define GDN_DECODE_W4(D_, T_) hipLaunchKernelGGL((gated_delta_decode_w4_kernel<D_, T_>), grid, block, 0, s, p)
+    if (x_dtype == GDN_DTYPE_BF16) { if (D == 128) GDN_DECODE_W4(128, bf16); else GDN_DECODE_W4(64, bf16); }
+    else if (x_dtype == GDN_DTYPE_F16) { if (D == 128) GDN_DECODE_W4(128, f16); else GDN_DECODE_W4(64, f16); }
+    else { if (D == 128) GDN_DECODE_W4(128, float); else GDN_DECODE_W4(64, float); }
+#undef GDN_DECODE_W4
+    return gdn_internal_check_launch("gated_delta_decode_w4_kernel");
+  }
   if (D == 128) hipLaunchKernelGGL((gated_delta_decode_kernel<128>), grid, block, 0, s, p);
   else hipLaunchKernelGGL((gated_delta_decode_kernel<64>), grid, block, 0, s, p);
   return gdn_internal_check_launch("gated_delta_decode_kernel");
