@@ -1,0 +1,119 @@
+"""GatedDeltaNet layer on the gfx950 ops: the reference layer with only its kernel imports swapped.
+
+Counterpart of ``GatedDeltaNet`` in ``sore/model/gdn.py:81-209`` (its ``fla`` backend with
+``gdn_fla_conv`` and ``fused_norm_gate`` on). The parameters, their names, shapes and init are the
+reference's (``gdn.py:97-132``), so a reference ``state_dict`` loads unchanged; the forward keeps
+the reference's call expressions (``gdn.py:145-189``) with ``chunk_gated_delta_rule``,
+``causal_conv1d`` and ``rms_norm_gated`` taken from ``sorernn_amd`` instead of FLA. The chunk-index
+patch of the FLA path (``gdn.py:31-78``) has no counterpart: the chunk kernel's grid depends only on
+the number of sequences, so nothing is read back from the device.
+
+Forward only (the ops raise on inputs that require grad); activations in bf16 (e.g. under
+``torch.autocast("cuda", dtype=torch.bfloat16)``, as the reference trains).
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+from torch import Tensor, nn
+
+from sorernn_amd.ops import causal_conv1d, chunk_gated_delta_rule, rms_norm_gated
+
+_DT_MIN, _DT_MAX = 1e-3, 1e-1
+
+
+@dataclass
+class GDNLayerConfig:
+    """The ``ModelConfig`` fields the layer reads (``sore/model/config.py:11,20-23,43,53``)."""
+
+    d_model: int
+    gdn_qk_heads: int = 1
+    gdn_v_heads: int = 1
+    gdn_head_dim: int = 128
+    conv_kernel: int = 4
+    norm_eps: float = 1e-6
+    gdn_kernel_gate: bool = False
+
+    def __post_init__(self) -> None:
+        if self.gdn_v_heads % self.gdn_qk_heads:
+            raise ValueError(f"gdn_v_heads={self.gdn_v_heads} must be a multiple of gdn_qk_heads={self.gdn_qk_heads}")
+
+
+class _NormWeight(nn.Module):
+    """Holds ``o_norm.weight`` / ``o_norm.eps`` with the reference's names (``sore/model/layers.py:7-13``)."""
+
+    def __init__(self, dim: int, eps: float) -> None:
+        super().__init__()
+        self.eps = eps
+        self.weight = nn.Parameter(torch.ones(dim))
+
+
+class GatedDeltaNet(nn.Module):
+    """``o_proj(RMSNorm(o) * silu(g_proj(x)))`` with ``o`` from the chunked gated delta rule on gfx950.
+
+    ``forward(x [B,T,D], cu_seqlens=None, cu_seqlens_cpu=None)``: with ``cu_seqlens`` (``[S+1]``,
+    ``B == 1``) the conv and the recurrent state restart at every document; without it every batch
+    row is one document. ``cu_seqlens_cpu`` (same values on the host) lets the ops validate the
+    bounds without a device sync.
+    """
+
+    def __init__(self, cfg: GDNLayerConfig) -> None:
+        super().__init__()
+        self.kernel_gate = cfg.gdn_kernel_gate
+        self.qk_heads = cfg.gdn_qk_heads
+        self.v_heads = cfg.gdn_v_heads
+        self.head_dim = cfg.gdn_head_dim
+        d = cfg.d_model
+        qk_dim = self.qk_heads * self.head_dim
+        v_dim = self.v_heads * self.head_dim
+        self.q_proj = nn.Linear(d, qk_dim, bias=False)
+        self.k_proj = nn.Linear(d, qk_dim, bias=False)
+        self.v_proj = nn.Linear(d, v_dim, bias=False)
+        self.g_proj = nn.Linear(d, v_dim, bias=False)
+        self.a_proj = nn.Linear(d, self.v_heads, bias=False)
+        self.b_proj = nn.Linear(d, self.v_heads, bias=False)
+        # depthwise conv weights [C, K] in fp32, nn.Conv1d's default init U(+-1/sqrt(K))
+        bound = cfg.conv_kernel**-0.5
+        self.conv_q = nn.Parameter(torch.empty(qk_dim, cfg.conv_kernel).uniform_(-bound, bound))
+        self.conv_k = nn.Parameter(torch.empty(qk_dim, cfg.conv_kernel).uniform_(-bound, bound))
+        self.conv_v = nn.Parameter(torch.empty(v_dim, cfg.conv_kernel).uniform_(-bound, bound))
+        # decay: A ~ U(1, 16); dt log-uniform in [1e-3, 1e-1], dt_bias = softplus^-1(dt)
+        self.A_log = nn.Parameter(torch.empty(self.v_heads).uniform_(1, 16).log())
+        log_dt = torch.rand(self.v_heads) * (math.log(_DT_MAX) - math.log(_DT_MIN)) + math.log(_DT_MIN)
+        dt = log_dt.exp()
+        self.dt_bias = nn.Parameter(dt + torch.log(-torch.expm1(-dt)))
+        self.o_norm = _NormWeight(self.head_dim, cfg.norm_eps)
+        self.o_proj = nn.Linear(v_dim, d, bias=False)
+
+    def forward(self, x: Tensor, cu_seqlens: Tensor | None = None, cu_seqlens_cpu: Tensor | None = None) -> Tensor:
+        b, t, _ = x.shape
+
+        def conv(h: Tensor, weight: Tensor) -> Tensor:
+            return causal_conv1d(h, weight, activation="silu", cu_seqlens=cu_seqlens, cu_seqlens_cpu=cu_seqlens_cpu)[0]
+
+        q = conv(self.q_proj(x), self.conv_q).view(b, t, self.qk_heads, self.head_dim)
+        k = conv(self.k_proj(x), self.conv_k).view(b, t, self.qk_heads, self.head_dim)
+        v = conv(self.v_proj(x), self.conv_v).view(b, t, self.v_heads, self.head_dim)
+        scale = self.head_dim**-0.5
+        if self.kernel_gate:
+            gate_kwargs = dict(use_gate_in_kernel=True, A_log=self.A_log, dt_bias=self.dt_bias,
+                               use_beta_sigmoid_in_kernel=True)
+            g, beta = self.a_proj(x), self.b_proj(x)
+        else:
+            gate_kwargs = {}
+            g, beta = self._gate_and_beta(x)
+        o, _ = chunk_gated_delta_rule(
+            q, k, v, g, beta, scale=scale, cu_seqlens=cu_seqlens, cu_seqlens_cpu=cu_seqlens_cpu,
+            use_qk_l2norm_in_kernel=True, **gate_kwargs,
+        )
+        gate = self.g_proj(x).view(b, t, self.v_heads, self.head_dim)
+        o = rms_norm_gated(o, gate, self.o_norm.weight, None, activation="swish", eps=self.o_norm.eps)
+        return self.o_proj(o.flatten(-2))
+
+    def _gate_and_beta(self, x: Tensor) -> tuple[Tensor, Tensor]:
+        # g (log-decay, <= 0) in fp32; beta may stay in the activation dtype (sore/model/gdn.py:191-194)
+        g = -self.A_log.float().exp() * F.softplus(self.a_proj(x).float() + self.dt_bias.float())
+        return g, self.b_proj(x).sigmoid()
