@@ -26,7 +26,7 @@ struct ConvParams {
 constexpr int kConvTokens = 64;
 
 template <int W>
-__global__ __launch_bounds__(256) void causal_conv1d_kernel(ConvParams p) {
+__global__ __launch_bounds__(256) void gated_delta_conv1d_kernel(ConvParams p) {
   const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (c >= p.C) return;
   const int64_t bb = blockIdx.z;  // batch row (B == 1 with cu_seqlens)
@@ -129,14 +129,14 @@ extern "C" int gdn_causal_conv1d_fwd(const void* x, const float* weight, const f
   dim3 grid((unsigned)((C + 255) / 256), (unsigned)tb, (unsigned)B), block(256);
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (W) {
-    case 1: hipLaunchKernelGGL(causal_conv1d_kernel<1>, grid, block, 0, s, p); break;
-    case 2: hipLaunchKernelGGL(causal_conv1d_kernel<2>, grid, block, 0, s, p); break;
-    case 3: hipLaunchKernelGGL(causal_conv1d_kernel<3>, grid, block, 0, s, p); break;
-    case 4: hipLaunchKernelGGL(causal_conv1d_kernel<4>, grid, block, 0, s, p); break;
-    case 5: hipLaunchKernelGGL(causal_conv1d_kernel<5>, grid, block, 0, s, p); break;
-    case 6: hipLaunchKernelGGL(causal_conv1d_kernel<6>, grid, block, 0, s, p); break;
-    case 7: hipLaunchKernelGGL(causal_conv1d_kernel<7>, grid, block, 0, s, p); break;
-    default: hipLaunchKernelGGL(causal_conv1d_kernel<8>, grid, block, 0, s, p); break;
+    case 1: hipLaunchKernelGGL(gated_delta_conv1d_kernel<1>, grid, block, 0, s, p); break;
+    case 2: hipLaunchKernelGGL(gated_delta_conv1d_kernel<2>, grid, block, 0, s, p); break;
+    case 3: hipLaunchKernelGGL(gated_delta_conv1d_kernel<3>, grid, block, 0, s, p); break;
+    case 4: hipLaunchKernelGGL(gated_delta_conv1d_kernel<4>, grid, block, 0, s, p); break;
+    case 5: hipLaunchKernelGGL(gated_delta_conv1d_kernel<5>, grid, block, 0, s, p); break;
+    case 6: hipLaunchKernelGGL(gated_delta_conv1d_kernel<6>, grid, block, 0, s, p); break;
+    case 7: hipLaunchKernelGGL(gated_delta_conv1d_kernel<7>, grid, block, 0, s, p); break;
+    default: hipLaunchKernelGGL(gated_delta_conv1d_kernel<8>, grid, block, 0, s, p); break;
   }
-  return gdn_internal_check_launch("causal_conv1d_kernel");
+  return gdn_internal_check_launch("gated_delta_conv1d_kernel");
 }
