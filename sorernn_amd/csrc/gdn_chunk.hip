@@ -58,7 +58,7 @@ constexpr int kCP = kC + 8;   // bf16 pitch of [*][64] operand tiles (144 B rows
 constexpr int kVP = kVB + 8;  // bf16 pitch of the V slice (80 B rows)
 constexpr int kAdP = 20;      // fp32 pitch of the diagonal A blocks
 constexpr int kAoP = 52;      // fp32 pitch of the off-diagonal A rows 16..63 x cols 0..47
-constexpr int kTfP = 36;      // fp32 pitch of the two 32x32 T blocks and the merge scratch
+constexpr int kTfP = 36;      // fp32 pitch of the two 32x32 T blocks
 
 typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
 typedef short i16x4 __attribute__((ext_vector_type(4)));
@@ -128,7 +128,9 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
   constexpr int KS = KD / 32;      // MFMA k-steps over the key dim
   constexpr int KCH = KD / 8;      // 16-byte chunks per q/k row
   constexpr int QKPT = kC * KCH / kNT;  // q/k 16-byte chunks per thread per matrix
-  constexpr int STW = KD / 64;     // state tiles (16 x 16) per wave
+  // State tiles (16 x 16; KD/8 of them) owned per wave: waves 0-1 hold KD/32 each, waves 4-7 KD/64
+  // each, waves 2-3 none (they run the 32 -> 64 merge of T in phase C instead).
+  constexpr int SMAX = KD / 32;
 
   __shared__ __align__(16) bf16 Kc[2][kC * KP];
   __shared__ __align__(16) bf16 Qc[2][kC * KP];
@@ -137,7 +139,6 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
   __shared__ __align__(16) float Ad[4][16 * kAdP];       // diagonal A blocks, row-major: Ad[b][r][m] = A[16b+r][16b+m]
   __shared__ __align__(16) float Ao[48 * kAoP];          // A rows 16..63 x cols 0..47 (off-diagonal lower blocks)
   __shared__ __align__(16) float Tf[2][32 * kTfP];       // T[0:32][0:32] and T[32:64][32:64] in fp32
-  __shared__ __align__(16) float Wsc[32 * kTfP];         // merge scratch
   __shared__ __align__(16) bf16 Tb[2][kC * kCP];         // T - I in bf16, A operand [t][j], per chunk parity
   __shared__ __align__(16) bf16 Pb[kC * kCP];
   __shared__ __align__(16) bf16 Xb[kVB * kCP];
@@ -244,13 +245,8 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
         if (p.flags & GDN_FLAG_GATE_IN_KERNEL) gval = -__expf(p.A_log[hv]) * softplus_f32(gval + p.dt_bias[hv]);
         if (p.flags & GDN_FLAG_BETA_SIGMOID) bval = sigmoid_f32(bval);
       }
-      float cs = gval;
-#pragma unroll
-      for (int off = 1; off < kWave; off <<= 1) {
-        const float y = __shfl_up(cs, off, kWave);
-        if (lane >= off) cs += y;
-      }
-      const float last = __shfl(cs, kWave - 1, kWave);
+      const float cs = wave_inclusive_sum(gval);
+      const float last = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cs), kWave - 1));
       const float e = __expf(cs);
       gv.gam[buf][lane] = cs;
       gv.egam[buf][lane] = e;
@@ -270,12 +266,15 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
     reinterpret_cast<bf16x8*>(Pb)[e] = bf16x8{};
   }
 
-  // state slice: 16x16 tiles ti = STW*w + u, row tile ti/2, column tile ti%2
-  f32x4 sacc[STW];
+  // state slice: 16x16 tiles ti = s_first + u (u < s_count), row tile ti/2, column tile ti%2
+  const int s_count = (w < 2) ? KD / 32 : (w >= 4 ? KD / 64 : 0);
+  const int s_first = (w < 2) ? w * (KD / 32) : 2 * (KD / 32) + (w - 4) * (KD / 64);
+  f32x4 sacc[SMAX];
   const int64_t sbase = (n * p.HV + hv) * (int64_t)KD * VD + vb * kVB;
 #pragma unroll
-  for (int u = 0; u < STW; ++u) {
-    const int ti = STW * w + u, kd0 = 16 * (ti >> 1) + 4 * g4, vv = 16 * (ti & 1) + li;
+  for (int u = 0; u < SMAX; ++u) {
+    if (u >= s_count) break;
+    const int ti = s_first + u, kd0 = 16 * (ti >> 1) + 4 * g4, vv = 16 * (ti & 1) + li;
 #pragma unroll
     for (int i = 0; i < 4; ++i) sacc[u][i] = p.h0 ? p.h0[sbase + (int64_t)(kd0 + i) * VD + vv] : 0.f;
     *reinterpret_cast<bf16x4*>(Sb + vv * KP + kd0) = to_bf16x4(sacc[u][0], sacc[u][1], sacc[u][2], sacc[u][3]);
@@ -458,9 +457,10 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
         }
       }
     } else if (w < 6 && k_on) {  // T 16 -> 32 merges: T_{2q+1,2q} = -T_{2q+1,2q+1} (A_{2q+1,2q} T_{2q,2q})
+      // W = A T_{2q,2q} lands in accumulator layout (lane (g, i): rows 4g..4g+3 of column i), which is
+      // the B-operand layout of the 16x16x16 MFMA, so the second product takes W from registers.
       const int q = w - 4;
       const float* tq = Tf[q];
-      float* wsc = &Wsc[16 * q];  // 16x16 scratch in columns 16q..16q+15
       f32x4 acc{};
       {
         float a[4], b[4];
@@ -470,15 +470,12 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
         for (int m = 0; m < 4; ++m) b[m] = tq[(4 * g4 + m) * kTfP + li];
         acc = mma16x3(a, b, acc);
       }
-#pragma unroll
-      for (int ii = 0; ii < 4; ++ii) wsc[(4 * g4 + ii) * kTfP + li] = acc[ii];
       f32x4 acc2{};
       {
-        float a[4], b[4];
+        float a[4];
+        const float b[4] = {acc[0], acc[1], acc[2], acc[3]};
         const float* ar = &tq[(16 + li) * kTfP + 16 + 4 * g4];
         a[0] = ar[0]; a[1] = ar[1]; a[2] = ar[2]; a[3] = ar[3];
-#pragma unroll
-        for (int m = 0; m < 4; ++m) b[m] = wsc[(4 * g4 + m) * kTfP + li];
         acc2 = mma16x3(a, b, acc2);
       }
       float* tw = &Tf[q][16 * kTfP];
@@ -517,8 +514,9 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
       const float ec = __expf(gv.gam[b0][kC - 1]);
       const bf16* kb = Kc[b0];
 #pragma unroll
-      for (int u = 0; u < STW; ++u) {
-        const int ti = STW * w + u, rt = ti >> 1, nt = ti & 1;
+      for (int u = 0; u < SMAX; ++u) {
+        if (u >= s_count) break;
+        const int ti = s_first + u, rt = ti >> 1, nt = ti & 1;
         sacc[u] *= ec;
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
@@ -529,34 +527,33 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
         }
       }
     }
-    if ((w == 2 || w == 3) && k_on) {  // T 32 -> 64: W' = A[32:64][0:32] T[0:32][0:32]; T[32:64][0:32] = -T[32:64][32:64] W'
-      const int ct = w - 2;
-      float* wsc = &Wsc[16 * ct];
+    if ((w == 2 || w == 3) && k_on) {  // T 32 -> 64: T[32:64][0:32] = -T[32:64][32:64] (A[32:64][0:32] T[0:32][0:32])
+      const int ct = w - 2;  // column block of the result
+      f32x4 wacc[2];         // W' tiles (rt, ct), kept in registers as the B operand of the second product
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt) {
-        f32x4 acc{};
+        wacc[rt] = f32x4{};
 #pragma unroll
-        for (int ks = ct; ks < 2; ++ks) {  // T[k][c] vanishes for k < c
+        for (int ks = 0; ks < 2; ++ks) {
+          if (ks < ct) continue;  // T[k][c] vanishes for k < c
           float a[4], b[4];
           const float* ar = &Ao[(16 + 16 * rt + li) * kAoP + 16 * ks + 4 * g4];
           a[0] = ar[0]; a[1] = ar[1]; a[2] = ar[2]; a[3] = ar[3];
 #pragma unroll
           for (int m = 0; m < 4; ++m) b[m] = Tf[0][(16 * ks + 4 * g4 + m) * kTfP + 16 * ct + li];
-          acc = mma16x3(a, b, acc);
+          wacc[rt] = mma16x3(a, b, wacc[rt]);
         }
-#pragma unroll
-        for (int ii = 0; ii < 4; ++ii) wsc[(16 * rt + 4 * g4 + ii) * kTfP + li] = acc[ii];
       }
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt) {
         f32x4 acc{};
 #pragma unroll
-        for (int ks = 0; ks <= rt; ++ks) {  // T[32+r][32+k] vanishes for k > r
-          float a[4], b[4];
+        for (int ks = 0; ks < 2; ++ks) {
+          if (ks > rt) continue;  // T[32+r][32+k] vanishes for k > r
+          float a[4];
+          const float b[4] = {wacc[ks][0], wacc[ks][1], wacc[ks][2], wacc[ks][3]};
           const float* ar = &Tf[1][(16 * rt + li) * kTfP + 16 * ks + 4 * g4];
           a[0] = ar[0]; a[1] = ar[1]; a[2] = ar[2]; a[3] = ar[3];
-#pragma unroll
-          for (int m = 0; m < 4; ++m) b[m] = wsc[(16 * ks + 4 * g4 + m) * kTfP + li];
           acc = mma16x3(a, b, acc);
         }
         bf16* tbw = &Tb[b1][(32 + 16 * rt) * kCP + 16 * ct];
@@ -566,8 +563,9 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
     }
     if (s_on) {
 #pragma unroll
-      for (int u = 0; u < STW; ++u) {
-        const int ti = STW * w + u, kd0 = 16 * (ti >> 1) + 4 * g4, vv = 16 * (ti & 1) + li;
+      for (int u = 0; u < SMAX; ++u) {
+        if (u >= s_count) break;
+        const int ti = s_first + u, kd0 = 16 * (ti >> 1) + 4 * g4, vv = 16 * (ti & 1) + li;
         *reinterpret_cast<bf16x4*>(Sb + vv * KP + kd0) = to_bf16x4(sacc[u][0], sacc[u][1], sacc[u][2], sacc[u][3]);
       }
     }
@@ -584,8 +582,9 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
 
   if (p.ht) {
 #pragma unroll
-    for (int u = 0; u < STW; ++u) {
-      const int ti = STW * w + u, kd0 = 16 * (ti >> 1) + 4 * g4, vv = 16 * (ti & 1) + li;
+    for (int u = 0; u < SMAX; ++u) {
+      if (u >= s_count) break;
+      const int ti = s_first + u, kd0 = 16 * (ti >> 1) + 4 * g4, vv = 16 * (ti & 1) + li;
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii) p.ht[sbase + (int64_t)(kd0 + ii) * VD + vv] = sacc[u][ii];
     }
@@ -642,3 +641,4 @@ extern "C" int gdn_chunk_fwd(const void* q, const void* k, const void* v, const 
   else hipLaunchKernelGGL((gated_delta_chunk_kernel<64, 128>), grid, block, 0, s, p);
   return gdn_internal_check_launch("gated_delta_chunk_kernel");
 }
+

@@ -75,6 +75,25 @@ __device__ __forceinline__ float wave_xor_sum(float x, int from_stride) {
   return x;
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave with DPP (no LDS): shifts of 1, 2, 4, 8 inside
+// each row of 16 lanes, then row_bcast:15 into rows 1 and 3 and row_bcast:31 into rows 2 and 3.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_add(float v) {
+  const int s = __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false);
+  return v + __int_as_float(s);
+}
+
+__device__ __forceinline__ float wave_inclusive_sum(float x) {
+  // DPP row_shr:n = 0x110 + n; row_bcast:15 = 0x142; row_bcast:31 = 0x143
+  x = dpp_add<0x111, 0xf>(x);
+  x = dpp_add<0x112, 0xf>(x);
+  x = dpp_add<0x114, 0xf>(x);
+  x = dpp_add<0x118, 0xf>(x);
+  x = dpp_add<0x142, 0xa>(x);
+  x = dpp_add<0x143, 0xc>(x);
+  return x;
+}
+
 }  // namespace gdn
 
 // Error channel shared by every entry point (defined in gdn_api.hip).
