@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define GDN_ABI_VERSION 1
+#define GDN_ABI_VERSION 2
 
 #if defined(__GNUC__) || defined(__clang__)
 #define GDN_API __attribute__((visibility("default")))
@@ -64,15 +64,25 @@ GDN_API const char* gdn_last_error(void);
  * output_final_state, use_qk_l2norm_in_kernel, use_beta_sigmoid_in_kernel, ..., cu_seqlens,
  * cu_seqlens_cpu) as called at sore/model/gdn.py:166-169 (signature:
  * docs/superpowers/plans/2026-10-23-sorernn-v2-core.md:141; gate kwargs gdn.py:157-162).
- * q/k/v/o share qkv_dtype (bf16 or f32); g and beta have their own dtypes. initial_state may be
- * NULL (zero state); final_state may be NULL (not written). A_log/dt_bias [HV] fp32 are read only
- * with GDN_FLAG_GATE_IN_KERNEL. K and V must each be 64 or 128.
+ * q/k/v/o are bf16; g and beta have their own dtypes. initial_state may be NULL (zero state);
+ * final_state may be NULL (not written). A_log/dt_bias [HV] fp32 are read only with
+ * GDN_FLAG_GATE_IN_KERNEL. K and V must each be 64 or 128.
+ * workspace: caller-owned device memory of at least gdn_chunk_workspace_size(B, T, HV, N,
+ * cu_seqlens != NULL) bytes (the per-chunk (I + A)^-1 rows passed between the two kernels of the
+ * call; its contents on entry do not matter). Calls that share a workspace must not overlap.
  */
 GDN_API int gdn_chunk_fwd(const void* q, const void* k, const void* v, const void* g, const void* beta,
                   const float* initial_state, void* o, float* final_state, const void* cu_seqlens,
                   int64_t B, int64_t T, int64_t H, int64_t HV, int64_t K, int64_t V, int64_t N,
                   int qkv_dtype, int g_dtype, int beta_dtype, float scale, unsigned flags,
-                  const float* A_log, const float* dt_bias, void* stream);
+                  const float* A_log, const float* dt_bias, void* workspace, size_t workspace_bytes,
+                  void* stream);
+
+/*
+ * Workspace bytes gdn_chunk_fwd needs for these sizes (varlen != 0 when cu_seqlens is passed);
+ * 0 for invalid sizes. No counterpart in the reference: FLA allocates its intermediates itself.
+ */
+GDN_API size_t gdn_chunk_workspace_size(int64_t B, int64_t T, int64_t HV, int64_t N, int varlen);
 
 /*
  * Recurrent gated delta rule forward: tokens in order, the state held on chip for the whole

@@ -20,25 +20,29 @@ FLAG_BETA_SIGMOID = 0x2
 FLAG_GATE_IN_KERNEL = 0x4
 FLAG_CU_INT32 = 0x8
 ACT_NONE, ACT_SILU = 0, 1
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
 _INT = ctypes.c_int
 _F = ctypes.c_float
 _U = ctypes.c_uint
+_SZ = ctypes.c_size_t
 
 # name -> argtypes, mirroring include/gdn.h
 SIGNATURES = {
     "gdn_abi_version": [],
     "gdn_last_error": [],
-    "gdn_chunk_fwd": [_P] * 9 + [_I64] * 7 + [_INT] * 3 + [_F, _U, _P, _P, _P],
+    "gdn_chunk_fwd": [_P] * 9 + [_I64] * 7 + [_INT] * 3 + [_F, _U, _P, _P, _P, _SZ, _P],
+    "gdn_chunk_workspace_size": [_I64] * 4 + [_INT],
     "gdn_recurrent_fwd": [_P] * 9 + [_I64] * 7 + [_INT] * 3 + [_F, _U, _P, _P, _P],
     "gdn_decode_step": [_P] * 7 + [_I64] * 5 + [_INT] * 4 + [_F, _U, _P, _P, _P],
     "gdn_causal_conv1d_fwd": [_P] * 7 + [_I64] * 5 + [_INT, _INT, _U, _P],
     "gdn_l2norm_fwd": [_P, _P, _I64, _I64, _INT, _F, _P],
     "gdn_rms_norm_gated_fwd": [_P] * 5 + [_I64, _I64, _INT, _F, _INT, _P],
 }
+
+RESTYPES = {"gdn_last_error": ctypes.c_char_p, "gdn_chunk_workspace_size": ctypes.c_size_t}
 
 _lib = None
 
@@ -61,7 +65,7 @@ def load() -> ctypes.CDLL:
     for name, argtypes in SIGNATURES.items():
         fn = getattr(lib, name)
         fn.argtypes = argtypes
-        fn.restype = ctypes.c_char_p if name == "gdn_last_error" else ctypes.c_int
+        fn.restype = RESTYPES.get(name, ctypes.c_int)
     ver = lib.gdn_abi_version()
     if ver != ABI_VERSION:
         raise RuntimeError(f"libgdn.so ABI version {ver} != expected {ABI_VERSION}; rebuild it")

@@ -1,0 +1,38 @@
+// Internal interface between the two kernels of the chunked prefill and its C-ABI entry point.
+//
+// The prefill runs as two launches on the caller's stream:
+//   1. gated_delta_chunk_prep_kernel (gdn_chunk_prep.hip): for every 64-token chunk and value head,
+//      the inverse T = (I + A)^-1 of the chunk's unit lower-triangular system, written to the
+//      workspace as bf16 rows of T - I. Chunks are independent, so this kernel is fully parallel.
+//   2. gated_delta_chunk_kernel (gdn_chunk.hip): the sequential state recurrence over the chunks
+//      of each sequence, reading T from the workspace.
+// With cu_seqlens, a one-block gated_delta_chunk_index_kernel first writes the number of chunks
+// before every sequence (the prep kernel's chunk -> sequence map) into the workspace.
+//
+// Workspace (caller-owned, gdn_chunk_workspace_size bytes):
+//   [0, tbytes)                T - I rows: bf16 [B*T][HV][64], row t of the chunk holding token t
+//   [tbytes, + (N+1)*4)        with cu_seqlens only: int32 chunk_first[N + 1]
+#pragma once
+
+#include "gdn_mfma.h"
+
+namespace gdn {
+
+struct ChunkPrepParams {
+  const void *k, *g, *beta;
+  bf16* tw;                // T - I rows (workspace)
+  const void* cu;
+  const int* chunk_first;  // with cu only
+  int cu_i32;
+  int64_t T, H, HV, N;
+  int dg, db;
+  unsigned flags;
+  const float *A_log, *dt_bias;
+};
+
+inline int64_t chunk_t_bytes(int64_t tokens, int64_t HV) { return ((tokens * HV * kC * 2 + 255) / 256) * 256; }
+
+// Launches the index kernel (with cu) and the prep kernel; returns a GDN status.
+int launch_chunk_prep(const ChunkPrepParams& p, int64_t B, int64_t K, hipStream_t s);
+
+}  // namespace gdn

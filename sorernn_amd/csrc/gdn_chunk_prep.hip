@@ -1,0 +1,309 @@
+// The T-solve kernel of the chunked prefill (gfx950): for every 64-token chunk and value head,
+// T = (I + A)^-1 with A_tj = beta_t exp(gam_t - gam_j) k_t.k_j for j < t (gam = in-chunk cumsum
+// of g). This is the UT/WY transform of the chunked gated delta rule
+// (oracle/gdn_oracle.py::_chunk_segment restates it; sore/model/gdn_ref.py:17-21 is the recurrence
+// it reorganises). T depends only on the chunk's k, g and beta, so every chunk is solved in
+// parallel here and the sequential state kernel only reads the result.
+//
+// One workgroup of 4 waves per (chunk, value head):
+//   load:   k rows (L2-normalised when asked, rounded to bf16 as the state kernel sees them) -> LDS;
+//           g/beta -> gate terms (wave 0, DPP scan).
+//   Gram:   wave r computes the 16x16 k.k tiles (r, cb >= r) with bf16 MFMA (exact products, fp32
+//           sums), scales them into A, and solves its diagonal block T_rr = (I + A_rr)^-1 by
+//           forward substitution on 64 lanes (fp32).
+//   merge:  T_{2q+1,2q} = -T_{2q+1,2q+1} A_{2q+1,2q} T_{2q,2q} (16 -> 32), then the 32 -> 64
+//           block, with three-term bf16 products (hi*hi + hi*lo + lo*hi, ~2^-16 relative).
+//   store:  rows of T - I (bf16, zeros above the diagonal) to the workspace, one 128-byte row per
+//           token: the A operand of Delta = X + (T - I) X in the state kernel.
+
+#include <type_traits>
+
+#include "gdn_chunk.h"
+
+namespace gdn {
+
+constexpr int kPrepNT = 256;
+
+template <int KD>
+__global__ __launch_bounds__(kPrepNT) void gated_delta_chunk_prep_kernel(ChunkPrepParams p) {
+  constexpr int KP = KD + 8;   // bf16 pitch of the k tile
+  constexpr int KS = KD / 32;  // MFMA k-steps over the key dim
+  constexpr int KCH = KD / 8;  // 16-byte chunks per k row
+  constexpr int KPT = kC * KCH / kPrepNT;
+
+  __shared__ __align__(16) bf16 Kc[kC * KP];
+  __shared__ __align__(16) float Ad[4][256];       // diagonal A blocks: Ad[b][(4m + k) * 4 + q] = A[16b+4q+k][16b+m]
+  __shared__ __align__(16) float Ao[48 * kAoP];     // A rows 16..63 x cols 0..47 (off-diagonal lower blocks)
+  __shared__ __align__(16) float Tf[2][32 * kTfP];  // T[0:32][0:32] and T[32:64][32:64] in fp32
+  __shared__ __align__(16) bf16 Tb[kC * kCP];       // T - I in bf16 [t][j]
+  __shared__ __align__(16) ChunkGates gs;
+
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6, g4 = lane >> 4, li = lane & 15;
+  const int hv = blockIdx.y;
+  const int h = hv / (int)(p.HV / p.H);
+
+  // chunk -> (sequence n, chunk c of n)
+  const int64_t item = blockIdx.x;
+  int64_t n, c, bos, eos;
+  if (p.cu) {
+    // largest n with chunk_first[n] <= item (skips empty sequences)
+    if (item >= p.chunk_first[p.N]) return;
+    int64_t lo = 0, hi = p.N - 1;
+    while (lo < hi) {
+      const int64_t mid = (lo + hi + 1) / 2;
+      if (p.chunk_first[mid] <= item) lo = mid;
+      else hi = mid - 1;
+    }
+    n = lo;
+    c = item - p.chunk_first[n];
+    bos = load_index(p.cu, p.cu_i32, n);
+    eos = load_index(p.cu, p.cu_i32, n + 1);
+  } else {
+    const int64_t ncs = (p.T + kC - 1) / kC;
+    n = item / ncs;
+    c = item % ncs;
+    bos = n * p.T;
+    eos = bos + p.T;
+  }
+  const int64_t c0 = bos + c * kC;
+  const int len = (int)((eos - c0) < kC ? (eos - c0) : kC);
+  const bf16* __restrict__ kg = static_cast<const bf16*>(p.k);
+
+  // ------------------------------------------------------------------ load
+  {
+    bf16x8 kv[KPT];
+#pragma unroll
+    for (int u = 0; u < KPT; ++u) {
+      const int e = t + u * kPrepNT, row = e / KCH, c8 = e % KCH;
+      kv[u] = bf16x8{};
+      if (row < len) kv[u] = *reinterpret_cast<const bf16x8*>(kg + ((c0 + row) * p.H + h) * KD + c8 * 8);
+    }
+    uint32_t graw = 0, braw = 0;
+    if (w == 0 && lane < len) {
+      const int64_t gi = (c0 + lane) * p.HV + hv;
+      graw = load_raw32(p.g, p.dg, gi);
+      braw = load_raw32(p.beta, p.db, gi);
+    }
+    for (int e = t; e < kC * kCP / 8; e += kPrepNT) reinterpret_cast<bf16x8*>(Tb)[e] = bf16x8{};
+#pragma unroll
+    for (int u = 0; u < KPT; ++u) {
+      const int e = t + u * kPrepNT, row = e / KCH, c8 = e % KCH;
+      const bf16x8 x = (p.flags & GDN_FLAG_QK_L2NORM) ? l2norm_row_chunk<KCH>(kv[u]) : kv[u];
+      *reinterpret_cast<bf16x8*>(&Kc[row * KP + c8 * 8]) = x;
+    }
+    if (w == 0)
+      chunk_gates_from_raw(gs, graw, braw, p.dg, p.db, len, p.flags, p.A_log ? p.A_log[hv] : 0.f,
+                           p.dt_bias ? p.dt_bias[hv] : 0.f, lane);
+  }
+  __syncthreads();
+
+  // ------------------------------------------------------------------ Gram tiles, A, diagonal solves
+  // Wave r: row tile r of A. The row tile is a template constant (one code copy per wave).
+  auto gram_row = [&](auto rc) {
+    constexpr int rk = decltype(rc)::value;
+    bf16x8 fk[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) fk[s] = ld8(Kc + (16 * rk + li) * KP + 32 * s + 8 * g4);
+    f32x4 dacc{}, oacc[3] = {};
+#pragma unroll
+    for (int s = 0; s < KS; ++s) dacc = mma(fk[s], fk[s], dacc);
+    // off-diagonal tiles (rk, cb > rk), issued before the solve so their MFMAs overlap it
+#pragma unroll
+    for (int cb = rk + 1; cb < 4; ++cb) {
+      bf16x8 fo[KS];
+#pragma unroll
+      for (int s = 0; s < KS; ++s) fo[s] = ld8(Kc + (16 * cb + li) * KP + 32 * s + 8 * g4);
+#pragma unroll
+      for (int s = 0; s < KS; ++s) oacc[cb - 1] = mma(fk[s], fo[s], oacc[cb - 1]);
+    }
+    // k.k is symmetric: dacc[i] = k_t.k_j with t = 16rk + li, j = 16rk + 4g + i; A[t][j] for j < t
+    const float gt = gs.gam[16 * rk + li], bt = gs.bet[16 * rk + li];
+    const float4 gj = ld4f(&gs.gam[16 * rk + 4 * g4]);
+    const float gjv[4] = {gj.x, gj.y, gj.z, gj.w};
+    float av[4];
+#pragma unroll
+    for (int ii = 0; ii < 4; ++ii) av[ii] = (4 * g4 + ii < li) ? bt * __expf(gt - gjv[ii]) * dacc[ii] : 0.f;
+    // A_rr, stored for the solve as ad[m][k][q] = A[4q + k][m] (private to this wave)
+    float* ad = Ad[rk];
+#pragma unroll
+    for (int ii = 0; ii < 4; ++ii) ad[((4 * g4 + ii) * 4 + (li & 3)) * 4 + (li >> 2)] = av[ii];
+    // Forward substitution on 64 lanes: lane (col = lane/4, k = lane%4) holds rows 4q+k of column
+    // col of T_rr; x_m is broadcast inside each quad with DPP, and step m reads the lane's four A
+    // entries of column m with one 16-byte LDS read. A is strictly lower, so no row mask is needed.
+    const int col = lane >> 2, kq = lane & 3;
+    float4 a4m[15];
+#pragma unroll
+    for (int m = 0; m < 15; ++m) a4m[m] = ld4f(ad + (m * 4 + kq) * 4);
+    float x[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) x[q] = (4 * q + kq == col) ? 1.f : 0.f;
+#pragma unroll
+    for (int m = 0; m < 15; ++m) {
+      const float xm = quad_bcast(x[m >> 2], m & 3);
+      x[0] -= a4m[m].x * xm;
+      x[1] -= a4m[m].y * xm;
+      x[2] -= a4m[m].z * xm;
+      x[3] -= a4m[m].w * xm;
+    }
+    float* tf = &Tf[rk >> 1][(16 * (rk & 1)) * kTfP + 16 * (rk & 1) + col];
+    bf16* tb = &Tb[(16 * rk) * kCP + 16 * rk + col];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int rr = 4 * q + kq;
+      tf[rr * kTfP] = x[q];
+      tb[rr * kCP] = static_cast<bf16>(rr == col ? 0.f : x[q]);
+    }
+    // off-diagonal A blocks: element (j = 16rk + 4g + i, t = 16cb + li) -> Ao[t - 16][j]
+#pragma unroll
+    for (int cb = rk + 1; cb < 4; ++cb) {
+      const int tt = 16 * cb + li, j0 = 16 * rk + 4 * g4;
+      const float gtt = gs.gam[tt], btt = gs.bet[tt];
+      float val[4];
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) val[ii] = btt * __expf(gtt - gjv[ii]) * oacc[cb - 1][ii];
+      *reinterpret_cast<float4*>(&Ao[(tt - 16) * kAoP + j0]) = make_float4(val[0], val[1], val[2], val[3]);
+    }
+  };
+  switch (w) {
+    case 0: gram_row(std::integral_constant<int, 0>{}); break;
+    case 1: gram_row(std::integral_constant<int, 1>{}); break;
+    case 2: gram_row(std::integral_constant<int, 2>{}); break;
+    default: gram_row(std::integral_constant<int, 3>{}); break;
+  }
+  __syncthreads();
+
+  // ------------------------------------------------------------------ 16 -> 32 merges (waves 2, 3)
+  // T_{2q+1,2q} = -T_{2q+1,2q+1} (A_{2q+1,2q} T_{2q,2q}). W = A T_{2q,2q} lands in accumulator layout,
+  // which is the B-operand layout of the 16x16x16 MFMA, so the second product takes W from registers.
+  if (w >= 2) {
+    const int q = w - 2;
+    const float* tq = Tf[q];
+    f32x4 acc{};
+    {
+      float a[4], b[4];
+      const float* ar = &Ao[(16 * (2 * q + 1) + li - 16) * kAoP + 32 * q + 4 * g4];
+      a[0] = ar[0]; a[1] = ar[1]; a[2] = ar[2]; a[3] = ar[3];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) b[m] = tq[(4 * g4 + m) * kTfP + li];
+      acc = mma16x3(a, b, acc);
+    }
+    f32x4 acc2{};
+    {
+      float a[4];
+      const float b[4] = {acc[0], acc[1], acc[2], acc[3]};
+      const float* ar = &tq[(16 + li) * kTfP + 16 + 4 * g4];
+      a[0] = ar[0]; a[1] = ar[1]; a[2] = ar[2]; a[3] = ar[3];
+      acc2 = mma16x3(a, b, acc2);
+    }
+    float* tw = &Tf[q][16 * kTfP];
+    bf16* tbw = &Tb[(32 * q + 16) * kCP + 32 * q];
+#pragma unroll
+    for (int ii = 0; ii < 4; ++ii) {
+      tw[(4 * g4 + ii) * kTfP + li] = -acc2[ii];
+      tbw[(4 * g4 + ii) * kCP + li] = static_cast<bf16>(-acc2[ii]);
+    }
+  }
+  __syncthreads();
+
+  // ------------------------------------------------------------------ 32 -> 64 merge (waves 2, 3)
+  // T[32:64][0:32] = -T[32:64][32:64] (A[32:64][0:32] T[0:32][0:32]), column block ct = w - 2.
+  if (w >= 2) {
+    const int ct = w - 2;
+    f32x4 wacc[2];  // W' tiles (rt, ct), kept in registers as the B operand of the second product
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      wacc[rt] = f32x4{};
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        if (ks < ct) continue;  // T[k][c] vanishes for k < c
+        float a[4], b[4];
+        const float* ar = &Ao[(16 + 16 * rt + li) * kAoP + 16 * ks + 4 * g4];
+        a[0] = ar[0]; a[1] = ar[1]; a[2] = ar[2]; a[3] = ar[3];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) b[m] = Tf[0][(16 * ks + 4 * g4 + m) * kTfP + 16 * ct + li];
+        wacc[rt] = mma16x3(a, b, wacc[rt]);
+      }
+    }
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      f32x4 acc{};
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        if (ks > rt) continue;  // T[32+r][32+k] vanishes for k > r
+        float a[4];
+        const float b[4] = {wacc[ks][0], wacc[ks][1], wacc[ks][2], wacc[ks][3]};
+        const float* ar = &Tf[1][(16 * rt + li) * kTfP + 16 * ks + 4 * g4];
+        a[0] = ar[0]; a[1] = ar[1]; a[2] = ar[2]; a[3] = ar[3];
+        acc = mma16x3(a, b, acc);
+      }
+      bf16* tbw = &Tb[(32 + 16 * rt) * kCP + 16 * ct];
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) tbw[(4 * g4 + ii) * kCP + li] = static_cast<bf16>(-acc[ii]);
+    }
+  }
+  __syncthreads();
+
+  // ------------------------------------------------------------------ store rows t < len
+#pragma unroll
+  for (int u = 0; u < kC * 8 / kPrepNT; ++u) {
+    const int e = t + u * kPrepNT, row = e >> 3, c8 = e & 7;
+    if (row < len)
+      *reinterpret_cast<bf16x8*>(p.tw + ((c0 + row) * p.HV + hv) * kC + c8 * 8) =
+          *reinterpret_cast<const bf16x8*>(&Tb[row * kCP + c8 * 8]);
+  }
+}
+
+// chunk_first[0] = 0, chunk_first[n + 1] = chunk_first[n] + ceil(len_n / 64): one block, a running
+// block-wide scan over tiles of 1024 sequences.
+__global__ __launch_bounds__(1024) void gated_delta_chunk_index_kernel(const void* cu, int cu_i32, int64_t N,
+                                                                        int* chunk_first) {
+  __shared__ int wsum[16];
+  __shared__ int carry;
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  if (t == 0) {
+    carry = 0;
+    chunk_first[0] = 0;
+  }
+  __syncthreads();
+  for (int64_t base = 0; base < N; base += 1024) {
+    const int64_t n = base + t;
+    int v = 0;
+    if (n < N) v = (int)((load_index(cu, cu_i32, n + 1) - load_index(cu, cu_i32, n) + kC - 1) / kC);
+    int incl = v;  // inclusive scan inside the wave
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+      const int o = __shfl_up(incl, d, kWave);
+      if (lane >= d) incl += o;
+    }
+    if (lane == kWave - 1) wsum[w] = incl;
+    __syncthreads();
+    int before = carry;
+    for (int j = 0; j < w; ++j) before += wsum[j];
+    if (n < N) chunk_first[n + 1] = before + incl;
+    __syncthreads();
+    if (t == 1023) carry = before + incl;
+    __syncthreads();
+  }
+}
+
+int launch_chunk_prep(const ChunkPrepParams& p, int64_t B, int64_t K, hipStream_t s) {
+  int64_t items;
+  if (p.cu) {
+    hipLaunchKernelGGL(gated_delta_chunk_index_kernel, dim3(1), dim3(1024), 0, s, p.cu, p.cu_i32, p.N,
+                       const_cast<int*>(p.chunk_first));
+    items = (p.T + kC - 1) / kC + p.N;  // upper bound on the number of chunks
+  } else {
+    items = B * ((p.T + kC - 1) / kC);
+  }
+  if (items > 0x7fffffff || p.HV > 65535) {
+    gdn_internal_set_error("gdn_chunk_fwd: %lld chunks x %lld heads exceed the grid limits", (long long)items,
+                           (long long)p.HV);
+    return GDN_ERR_UNSUPPORTED;
+  }
+  dim3 grid((unsigned)items, (unsigned)p.HV), block(kPrepNT);
+  if (K == 128) hipLaunchKernelGGL(gated_delta_chunk_prep_kernel<128>, grid, block, 0, s, p);
+  else hipLaunchKernelGGL(gated_delta_chunk_prep_kernel<64>, grid, block, 0, s, p);
+  return gdn_internal_check_launch("gated_delta_chunk_prep_kernel");
+}
+
+}  // namespace gdn

@@ -83,6 +83,19 @@ __device__ __forceinline__ float dpp_add(float v) {
   return v + __int_as_float(s);
 }
 
+// Sum over aligned groups of N lanes (N = 8 or 16) with DPP: quad_perm [1,0,3,2] and [2,3,0,1]
+// (0xb1, 0x4e), row_half_mirror (0x141, pairs the two quads of an 8-lane half) and row_mirror
+// (0x140, pairs the two halves of a 16-lane row). Every lane of a group ends with the group sum.
+template <int N>
+__device__ __forceinline__ float group_sum(float x) {
+  static_assert(N == 8 || N == 16, "group of 8 or 16 lanes");
+  x = dpp_add<0xb1, 0xf>(x);
+  x = dpp_add<0x4e, 0xf>(x);
+  x = dpp_add<0x141, 0xf>(x);
+  if (N == 16) x = dpp_add<0x140, 0xf>(x);
+  return x;
+}
+
 __device__ __forceinline__ float wave_inclusive_sum(float x) {
   // DPP row_shr:n = 0x110 + n; row_bcast:15 = 0x142; row_bcast:31 = 0x143
   x = dpp_add<0x111, 0xf>(x);

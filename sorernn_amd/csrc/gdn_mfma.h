@@ -1,0 +1,121 @@
+// MFMA fragment helpers and the per-chunk building blocks shared by the two chunked-prefill
+// kernels (the T-solve kernel and the state kernel) for gfx950.
+//
+// MFMA operand layouts used throughout (64 lanes, g = lane/16, i = lane%16):
+//   v_mfma_f32_16x16x32_bf16: A lane holds row i, k = 8g..8g+7; B lane holds column i, same k;
+//     the accumulator lane holds column i, rows 4g..4g+3.
+//   v_mfma_f32_16x16x16_bf16 (1k): A row i, k = 4g..4g+3; B column i, same k; accumulator as
+//     above, which is also this instruction's B-operand layout.
+#pragma once
+
+#include "gdn_common.h"
+
+namespace gdn {
+
+constexpr int kC = 64;       // chunk length (tokens)
+constexpr int kCP = kC + 8;  // bf16 pitch of [*][64] operand tiles (144 B rows)
+constexpr int kAoP = 52;     // fp32 pitch of the off-diagonal A rows 16..63 x cols 0..47
+constexpr int kTfP = 36;     // fp32 pitch of the two 32x32 diagonal T blocks
+
+typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ bf16x8 ld8(const bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
+__device__ __forceinline__ float4 ld4f(const float* p) { return *reinterpret_cast<const float4*>(p); }
+
+__device__ __forceinline__ f32x4 mma(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mma16(bf16x4 a, bf16x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, a), __builtin_bit_cast(i16x4, b), c, 0, 0, 0);
+}
+
+// Transposed fragment from a row-major bf16 LDS tile M (pitch in elements): lane (g, i) receives
+// M[j0 + 8g + m][c0 + i] for m = 0..7, i.e. the fragment of M^T with rows c0.. and the
+// contraction index j0.. contiguous. Each ds_read_b64_tr_b16 covers 4 rows: inside a group of 16
+// lanes, lane 4m+q reads row m at columns c0+4q..+3 and the instruction hands lane i the element
+// i%4 of lanes 4m + i/4, m = 0..3.
+__device__ __forceinline__ bf16x8 ld8_tr(const bf16* tile, int pitch, int j0, int c0, int lane) {
+  const int g = lane >> 4, li = lane & 15;
+  const bf16* p0 = tile + (j0 + 8 * g + (li >> 2)) * pitch + c0 + 4 * (li & 3);
+  const bf16* p1 = p0 + 4 * pitch;
+  const bf16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p0));
+  const bf16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p1));
+  return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
+// Value of lane (quad base + q) broadcast to the 4 lanes of each quad (DPP quad_perm q,q,q,q).
+__device__ __forceinline__ float quad_bcast(float x, int q) {
+  const int v = __float_as_int(x);
+  switch (q) {
+    case 0: return __int_as_float(__builtin_amdgcn_mov_dpp(v, 0x00, 0xf, 0xf, false));
+    case 1: return __int_as_float(__builtin_amdgcn_mov_dpp(v, 0x55, 0xf, 0xf, false));
+    case 2: return __int_as_float(__builtin_amdgcn_mov_dpp(v, 0xaa, 0xf, 0xf, false));
+    default: return __int_as_float(__builtin_amdgcn_mov_dpp(v, 0xff, 0xf, 0xf, false));
+  }
+}
+
+__device__ __forceinline__ bf16x4 to_bf16x4(float a, float b, float c, float d) {
+  return bf16x4{static_cast<bf16>(a), static_cast<bf16>(b), static_cast<bf16>(c), static_cast<bf16>(d)};
+}
+
+// fp32 x4 -> bf16 hi and lo parts (x ~= hi + lo to about 2^-16 relative)
+__device__ __forceinline__ void split4(float a, float b, float c, float d, bf16x4& hi, bf16x4& lo) {
+  hi = to_bf16x4(a, b, c, d);
+  lo = to_bf16x4(a - (float)hi[0], b - (float)hi[1], c - (float)hi[2], d - (float)hi[3]);
+}
+
+// Three-term bf16 product step for a 16x16x16 fp32 tile: acc += A(4 k) * B(4 k).
+__device__ __forceinline__ f32x4 mma16x3(const float (&a)[4], const float (&b)[4], f32x4 acc) {
+  bf16x4 ah, al, bh, bl;
+  split4(a[0], a[1], a[2], a[3], ah, al);
+  split4(b[0], b[1], b[2], b[3], bh, bl);
+  acc = mma16(ah, bh, acc);
+  acc = mma16(ah, bl, acc);
+  acc = mma16(al, bh, acc);
+  return acc;
+}
+
+// Per-token gate terms of one chunk: gam = in-chunk cumsum of g, egam = exp(gam), bet = beta,
+// begam = beta exp(gam), dlast = exp(gam_last - gam). Padding rows carry g = 0 and beta = 0.
+struct ChunkGates {
+  float gam[kC], egam[kC], bet[kC], begam[kC], dlast[kC];
+};
+
+// One wave (lane = token) turns the raw gate bits of a chunk into its ChunkGates: optional
+// in-kernel gate (g = -exp(A_log) softplus(a + dt_bias)) and sigmoid of beta, then a DPP scan.
+__device__ __forceinline__ void chunk_gates_from_raw(ChunkGates& gs, uint32_t graw, uint32_t braw, int dg, int db,
+                                                     int valid_rows, unsigned flags, float A_log, float dt_bias,
+                                                     int lane) {
+  float gval = raw32_to_f32(graw, dg), bval = raw32_to_f32(braw, db);
+  if (lane < valid_rows) {
+    if (flags & GDN_FLAG_GATE_IN_KERNEL) gval = -__expf(A_log) * softplus_f32(gval + dt_bias);
+    if (flags & GDN_FLAG_BETA_SIGMOID) bval = sigmoid_f32(bval);
+  } else {
+    gval = 0.f;
+    bval = 0.f;
+  }
+  const float cs = wave_inclusive_sum(gval);
+  const float last = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cs), kWave - 1));
+  const float e = __expf(cs);
+  gs.gam[lane] = cs;
+  gs.egam[lane] = e;
+  gs.bet[lane] = bval;
+  gs.begam[lane] = bval * e;
+  gs.dlast[lane] = __expf(last - cs);
+}
+
+// F.normalize over a q/k row held by KCH consecutive lanes (8 bf16 each), rounded back to bf16.
+template <int KCH>
+__device__ __forceinline__ bf16x8 l2norm_row_chunk(bf16x8 x) {
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ss += (float)x[i] * (float)x[i];
+  ss = group_sum<KCH>(ss);
+  const float inv = 1.f / fmaxf(sqrtf(ss), 1e-12f);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) x[i] = static_cast<bf16>((float)x[i] * inv);
+  return x;
+}
+
+}  // namespace gdn

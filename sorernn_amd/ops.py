@@ -123,10 +123,10 @@ def _gdn_call(entry, name, q, k, v, g, beta, scale, initial_state, output_final_
     b, t, h, kd, hv, vd, n, flags, scale, A_log, dt_bias = _delta_rule_args(
         name, q, k, v, g, beta, scale, initial_state, cu_seqlens, cu_seqlens_cpu,
         use_qk_l2norm_in_kernel, use_beta_sigmoid_in_kernel, use_gate_in_kernel, A_log, dt_bias)
-    out_dtype = v.dtype
-    if out_dtype == torch.float16 and entry == "gdn_chunk_fwd":
-        # the chunk kernel stages bf16 or fp32 operands; fp16 runs on the fp32 (split-bf16) path
-        q, k, v = q.float(), k.float(), v.float()
+    if entry == "gdn_chunk_fwd" and q.dtype != torch.bfloat16:
+        # The chunk kernels stage bf16 MFMA operands. fp32/fp16 q/k/v keep their precision on the
+        # recurrent kernel, which computes the same recurrence token by token in fp32.
+        entry = "gdn_recurrent_fwd"
     q, k, v, g, beta = (x.contiguous() for x in (q, k, v, g, beta))
     h0 = None
     if initial_state is not None:
@@ -142,13 +142,21 @@ def _gdn_call(entry, name, q, k, v, g, beta, scale, initial_state, output_final_
     o = torch.empty(b, t, hv, vd, device=q.device, dtype=q.dtype)
     if t > 0 or final is not None:
         cu = cu_seqlens.contiguous() if cu_seqlens is not None else None
-        _lib.call(entry, _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.ptr(beta), _lib.ptr(h0),
-                  _lib.ptr(o), _lib.ptr(final), _lib.ptr(cu), b, t, h, hv, kd, vd, n,
-                  _lib.dtype_code(q.dtype), _lib.dtype_code(g.dtype), _lib.dtype_code(beta.dtype),
-                  scale, flags, _lib.ptr(A_log), _lib.ptr(dt_bias), _lib.stream_of(q))
-    if o.dtype != out_dtype:
-        o = o.to(out_dtype)
+        args = [_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.ptr(beta), _lib.ptr(h0),
+                _lib.ptr(o), _lib.ptr(final), _lib.ptr(cu), b, t, h, hv, kd, vd, n,
+                _lib.dtype_code(q.dtype), _lib.dtype_code(g.dtype), _lib.dtype_code(beta.dtype),
+                scale, flags, _lib.ptr(A_log), _lib.ptr(dt_bias)]
+        if entry == "gdn_chunk_fwd":
+            nbytes = chunk_workspace_bytes(b, t, hv, n, cu is not None)
+            ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
+            args += [_lib.ptr(ws), nbytes]
+        _lib.call(entry, *args, _lib.stream_of(q))
     return o, final
+
+
+def chunk_workspace_bytes(batch: int, seqlen: int, num_v_heads: int, num_seqs: int, varlen: bool) -> int:
+    """Bytes of device workspace ``gdn_chunk_fwd`` needs (the per-chunk ``(I + A)^-1`` rows)."""
+    return int(_lib.load().gdn_chunk_workspace_size(batch, seqlen, num_v_heads, num_seqs, int(varlen)))
 
 
 def chunk_gated_delta_rule(
