@@ -54,6 +54,10 @@ constexpr int kVB = 32;       // value columns per workgroup
 constexpr int kNT = 512;      // threads per workgroup (8 waves)
 constexpr int kVP = kVB + 8;  // bf16 pitch of the V slice (80 B rows)
 
+// A wave's list of P tiles (rb * 4 + cb each, up to three) packed into one template constant
+constexpr int kNoTile = 31;
+constexpr int p_tiles(int a, int b, int c) { return a | (b << 5) | (c << 10); }
+
 template <int KD, int VD>
 __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p) {
   constexpr int NVB = VD / kVB;
@@ -171,50 +175,60 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
     *reinterpret_cast<bf16x8*>(Tb + (t >> 3) * kCP + (t & 7) * 8) = pt;
   };
 
-  // P of the chunk in buffer `buf` for row tile rb = w - 4 (waves 4-7): tiles (rb, cb >= rb),
-  // element (j = 16rb + 4g + i, t = 16cb + li) = exp(gam_t - gam_j) k_j.q_t for j <= t.
-  auto p_side = [&](auto rc, int buf, const ChunkGates& gs) {
-    constexpr int rb = decltype(rc)::value;
+  // P of the chunk in buffer `buf`: tile (rb, cb), rb <= cb, holds element (j = 16rb + 4g + i,
+  // t = 16cb + li) = exp(gam_t - gam_j) k_j.q_t for j <= t. The 10 tiles are dealt to waves 4-7 as
+  // 3, 3, 2, 2 (code: up to three 5-bit fields rb * 4 + cb, kNoTile = none), so with Delta on
+  // waves 0-3 every SIMD issues 12-14 MFMAs in phase B.
+  auto p_job = [&](auto code_c, int buf, const ChunkGates& gs) {
+    constexpr int code = decltype(code_c)::value;
     const bf16* kb = Kc[buf];
     const bf16* qb = Qc[buf];
-    const int j0 = 16 * rb + 4 * g4;
-    bf16x8 fk[KS], fqc[4][KS];
-    float gtc[4];
+    bf16x8 fa[3][KS], fb[3][KS];
+    float gtc[3];
+    float4 gjs[3];
 #pragma unroll
-    for (int s = 0; s < KS; ++s) fk[s] = ld8(kb + (16 * rb + li) * KP + 32 * s + 8 * g4);
+    for (int q = 0; q < 3; ++q) {
+      const int tc = (code >> (5 * q)) & 31;
+      if (tc == kNoTile) continue;
+      const int rb = tc >> 2, cb = tc & 3;
+      gtc[q] = gs.gam[16 * cb + li];
+      gjs[q] = ld4f(&gs.gam[16 * rb + 4 * g4]);
 #pragma unroll
-    for (int cb = rb; cb < 4; ++cb) {
-      gtc[cb] = gs.gam[16 * cb + li];
-#pragma unroll
-      for (int s = 0; s < KS; ++s) fqc[cb][s] = ld8(qb + (16 * cb + li) * KP + 32 * s + 8 * g4);
+      for (int s = 0; s < KS; ++s) {
+        fa[q][s] = ld8(kb + (16 * rb + li) * KP + 32 * s + 8 * g4);
+        fb[q][s] = ld8(qb + (16 * cb + li) * KP + 32 * s + 8 * g4);
+      }
     }
-    const float4 gj = ld4f(&gs.gam[j0]);
     __builtin_amdgcn_sched_barrier(0);  // every read of the job ahead of its MFMAs
-    f32x4 pacc[4];
+    f32x4 pacc[3];
 #pragma unroll
-    for (int cb = rb; cb < 4; ++cb) {
-      pacc[cb] = f32x4{};
+    for (int q = 0; q < 3; ++q) {
+      if (((code >> (5 * q)) & 31) == kNoTile) continue;
+      pacc[q] = f32x4{};
 #pragma unroll
-      for (int s = 0; s < KS; ++s) pacc[cb] = mma(fk[s], fqc[cb][s], pacc[cb]);
+      for (int s = 0; s < KS; ++s) pacc[q] = mma(fa[q][s], fb[q][s], pacc[q]);
     }
     bf16* pw = Pb[buf];
 #pragma unroll
-    for (int cb = rb; cb < 4; ++cb) {
-      const int tt = 16 * cb + li;
-      const float gt = gtc[cb];
-      const float dd[4] = {__expf(gt - gj.x), __expf(gt - gj.y), __expf(gt - gj.z), __expf(gt - gj.w)};
+    for (int q = 0; q < 3; ++q) {
+      const int tc = (code >> (5 * q)) & 31;
+      if (tc == kNoTile) continue;
+      const int rb = tc >> 2, cb = tc & 3;
+      const int tt = 16 * cb + li, j0 = 16 * rb + 4 * g4;
+      const float gt = gtc[q];
+      const float dd[4] = {__expf(gt - gjs[q].x), __expf(gt - gjs[q].y), __expf(gt - gjs[q].z), __expf(gt - gjs[q].w)};
       float val[4];
 #pragma unroll
-      for (int ii = 0; ii < 4; ++ii) val[ii] = (cb > rb || j0 + ii <= tt) ? dd[ii] * pacc[cb][ii] : 0.f;
+      for (int ii = 0; ii < 4; ++ii) val[ii] = (cb > rb || j0 + ii <= tt) ? dd[ii] * pacc[q][ii] : 0.f;
       *reinterpret_cast<bf16x4*>(pw + tt * kCP + j0) = to_bf16x4(val[0], val[1], val[2], val[3]);
     }
   };
   auto run_p_side = [&](int buf, const ChunkGates& gs) {
-    switch (w) {
-      case 4: p_side(std::integral_constant<int, 0>{}, buf, gs); break;
-      case 5: p_side(std::integral_constant<int, 1>{}, buf, gs); break;
-      case 6: p_side(std::integral_constant<int, 2>{}, buf, gs); break;
-      default: p_side(std::integral_constant<int, 3>{}, buf, gs); break;
+    switch (w) {  // tiles (0,0) (0,1) (0,2) | (0,3) (1,1) (1,2) | (1,3) (2,2) | (2,3) (3,3)
+      case 4: p_job(std::integral_constant<int, p_tiles(0, 1, 2)>{}, buf, gs); break;
+      case 5: p_job(std::integral_constant<int, p_tiles(3, 5, 6)>{}, buf, gs); break;
+      case 6: p_job(std::integral_constant<int, p_tiles(7, 10, kNoTile)>{}, buf, gs); break;
+      default: p_job(std::integral_constant<int, p_tiles(11, 15, kNoTile)>{}, buf, gs); break;
     }
   };
 
