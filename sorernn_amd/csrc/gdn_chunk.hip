@@ -14,18 +14,21 @@
 //   S'    = exp(gam_c) S + K^T diag(exp(gam_c - gam)) Delta
 //
 // Phases per chunk i (one barrier each; SIMD s runs waves s and s + 4):
-//   A: waves 0-3 Y = K S (row tile w) -> X;        waves 4-7 Z = Q S (row tile w - 4).
-//   B: waves 0-3 Delta (row tile w);                waves 4-7 P of chunk i+1 (off the chain).
-//   C: waves 0-3 S' (4 state tiles each);           waves 4-7 O (row tile w - 4) -> LDS.
-//   stage: O of chunk i to HBM (16-byte stores), the prefetched K/Q/gates of chunk i+2, V and T
-//          of chunk i+1 into LDS (their global loads are issued at the top of the iteration).
+//   A: waves 0-3 Y = K S (row tile w) -> X;        waves 4-7 Z = Q S (row tile w - 4), O of chunk
+//                                                   i-1 to HBM (16-byte stores), V/T loads of i+1.
+//   B: waves 0-3 Delta (row tile w), then stage      waves 4-7 P of chunk i+1 (off the chain).
+//      K/gates of chunk i+2, load chunk i+3.
+//   C: waves 0-3 S' (4 state tiles each);           waves 4-7 O (row tile w - 4) -> LDS, stage
+//                                                   V/T of i+1 and Q of i+2, load Q of i+3.
+// Loads are issued one iteration before their data is written to LDS, and every LDS slot is
+// rewritten only after the phase that last reads it (K and gates: three slots, Q and P: two).
 //
 // Precision: q/k/v are bf16, so P tiles are exact products with fp32 accumulation. S, X and Delta
 // enter MFMA as single bf16; the state update's right operand is split into bf16 hi + lo (two
 // MFMAs), which keeps the fp32 final state within 1e-3 relative L2 over 64 chunks.
 //
 // LDS operand layouts (bf16 rows padded by 8 elements):
-//   Kc, Qc [token][key]  natural tiles (two chunk buffers): A/B operands with the key dim contiguous;
+//   Kc, Qc [token][key]  natural tiles: A/B operands with the key dim contiguous;
 //                        K^T for the state update is read with ds_read_b64_tr_b16.
 //   Sb [v][key], Xb/Db/DtH/DtL [v][token], Tb/Pb [t][j]: written from accumulators with 8-byte stores.
 
@@ -64,12 +67,13 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
   constexpr int KP = KD + 8;            // bf16 pitch of the q/k tiles
   constexpr int KS = KD / 32;           // MFMA k-steps over the key dim
   constexpr int KCH = KD / 8;           // 16-byte chunks per q/k row
-  constexpr int QKPT = kC * KCH / kNT;  // q/k 16-byte chunks per thread per matrix
+  constexpr int QKPT = kC * KCH / (kNT / 2);  // 16-byte chunks per thread of a q or k tile (half the waves)
   constexpr int SPW = KD / 32;          // state tiles (16 x 16) per wave on waves 0-3
 
-  __shared__ __align__(16) bf16 Kc[2][kC * KP];
-  __shared__ __align__(16) bf16 Qc[2][kC * KP];
-  __shared__ __align__(16) bf16 Vc[kC * kVP];  // V slice of chunk i; O of chunk i after phase C
+  __shared__ __align__(16) bf16 Kc[3][kC * KP];  // K of chunk c in slot c % 3 (i, i+1, i+2 staged)
+  __shared__ __align__(16) bf16 Qc[2][kC * KP];  // Q of chunk c in slot c % 2
+  __shared__ __align__(16) bf16 Vc[kC * kVP];    // V slice of chunk i
+  __shared__ __align__(16) bf16 Ob[kC * kVP];    // O of chunk i, stored to HBM in the next phase A
   __shared__ __align__(16) bf16 Sb[kVB * KP];
   __shared__ __align__(16) bf16 Tb[kC * kCP];     // T - I of chunk i, A operand [t][j]
   __shared__ __align__(16) bf16 Pb[2][kC * kCP];  // P of chunks i and i+1
@@ -77,7 +81,7 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
   __shared__ __align__(16) bf16 Db[kVB * kCP];
   __shared__ __align__(16) bf16 DtH[kVB * kCP];
   __shared__ __align__(16) bf16 DtL[kVB * kCP];
-  __shared__ __align__(16) ChunkGates gv[2];
+  __shared__ __align__(16) ChunkGates gv[3];      // gate terms of chunk c in slot c % 3
 
   const int t = threadIdx.x, lane = t & 63, w = t >> 6, g4 = lane >> 4, li = lane & 15;
 
@@ -108,7 +112,7 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
   const bf16* __restrict__ kg = static_cast<const bf16*>(p.k);
   const bf16* __restrict__ vg = static_cast<const bf16*>(p.v);
   bf16* __restrict__ og = static_cast<bf16*>(p.o);
-  constexpr int kGateWave = 7;  // loads and scans the gates
+  constexpr int kGateWave = 0;  // loads and scans the gates
 
   auto chunk_len = [&](int c) {
     const int64_t c0 = bos + (int64_t)c * kC;
@@ -116,73 +120,85 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
   };
 
   // ------------------------------------------------------------------ prefetch registers
-  // Loaded at the top of an iteration, consumed only in the stage step, so no wait for a load in
-  // flight is needed inside the phases (rows past the end load as zeros: the load count is fixed).
-  bf16x8 pk[QKPT], pq[QKPT], pv{}, pt{};
+  // Waves 0-3 load K/gates of a chunk at the end of phase B and stage them one iteration later
+  // (end of the next phase B); waves 4-7 load Q at the end of phase C and V/T at the start of phase
+  // A, and stage them at the end of the next phase C. Each prefetch register is consumed at one
+  // point only, so no wait for a load in flight is needed anywhere else (rows past the end load as
+  // zeros: the load count is fixed).
+  // pr holds K rows in waves 0-3 and Q rows in waves 4-7 (one register array for both roles)
+  bf16x8 pr[QKPT], pv{}, pt[2];
   uint32_t pgraw = 0, pbraw = 0;
-  auto fetch_kq = [&](int c) {  // K/Q/gates of chunk c
+  const int th = t & (kNT / 2 - 1);  // thread index within its half (waves 0-3 or 4-7)
+  // Rows u0..u1-1 of this thread's share of a q/k tile. The loads of one tile are issued in three
+  // parts at different phases (u in [0, QA), [QA, QB), [QB, QKPT)). All loads go through buffer
+  // resources sized to the chunk's valid rows, so rows past the end read as zeros.
+  constexpr int QA = QKPT / 2, QB = QKPT * 3 / 4;
+  const uint32_t qk_row = (uint32_t)(p.H * KD * 2), v_row = (uint32_t)(p.HV * VD * 2), t_row = (uint32_t)(p.HV * kC * 2);
+  auto fetch_rows = [&](bf16x8 (&dst)[QKPT], const bf16* src, int c, int u0, int u1) {
     const int64_t c0 = bos + (int64_t)c * kC;
-    const int len = chunk_len(c);
+    const auto rs = make_rsrc(src + (c0 * p.H + h) * KD, (uint32_t)chunk_len(c) * qk_row);
 #pragma unroll
     for (int u = 0; u < QKPT; ++u) {
-      const int e = t + u * kNT, row = e / KCH, c8 = e % KCH;
-      pk[u] = bf16x8{};
-      pq[u] = bf16x8{};
-      if (row < len) {
-        const int64_t base = ((c0 + row) * p.H + h) * KD + c8 * 8;
-        pk[u] = *reinterpret_cast<const bf16x8*>(kg + base);
-        pq[u] = *reinterpret_cast<const bf16x8*>(qg + base);
-      }
-    }
-    pgraw = 0;
-    pbraw = 0;
-    if (w == kGateWave && lane < len) {
-      const int64_t gi = (c0 + lane) * p.HV + hv;
-      pgraw = load_raw32(p.g, p.dg, gi);
-      pbraw = load_raw32(p.beta, p.db, gi);
+      if (u < u0 || u >= u1) continue;
+      const int e = th + u * (kNT / 2), row = e / KCH, c8 = e % KCH;
+      dst[u] = buf_load16(rs, row * qk_row + c8 * 16);
     }
   };
-  auto fetch_vt = [&](int c) {  // V slice and T - I rows of chunk c
-    const int64_t c0 = bos + (int64_t)c * kC;
-    const int len = chunk_len(c);
-    pv = bf16x8{};
-    if (t < kC * 4) {
-      const int row = t >> 2, c8 = t & 3;
-      if (row < len) pv = *reinterpret_cast<const bf16x8*>(vg + ((c0 + row) * p.HV + hv) * VD + vb * kVB + c8 * 8);
-    }
-    pt = bf16x8{};
-    {
-      const int row = t >> 3, c8 = t & 7;
-      if (row < len) pt = *reinterpret_cast<const bf16x8*>(p.tw + ((c0 + row) * p.HV + hv) * kC + c8 * 8);
-    }
-  };
-  auto stage_kq = [&](int buf, ChunkGates& gs, int len) {
+  auto stage_rows = [&](const bf16x8 (&src)[QKPT], bf16* dst) {
 #pragma unroll
     for (int u = 0; u < QKPT; ++u) {
-      const int e = t + u * kNT, row = e / KCH, c8 = e % KCH;
-      bf16x8 kv = pk[u], qv = pq[u];
-      if (l2) {
-        kv = l2norm_row_chunk<KCH>(kv);
-        qv = l2norm_row_chunk<KCH>(qv);
-      }
-      *reinterpret_cast<bf16x8*>(&Kc[buf][row * KP + c8 * 8]) = kv;
-      *reinterpret_cast<bf16x8*>(&Qc[buf][row * KP + c8 * 8]) = qv;
+      const int e = th + u * (kNT / 2), row = e / KCH, c8 = e % KCH;
+      *reinterpret_cast<bf16x8*>(&dst[row * KP + c8 * 8]) = l2 ? l2norm_row_chunk<KCH>(src[u]) : src[u];
     }
-    if (w == kGateWave) chunk_gates_from_raw(gs, pgraw, pbraw, p.dg, p.db, len, p.flags, a_log, dt_b, lane);
   };
-  auto stage_vt = [&]() {
-    if (t < kC * 4) *reinterpret_cast<bf16x8*>(Vc + (t >> 2) * kVP + (t & 3) * 8) = pv;
-    *reinterpret_cast<bf16x8*>(Tb + (t >> 3) * kCP + (t & 7) * 8) = pt;
+  auto fetch_k = [&](int c, int u0, int u1) {  // waves 0-3: K rows of chunk c (and with u0 == 0 its gates)
+    fetch_rows(pr, kg, c, u0, u1);
+    if (u0 > 0) return;
+    const int64_t c0 = bos + (int64_t)c * kC;
+    const uint32_t gb = (uint32_t)(p.HV * dtype_bytes(p.dg)), bb = (uint32_t)(p.HV * dtype_bytes(p.db));
+    const uint32_t len = (uint32_t)chunk_len(c);
+    const auto rg = make_rsrc(static_cast<const char*>(p.g) + (c0 * p.HV + hv) * dtype_bytes(p.dg), len * gb);
+    const auto rb = make_rsrc(static_cast<const char*>(p.beta) + (c0 * p.HV + hv) * dtype_bytes(p.db), len * bb);
+    pgraw = buf_load_raw32(rg, lane * gb, p.dg);
+    pbraw = buf_load_raw32(rb, lane * bb, p.db);
+  };
+  auto stage_gates = [&](int c) {  // wave kGateWave: gate slot c % 3
+    if (w == kGateWave)
+      chunk_gates_from_raw(gv[c % 3], pgraw, pbraw, p.dg, p.db, chunk_len(c), p.flags, a_log, dt_b, lane);
+  };
+  auto fetch_vt = [&](int c) {  // waves 4-7: V slice and T - I rows of chunk c
+    const int64_t c0 = bos + (int64_t)c * kC;
+    const uint32_t len = (uint32_t)chunk_len(c);
+    const auto rv = make_rsrc(vg + (c0 * p.HV + hv) * VD + vb * kVB, len * v_row);
+    pv = buf_load16(rv, (th >> 2) * v_row + (th & 3) * 16);
+    const auto rt = make_rsrc(p.tw + (c0 * p.HV + hv) * kC, len * t_row);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int e = th + u * (kNT / 2);
+      pt[u] = buf_load16(rt, (e >> 3) * t_row + (e & 7) * 16);
+    }
+  };
+  auto stage_vt = [&]() {  // waves 4-7
+    *reinterpret_cast<bf16x8*>(Vc + (th >> 2) * kVP + (th & 3) * 8) = pv;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int e = th + u * (kNT / 2);
+      *reinterpret_cast<bf16x8*>(Tb + (e >> 3) * kCP + (e & 7) * 8) = pt[u];
+    }
+  };
+  auto store_o = [&](int c) {  // waves 4-7: O of chunk c from Ob to HBM, 16 bytes per thread
+    const int64_t c0 = bos + (int64_t)c * kC;
+    const auto ro = make_rsrc(og + (c0 * p.HV + hv) * VD + vb * kVB, (uint32_t)chunk_len(c) * v_row);
+    const int row = th >> 2, c8 = th & 3;
+    buf_store16(*reinterpret_cast<const bf16x8*>(Ob + row * kVP + c8 * 8), ro, row * v_row + c8 * 16);
   };
 
   // P of the chunk in buffer `buf`: tile (rb, cb), rb <= cb, holds element (j = 16rb + 4g + i,
   // t = 16cb + li) = exp(gam_t - gam_j) k_j.q_t for j <= t. The 10 tiles are dealt to waves 4-7 as
   // 3, 3, 2, 2 (code: up to three 5-bit fields rb * 4 + cb, kNoTile = none), so with Delta on
   // waves 0-3 every SIMD issues 12-14 MFMAs in phase B.
-  auto p_job = [&](auto code_c, int buf, const ChunkGates& gs) {
+  auto p_job = [&](auto code_c, const bf16* kb, const bf16* qb, bf16* pw, const ChunkGates& gs) {
     constexpr int code = decltype(code_c)::value;
-    const bf16* kb = Kc[buf];
-    const bf16* qb = Qc[buf];
     bf16x8 fa[3][KS], fb[3][KS];
     float gtc[3];
     float4 gjs[3];
@@ -199,7 +215,6 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
         fb[q][s] = ld8(qb + (16 * cb + li) * KP + 32 * s + 8 * g4);
       }
     }
-    __builtin_amdgcn_sched_barrier(0);  // every read of the job ahead of its MFMAs
     f32x4 pacc[3];
 #pragma unroll
     for (int q = 0; q < 3; ++q) {
@@ -208,7 +223,6 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
 #pragma unroll
       for (int s = 0; s < KS; ++s) pacc[q] = mma(fa[q][s], fb[q][s], pacc[q]);
     }
-    bf16* pw = Pb[buf];
 #pragma unroll
     for (int q = 0; q < 3; ++q) {
       const int tc = (code >> (5 * q)) & 31;
@@ -223,12 +237,16 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
       *reinterpret_cast<bf16x4*>(pw + tt * kCP + j0) = to_bf16x4(val[0], val[1], val[2], val[3]);
     }
   };
-  auto run_p_side = [&](int buf, const ChunkGates& gs) {
+  auto run_p_side = [&](int c) {  // waves 4-7: P of chunk c into Pb[c % 2]
+    const bf16* kb = Kc[c % 3];
+    const bf16* qb = Qc[c & 1];
+    bf16* pw = Pb[c & 1];
+    const ChunkGates& gs = gv[c % 3];
     switch (w) {  // tiles (0,0) (0,1) (0,2) | (0,3) (1,1) (1,2) | (1,3) (2,2) | (2,3) (3,3)
-      case 4: p_job(std::integral_constant<int, p_tiles(0, 1, 2)>{}, buf, gs); break;
-      case 5: p_job(std::integral_constant<int, p_tiles(3, 5, 6)>{}, buf, gs); break;
-      case 6: p_job(std::integral_constant<int, p_tiles(7, 10, kNoTile)>{}, buf, gs); break;
-      default: p_job(std::integral_constant<int, p_tiles(11, 15, kNoTile)>{}, buf, gs); break;
+      case 4: p_job(std::integral_constant<int, p_tiles(0, 1, 2)>{}, kb, qb, pw, gs); break;
+      case 5: p_job(std::integral_constant<int, p_tiles(3, 5, 6)>{}, kb, qb, pw, gs); break;
+      case 6: p_job(std::integral_constant<int, p_tiles(7, 10, kNoTile)>{}, kb, qb, pw, gs); break;
+      default: p_job(std::integral_constant<int, p_tiles(11, 15, kNoTile)>{}, kb, qb, pw, gs); break;
     }
   };
 
@@ -252,28 +270,35 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
     *reinterpret_cast<bf16x4*>(Sb + vv * KP + kd0) = to_bf16x4(racc[u][0], racc[u][1], racc[u][2], racc[u][3]);
   }
 
-  // prologue: chunks 0 and 1 staged, P of chunk 0
-  fetch_kq(0);
-  fetch_vt(0);
-  stage_kq(0, gv[0], chunk_len(0));
-  stage_vt();
-  fetch_kq(1);
-  stage_kq(1, gv[1], chunk_len(1));
+  // prologue: K/Q/gates of chunks 0 and 1, V/T of chunk 0 staged, K/Q of chunk 2 in flight, P of chunk 0
+  if (w < 4) {
+    fetch_k(0, 0, QKPT);
+    stage_rows(pr, Kc[0]);
+    stage_gates(0);
+    fetch_k(1, 0, QKPT);
+    stage_rows(pr, Kc[1]);
+    stage_gates(1);
+    fetch_k(2, 0, QB);  // the rest in phase A of chunk 0
+  } else {
+    fetch_rows(pr, qg, 0, 0, QKPT);
+    stage_rows(pr, Qc[0]);
+    fetch_rows(pr, qg, 1, 0, QKPT);
+    stage_rows(pr, Qc[1]);
+    fetch_rows(pr, qg, 2, 0, QA);  // the rest in phases A and B of chunk 0
+    fetch_vt(0);
+    stage_vt();
+  }
   __syncthreads();
-  if (w >= 4 && nc > 0) run_p_side(0, gv[0]);
+  if (w >= 4 && nc > 0) run_p_side(0);
   __syncthreads();
 
   for (int i = 0; i < nc; ++i) {
-    const int b0 = i & 1, b1 = b0 ^ 1;  // buffers of chunk i and chunk i+1
-    const ChunkGates& G0 = gv[b0];
-    const int64_t c0 = bos + (int64_t)i * kC;
-    const int len = chunk_len(i);
-    // prefetch: K/Q/gates of chunk i+2, V and T of chunk i+1 (held in registers until the stage step)
-    fetch_kq(i + 2);
-    fetch_vt(i + 1);
+    const int ks = i % 3, qs = i & 1;  // K/gate slot and Q/P slot of chunk i
+    const ChunkGates& G0 = gv[ks];
 
     // ================================================================ phase A
     if (w < 4) {  // Y = K S for row tile w, then X = beta V - beta e^gam Y -> Xb (fp32 copy kept)
+      fetch_k(i + 2, QB, QKPT);
       const int r = w, j0 = 16 * r + 4 * g4;
       float vx[2][4];
 #pragma unroll
@@ -284,7 +309,7 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
       bf16x8 fk[KS], sf[2][KS];
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        fk[s] = ld8(Kc[b0] + (16 * r + li) * KP + 32 * s + 8 * g4);
+        fk[s] = ld8(Kc[ks] + (16 * r + li) * KP + 32 * s + 8 * g4);
         sf[0][s] = ld8(Sb + li * KP + 32 * s + 8 * g4);
         sf[1][s] = ld8(Sb + (16 + li) * KP + 32 * s + 8 * g4);
       }
@@ -303,12 +328,14 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
         *reinterpret_cast<bf16x4*>(Xb + (16 * nt + li) * kCP + j0) =
             to_bf16x4(racc[SPW + nt][0], racc[SPW + nt][1], racc[SPW + nt][2], racc[SPW + nt][3]);
       }
-    } else {  // Z = Q S for row tile w - 4 (kept for O)
+    } else {  // V/T of chunk i+1 requested; Z = Q S for row tile w - 4 (kept for O); O of chunk i-1 out
+      fetch_vt(i + 1);
+      fetch_rows(pr, qg, i + 2, QA, QB);
       const int r = w - 4;
       bf16x8 fq[KS], sf[2][KS];
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        fq[s] = ld8(Qc[b0] + (16 * r + li) * KP + 32 * s + 8 * g4);
+        fq[s] = ld8(Qc[qs] + (16 * r + li) * KP + 32 * s + 8 * g4);
         sf[0][s] = ld8(Sb + li * KP + 32 * s + 8 * g4);
         sf[1][s] = ld8(Sb + (16 + li) * KP + 32 * s + 8 * g4);
       }
@@ -320,6 +347,7 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
         racc[0] = mma(fq[s], sf[0][s], racc[0]);
         racc[1] = mma(fq[s], sf[1][s], racc[1]);
       }
+      if (i > 0) store_o(i - 1);
     }
     __syncthreads();
 
@@ -345,18 +373,23 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
         *reinterpret_cast<bf16x4*>(DtH + vv * kCP + tb0) = hi;
         *reinterpret_cast<bf16x4*>(DtL + vv * kCP + tb0) = lo;
       }
-    } else if (i + 1 < nc) {  // P of chunk i+1, off the state chain
-      run_p_side(b1, gv[b1]);
+      // K/gates of chunk i+2 into their slots (last read by chunk i-1), then the first loads of chunk i+3
+      stage_rows(pr, Kc[(i + 2) % 3]);
+      stage_gates(i + 2);
+      fetch_k(i + 3, 0, QA);
+    } else {  // P of chunk i+1, off the state chain
+      fetch_rows(pr, qg, i + 2, QB, QKPT);
+      if (i + 1 < nc) run_p_side(i + 1);
     }
     __syncthreads();
 
     // ================================================================ phase C
-    if (w >= 4) {  // O = scale (e^gam Z + P Delta) for row tile r, staged as bf16 in Vc
+    if (w >= 4) {  // O = scale (e^gam Z + P Delta) for row tile r -> Ob; V/T of chunk i+1 staged
       const int r = w - 4;
       f32x4 oacc[2] = {};
       const int ksteps = (r >= 2) ? 2 : 1;
       for (int s = 0; s < ksteps; ++s) {
-        const bf16x8 a = ld8(Pb[b0] + (16 * r + li) * kCP + 32 * s + 8 * g4);
+        const bf16x8 a = ld8(Pb[qs] + (16 * r + li) * kCP + 32 * s + 8 * g4);
         oacc[0] = mma(a, ld8(Db + li * kCP + 32 * s + 8 * g4), oacc[0]);
         oacc[1] = mma(a, ld8(Db + (16 + li) * kCP + 32 * s + 8 * g4), oacc[1]);
       }
@@ -365,12 +398,16 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii) {
         const int tt = 16 * r + 4 * g4 + ii;
-        Vc[tt * kVP + li] = static_cast<bf16>(p.scale * (egv[ii] * racc[0][ii] + oacc[0][ii]));
-        Vc[tt * kVP + 16 + li] = static_cast<bf16>(p.scale * (egv[ii] * racc[1][ii] + oacc[1][ii]));
+        Ob[tt * kVP + li] = static_cast<bf16>(p.scale * (egv[ii] * racc[0][ii] + oacc[0][ii]));
+        Ob[tt * kVP + 16 + li] = static_cast<bf16>(p.scale * (egv[ii] * racc[1][ii] + oacc[1][ii]));
       }
+      stage_vt();                 // V_i was last read in phase A, T_i in phase B
+      stage_rows(pr, Qc[qs]);     // Q of chunk i+2 (Q_i was last read by Z in phase A)
+      fetch_rows(pr, qg, i + 3, 0, QA);
     } else {  // S' = e^{gam_c} S + K^T Delta~ (hi + lo) for this wave's state tiles
+      fetch_k(i + 3, QA, QB);
       const float ec = __expf(G0.gam[kC - 1]);
-      const bf16* kb = Kc[b0];
+      const bf16* kb = Kc[ks];
 #pragma unroll
       for (int u = 0; u < SPW; ++u) {
         const int ti = s_first + u, rt = ti >> 1, nt = ti & 1;
@@ -390,18 +427,8 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
       }
     }
     __syncthreads();
-
-    // ================================================================ stage
-    if (t < kC * 4) {  // O of chunk i (staged in Vc by phase C) to HBM; V of chunk i+1 replaces it
-      const int row = t >> 2, c8 = t & 3;
-      if (row < len)
-        *reinterpret_cast<bf16x8*>(og + ((c0 + row) * p.HV + hv) * VD + vb * kVB + c8 * 8) =
-            *reinterpret_cast<const bf16x8*>(Vc + row * kVP + c8 * 8);
-    }
-    stage_kq(b0, gv[b0], chunk_len(i + 2));  // chunk i+2 into the buffers of chunk i
-    stage_vt();
-    __syncthreads();
   }
+  if (w >= 4 && nc > 0) store_o(nc - 1);
 
   if (p.ht && w < 4) {
 #pragma unroll

@@ -44,6 +44,30 @@ __device__ __forceinline__ bf16x8 ld8_tr(const bf16* tile, int pitch, int j0, in
   return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
 
+// ---------------------------------------------------------------- raw buffer access
+// A buffer resource covers [base, base + bytes); a load past the end returns zeros and a store
+// past the end is dropped by the hardware range check. The loads are therefore unconditional
+// instructions (no branch around them, no zero fill of the destination in between), which keeps
+// the vector-memory counter waits at the points where the data is used.
+constexpr int kRsrcWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit dword format, no swizzle
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kRsrcWord3);
+}
+__device__ __forceinline__ bf16x8 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+__device__ __forceinline__ void buf_store16(bf16x8 v, __amdgpu_buffer_rsrc_t r, uint32_t off) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, (int)off, 0, 0);
+}
+// Raw bits of one gate element (fp32 as is, 16-bit types zero-extended), like load_raw32.
+__device__ __forceinline__ uint32_t buf_load_raw32(__amdgpu_buffer_rsrc_t r, uint32_t off, int dtype) {
+  if (dtype == GDN_DTYPE_F32) return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0);
+}
+__device__ __forceinline__ int dtype_bytes(int dtype) { return dtype == GDN_DTYPE_F32 ? 4 : 2; }
+
 // Value of lane (quad base + q) broadcast to the 4 lanes of each quad (DPP quad_perm q,q,q,q).
 __device__ __forceinline__ float quad_bcast(float x, int q) {
   const int v = __float_as_int(x);
