@@ -6,10 +6,12 @@
 fp32 g/beta/h0, final state out), inputs already resident in HBM; ``value`` is prefill tokens/s.
 
 The same line carries
-- ``roofline``: the fused chunk kernel against bf16 dense MFMA peak, from HIP events around each
-  launch on the stream it runs on; algorithmic FLOPs per launch = (10 C^2 d + 6 C d^2) per
-  (chunk, head) x 4096 chunk-heads = 47,244,640,256 (C = 64, d = 128, solve excluded);
-  ``traffic`` (HBM bytes per launch) comes from the committed rocprofv3 PMC summary when present;
+- ``roofline``: the chunked prefill op -- its two kernels, gated_delta_chunk_prep_kernel (the
+  per-chunk (I + A)^-1) then gated_delta_chunk_kernel (the state recurrence), launched back to back
+  on one stream -- against bf16 dense MFMA peak, from HIP events around each op launch on that
+  stream; algorithmic FLOPs per launch = (10 C^2 d + 6 C d^2) per (chunk, head) x 4096 chunk-heads
+  = 47,244,640,256 (C = 64, d = 128, solve excluded); ``traffic`` (HBM bytes per launch, both
+  kernels) comes from the committed rocprofv3 PMC summary when present;
 - ``decode``: config 2, 1000 back-to-back fused decode steps (conv cache + SiLU + L2 norm + state
   update, state updated in place) with HBM bytes/step = 141,664,256, plus a run rotating over
   5 state copies (335 MB > the 256 MB Infinity Cache) that forces DRAM traffic;
@@ -32,6 +34,7 @@ sys.path.insert(0, ROOT)
 BF16_PEAK_TFLOPS = 2516.6  # MI355X dense bf16 MFMA
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
 C = 64
+PREFILL_KERNELS = ("gated_delta_chunk_prep_kernel", "gated_delta_chunk_kernel")  # one op = these two launches
 
 
 def chunk_flops(lengths, heads: int, d: int) -> int:
@@ -231,7 +234,8 @@ def main() -> int:
     achieved = flops / (ms_launch * 1e-3) / 1e12
     tok_s = B * T / (ms_step * 1e-3)
     min_bytes = 4 * inp.q.numel() * 2 + 2 * inp.g.numel() * 4 + 2 * inp.h0.numel() * 4
-    traffic = load_traffic("gated_delta_chunk_kernel")
+    tparts = [load_traffic(k) for k in PREFILL_KERNELS]
+    traffic = sum(tparts) if all(x is not None for x in tparts) else None
 
     # ------------------------------------------------------------------ config 2: decode
     # The step is captured once into a HIP graph and replayed back to back (a serving loop launches
@@ -302,7 +306,7 @@ def main() -> int:
                    "global_batch": B, "seq_len": T, "parallelism": "single GPU"},
         "roofline": {
             "bound": "mfma",
-            "kernel": "gated_delta_chunk_kernel",
+            "kernel": " + ".join(PREFILL_KERNELS),
             "achieved": round(achieved, 2),
             "peak": BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s",

@@ -5,7 +5,7 @@
 // it reorganises). T depends only on the chunk's k, g and beta, so every chunk is solved in
 // parallel here and the sequential state kernel only reads the result.
 //
-// One workgroup of 4 waves per (chunk, value head):
+// One workgroup of 4 waves per (chunk, value head), four workgroups per CU:
 //   load:   k rows (L2-normalised when asked, rounded to bf16 as the state kernel sees them) -> LDS;
 //           g/beta -> gate terms (wave 0, DPP scan).
 //   Gram:   wave r computes the 16x16 k.k tiles (r, cb >= r) with bf16 MFMA (exact products, fp32
@@ -31,12 +31,21 @@ __global__ __launch_bounds__(kPrepNT) void gated_delta_chunk_prep_kernel(ChunkPr
   constexpr int KCH = KD / 8;  // 16-byte chunks per k row
   constexpr int KPT = kC * KCH / kPrepNT;
 
-  __shared__ __align__(16) bf16 Kc[kC * KP];
-  __shared__ __align__(16) float Ad[4][256];       // diagonal A blocks: Ad[b][(4m + k) * 4 + q] = A[16b+4q+k][16b+m]
-  __shared__ __align__(16) float Ao[48 * kAoP];     // A rows 16..63 x cols 0..47 (off-diagonal lower blocks)
-  __shared__ __align__(16) float Tf[2][32 * kTfP];  // T[0:32][0:32] and T[32:64][32:64] in fp32
-  __shared__ __align__(16) bf16 Tb[kC * kCP];       // T - I in bf16 [t][j]
+  // The k tile is dead once the Gram MFMAs have read it, so the solve's buffers reuse its space
+  // (about 34 KB per workgroup in all: four workgroups fit a CU's LDS):
+  //   Ad  diagonal A blocks: Ad[b][(4m + k) * 4 + q] = A[16b+4q+k][16b+m]
+  //   Ao  A rows 16..63 x cols 0..47 (the off-diagonal lower blocks)
+  //   Tf  T[0:32][0:32] and T[32:64][32:64] in fp32
+  //   Tb  T - I in bf16 [t][j] (blocks above the diagonal are never written: the store zero-fills them)
+  constexpr int kAdB = 4 * 256 * 4, kAoB = 48 * kAoP * 4, kTfB = 2 * 32 * kTfP * 4, kTbB = kC * kCP * 2;
+  constexpr int kSolveB = kAdB + kAoB + kTfB + kTbB, kKcB = kC * KP * 2;
+  __shared__ __align__(16) char smem[kSolveB > kKcB ? kSolveB : kKcB];
   __shared__ __align__(16) ChunkGates gs;
+  bf16* const Kc = reinterpret_cast<bf16*>(smem);
+  float(*const Ad)[256] = reinterpret_cast<float(*)[256]>(smem);
+  float* const Ao = reinterpret_cast<float*>(smem + kAdB);
+  float(*const Tf)[32 * kTfP] = reinterpret_cast<float(*)[32 * kTfP]>(smem + kAdB + kAoB);
+  bf16* const Tb = reinterpret_cast<bf16*>(smem + kAdB + kAoB + kTfB);
 
   const int t = threadIdx.x, lane = t & 63, w = t >> 6, g4 = lane >> 4, li = lane & 15;
   const int hv = blockIdx.y;
@@ -84,7 +93,6 @@ __global__ __launch_bounds__(kPrepNT) void gated_delta_chunk_prep_kernel(ChunkPr
       graw = load_raw32(p.g, p.dg, gi);
       braw = load_raw32(p.beta, p.db, gi);
     }
-    for (int e = t; e < kC * kCP / 8; e += kPrepNT) reinterpret_cast<bf16x8*>(Tb)[e] = bf16x8{};
 #pragma unroll
     for (int u = 0; u < KPT; ++u) {
       const int e = t + u * kPrepNT, row = e / KCH, c8 = e % KCH;
@@ -98,16 +106,16 @@ __global__ __launch_bounds__(kPrepNT) void gated_delta_chunk_prep_kernel(ChunkPr
   __syncthreads();
 
   // ------------------------------------------------------------------ Gram tiles, A, diagonal solves
-  // Wave r: row tile r of A. The row tile is a template constant (one code copy per wave).
-  auto gram_row = [&](auto rc) {
+  // Wave r: row tile r of A (a template constant: one code copy per wave). The k.k tiles stay in
+  // registers across the barrier that retires the k tile.
+  f32x4 dacc{}, oacc[3] = {};
+  auto gram_mfma = [&](auto rc) {
     constexpr int rk = decltype(rc)::value;
     bf16x8 fk[KS];
 #pragma unroll
     for (int s = 0; s < KS; ++s) fk[s] = ld8(Kc + (16 * rk + li) * KP + 32 * s + 8 * g4);
-    f32x4 dacc{}, oacc[3] = {};
 #pragma unroll
     for (int s = 0; s < KS; ++s) dacc = mma(fk[s], fk[s], dacc);
-    // off-diagonal tiles (rk, cb > rk), issued before the solve so their MFMAs overlap it
 #pragma unroll
     for (int cb = rk + 1; cb < 4; ++cb) {
       bf16x8 fo[KS];
@@ -116,6 +124,9 @@ __global__ __launch_bounds__(kPrepNT) void gated_delta_chunk_prep_kernel(ChunkPr
 #pragma unroll
       for (int s = 0; s < KS; ++s) oacc[cb - 1] = mma(fk[s], fo[s], oacc[cb - 1]);
     }
+  };
+  auto gram_post = [&](auto rc) {
+    constexpr int rk = decltype(rc)::value;
     // k.k is symmetric: dacc[i] = k_t.k_j with t = 16rk + li, j = 16rk + 4g + i; A[t][j] for j < t
     const float gt = gs.gam[16 * rk + li], bt = gs.bet[16 * rk + li];
     const float4 gj = ld4f(&gs.gam[16 * rk + 4 * g4]);
@@ -127,6 +138,16 @@ __global__ __launch_bounds__(kPrepNT) void gated_delta_chunk_prep_kernel(ChunkPr
     float* ad = Ad[rk];
 #pragma unroll
     for (int ii = 0; ii < 4; ++ii) ad[((4 * g4 + ii) * 4 + (li & 3)) * 4 + (li >> 2)] = av[ii];
+    // off-diagonal A blocks: element (j = 16rk + 4g + i, t = 16cb + li) -> Ao[t - 16][j]
+#pragma unroll
+    for (int cb = rk + 1; cb < 4; ++cb) {
+      const int tt = 16 * cb + li, j0 = 16 * rk + 4 * g4;
+      const float gtt = gs.gam[tt], btt = gs.bet[tt];
+      float val[4];
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) val[ii] = btt * __expf(gtt - gjv[ii]) * oacc[cb - 1][ii];
+      *reinterpret_cast<float4*>(&Ao[(tt - 16) * kAoP + j0]) = make_float4(val[0], val[1], val[2], val[3]);
+    }
     // Forward substitution on 64 lanes: lane (col = lane/4, k = lane%4) holds rows 4q+k of column
     // col of T_rr; x_m is broadcast inside each quad with DPP, and step m reads the lane's four A
     // entries of column m with one 16-byte LDS read. A is strictly lower, so no row mask is needed.
@@ -153,22 +174,19 @@ __global__ __launch_bounds__(kPrepNT) void gated_delta_chunk_prep_kernel(ChunkPr
       tf[rr * kTfP] = x[q];
       tb[rr * kCP] = static_cast<bf16>(rr == col ? 0.f : x[q]);
     }
-    // off-diagonal A blocks: element (j = 16rk + 4g + i, t = 16cb + li) -> Ao[t - 16][j]
-#pragma unroll
-    for (int cb = rk + 1; cb < 4; ++cb) {
-      const int tt = 16 * cb + li, j0 = 16 * rk + 4 * g4;
-      const float gtt = gs.gam[tt], btt = gs.bet[tt];
-      float val[4];
-#pragma unroll
-      for (int ii = 0; ii < 4; ++ii) val[ii] = btt * __expf(gtt - gjv[ii]) * oacc[cb - 1][ii];
-      *reinterpret_cast<float4*>(&Ao[(tt - 16) * kAoP + j0]) = make_float4(val[0], val[1], val[2], val[3]);
-    }
   };
   switch (w) {
-    case 0: gram_row(std::integral_constant<int, 0>{}); break;
-    case 1: gram_row(std::integral_constant<int, 1>{}); break;
-    case 2: gram_row(std::integral_constant<int, 2>{}); break;
-    default: gram_row(std::integral_constant<int, 3>{}); break;
+    case 0: gram_mfma(std::integral_constant<int, 0>{}); break;
+    case 1: gram_mfma(std::integral_constant<int, 1>{}); break;
+    case 2: gram_mfma(std::integral_constant<int, 2>{}); break;
+    default: gram_mfma(std::integral_constant<int, 3>{}); break;
+  }
+  __syncthreads();  // the k tile is dead from here on
+  switch (w) {
+    case 0: gram_post(std::integral_constant<int, 0>{}); break;
+    case 1: gram_post(std::integral_constant<int, 1>{}); break;
+    case 2: gram_post(std::integral_constant<int, 2>{}); break;
+    default: gram_post(std::integral_constant<int, 3>{}); break;
   }
   __syncthreads();
 
@@ -247,9 +265,11 @@ __global__ __launch_bounds__(kPrepNT) void gated_delta_chunk_prep_kernel(ChunkPr
 #pragma unroll
   for (int u = 0; u < kC * 8 / kPrepNT; ++u) {
     const int e = t + u * kPrepNT, row = e >> 3, c8 = e & 7;
-    if (row < len)
+    if (row < len) {
+      const bool upper = (c8 >> 1) > (row >> 4);  // a 16x16 block above the diagonal: zero
       *reinterpret_cast<bf16x8*>(p.tw + ((c0 + row) * p.HV + hv) * kC + c8 * 8) =
-          *reinterpret_cast<const bf16x8*>(&Tb[row * kCP + c8 * 8]);
+          upper ? bf16x8{} : *reinterpret_cast<const bf16x8*>(&Tb[row * kCP + c8 * 8]);
+    }
   }
 }
 
