@@ -11,7 +11,7 @@
 //
 // Workspace (caller-owned, gdn_chunk_workspace_size bytes):
 //   [0, tbytes)                T - I rows: bf16 [B*T][HV][64], row t of the chunk holding token t
-//   [tbytes, + (N+1)*4)        with cu_seqlens only: int32 chunk_first[N + 1]
+//   then, with cu_seqlens only: int32 chunk_first[N + 1] and int32 order[N] (256-byte aligned each)
 #pragma once
 
 #include "gdn_mfma.h"
@@ -23,6 +23,7 @@ struct ChunkPrepParams {
   bf16* tw;                // T - I rows (workspace)
   const void* cu;
   const int* chunk_first;  // with cu only
+  const int* order;        // with cu only: sequences by length, longest first (written by the index kernel)
   int cu_i32;
   int64_t T, H, HV, N;
   int dg, db;
@@ -30,7 +31,8 @@ struct ChunkPrepParams {
   const float *A_log, *dt_bias;
 };
 
-inline int64_t chunk_t_bytes(int64_t tokens, int64_t HV) { return ((tokens * HV * kC * 2 + 255) / 256) * 256; }
+inline int64_t align256(int64_t b) { return (b + 255) / 256 * 256; }
+inline int64_t chunk_t_bytes(int64_t tokens, int64_t HV) { return align256(tokens * HV * kC * 2); }
 
 // Launches the index kernel (with cu) and the prep kernel; returns a GDN status.
 int launch_chunk_prep(const ChunkPrepParams& p, int64_t B, int64_t K, hipStream_t s);

@@ -45,6 +45,7 @@ struct ChunkParams {
   float* ht;
   const bf16* tw;  // T - I rows from the prep kernel
   const void* cu;
+  const int* order;  // with cu: sequences by length, longest first
   int cu_i32;
   int64_t T, H, HV, N;
   int dg, db;
@@ -85,17 +86,24 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
 
   const int t = threadIdx.x, lane = t & 63, w = t >> 6, g4 = lane >> 4, li = lane & 15;
 
-  // workgroup -> (sequence n, value head hv, slice vb); the NVB slices of a chain share an XCD
+  // workgroup -> (chain rank k, slice vb) -> (sequence n, value head hv). Workgroups are dispatched
+  // in blockIdx order and blockIdx b lands on XCD b % 8: XCD x takes chain ranks x, x + 8, ..., all
+  // NVB slices of a chain on one XCD (its q/k tiles are then read from one L2). Chain ranks follow
+  // the longest-first sequence order with cu_seqlens, so a grid larger than the machine starts the
+  // longest recurrences first.
   const int64_t chains = p.N * p.HV;
-  int64_t id = blockIdx.x;
+  int64_t k_rank;
+  int vb;
   if (chains % 8 == 0) {
-    const int64_t per = chains * NVB / 8;
-    id = (id % 8) * per + id / 8;
+    const int64_t x = blockIdx.x % 8, j = blockIdx.x / 8;
+    k_rank = 8 * (j / NVB) + x;
+    vb = (int)(j % NVB);
+  } else {
+    k_rank = blockIdx.x / NVB;
+    vb = (int)(blockIdx.x % NVB);
   }
-  const int vb = (int)(id % NVB);
-  const int64_t chain = id / NVB;
-  const int hv = (int)(chain % p.HV);
-  const int64_t n = chain / p.HV;
+  const int hv = (int)(k_rank % p.HV);
+  const int64_t n = p.order ? (int64_t)p.order[k_rank / p.HV] : k_rank / p.HV;
   const int h = hv / (int)(p.HV / p.H);
   int64_t bos, eos;
   if (p.cu) {
@@ -447,7 +455,7 @@ using namespace gdn;
 extern "C" size_t gdn_chunk_workspace_size(int64_t B, int64_t T, int64_t HV, int64_t N, int varlen) {
   if (B <= 0 || T < 0 || HV <= 0 || N <= 0) return 0;
   size_t bytes = (size_t)chunk_t_bytes(B * T, HV);
-  if (varlen) bytes += (size_t)(((N + 1) * 4 + 255) / 256) * 256;
+  if (varlen) bytes += (size_t)(align256((N + 1) * 4) + align256(N * 4));
   return bytes;
 }
 
@@ -498,13 +506,15 @@ extern "C" int gdn_chunk_fwd(const void* q, const void* k, const void* v, const 
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int cu_i32 = (flags & GDN_FLAG_CU_INT32) ? 1 : 0;
   bf16* tw = static_cast<bf16*>(workspace);
-  const int* chunk_first =
-      cu_seqlens ? reinterpret_cast<const int*>(static_cast<char*>(workspace) + chunk_t_bytes(B * T, HV)) : nullptr;
-  ChunkPrepParams pp{k, g, beta, tw, cu_seqlens, chunk_first, cu_i32, T, H, HV, N, g_dtype, beta_dtype, flags, A_log,
-                     dt_bias};
+  char* const ws = static_cast<char*>(workspace);
+  const int* chunk_first = cu_seqlens ? reinterpret_cast<const int*>(ws + chunk_t_bytes(B * T, HV)) : nullptr;
+  const int* order =
+      cu_seqlens ? reinterpret_cast<const int*>(ws + chunk_t_bytes(B * T, HV) + align256((N + 1) * 4)) : nullptr;
+  ChunkPrepParams pp{k, g, beta, tw, cu_seqlens, chunk_first, order, cu_i32, T, H, HV, N, g_dtype, beta_dtype, flags,
+                     A_log, dt_bias};
   const int rc = launch_chunk_prep(pp, B, K, s);
   if (rc != GDN_OK) return rc;
-  ChunkParams p{q, k, v, g, beta, initial_state, o, final_state, tw, cu_seqlens, cu_i32, T, H, HV, N,
+  ChunkParams p{q, k, v, g, beta, initial_state, o, final_state, tw, cu_seqlens, order, cu_i32, T, H, HV, N,
                 g_dtype, beta_dtype, scale, flags, A_log, dt_bias};
   dim3 grid((unsigned)blocks), block(kNT);
   if (K == 128 && V == 128) hipLaunchKernelGGL((gated_delta_chunk_kernel<128, 128>), grid, block, 0, s, p);

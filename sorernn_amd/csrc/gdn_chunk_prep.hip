@@ -273,12 +273,18 @@ __global__ __launch_bounds__(kPrepNT) void gated_delta_chunk_prep_kernel(ChunkPr
   }
 }
 
-// chunk_first[0] = 0, chunk_first[n + 1] = chunk_first[n] + ceil(len_n / 64): one block, a running
-// block-wide scan over tiles of 1024 sequences.
+// One block, with cu_seqlens:
+//   chunk_first[0] = 0, chunk_first[n + 1] = chunk_first[n] + ceil(len_n / 64) (a running block-wide
+//   scan over tiles of 1024 sequences): the prep kernel's chunk -> sequence map;
+//   order[k] = the sequence of rank k by length, longest first (ties by index), for N <= kOrderMax
+//   (a bitonic sort in LDS; identity above that): the state kernel starts the longest recurrences
+//   first, so a grid larger than the machine finishes near the longest sequence's own time.
+constexpr int kOrderMax = 2048;
 __global__ __launch_bounds__(1024) void gated_delta_chunk_index_kernel(const void* cu, int cu_i32, int64_t N,
-                                                                        int* chunk_first) {
+                                                                        int* chunk_first, int* order) {
   __shared__ int wsum[16];
   __shared__ int carry;
+  __shared__ unsigned long long keys[kOrderMax];
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   if (t == 0) {
     carry = 0;
@@ -304,13 +310,46 @@ __global__ __launch_bounds__(1024) void gated_delta_chunk_index_kernel(const voi
     if (t == 1023) carry = before + incl;
     __syncthreads();
   }
+  if (N > kOrderMax) {
+    for (int64_t n = t; n < N; n += 1024) order[n] = (int)n;
+    return;
+  }
+  // key = (chunks descending, index ascending); padding sorts last
+  int m = 1;
+  while (m < N) m <<= 1;
+  for (int n = t; n < m; n += 1024) {
+    unsigned long long key = ~0ull;
+    if (n < N) {
+      const unsigned nch = (unsigned)((load_index(cu, cu_i32, n + 1) - load_index(cu, cu_i32, n) + kC - 1) / kC);
+      key = ((unsigned long long)(0xffffffffu - nch) << 32) | (unsigned)n;
+    }
+    keys[n] = key;
+  }
+  __syncthreads();
+  for (int size = 2; size <= m; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int n = t; n < m; n += 1024) {
+        const int partner = n ^ stride;
+        if (partner > n) {
+          const bool up = (n & size) == 0;
+          const unsigned long long a = keys[n], b = keys[partner];
+          if ((a > b) == up) {
+            keys[n] = b;
+            keys[partner] = a;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+  for (int n = t; n < N; n += 1024) order[n] = (int)(keys[n] & 0xffffffffu);
 }
 
 int launch_chunk_prep(const ChunkPrepParams& p, int64_t B, int64_t K, hipStream_t s) {
   int64_t items;
   if (p.cu) {
     hipLaunchKernelGGL(gated_delta_chunk_index_kernel, dim3(1), dim3(1024), 0, s, p.cu, p.cu_i32, p.N,
-                       const_cast<int*>(p.chunk_first));
+                       const_cast<int*>(p.chunk_first), const_cast<int*>(p.order));
     items = (p.T + kC - 1) / kC + p.N;  // upper bound on the number of chunks
   } else {
     items = B * ((p.T + kC - 1) / kC);
