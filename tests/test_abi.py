@@ -49,3 +49,13 @@ def test_unsupported_options_raise():
     q = torch.randn(1, 4, 1, 64)
     with pytest.raises(NotImplementedError):
         chunk_gated_delta_rule(q, q, q, torch.zeros(1, 4, 1), torch.ones(1, 4, 1), allow_neg_eigval=True)
+
+
+def test_chunk_workspace_size_matches_layout():
+    """gdn_chunk_workspace_size: one 128-byte row of T - I per token-head, plus the varlen index
+    arrays (chunk_first[N + 1] and order[N], int32, 256-byte aligned each); 0 for invalid sizes."""
+    from sorernn_amd.ops import chunk_workspace_bytes
+    assert chunk_workspace_bytes(4, 4096, 16, 4, False) == 4 * 4096 * 16 * 128
+    assert chunk_workspace_bytes(1, 32768, 16, 8, True) == 32768 * 16 * 128 + 256 + 256
+    assert chunk_workspace_bytes(1, 100, 3, 300, True) == 100 * 3 * 128 + 1280 + 1280
+    assert chunk_workspace_bytes(0, 100, 3, 1, False) == 0

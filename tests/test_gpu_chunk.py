@@ -152,3 +152,18 @@ def test_chunk_extreme_inputs_stay_finite():
     o_ref, st_ref = _oracle(inp)
     assert_output_close(o.cpu(), o_ref, tol=2e-2 * float(o_ref.abs().max()))
     assert_state_close(st.cpu(), st_ref)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16], ids=["fp32", "fp16"])
+def test_chunk_config0_full_precision_inputs(dtype):
+    """BASELINE config 0 (B=1, T=256, H=4, d=64, fp32) through ``chunk_gated_delta_rule``: fp32/fp16
+    q/k/v run the token-by-token fp32 kernel, compared with the oracle at the fp32/fp16 bar."""
+    print(f"chunk config0 {dtype}", flush=True)
+    inp = config_inputs(0)
+    inp.q, inp.k, inp.v = inp.q.to(dtype), inp.k.to(dtype), inp.v.to(dtype)
+    o, st = _chunk(inp)
+    assert o.dtype == dtype
+    o_ref, st_ref = _oracle(inp)
+    assert_output_close(o.cpu(), o_ref)
+    assert_state_close(st.cpu(), st_ref)
+
