@@ -300,6 +300,19 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
   if (w >= 4 && nc > 0) run_p_side(0);
   __syncthreads();
 
+  // Operands that do not depend on the previous phase are read from LDS one phase early, so each
+  // phase starts with only its state-dependent reads outstanding: fpre (K rows of the Y tile in
+  // waves 0-3, Q rows of the Z tile in waves 4-7) at the end of phase C for the next chunk, the T
+  // fragments of Delta at the end of phase A, the K^T fragments of the state update at the end of B.
+  constexpr int NRT = SPW / 2;  // row tiles of K in a wave's state tiles
+  bf16x8 fpre[KS], tpre[2], ktr[NRT][2];
+  auto preload_f = [&](int c) {
+    const bf16* src = (w < 4) ? Kc[c % 3] + (16 * w + li) * KP : Qc[c & 1] + (16 * (w - 4) + li) * KP;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) fpre[s] = ld8(src + 32 * s + 8 * g4);
+  };
+  preload_f(0);
+
   for (int i = 0; i < nc; ++i) {
     const int ks = i % 3, qs = i & 1;  // K/gate slot and Q/P slot of chunk i
     const ChunkGates& G0 = gv[ks];
@@ -314,10 +327,9 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
 #pragma unroll
         for (int ii = 0; ii < 4; ++ii) vx[nt][ii] = (float)Vc[(j0 + ii) * kVP + 16 * nt + li];
       const float4 bj = ld4f(&G0.bet[j0]), bgj = ld4f(&G0.begam[j0]);
-      bf16x8 fk[KS], sf[2][KS];
+      bf16x8 sf[2][KS];
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        fk[s] = ld8(Kc[ks] + (16 * r + li) * KP + 32 * s + 8 * g4);
         sf[0][s] = ld8(Sb + li * KP + 32 * s + 8 * g4);
         sf[1][s] = ld8(Sb + (16 + li) * KP + 32 * s + 8 * g4);
       }
@@ -325,8 +337,8 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
       f32x4 yacc[2] = {};
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        yacc[0] = mma(fk[s], sf[0][s], yacc[0]);
-        yacc[1] = mma(fk[s], sf[1][s], yacc[1]);
+        yacc[0] = mma(fpre[s], sf[0][s], yacc[0]);
+        yacc[1] = mma(fpre[s], sf[1][s], yacc[1]);
       }
       const float bjv[4] = {bj.x, bj.y, bj.z, bj.w}, bgjv[4] = {bgj.x, bgj.y, bgj.z, bgj.w};
 #pragma unroll
@@ -336,14 +348,15 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
         *reinterpret_cast<bf16x4*>(Xb + (16 * nt + li) * kCP + j0) =
             to_bf16x4(racc[SPW + nt][0], racc[SPW + nt][1], racc[SPW + nt][2], racc[SPW + nt][3]);
       }
+#pragma unroll
+      for (int s = 0; s < 2; ++s) tpre[s] = ld8(Tb + (16 * w + li) * kCP + 32 * s + 8 * g4);
     } else {  // V/T of chunk i+1 requested; Z = Q S for row tile w - 4 (kept for O); O of chunk i-1 out
       fetch_vt(i + 1);
       fetch_rows(pr, qg, i + 2, QA, QB);
       const int r = w - 4;
-      bf16x8 fq[KS], sf[2][KS];
+      bf16x8 sf[2][KS];
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        fq[s] = ld8(Qc[qs] + (16 * r + li) * KP + 32 * s + 8 * g4);
         sf[0][s] = ld8(Sb + li * KP + 32 * s + 8 * g4);
         sf[1][s] = ld8(Sb + (16 + li) * KP + 32 * s + 8 * g4);
       }
@@ -352,8 +365,8 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
       racc[1] = f32x4{};
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        racc[0] = mma(fq[s], sf[0][s], racc[0]);
-        racc[1] = mma(fq[s], sf[1][s], racc[1]);
+        racc[0] = mma(fpre[s], sf[0][s], racc[0]);
+        racc[1] = mma(fpre[s], sf[1][s], racc[1]);
       }
       if (i > 0) store_o(i - 1);
     }
@@ -364,7 +377,7 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
       f32x4 dacc[2] = {racc[SPW], racc[SPW + 1]};
       const int ksteps = (w >= 2) ? 2 : 1;  // (T - I) vanishes for j >= t
       for (int s = 0; s < ksteps; ++s) {
-        const bf16x8 a = ld8(Tb + (16 * w + li) * kCP + 32 * s + 8 * g4);
+        const bf16x8 a = tpre[s];
         const bf16x8 x0 = ld8(Xb + li * kCP + 32 * s + 8 * g4);
         const bf16x8 x1 = ld8(Xb + (16 + li) * kCP + 32 * s + 8 * g4);
         dacc[0] = mma(a, x0, dacc[0]);
@@ -385,6 +398,10 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
       stage_rows(pr, Kc[(i + 2) % 3]);
       stage_gates(i + 2);
       fetch_k(i + 3, 0, QA);
+#pragma unroll
+      for (int u = 0; u < NRT; ++u)
+#pragma unroll
+        for (int s = 0; s < 2; ++s) ktr[u][s] = ld8_tr(Kc[ks], KP, 32 * s, 16 * (NRT * w + u), lane);
     } else {  // P of chunk i+1, off the state chain
       fetch_rows(pr, qg, i + 2, QB, QKPT);
       if (i + 1 < nc) run_p_side(i + 1);
@@ -415,14 +432,13 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
     } else {  // S' = e^{gam_c} S + K^T Delta~ (hi + lo) for this wave's state tiles
       fetch_k(i + 3, QA, QB);
       const float ec = __expf(G0.gam[kC - 1]);
-      const bf16* kb = Kc[ks];
 #pragma unroll
       for (int u = 0; u < SPW; ++u) {
-        const int ti = s_first + u, rt = ti >> 1, nt = ti & 1;
+        const int ti = s_first + u, nt = ti & 1;
         racc[u] *= ec;
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-          const bf16x8 a = ld8_tr(kb, KP, 32 * s, 16 * rt, lane);
+          const bf16x8 a = ktr[u >> 1][s];  // row tile ti / 2 = s_first / 2 + u / 2
           const int off = (16 * nt + li) * kCP + 32 * s + 8 * g4;
           racc[u] = mma(a, ld8(DtH + off), racc[u]);
           racc[u] = mma(a, ld8(DtL + off), racc[u]);
@@ -434,6 +450,7 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
         *reinterpret_cast<bf16x4*>(Sb + vv * KP + kd0) = to_bf16x4(racc[u][0], racc[u][1], racc[u][2], racc[u][3]);
       }
     }
+    if (i + 1 < nc) preload_f(i + 1);  // K_{i+1} was staged in phase B of chunk i-1, Q_{i+1} in phase C
     __syncthreads();
   }
   if (w >= 4 && nc > 0) store_o(nc - 1);
