@@ -10,7 +10,8 @@
 // before every sequence (the prep kernel's chunk -> sequence map) into the workspace.
 //
 // Workspace (caller-owned, gdn_chunk_workspace_size bytes):
-//   [0, tbytes)                T - I rows: bf16 [B*T][HV][64], row t of the chunk holding token t
+//   [0, tbytes)                T - I rows: bf16 [B*T][HV][64], row t of the chunk holding token t,
+//                              columns in tok_col order (gdn_mfma.h)
 //   then, with cu_seqlens only: int32 chunk_first[N + 1] and int32 order[N] (256-byte aligned each)
 #pragma once
 

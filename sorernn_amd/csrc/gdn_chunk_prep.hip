@@ -14,7 +14,8 @@
 //   merge:  T_{2q+1,2q} = -T_{2q+1,2q+1} A_{2q+1,2q} T_{2q,2q} (16 -> 32), then the 32 -> 64
 //           block, with three-term bf16 products (hi*hi + hi*lo + lo*hi, ~2^-16 relative).
 //   store:  rows of T - I (bf16, zeros above the diagonal) to the workspace, one 128-byte row per
-//           token: the A operand of Delta = X + (T - I) X in the state kernel.
+//           token with the columns in the state kernel's contraction order (tok_col): the A
+//           operand of Delta = X + (T - I) X there.
 
 #include <type_traits>
 
@@ -262,13 +263,18 @@ __global__ __launch_bounds__(kPrepNT) void gated_delta_chunk_prep_kernel(ChunkPr
   __syncthreads();
 
   // ------------------------------------------------------------------ store rows t < len
+  // Columns in the state kernel's contraction order (tok_col): the 16 bytes at columns 8p..8p+7,
+  // p = 4u + g, hold the tokens 32u + 4g + 0..3 and 32u + 16 + 4g + 0..3. A piece whose 16x16 block
+  // lies above the diagonal is zero.
 #pragma unroll
   for (int u = 0; u < kC * 8 / kPrepNT; ++u) {
-    const int e = t + u * kPrepNT, row = e >> 3, c8 = e & 7;
+    const int e = t + u * kPrepNT, row = e >> 3, p8 = e & 7;
     if (row < len) {
-      const bool upper = (c8 >> 1) > (row >> 4);  // a 16x16 block above the diagonal: zero
-      *reinterpret_cast<bf16x8*>(p.tw + ((c0 + row) * p.HV + hv) * kC + c8 * 8) =
-          upper ? bf16x8{} : *reinterpret_cast<const bf16x8*>(&Tb[row * kCP + c8 * 8]);
+      const int j0 = 32 * (p8 >> 2) + 4 * (p8 & 3), j1 = j0 + 16;
+      const bf16x4 a = (j0 >> 4) > (row >> 4) ? bf16x4{} : *reinterpret_cast<const bf16x4*>(&Tb[row * kCP + j0]);
+      const bf16x4 b = (j1 >> 4) > (row >> 4) ? bf16x4{} : *reinterpret_cast<const bf16x4*>(&Tb[row * kCP + j1]);
+      *reinterpret_cast<bf16x8*>(p.tw + ((c0 + row) * p.HV + hv) * kC + p8 * 8) =
+          bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
     }
   }
 }

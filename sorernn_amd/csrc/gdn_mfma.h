@@ -21,6 +21,13 @@ typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ bf16x8 ld8(const bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
+
+// x, with its value hidden from the optimiser: values derived from the result inside a loop are
+// computed there instead of being hoisted out of the loop and kept in registers.
+__device__ __forceinline__ int opaque_int(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
 __device__ __forceinline__ float4 ld4f(const float* p) { return *reinterpret_cast<const float4*>(p); }
 
 __device__ __forceinline__ f32x4 mma(bf16x8 a, bf16x8 b, f32x4 c) {
@@ -30,18 +37,43 @@ __device__ __forceinline__ f32x4 mma16(bf16x4 a, bf16x4 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, a), __builtin_bit_cast(i16x4, b), c, 0, 0, 0);
 }
 
-// Transposed fragment from a row-major bf16 LDS tile M (pitch in elements): lane (g, i) receives
-// M[j0 + 8g + m][c0 + i] for m = 0..7, i.e. the fragment of M^T with rows c0.. and the
-// contraction index j0.. contiguous. Each ds_read_b64_tr_b16 covers 4 rows: inside a group of 16
-// lanes, lane 4m+q reads row m at columns c0+4q..+3 and the instruction hands lane i the element
-// i%4 of lanes 4m + i/4, m = 0..3.
-__device__ __forceinline__ bf16x8 ld8_tr(const bf16* tile, int pitch, int j0, int c0, int lane) {
+// Transposed reads of a row-major bf16 LDS tile M (pitch in elements) with ds_read_b64_tr_b16.
+// The instruction works inside groups of 16 lanes: each lane supplies 4 consecutive elements
+// from its own address, and lane i receives element i % 4 of the lanes 4m + i / 4, m = 0..3.
+// When lane 4m + q of group g reads row R_g + m at columns C_q..C_q+3, lane i of the group
+// therefore receives M[R_g + m][C_{i/4} + i%4] for m = 0..3.
+//
+// ld4_tr: C_q = c0 + 4q, R_g = r0 + 4g: lane (g, i) gets M[r0 + 4g + m][c0 + i], m = 0..3 (the
+// accumulator-layout fragment of a 16 x 16 tile at (r0, c0)).
+__device__ __forceinline__ bf16x4 ld4_tr(const bf16* tile, int pitch, int r0, int c0, int lane) {
   const int g = lane >> 4, li = lane & 15;
-  const bf16* p0 = tile + (j0 + 8 * g + (li >> 2)) * pitch + c0 + 4 * (li & 3);
-  const bf16* p1 = p0 + 4 * pitch;
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+      (lds_bf16x4*)(tile + (r0 + 4 * g + (li >> 2)) * pitch + c0 + 4 * (li & 3)));
+}
+// ld8_tr_pair: C_q = c0 + 8q, rows r0 + 4g + m then r0 + 16 + 4g + m: lane (g, i) gets column
+// c0 + 8(i/4) + i%4 at rows {r0 + 4g + m, r0 + 16 + 4g + m}, m = 0..3 -- the A operand of a
+// 16x16x32 MFMA whose contraction index pairs two row tiles (16 rows apart) of M.
+__device__ __forceinline__ bf16x8 ld8_tr_pair(const bf16* tile, int pitch, int r0, int c0, int lane) {
+  const int g = lane >> 4, li = lane & 15;
+  const bf16* p0 = tile + (r0 + 4 * g + (li >> 2)) * pitch + c0 + 8 * (li & 3);
   const bf16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p0));
-  const bf16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p1));
+  const bf16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p0 + 16 * pitch));
   return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
+// Contraction order of the chunk's token index used by the state kernel: a 16x16x32 MFMA whose
+// B operand is a pair of accumulator tiles (rows 32u..32u+15 and 32u+16..32u+31) gives lane group
+// g the tokens 32u + 4g + r and 32u + 16 + 4g + r, r = 0..3. T - I and P are stored with their
+// columns in that order, so the matching A operand is one 16-byte row read: token
+// j = 32u + 16h + 4g + r sits at column 32u + 8g + 4h + r.
+__device__ __forceinline__ constexpr int tok_col(int j) {
+  return (j & ~31) + 8 * ((j >> 2) & 3) + 4 * ((j >> 4) & 1) + (j & 3);
+}
+
+// Two fp32 accumulator fragments (4 elements each) as one bf16 MFMA operand of 8
+__device__ __forceinline__ bf16x8 pack8(f32x4 a, f32x4 b) {
+  return bf16x8{static_cast<bf16>(a[0]), static_cast<bf16>(a[1]), static_cast<bf16>(a[2]), static_cast<bf16>(a[3]),
+                static_cast<bf16>(b[0]), static_cast<bf16>(b[1]), static_cast<bf16>(b[2]), static_cast<bf16>(b[3])};
 }
 
 // ---------------------------------------------------------------- raw buffer access
@@ -87,6 +119,13 @@ __device__ __forceinline__ bf16x4 to_bf16x4(float a, float b, float c, float d) 
 __device__ __forceinline__ void split4(float a, float b, float c, float d, bf16x4& hi, bf16x4& lo) {
   hi = to_bf16x4(a, b, c, d);
   lo = to_bf16x4(a - (float)hi[0], b - (float)hi[1], c - (float)hi[2], d - (float)hi[3]);
+}
+// Two fp32 accumulator fragments as the hi and lo bf16 operands of 8 (see pack8)
+__device__ __forceinline__ void split8(f32x4 a, f32x4 b, bf16x8& hi, bf16x8& lo) {
+  hi = pack8(a, b);
+  const f32x4 ra = {a[0] - (float)hi[0], a[1] - (float)hi[1], a[2] - (float)hi[2], a[3] - (float)hi[3]};
+  const f32x4 rb = {b[0] - (float)hi[4], b[1] - (float)hi[5], b[2] - (float)hi[6], b[3] - (float)hi[7]};
+  lo = pack8(ra, rb);
 }
 
 // Three-term bf16 product step for a 16x16x16 fp32 tile: acc += A(4 k) * B(4 k).
