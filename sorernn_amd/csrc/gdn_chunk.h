@@ -3,14 +3,14 @@
 // The prefill runs as two launches on the caller's stream:
 //   1. gated_delta_chunk_prep_kernel (gdn_chunk_prep.hip): for every 64-token chunk and value head,
 //      the inverse T = (I + A)^-1 of the chunk's unit lower-triangular system, written to the
-//      workspace as bf16 rows of T - I. Chunks are independent, so this kernel is fully parallel.
+//      workspace as fp16 rows of T - I. Chunks are independent, so this kernel is fully parallel.
 //   2. gated_delta_chunk_kernel (gdn_chunk.hip): the sequential state recurrence over the chunks
 //      of each sequence, reading T from the workspace.
 // With cu_seqlens, a one-block gated_delta_chunk_index_kernel first writes the number of chunks
 // before every sequence (the prep kernel's chunk -> sequence map) into the workspace.
 //
 // Workspace (caller-owned, gdn_chunk_workspace_size bytes):
-//   [0, tbytes)                T - I rows: bf16 [B*T][HV][64], row t of the chunk holding token t,
+//   [0, tbytes)                T - I rows: fp16 [B*T][HV][64], row t of the chunk holding token t,
 //                              columns in tok_col order (gdn_mfma.h)
 //   then, with cu_seqlens only: int32 chunk_first[N + 1] and int32 order[N] (256-byte aligned each)
 #pragma once
@@ -21,7 +21,7 @@ namespace gdn {
 
 struct ChunkPrepParams {
   const void *k, *g, *beta;
-  bf16* tw;                // T - I rows (workspace)
+  f16* tw;                 // T - I rows (workspace)
   const void* cu;
   const int* chunk_first;  // with cu only
   const int* order;        // with cu only: sequences by length, longest first (written by the index kernel)

@@ -14,23 +14,29 @@
 //   whole recurrence of their columns: every operand that depends on the state (S itself, X,
 //   Delta, Delta~) is an accumulator fragment used in place as the next MFMA's operand, so the
 //   state never passes through LDS. Per chunk: Y = K S, X, Delta, O^T = scale(e^gam Z^T +
-//   Delta^T P^T), the hi/lo state update, then Z^T = S^T Q^T of the next chunk (76 MFMAs).
-//   Helper waves 2-7 stage the chunk-wide operands one chunk ahead: q/k rows (waves 4-7, L2-norm
-//   when asked), T - I rows and the V slice (waves 2-3), gate terms (wave 2), the scaled P of the
-//   next chunk (waves 2, 3, 6, 7 on SIMDs 2 and 3), and store O of the previous chunk (waves 4-7).
+//   Delta^T P^T), the state update, then Z^T = S^T Q^T of the next chunk (60 MFMAs).
+//   Helper waves 2-7 stage the chunk-wide operands one chunk ahead. Waves 2, 3, 6 and 7 (SIMDs 2
+//   and 3, which hold no state wave) take the heavier work: q/k rows (L2-norm when asked, fp16
+//   conversion) and the scaled P of the next chunk. Waves 4 and 5, which share SIMDs 0 and 1 with
+//   the state waves, copy the T - I rows and the V slice, scan the gates (wave 4) and store O of
+//   the previous chunk.
 // One barrier per chunk separates the two sides.
 //
 // Fragment layouts (16x16x32 MFMA, lane (g, i), element r = 0..3 of an accumulator):
 //   S tile a = 2s + h (s = 32-deep key step): row 4g + r is key 32s + 8g + 4h + r, so the pair
-//     (S_2s, S_2s+1) in bf16 is the B operand of K S (keys 32s + 8g..+7) and the A operand of S^T Q^T;
+//     (S_2s, S_2s+1) in fp16 is the B operand of K S (keys 32s + 8g..+7) and the A operand of S^T Q^T;
 //     the K^T operand of the update reads K columns in that order (ld8_tr_pair).
 //   Y, X, Delta tile b: rows 16b + 4g + r (tokens), column i; pairs (2u, 2u+1) contract over the
 //     tokens 32u + 4g + r and 32u + 16 + 4g + r, which is the column order of T - I and P (tok_col).
 //   Z^T, O^T tile tb: row 4g + r is the wave's value column, column i the token 16tb + i.
 //
-// Precision: q/k/v are bf16, so P tiles are exact products with fp32 accumulation. S, X and Delta
-// enter MFMA as single bf16; the state update's right operand is split into bf16 hi + lo (two
-// MFMAs), which keeps the fp32 final state within 1e-3 relative L2 over 64 chunks.
+// Precision: MFMA operands are fp16 (v_mfma_f32_16x16x32_f16) with fp32 accumulation. The bf16
+// q/k (rounded to bf16 after the optional L2 norm, as the reference's bf16 pipeline holds them)
+// convert to fp16 exactly, so P and the K products are exact products; S, X, Delta and T - I enter
+// as fp16 (11-bit significand, 8x finer than bf16), which keeps the fp32 final state within about
+// 3e-4 relative L2 over 64 chunks without splitting any operand. The operands' magnitudes must
+// stay inside the fp16 range (65504): true of L2-normalised q/k, activation-scale v and the
+// states they produce.
 //
 // LDS: K (3 slots), Q (2 slots), T - I, P, V and O (2 slots each), gate terms (3 slots).
 
@@ -45,7 +51,7 @@ struct ChunkParams {
   const float* h0;
   void* o;
   float* ht;
-  const bf16* tw;  // T - I rows from the prep kernel
+  const f16* tw;  // T - I rows from the prep kernel
   const void* cu;
   const int* order;  // with cu: sequences by length, longest first
   int cu_i32;
@@ -67,12 +73,12 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
   constexpr int KS = KD / 32;                 // MFMA k-steps over the key dim
   constexpr int KT = KD / 16;                 // 16-row state tiles
   constexpr int KCH = KD / 8;                 // 16-byte chunks per q/k row
-  constexpr int QKPT = kC * KCH / 256;        // 16-byte chunks per thread of a q or k tile (waves 4-7)
+  constexpr int QKPT = kC * KCH / 256;        // 16-byte chunks per thread of a q or k tile (waves 2, 3, 6, 7)
 
-  __shared__ __align__(16) bf16 Kc[3][kC * KP];   // K of chunk c in slot c % 3
-  __shared__ __align__(16) bf16 Qc[2][kC * KP];   // Q of chunk c in slot c % 2
-  __shared__ __align__(16) bf16 Tb[2][kC * kCP];  // T - I of chunk c in slot c % 2 (tok_col columns)
-  __shared__ __align__(16) bf16 Pb[2][kC * kCP];  // scale * P of chunk c in slot c % 2 (tok_col columns)
+  __shared__ __align__(16) f16 Kc[3][kC * KP];   // K of chunk c in slot c % 3 (fp16)
+  __shared__ __align__(16) f16 Qc[2][kC * KP];   // Q of chunk c in slot c % 2 (fp16)
+  __shared__ __align__(16) f16 Tb[2][kC * kCP];  // T - I of chunk c in slot c % 2 (tok_col columns)
+  __shared__ __align__(16) f16 Pb[2][kC * kCP];  // scale * P of chunk c in slot c % 2 (tok_col columns)
   __shared__ __align__(16) bf16 Vc[2][kC * kVP];  // V slice of chunk c in slot c % 2
   __shared__ __align__(16) bf16 Ob[2][kC * kVP];  // O of chunk c, stored to HBM during chunk c + 1
   __shared__ __align__(16) ChunkGates gv[3];      // gate terms of chunk c in slot c % 3
@@ -121,83 +127,80 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
   };
 
   // ------------------------------------------------------------------ helper-side staging
-  // Each helper loads a chunk's operands into registers one chunk before it writes them to LDS, so
-  // the loads have a whole chunk step to land. All loads go through buffer resources sized to the
-  // chunk's valid rows: rows past the end (and chunks past the sequence) read as zeros.
+  // A helper issues the global loads of its tiles at the start of a chunk step and writes them to
+  // LDS at the end of the same step, so the load registers are not live across the loop (sharing
+  // loop-carried registers with the state waves' values would put register copies, and with them
+  // waits for the loads, at the loop's join point). All loads go through buffer resources sized to
+  // the chunk's valid rows: rows past the end (and chunks past the sequence) read as zeros.
   const uint32_t qk_row = (uint32_t)(p.H * KD * 2), v_row = (uint32_t)(p.HV * VD * 2), t_row = (uint32_t)(p.HV * kC * 2);
-  const int th4 = t & 255;         // waves 4-7: q/k rows, O store
-  const int th2 = (t - 128) & 127;  // waves 2-3: T - I rows, V slice
-  // Loop-carried registers, one array for both sides (a wave uses one role only):
-  //   state waves: R[0, KT) = S tiles, R[KT, KT+4) = Z^T tiles, R[KT+4, KT+4+KS) = S pairs in bf16,
-  //                R[KT+4+KS, KT+4+3KS) = the K row fragments of the next Y = K S for its first
-  //                half of key steps (read ahead across the barrier);
-  //   waves 4-7:   R[0, QKPT) = k rows, R[QKPT, 2 QKPT) = q rows in flight;
-  //   waves 2-3:   R[0, 4) = T - I rows, R[4, 6) = V rows in flight.
-  constexpr int NR = KT + 4 + 3 * KS;
-  constexpr int KSH = KS / 2;  // key steps of Y whose K fragments are read ahead
-  static_assert(2 * QKPT <= NR && 6 <= NR, "register roles");
-  f32x4 R[NR];
-  uint32_t pgraw = 0, pbraw = 0;
-  // The helpers' per-thread offsets are computed from `tq` (th4 or th2 passed through an empty asm
-  // inside the loop), so they are rebuilt in the helper branch each step instead of being hoisted
-  // out of the loop into registers that would stay live through the state waves' code.
-  // Thread tq of waves 4-7 handles the 16-byte chunks tq + 256u of a q/k tile: row tq / KCH + u (256
+  const bool qk_wave = (w & 2) != 0;  // waves 2, 3, 6, 7
+  // helper thread index of a lane value ln: 0..255 on the q/k waves, 0..127 on waves 4, 5
+  auto thq_of = [&](int ln) { return (((w >> 2) << 1) | (w & 1)) * kWave + ln; };
+  auto thv_of = [&](int ln) { return (w & 1) * kWave + ln; };
+  const int thq = thq_of(lane), thv = thv_of(lane);
+  constexpr int KSH = KS / 2;  // key steps of Y whose K fragments the state waves read ahead
+  // The helpers' per-thread offsets are computed from `tq` (thq or thv of a lane id passed through
+  // an empty asm inside the loop), so they are rebuilt in the helper branch each step instead of
+  // being hoisted out of the loop into registers that would stay live through the state waves' code.
+  // Thread tq of the q/k waves handles the 16-byte chunks tq + 256u of a q/k tile: row tq / KCH + u (256
   // / KCH), chunk tq % KCH.
-  auto fetch_rows = [&](int r0, const bf16* src, int c, int tq) {
+  auto fetch_rows = [&](bf16x8 (&dst)[QKPT], const bf16* src, int c, int tq) {
     const int64_t c0 = bos + (int64_t)c * kC;
     const auto rs = make_rsrc(src + (c0 * p.H + h) * KD, (uint32_t)chunk_len(c) * qk_row);
     const uint32_t base = (uint32_t)(tq / KCH) * qk_row + (uint32_t)(tq % KCH) * 16;
 #pragma unroll
-    for (int u = 0; u < QKPT; ++u)
-      R[r0 + u] = __builtin_bit_cast(f32x4, buf_load16(rs, base + (uint32_t)(u * (256 / KCH)) * qk_row));
+    for (int u = 0; u < QKPT; ++u) dst[u] = buf_load16(rs, base + (uint32_t)(u * (256 / KCH)) * qk_row);
   };
-  auto stage_rows = [&](int r0, bf16* dst, int tq) {
-    bf16* const d0 = dst + (tq / KCH) * KP + (tq % KCH) * 8;
+  auto stage_rows = [&](const bf16x8 (&src)[QKPT], f16* dst, int tq) {  // bf16 rows (L2-normalised when asked) -> fp16
+    f16* const d0 = dst + (tq / KCH) * KP + (tq % KCH) * 8;
 #pragma unroll
-    for (int u = 0; u < QKPT; ++u) {
-      const bf16x8 x = __builtin_bit_cast(bf16x8, R[r0 + u]);
-      *reinterpret_cast<bf16x8*>(d0 + u * (256 / KCH) * KP) = l2 ? l2norm_row_chunk<KCH>(x) : x;
-    }
+    for (int u = 0; u < QKPT; ++u)
+      *reinterpret_cast<f16x8*>(d0 + u * (256 / KCH) * KP) = bf16_to_f16x8(l2 ? l2norm_row_chunk<KCH>(src[u]) : src[u]);
   };
-  // Thread tq of waves 2-3: T - I chunks tq + 128u (row tq / 8 + 16u, 8 chunks of 16 B per row)
+  // Thread tq of waves 4-5: T - I chunks tq + 128u (row tq / 8 + 16u, 8 chunks of 16 B per row)
   // and V-slice chunks tq + 128u (row tq / 4 + 32u, 4 chunks per row).
-  auto fetch_tv = [&](int c, int tq) {
+  auto fetch_tv = [&](bf16x8 (&pt)[4], bf16x8 (&pv)[2], int c, int tq) {
     const int64_t c0 = bos + (int64_t)c * kC;
     const uint32_t len = (uint32_t)chunk_len(c);
     const auto rt = make_rsrc(p.tw + (c0 * p.HV + hv) * kC, len * t_row);
     const uint32_t bt = (uint32_t)(tq >> 3) * t_row + (uint32_t)(tq & 7) * 16;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) R[u] = __builtin_bit_cast(f32x4, buf_load16(rt, bt + (uint32_t)(16 * u) * t_row));
+    for (int u = 0; u < 4; ++u) pt[u] = buf_load16(rt, bt + (uint32_t)(16 * u) * t_row);
     const auto rv = make_rsrc(vg + (c0 * p.HV + hv) * VD + vb * kVB, len * v_row);
     const uint32_t bv = (uint32_t)(tq >> 2) * v_row + (uint32_t)(tq & 3) * 16;
 #pragma unroll
-    for (int u = 0; u < 2; ++u) R[4 + u] = __builtin_bit_cast(f32x4, buf_load16(rv, bv + (uint32_t)(32 * u) * v_row));
+    for (int u = 0; u < 2; ++u) pv[u] = buf_load16(rv, bv + (uint32_t)(32 * u) * v_row);
   };
-  auto stage_tv = [&](int slot, int tq) {
-    bf16* const t0 = Tb[slot] + (tq >> 3) * kCP + (tq & 7) * 8;
+  auto stage_tv = [&](const bf16x8 (&pt)[4], const bf16x8 (&pv)[2], int slot, int tq) {
+    f16* const t0 = Tb[slot] + (tq >> 3) * kCP + (tq & 7) * 8;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) *reinterpret_cast<f32x4*>(t0 + 16 * u * kCP) = R[u];
+    for (int u = 0; u < 4; ++u) *reinterpret_cast<bf16x8*>(t0 + 16 * u * kCP) = pt[u];  // fp16 bits, copied
     bf16* const v0 = Vc[slot] + (tq >> 2) * kVP + (tq & 3) * 8;
 #pragma unroll
-    for (int u = 0; u < 2; ++u) *reinterpret_cast<f32x4*>(v0 + 32 * u * kVP) = R[4 + u];
+    for (int u = 0; u < 2; ++u) *reinterpret_cast<bf16x8*>(v0 + 32 * u * kVP) = pv[u];
   };
-  auto fetch_gates = [&](int c) {  // wave 2, lane = token
+  auto fetch_gates = [&](int c, uint32_t& graw, uint32_t& braw) {  // wave 4, lane = token
     const int64_t c0 = bos + (int64_t)c * kC;
     const uint32_t gb = (uint32_t)(p.HV * dtype_bytes(p.dg)), bb = (uint32_t)(p.HV * dtype_bytes(p.db));
     const uint32_t len = (uint32_t)chunk_len(c);
     const auto rg = make_rsrc(static_cast<const char*>(p.g) + (c0 * p.HV + hv) * dtype_bytes(p.dg), len * gb);
     const auto rb = make_rsrc(static_cast<const char*>(p.beta) + (c0 * p.HV + hv) * dtype_bytes(p.db), len * bb);
-    pgraw = buf_load_raw32(rg, lane * gb, p.dg);
-    pbraw = buf_load_raw32(rb, lane * bb, p.db);
+    graw = buf_load_raw32(rg, lane * gb, p.dg);
+    braw = buf_load_raw32(rb, lane * bb, p.db);
   };
-  auto stage_gates = [&](int c) {
-    chunk_gates_from_raw(gv[c % 3], pgraw, pbraw, p.dg, p.db, chunk_len(c), p.flags, a_log, dt_b, lane);
+  auto stage_gates = [&](int c, uint32_t graw, uint32_t braw) {
+    // (A_log through opaque_int: its exp is recomputed here, not held in a register)
+    const float al = __int_as_float(opaque_int(__float_as_int(a_log)));
+    chunk_gates_from_raw(gv[c % 3], graw, braw, p.dg, p.db, chunk_len(c), p.flags, al, dt_b, lane);
   };
-  auto store_o = [&](int c, int tq) {  // waves 4-7: O of chunk c from Ob to HBM, 16 bytes per thread
+  auto store_o = [&](int c, int tq) {  // waves 4-5: O of chunk c from Ob to HBM, rows tq / 4 + 32u
     const int64_t c0 = bos + (int64_t)c * kC;
     const auto ro = make_rsrc(og + (c0 * p.HV + hv) * VD + vb * kVB, (uint32_t)chunk_len(c) * v_row);
     const int row = tq >> 2, c8 = tq & 3;
-    buf_store16(*reinterpret_cast<const bf16x8*>(&Ob[c & 1][row * kVP + c8 * 8]), ro, row * v_row + c8 * 16);
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+      buf_store16(*reinterpret_cast<const bf16x8*>(&Ob[c & 1][(row + 32 * u) * kVP + c8 * 8]), ro,
+                  (uint32_t)(row + 32 * u) * v_row + c8 * 16);
   };
 
   // scale * P^T of chunk c for key-row tiles JA..JA+JN-1 and query-row tiles TA..TA+TN-1 (tiles
@@ -207,9 +210,9 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
     const int li = ln & 15, g4 = ln >> 4;
     constexpr int JA = decltype(ja_c)::value, JN = decltype(jn_c)::value;
     constexpr int TA = decltype(ta_c)::value, TN = decltype(tn_c)::value;
-    const bf16* kb = Kc[c % 3];
-    const bf16* qb = Qc[c & 1];
-    bf16* pw = Pb[c & 1];
+    const f16* kb = Kc[c % 3];
+    const f16* qb = Qc[c & 1];
+    f16* pw = Pb[c & 1];
     const ChunkGates& gs = gv[c % 3];
     f32x4 acc[JN][TN];
 #pragma unroll
@@ -218,16 +221,16 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
       for (int b = 0; b < TN; ++b) acc[a][b] = f32x4{};
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
-      bf16x8 fk[JN], fq[TN];
+      f16x8 fk[JN], fq[TN];
 #pragma unroll
-      for (int a = 0; a < JN; ++a) fk[a] = ld8(kb + (16 * (JA + a) + li) * KP + 32 * s + 8 * g4);
+      for (int a = 0; a < JN; ++a) fk[a] = ld8h(kb + (16 * (JA + a) + li) * KP + 32 * s + 8 * g4);
 #pragma unroll
-      for (int b = 0; b < TN; ++b) fq[b] = ld8(qb + (16 * (TA + b) + li) * KP + 32 * s + 8 * g4);
+      for (int b = 0; b < TN; ++b) fq[b] = ld8h(qb + (16 * (TA + b) + li) * KP + 32 * s + 8 * g4);
 #pragma unroll
       for (int a = 0; a < JN; ++a)
 #pragma unroll
         for (int b = 0; b < TN; ++b)
-          if (JA + a <= TA + b) acc[a][b] = mma(fk[a], fq[b], acc[a][b]);
+          if (JA + a <= TA + b) acc[a][b] = mmah(fk[a], fq[b], acc[a][b]);
     }
 #pragma unroll
     for (int a = 0; a < JN; ++a)
@@ -242,7 +245,7 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
         float val[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) val[r] = (jt < tt_ || j0 + r <= tt) ? p.scale * __expf(gt - gjv[r]) * acc[a][b][r] : 0.f;
-        *reinterpret_cast<bf16x4*>(pw + tt * kCP + tok_col(j0)) = to_bf16x4(val[0], val[1], val[2], val[3]);
+        *reinterpret_cast<f16x4*>(pw + tt * kCP + tok_col(j0)) = to_f16x4(val[0], val[1], val[2], val[3]);
       }
   };
   using I0 = std::integral_constant<int, 0>;
@@ -261,24 +264,23 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
 
   // ------------------------------------------------------------------ state-side registers
   const int sw = w & 1;  // state wave 0 or 1: value columns 16 sw .. 16 sw + 15 of the slice
-  // S tile a = R[a]; Z^T = S^T Q^T of the current chunk, tile tb = R[KT + tb] (value column 4g + r,
-  // token 16tb + i); (S_2s, S_2s+1) in bf16 = R[KT + 4 + s]
-  f32x4* const S = R;
-  f32x4* const Zt = R + KT;
-  auto sb = [&](int s) { return __builtin_bit_cast(bf16x8, R[KT + 4 + s]); };
+  // Loop-carried: S tiles; Z^T = S^T Q^T of the current chunk, tile tb (value column 4g + r, token
+  // 16tb + i); (S_2s, S_2s+1) in fp16 (SB); the K row fragments of the next Y = K S for its first
+  // KSH key steps (KF, read ahead across the barrier).
+  f32x4 S[KT], Zt[4], SB[KS], KF[4 * KSH];
+  auto sb = [&](int s) { return __builtin_bit_cast(f16x8, SB[s]); };
   const int64_t sbase = (n * p.HV + hv) * (int64_t)KD * VD + vb * kVB + 16 * sw;
   auto make_sb = [&]() {
 #pragma unroll
-    for (int s = 0; s < KS; ++s) R[KT + 4 + s] = __builtin_bit_cast(f32x4, pack8(S[2 * s], S[2 * s + 1]));
+    for (int s = 0; s < KS; ++s) SB[s] = __builtin_bit_cast(f32x4, pack8h(S[2 * s], S[2 * s + 1]));
   };
-  // K row fragments of Y = K S for chunk c, key steps s < KSH (row tile b), read ahead into R
-  f32x4* const KF = R + KT + 4 + KS;
+  // K row fragments of Y = K S for chunk c, key steps s < KSH (row tile b), read ahead
   auto load_kf = [&](int c) {
-    const bf16* kb = Kc[c % 3];
+    const f16* kb = Kc[c % 3];
 #pragma unroll
     for (int s = 0; s < KSH; ++s)
 #pragma unroll
-      for (int b = 0; b < 4; ++b) KF[4 * s + b] = __builtin_bit_cast(f32x4, ld8(kb + (16 * b + li) * KP + 32 * s + 8 * g4));
+      for (int b = 0; b < 4; ++b) KF[4 * s + b] = __builtin_bit_cast(f32x4, ld8h(kb + (16 * b + li) * KP + 32 * s + 8 * g4));
   };
   // Each phase of the state step issues the LDS reads of the next phase before its own MFMAs, and
   // the scheduler may not move instructions across the phase boundaries: LDS reads complete in
@@ -288,8 +290,8 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
   // ------------------------------------------------------------------ prologue
   // P is causally lower: its tiles above the diagonal stay zero for the whole run
   for (int e = t; e < kC * kCP / 8; e += kNT) {
-    reinterpret_cast<bf16x8*>(Pb[0])[e] = bf16x8{};
-    reinterpret_cast<bf16x8*>(Pb[1])[e] = bf16x8{};
+    reinterpret_cast<f16x8*>(Pb[0])[e] = f16x8{};
+    reinterpret_cast<f16x8*>(Pb[1])[e] = f16x8{};
   }
   if (w < 2) {
 #pragma unroll
@@ -299,44 +301,41 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
       for (int r = 0; r < 4; ++r) S[a][r] = p.h0 ? p.h0[sbase + (int64_t)(kd0 + r) * VD + li] : 0.f;
     }
     make_sb();
-  } else if (w >= 4) {  // K/Q of chunks 0 and 1 staged, chunk 2 in flight
-    fetch_rows(0, kg, 0, th4);
-    fetch_rows(QKPT, qg, 0, th4);
-    stage_rows(0, Kc[0], th4);
-    stage_rows(QKPT, Qc[0], th4);
-    fetch_rows(0, kg, 1, th4);
-    fetch_rows(QKPT, qg, 1, th4);
-    stage_rows(0, Kc[1], th4);
-    stage_rows(QKPT, Qc[1], th4);
-    fetch_rows(0, kg, 2, th4);
-    fetch_rows(QKPT, qg, 2, th4);
-  } else {  // T/V of chunk 0 staged, chunk 1 in flight; gates of chunks 0, 1 staged, chunk 2 in flight
-    fetch_tv(0, th2);
-    stage_tv(0, th2);
-    fetch_tv(1, th2);
-    if (w == 2) {
-      fetch_gates(0);
-      stage_gates(0);
-      fetch_gates(1);
-      stage_gates(1);
-      fetch_gates(2);
+  } else if (qk_wave) {  // K/Q of chunks 0 and 1
+    bf16x8 pk[QKPT], pq[QKPT];
+    for (int c = 0; c < 2; ++c) {
+      fetch_rows(pk, kg, c, thq);
+      fetch_rows(pq, qg, c, thq);
+      stage_rows(pk, Kc[c], thq);
+      stage_rows(pq, Qc[c], thq);
+    }
+  } else {  // T/V of chunk 0, gates of chunks 0 and 1
+    bf16x8 pt[4], pv[2];
+    fetch_tv(pt, pv, 0, thv);
+    stage_tv(pt, pv, 0, thv);
+    if (w == 4) {
+      for (int c = 0; c < 2; ++c) {
+        uint32_t graw, braw;
+        fetch_gates(c, graw, braw);
+        stage_gates(c, graw, braw);
+      }
     }
   }
   __syncthreads();
   if (nc > 0) {
     if (w < 2) {
-      bf16x8 qf[KS][4];
+      f16x8 qf[KS][4];
 #pragma unroll
       for (int s2 = 0; s2 < KS; ++s2)
 #pragma unroll
-        for (int tb = 0; tb < 4; ++tb) qf[s2][tb] = ld8(Qc[0] + (16 * tb + li) * KP + 32 * s2 + 8 * g4);
+        for (int tb = 0; tb < 4; ++tb) qf[s2][tb] = ld8h(Qc[0] + (16 * tb + li) * KP + 32 * s2 + 8 * g4);
       load_kf(0);
 #pragma unroll
       for (int tb = 0; tb < 4; ++tb) Zt[tb] = f32x4{};
 #pragma unroll
       for (int s2 = 0; s2 < KS; ++s2)
 #pragma unroll
-        for (int tb = 0; tb < 4; ++tb) Zt[tb] = mma(sb(s2), qf[s2][tb], Zt[tb]);
+        for (int tb = 0; tb < 4; ++tb) Zt[tb] = mmah(sb(s2), qf[s2][tb], Zt[tb]);
     } else {
       run_p_side(0, lane);
     }
@@ -349,20 +348,20 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
   // T_{i+1}, V_{i+1}, P_{i+1}, gates_{i+2}. No slot is written and read in the same step.
   for (int i = 0; i < nc; ++i) {
     if (w < 2) {
-      const bf16* kb = Kc[i % 3];
-      const bf16* tp = Tb[i & 1];
+      const f16* kb = Kc[i % 3];
+      const f16* tp = Tb[i & 1];
       const bf16* vp = Vc[i & 1];
-      const bf16* pp = Pb[i & 1];
+      const f16* pp = Pb[i & 1];
       bf16* op = Ob[i & 1];
       const ChunkGates& G = gv[i % 3];
 
       // ---- 1: K reads for the second half of Y and the reads for X (V, beta, beta e^gam); Y = K S
       //      starts on the fragments read ahead in the previous step
-      bf16x8 kf2[KS - KSH][4];
+      f16x8 kf2[KS - KSH][4];
 #pragma unroll
       for (int s2 = KSH; s2 < KS; ++s2)
 #pragma unroll
-        for (int b = 0; b < 4; ++b) kf2[s2 - KSH][b] = ld8(kb + (16 * b + li) * KP + 32 * s2 + 8 * g4);
+        for (int b = 0; b < 4; ++b) kf2[s2 - KSH][b] = ld8h(kb + (16 * b + li) * KP + 32 * s2 + 8 * g4);
       bf16x4 vv[4];
       float4 bt[4], bg[4];
 #pragma unroll
@@ -379,16 +378,16 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
       for (int s2 = 0; s2 < KS; ++s2)
 #pragma unroll
         for (int b = 0; b < 4; ++b)
-          D[b] = mma(s2 < KSH ? __builtin_bit_cast(bf16x8, KF[4 * s2 + b]) : kf2[s2 - KSH][b], sb(s2), D[b]);
+          D[b] = mmah(s2 < KSH ? __builtin_bit_cast(f16x8, KF[4 * s2 + b]) : kf2[s2 - KSH][b], sb(s2), D[b]);
       phase();
       // ---- 2: reads of T - I; X = beta V - beta e^gam Y (kept in fp32 as the Delta accumulator's start)
-      bf16x8 tf[6];
-      tf[0] = ld8(tp + li * kCP + 8 * g4);
-      tf[1] = ld8(tp + (16 + li) * kCP + 8 * g4);
-      tf[2] = ld8(tp + (32 + li) * kCP + 8 * g4);
-      tf[3] = ld8(tp + (48 + li) * kCP + 8 * g4);
-      tf[4] = ld8(tp + (32 + li) * kCP + 32 + 8 * g4);
-      tf[5] = ld8(tp + (48 + li) * kCP + 32 + 8 * g4);
+      f16x8 tf[6];
+      tf[0] = ld8h(tp + li * kCP + 8 * g4);
+      tf[1] = ld8h(tp + (16 + li) * kCP + 8 * g4);
+      tf[2] = ld8h(tp + (32 + li) * kCP + 8 * g4);
+      tf[3] = ld8h(tp + (48 + li) * kCP + 8 * g4);
+      tf[4] = ld8h(tp + (32 + li) * kCP + 32 + 8 * g4);
+      tf[5] = ld8h(tp + (48 + li) * kCP + 32 + 8 * g4);
       phase();
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
@@ -397,16 +396,16 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
         D[b][2] = bt[b].z * (float)vv[b][2] - bg[b].z * D[b][2];
         D[b][3] = bt[b].w * (float)vv[b][3] - bg[b].w * D[b][3];
       }
-      const bf16x8 xb0 = pack8(D[0], D[1]), xb1 = pack8(D[2], D[3]);
+      const f16x8 xb0 = pack8h(D[0], D[1]), xb1 = pack8h(D[2], D[3]);
       phase();
       // ---- 3: reads of P, e^{gam_c - gam}, scale e^gam; Delta = X + (T - I) X (T - I vanishes above the diagonal)
-      bf16x8 pf[6];
+      f16x8 pf[6];
       float4 dla[2], dlb[2];
       float eg[4];
 #pragma unroll
-      for (int tb = 0; tb < 4; ++tb) pf[tb] = ld8(pp + (16 * tb + li) * kCP + 8 * g4);
-      pf[4] = ld8(pp + (32 + li) * kCP + 32 + 8 * g4);
-      pf[5] = ld8(pp + (48 + li) * kCP + 32 + 8 * g4);
+      for (int tb = 0; tb < 4; ++tb) pf[tb] = ld8h(pp + (16 * tb + li) * kCP + 8 * g4);
+      pf[4] = ld8h(pp + (32 + li) * kCP + 32 + 8 * g4);
+      pf[5] = ld8h(pp + (48 + li) * kCP + 32 + 8 * g4);
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         dla[u] = ld4f(&G.dlast[32 * u + 4 * g4]);
@@ -416,75 +415,69 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
       for (int tb = 0; tb < 4; ++tb) eg[tb] = G.egam[16 * tb + li];
       const float ec = __expf(G.gam[kC - 1]);
       phase();
-      D[0] = mma(tf[0], xb0, D[0]);
-      D[1] = mma(tf[1], xb0, D[1]);
-      D[2] = mma(tf[2], xb0, D[2]);
-      D[3] = mma(tf[3], xb0, D[3]);
-      D[2] = mma(tf[4], xb1, D[2]);
-      D[3] = mma(tf[5], xb1, D[3]);
-      const bf16x8 db0 = pack8(D[0], D[1]), db1 = pack8(D[2], D[3]);
+      D[0] = mmah(tf[0], xb0, D[0]);
+      D[1] = mmah(tf[1], xb0, D[1]);
+      D[2] = mmah(tf[2], xb0, D[2]);
+      D[3] = mmah(tf[3], xb0, D[3]);
+      D[2] = mmah(tf[4], xb1, D[2]);
+      D[3] = mmah(tf[5], xb1, D[3]);
+      const f16x8 db0 = pack8h(D[0], D[1]), db1 = pack8h(D[2], D[3]);
       phase();
       // ---- 4: K^T reads for the first half of the state tiles; O^T = scale e^gam Z^T + Delta^T
-      //      (scale P)^T -> Ob[token][column]; Delta~ = e^{gam_c - gam} Delta as bf16 hi + lo
+      //      (scale P)^T -> Ob[token][column]; Delta~ = e^{gam_c - gam} Delta in fp16
       constexpr int KH = KT / 2;
-      bf16x8 ktf[KT][2];
+      f16x8 ktf[KT][2];
 #pragma unroll
       for (int a = 0; a < KH; ++a)
 #pragma unroll
-        for (int u = 0; u < 2; ++u) ktf[a][u] = ld8_tr_pair(kb, KP, 32 * u, 32 * (a >> 1) + 4 * (a & 1), lane);
+        for (int u = 0; u < 2; ++u) ktf[a][u] = ld8h_tr_pair(kb, KP, 32 * u, 32 * (a >> 1) + 4 * (a & 1), lane);
       phase();
 #pragma unroll
       for (int tb = 0; tb < 4; ++tb) {
         f32x4 o = Zt[tb] * (p.scale * eg[tb]);
-        o = mma(db0, pf[tb], o);
-        if (tb >= 2) o = mma(db1, pf[tb + 2], o);
+        o = mmah(db0, pf[tb], o);
+        if (tb >= 2) o = mmah(db1, pf[tb + 2], o);
         *reinterpret_cast<bf16x4*>(op + (16 * tb + li) * kVP + 16 * sw + 4 * g4) = to_bf16x4(o[0], o[1], o[2], o[3]);
       }
-      bf16x8 dh[2], dl[2];
+      f16x8 dt[2];
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         const f32x4 x0 = {dla[u].x * D[2 * u][0], dla[u].y * D[2 * u][1], dla[u].z * D[2 * u][2], dla[u].w * D[2 * u][3]};
         const f32x4 x1 = {dlb[u].x * D[2 * u + 1][0], dlb[u].y * D[2 * u + 1][1], dlb[u].z * D[2 * u + 1][2],
                           dlb[u].w * D[2 * u + 1][3]};
-        split8(x0, x1, dh[u], dl[u]);
+        dt[u] = pack8h(x0, x1);
       }
       phase();
       // ---- 5: K^T reads for the second half; S' = e^{gam_c} S + K^T Delta~ on the first half
 #pragma unroll
       for (int a = KH; a < KT; ++a)
 #pragma unroll
-        for (int u = 0; u < 2; ++u) ktf[a][u] = ld8_tr_pair(kb, KP, 32 * u, 32 * (a >> 1) + 4 * (a & 1), lane);
+        for (int u = 0; u < 2; ++u) ktf[a][u] = ld8h_tr_pair(kb, KP, 32 * u, 32 * (a >> 1) + 4 * (a & 1), lane);
       phase();
 #pragma unroll
       for (int a = 0; a < KH; ++a) {
         S[a] *= ec;
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          S[a] = mma(ktf[a][u], dh[u], S[a]);
-          S[a] = mma(ktf[a][u], dl[u], S[a]);
-        }
+        for (int u = 0; u < 2; ++u) S[a] = mmah(ktf[a][u], dt[u], S[a]);
       }
       phase();
       // ---- 6: Q reads of the next chunk (first half of the key steps); the second half of the
       //      update; S in bf16
       const bool more = i + 1 < nc;
-      const bf16* qb = Qc[(i + 1) & 1];
-      bf16x8 qf[KS][4];
+      const f16* qb = Qc[(i + 1) & 1];
+      f16x8 qf[KS][4];
       if (more) {
 #pragma unroll
         for (int s2 = 0; s2 < KSH; ++s2)
 #pragma unroll
-          for (int tb = 0; tb < 4; ++tb) qf[s2][tb] = ld8(qb + (16 * tb + li) * KP + 32 * s2 + 8 * g4);
+          for (int tb = 0; tb < 4; ++tb) qf[s2][tb] = ld8h(qb + (16 * tb + li) * KP + 32 * s2 + 8 * g4);
       }
       phase();
 #pragma unroll
       for (int a = KH; a < KT; ++a) {
         S[a] *= ec;
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          S[a] = mma(ktf[a][u], dh[u], S[a]);
-          S[a] = mma(ktf[a][u], dl[u], S[a]);
-        }
+        for (int u = 0; u < 2; ++u) S[a] = mmah(ktf[a][u], dt[u], S[a]);
       }
       make_sb();
       phase();
@@ -493,7 +486,7 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
 #pragma unroll
         for (int s2 = KSH; s2 < KS; ++s2)
 #pragma unroll
-          for (int tb = 0; tb < 4; ++tb) qf[s2][tb] = ld8(qb + (16 * tb + li) * KP + 32 * s2 + 8 * g4);
+          for (int tb = 0; tb < 4; ++tb) qf[s2][tb] = ld8h(qb + (16 * tb + li) * KP + 32 * s2 + 8 * g4);
         load_kf(i + 1);
         phase();
 #pragma unroll
@@ -501,27 +494,29 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
 #pragma unroll
         for (int s2 = 0; s2 < KS; ++s2)
 #pragma unroll
-          for (int tb = 0; tb < 4; ++tb) Zt[tb] = mma(sb(s2), qf[s2][tb], Zt[tb]);
+          for (int tb = 0; tb < 4; ++tb) Zt[tb] = mmah(sb(s2), qf[s2][tb], Zt[tb]);
       }
-    } else if (w >= 4) {
-      const int tq = opaque_int(th4);
+    } else if (qk_wave) {  // K/Q of chunk i+2 (loads first, P of chunk i+1 while they land)
+      const int tq = thq_of(opaque_int(lane));
+      bf16x8 pk[QKPT], pq[QKPT];
+      fetch_rows(pk, kg, i + 2, tq);
+      fetch_rows(pq, qg, i + 2, tq);
+      if (i + 1 < nc) run_p_side(i + 1, opaque_int(lane));
+      stage_rows(pk, Kc[(i + 2) % 3], tq);
+      stage_rows(pq, Qc[i & 1], tq);
+    } else {  // T/V of chunk i+1, gates of chunk i+2, O of chunk i-1 out
+      const int tq = thv_of(opaque_int(lane));
+      bf16x8 pt[4], pv[2];
+      uint32_t graw = 0, braw = 0;
+      fetch_tv(pt, pv, i + 1, tq);
+      if (w == 4) fetch_gates(i + 2, graw, braw);
       if (i > 0) store_o(i - 1, tq);
-      stage_rows(0, Kc[(i + 2) % 3], tq);
-      stage_rows(QKPT, Qc[i & 1], tq);
-      fetch_rows(0, kg, i + 3, tq);
-      fetch_rows(QKPT, qg, i + 3, tq);
-      if (i + 1 < nc) run_p_side(i + 1, opaque_int(lane));
-    } else {
-      const int tq = opaque_int(th2);
-      stage_tv((i + 1) & 1, tq);
-      if (w == 2) stage_gates(i + 2);
-      fetch_tv(i + 2, tq);
-      if (w == 2) fetch_gates(i + 3);
-      if (i + 1 < nc) run_p_side(i + 1, opaque_int(lane));
+      stage_tv(pt, pv, (i + 1) & 1, tq);
+      if (w == 4) stage_gates(i + 2, graw, braw);
     }
     __syncthreads();
   }
-  if (w >= 4 && nc > 0) store_o(nc - 1, th4);
+  if (w >= 4 && !qk_wave && nc > 0) store_o(nc - 1, thv);
 
   if (p.ht && w < 2) {
 #pragma unroll
@@ -590,7 +585,7 @@ extern "C" int gdn_chunk_fwd(const void* q, const void* k, const void* v, const 
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int cu_i32 = (flags & GDN_FLAG_CU_INT32) ? 1 : 0;
-  bf16* tw = static_cast<bf16*>(workspace);
+  f16* tw = static_cast<f16*>(workspace);
   char* const ws = static_cast<char*>(workspace);
   const int* chunk_first = cu_seqlens ? reinterpret_cast<const int*>(ws + chunk_t_bytes(B * T, HV)) : nullptr;
   const int* order =

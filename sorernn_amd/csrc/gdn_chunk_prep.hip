@@ -13,7 +13,7 @@
 //           forward substitution on 64 lanes (fp32).
 //   merge:  T_{2q+1,2q} = -T_{2q+1,2q+1} A_{2q+1,2q} T_{2q,2q} (16 -> 32), then the 32 -> 64
 //           block, with three-term bf16 products (hi*hi + hi*lo + lo*hi, ~2^-16 relative).
-//   store:  rows of T - I (bf16, zeros above the diagonal) to the workspace, one 128-byte row per
+//   store:  rows of T - I (fp16, zeros above the diagonal) to the workspace, one 128-byte row per
 //           token with the columns in the state kernel's contraction order (tok_col): the A
 //           operand of Delta = X + (T - I) X there.
 
@@ -37,7 +37,7 @@ __global__ __launch_bounds__(kPrepNT) void gated_delta_chunk_prep_kernel(ChunkPr
   //   Ad  diagonal A blocks: Ad[b][(4m + k) * 4 + q] = A[16b+4q+k][16b+m]
   //   Ao  A rows 16..63 x cols 0..47 (the off-diagonal lower blocks)
   //   Tf  T[0:32][0:32] and T[32:64][32:64] in fp32
-  //   Tb  T - I in bf16 [t][j] (blocks above the diagonal are never written: the store zero-fills them)
+  //   Tb  T - I in fp16 [t][j] (blocks above the diagonal are never written: the store zero-fills them)
   constexpr int kAdB = 4 * 256 * 4, kAoB = 48 * kAoP * 4, kTfB = 2 * 32 * kTfP * 4, kTbB = kC * kCP * 2;
   constexpr int kSolveB = kAdB + kAoB + kTfB + kTbB, kKcB = kC * KP * 2;
   __shared__ __align__(16) char smem[kSolveB > kKcB ? kSolveB : kKcB];
@@ -46,7 +46,7 @@ __global__ __launch_bounds__(kPrepNT) void gated_delta_chunk_prep_kernel(ChunkPr
   float(*const Ad)[256] = reinterpret_cast<float(*)[256]>(smem);
   float* const Ao = reinterpret_cast<float*>(smem + kAdB);
   float(*const Tf)[32 * kTfP] = reinterpret_cast<float(*)[32 * kTfP]>(smem + kAdB + kAoB);
-  bf16* const Tb = reinterpret_cast<bf16*>(smem + kAdB + kAoB + kTfB);
+  f16* const Tb = reinterpret_cast<f16*>(smem + kAdB + kAoB + kTfB);
 
   const int t = threadIdx.x, lane = t & 63, w = t >> 6, g4 = lane >> 4, li = lane & 15;
   const int hv = blockIdx.y;
@@ -168,12 +168,12 @@ __global__ __launch_bounds__(kPrepNT) void gated_delta_chunk_prep_kernel(ChunkPr
       x[3] -= a4m[m].w * xm;
     }
     float* tf = &Tf[rk >> 1][(16 * (rk & 1)) * kTfP + 16 * (rk & 1) + col];
-    bf16* tb = &Tb[(16 * rk) * kCP + 16 * rk + col];
+    f16* tb = &Tb[(16 * rk) * kCP + 16 * rk + col];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int rr = 4 * q + kq;
       tf[rr * kTfP] = x[q];
-      tb[rr * kCP] = static_cast<bf16>(rr == col ? 0.f : x[q]);
+      tb[rr * kCP] = static_cast<f16>(rr == col ? 0.f : x[q]);
     }
   };
   switch (w) {
@@ -215,11 +215,11 @@ __global__ __launch_bounds__(kPrepNT) void gated_delta_chunk_prep_kernel(ChunkPr
       acc2 = mma16x3(a, b, acc2);
     }
     float* tw = &Tf[q][16 * kTfP];
-    bf16* tbw = &Tb[(32 * q + 16) * kCP + 32 * q];
+    f16* tbw = &Tb[(32 * q + 16) * kCP + 32 * q];
 #pragma unroll
     for (int ii = 0; ii < 4; ++ii) {
       tw[(4 * g4 + ii) * kTfP + li] = -acc2[ii];
-      tbw[(4 * g4 + ii) * kCP + li] = static_cast<bf16>(-acc2[ii]);
+      tbw[(4 * g4 + ii) * kCP + li] = static_cast<f16>(-acc2[ii]);
     }
   }
   __syncthreads();
@@ -255,9 +255,9 @@ __global__ __launch_bounds__(kPrepNT) void gated_delta_chunk_prep_kernel(ChunkPr
         a[0] = ar[0]; a[1] = ar[1]; a[2] = ar[2]; a[3] = ar[3];
         acc = mma16x3(a, b, acc);
       }
-      bf16* tbw = &Tb[(32 + 16 * rt) * kCP + 16 * ct];
+      f16* tbw = &Tb[(32 + 16 * rt) * kCP + 16 * ct];
 #pragma unroll
-      for (int ii = 0; ii < 4; ++ii) tbw[(4 * g4 + ii) * kCP + li] = static_cast<bf16>(-acc[ii]);
+      for (int ii = 0; ii < 4; ++ii) tbw[(4 * g4 + ii) * kCP + li] = static_cast<f16>(-acc[ii]);
     }
   }
   __syncthreads();
@@ -271,10 +271,10 @@ __global__ __launch_bounds__(kPrepNT) void gated_delta_chunk_prep_kernel(ChunkPr
     const int e = t + u * kPrepNT, row = e >> 3, p8 = e & 7;
     if (row < len) {
       const int j0 = 32 * (p8 >> 2) + 4 * (p8 & 3), j1 = j0 + 16;
-      const bf16x4 a = (j0 >> 4) > (row >> 4) ? bf16x4{} : *reinterpret_cast<const bf16x4*>(&Tb[row * kCP + j0]);
-      const bf16x4 b = (j1 >> 4) > (row >> 4) ? bf16x4{} : *reinterpret_cast<const bf16x4*>(&Tb[row * kCP + j1]);
-      *reinterpret_cast<bf16x8*>(p.tw + ((c0 + row) * p.HV + hv) * kC + p8 * 8) =
-          bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+      const f16x4 a = (j0 >> 4) > (row >> 4) ? f16x4{} : *reinterpret_cast<const f16x4*>(&Tb[row * kCP + j0]);
+      const f16x4 b = (j1 >> 4) > (row >> 4) ? f16x4{} : *reinterpret_cast<const f16x4*>(&Tb[row * kCP + j1]);
+      *reinterpret_cast<f16x8*>(p.tw + ((c0 + row) * p.HV + hv) * kC + p8 * 8) =
+          f16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
     }
   }
 }

@@ -33,6 +33,10 @@ __device__ __forceinline__ float4 ld4f(const float* p) { return *reinterpret_cas
 __device__ __forceinline__ f32x4 mma(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
+__device__ __forceinline__ f32x4 mmah(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f16x8 ld8h(const f16* p) { return *reinterpret_cast<const f16x8*>(p); }
 __device__ __forceinline__ f32x4 mma16(bf16x4 a, bf16x4 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, a), __builtin_bit_cast(i16x4, b), c, 0, 0, 0);
 }
@@ -61,6 +65,10 @@ __device__ __forceinline__ bf16x8 ld8_tr_pair(const bf16* tile, int pitch, int r
   return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
 
+__device__ __forceinline__ f16x8 ld8h_tr_pair(const f16* tile, int pitch, int r0, int c0, int lane) {
+  return __builtin_bit_cast(f16x8, ld8_tr_pair(reinterpret_cast<const bf16*>(tile), pitch, r0, c0, lane));
+}
+
 // Contraction order of the chunk's token index used by the state kernel: a 16x16x32 MFMA whose
 // B operand is a pair of accumulator tiles (rows 32u..32u+15 and 32u+16..32u+31) gives lane group
 // g the tokens 32u + 4g + r and 32u + 16 + 4g + r, r = 0..3. T - I and P are stored with their
@@ -70,10 +78,21 @@ __device__ __forceinline__ constexpr int tok_col(int j) {
   return (j & ~31) + 8 * ((j >> 2) & 3) + 4 * ((j >> 4) & 1) + (j & 3);
 }
 
-// Two fp32 accumulator fragments (4 elements each) as one bf16 MFMA operand of 8
+// Two fp32 accumulator fragments (4 elements each) as one bf16 / fp16 MFMA operand of 8
 __device__ __forceinline__ bf16x8 pack8(f32x4 a, f32x4 b) {
   return bf16x8{static_cast<bf16>(a[0]), static_cast<bf16>(a[1]), static_cast<bf16>(a[2]), static_cast<bf16>(a[3]),
                 static_cast<bf16>(b[0]), static_cast<bf16>(b[1]), static_cast<bf16>(b[2]), static_cast<bf16>(b[3])};
+}
+__device__ __forceinline__ f16x8 pack8h(f32x4 a, f32x4 b) {
+  return f16x8{static_cast<f16>(a[0]), static_cast<f16>(a[1]), static_cast<f16>(a[2]), static_cast<f16>(a[3]),
+               static_cast<f16>(b[0]), static_cast<f16>(b[1]), static_cast<f16>(b[2]), static_cast<f16>(b[3])};
+}
+// bf16 -> fp16, exact for magnitudes in [2^-14, 65504]
+__device__ __forceinline__ f16x8 bf16_to_f16x8(bf16x8 x) {
+  f16x8 r;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r[i] = static_cast<f16>(static_cast<float>(x[i]));
+  return r;
 }
 
 // ---------------------------------------------------------------- raw buffer access
@@ -113,6 +132,9 @@ __device__ __forceinline__ float quad_bcast(float x, int q) {
 
 __device__ __forceinline__ bf16x4 to_bf16x4(float a, float b, float c, float d) {
   return bf16x4{static_cast<bf16>(a), static_cast<bf16>(b), static_cast<bf16>(c), static_cast<bf16>(d)};
+}
+__device__ __forceinline__ f16x4 to_f16x4(float a, float b, float c, float d) {
+  return f16x4{static_cast<f16>(a), static_cast<f16>(b), static_cast<f16>(c), static_cast<f16>(d)};
 }
 
 // fp32 x4 -> bf16 hi and lo parts (x ~= hi + lo to about 2^-16 relative)
