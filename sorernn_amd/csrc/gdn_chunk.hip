@@ -355,8 +355,13 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
       bf16* op = Ob[i & 1];
       const ChunkGates& G = gv[i % 3];
 
-      // ---- 1: K reads for the second half of Y and the reads for X (V, beta, beta e^gam); Y = K S
-      //      starts on the fragments read ahead in the previous step
+      // The chain S -> Y -> X -> Delta -> Delta~ -> S' runs through phases 1-5; the rest is placed
+      // where it overlaps the chain's MFMAs: the e^{gam_c} scaling of S under Y, and O of this chunk
+      // with Z^T of the next under phase 6. Phases 5 and 6 run unconditionally: after the last chunk
+      // they read slots holding stale tiles and compute values nobody uses, which keeps the step
+      // free of branches (a branch around loads costs the register allocator dearly here).
+      // ---- 1: reads for Y's second half and for X (V, beta, beta e^gam); Y = K S from the
+      //      fragments read ahead in the previous step; S *= e^{gam_c} (Y used S in fp16)
       f16x8 kf2[KS - KSH][4];
 #pragma unroll
       for (int s2 = KSH; s2 < KS; ++s2)
@@ -370,6 +375,7 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
         bt[b] = ld4f(&G.bet[16 * b + 4 * g4]);
         bg[b] = ld4f(&G.begam[16 * b + 4 * g4]);
       }
+      const float ec = __expf(G.gam[kC - 1]);
       phase();
       f32x4 D[4];
 #pragma unroll
@@ -379,6 +385,8 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
 #pragma unroll
         for (int b = 0; b < 4; ++b)
           D[b] = mmah(s2 < KSH ? __builtin_bit_cast(f16x8, KF[4 * s2 + b]) : kf2[s2 - KSH][b], sb(s2), D[b]);
+#pragma unroll
+      for (int a = 0; a < KT; ++a) S[a] *= ec;
       phase();
       // ---- 2: reads of T - I; X = beta V - beta e^gam Y (kept in fp32 as the Delta accumulator's start)
       f16x8 tf[6];
@@ -398,22 +406,20 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
       }
       const f16x8 xb0 = pack8h(D[0], D[1]), xb1 = pack8h(D[2], D[3]);
       phase();
-      // ---- 3: reads of P, e^{gam_c - gam}, scale e^gam; Delta = X + (T - I) X (T - I vanishes above the diagonal)
-      f16x8 pf[6];
+      // ---- 3: reads of e^{gam_c - gam} and of K^T for the first half of the state tiles;
+      //      Delta = X + (T - I) X (T - I vanishes above the diagonal); Delta~ = e^{gam_c - gam} Delta
+      constexpr int KH = KT / 2;
       float4 dla[2], dlb[2];
-      float eg[4];
-#pragma unroll
-      for (int tb = 0; tb < 4; ++tb) pf[tb] = ld8h(pp + (16 * tb + li) * kCP + 8 * g4);
-      pf[4] = ld8h(pp + (32 + li) * kCP + 32 + 8 * g4);
-      pf[5] = ld8h(pp + (48 + li) * kCP + 32 + 8 * g4);
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         dla[u] = ld4f(&G.dlast[32 * u + 4 * g4]);
         dlb[u] = ld4f(&G.dlast[32 * u + 16 + 4 * g4]);
       }
+      f16x8 ktf[KT][2];
 #pragma unroll
-      for (int tb = 0; tb < 4; ++tb) eg[tb] = G.egam[16 * tb + li];
-      const float ec = __expf(G.gam[kC - 1]);
+      for (int a = 0; a < KH; ++a)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) ktf[a][u] = ld8h_tr_pair(kb, KP, 32 * u, 32 * (a >> 1) + 4 * (a & 1), lane);
       phase();
       D[0] = mmah(tf[0], xb0, D[0]);
       D[1] = mmah(tf[1], xb0, D[1]);
@@ -421,24 +427,6 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
       D[3] = mmah(tf[3], xb0, D[3]);
       D[2] = mmah(tf[4], xb1, D[2]);
       D[3] = mmah(tf[5], xb1, D[3]);
-      const f16x8 db0 = pack8h(D[0], D[1]), db1 = pack8h(D[2], D[3]);
-      phase();
-      // ---- 4: K^T reads for the first half of the state tiles; O^T = scale e^gam Z^T + Delta^T
-      //      (scale P)^T -> Ob[token][column]; Delta~ = e^{gam_c - gam} Delta in fp16
-      constexpr int KH = KT / 2;
-      f16x8 ktf[KT][2];
-#pragma unroll
-      for (int a = 0; a < KH; ++a)
-#pragma unroll
-        for (int u = 0; u < 2; ++u) ktf[a][u] = ld8h_tr_pair(kb, KP, 32 * u, 32 * (a >> 1) + 4 * (a & 1), lane);
-      phase();
-#pragma unroll
-      for (int tb = 0; tb < 4; ++tb) {
-        f32x4 o = Zt[tb] * (p.scale * eg[tb]);
-        o = mmah(db0, pf[tb], o);
-        if (tb >= 2) o = mmah(db1, pf[tb + 2], o);
-        *reinterpret_cast<bf16x4*>(op + (16 * tb + li) * kVP + 16 * sw + 4 * g4) = to_bf16x4(o[0], o[1], o[2], o[3]);
-      }
       f16x8 dt[2];
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
@@ -447,55 +435,55 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
                           dlb[u].w * D[2 * u + 1][3]};
         dt[u] = pack8h(x0, x1);
       }
+      const f16x8 db0 = pack8h(D[0], D[1]), db1 = pack8h(D[2], D[3]);
       phase();
-      // ---- 5: K^T reads for the second half; S' = e^{gam_c} S + K^T Delta~ on the first half
+      // ---- 4: K^T reads for the second half, P and scale e^gam reads; S' = e^{gam_c} S + K^T Delta~
 #pragma unroll
       for (int a = KH; a < KT; ++a)
 #pragma unroll
         for (int u = 0; u < 2; ++u) ktf[a][u] = ld8h_tr_pair(kb, KP, 32 * u, 32 * (a >> 1) + 4 * (a & 1), lane);
+      f16x8 pf[6];
+      float eg[4];
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) pf[tb] = ld8h(pp + (16 * tb + li) * kCP + 8 * g4);
+      pf[4] = ld8h(pp + (32 + li) * kCP + 32 + 8 * g4);
+      pf[5] = ld8h(pp + (48 + li) * kCP + 32 + 8 * g4);
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) eg[tb] = p.scale * G.egam[16 * tb + li];
       phase();
 #pragma unroll
-      for (int a = 0; a < KH; ++a) {
-        S[a] *= ec;
+      for (int a = 0; a < KT; ++a)
 #pragma unroll
         for (int u = 0; u < 2; ++u) S[a] = mmah(ktf[a][u], dt[u], S[a]);
-      }
       phase();
-      // ---- 6: Q reads of the next chunk (first half of the key steps); the second half of the
-      //      update; S in bf16
-      const bool more = i + 1 < nc;
-      const f16* qb = Qc[(i + 1) & 1];
+      // ---- 5: Q reads of the next chunk; S in fp16
       f16x8 qf[KS][4];
-      if (more) {
-#pragma unroll
-        for (int s2 = 0; s2 < KSH; ++s2)
-#pragma unroll
-          for (int tb = 0; tb < 4; ++tb) qf[s2][tb] = ld8h(qb + (16 * tb + li) * KP + 32 * s2 + 8 * g4);
-      }
-      phase();
-#pragma unroll
-      for (int a = KH; a < KT; ++a) {
-        S[a] *= ec;
-#pragma unroll
-        for (int u = 0; u < 2; ++u) S[a] = mmah(ktf[a][u], dt[u], S[a]);
-      }
-      make_sb();
-      phase();
-      // ---- 7: the other Q reads and the K reads for the next Y; Z^T = S^T Q^T of the next chunk
-      if (more) {
-#pragma unroll
-        for (int s2 = KSH; s2 < KS; ++s2)
-#pragma unroll
-          for (int tb = 0; tb < 4; ++tb) qf[s2][tb] = ld8h(qb + (16 * tb + li) * KP + 32 * s2 + 8 * g4);
-        load_kf(i + 1);
-        phase();
-#pragma unroll
-        for (int tb = 0; tb < 4; ++tb) Zt[tb] = f32x4{};
+      {
+        const f16* qb = Qc[(i + 1) & 1];
 #pragma unroll
         for (int s2 = 0; s2 < KS; ++s2)
 #pragma unroll
-          for (int tb = 0; tb < 4; ++tb) Zt[tb] = mmah(sb(s2), qf[s2][tb], Zt[tb]);
+          for (int tb = 0; tb < 4; ++tb) qf[s2][tb] = ld8h(qb + (16 * tb + li) * KP + 32 * s2 + 8 * g4);
       }
+      make_sb();
+      phase();
+      // ---- 6: K reads for the next Y; O^T = scale e^gam Z^T + Delta^T (scale P)^T -> Ob[token][column];
+      //      Z^T = S^T Q^T of the next chunk
+      load_kf(i + 1);
+      phase();
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) {
+        f32x4 o = Zt[tb] * eg[tb];
+        o = mmah(db0, pf[tb], o);
+        if (tb >= 2) o = mmah(db1, pf[tb + 2], o);
+        *reinterpret_cast<bf16x4*>(op + (16 * tb + li) * kVP + 16 * sw + 4 * g4) = to_bf16x4(o[0], o[1], o[2], o[3]);
+      }
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) Zt[tb] = f32x4{};
+#pragma unroll
+      for (int s2 = 0; s2 < KS; ++s2)
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) Zt[tb] = mmah(sb(s2), qf[s2][tb], Zt[tb]);
     } else if (qk_wave) {  // K/Q of chunk i+2 (loads first, P of chunk i+1 while they land)
       const int tq = thq_of(opaque_int(lane));
       bf16x8 pk[QKPT], pq[QKPT];
