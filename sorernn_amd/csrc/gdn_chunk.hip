@@ -268,6 +268,7 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
   // 16tb + i); (S_2s, S_2s+1) in fp16 (SB); the K row fragments of the next Y = K S for its first
   // KSH key steps (KF, read ahead across the barrier).
   f32x4 S[KT], Zt[4], SB[KS], KF[4 * KSH];
+  float ec_next = 1.f;  // e^{gam_c} of the chunk the next step processes
   auto sb = [&](int s) { return __builtin_bit_cast(f16x8, SB[s]); };
   const int64_t sbase = (n * p.HV + hv) * (int64_t)KD * VD + vb * kVB + 16 * sw;
   auto make_sb = [&]() {
@@ -286,6 +287,8 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
   // the scheduler may not move instructions across the phase boundaries: LDS reads complete in
   // order, so every phase finds its operands arrived or in flight instead of starting a round trip.
   auto phase = [] { __builtin_amdgcn_sched_barrier(0); };
+
+  uint32_t ngraw = 0, nbraw = 0;  // wave 4: raw gate bits of the chunk two steps ahead, in flight
 
   // ------------------------------------------------------------------ prologue
   // P is causally lower: its tiles above the diagonal stay zero for the whole run
@@ -319,6 +322,7 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
         fetch_gates(c, graw, braw);
         stage_gates(c, graw, braw);
       }
+      fetch_gates(2, ngraw, nbraw);
     }
   }
   __syncthreads();
@@ -330,6 +334,7 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb) qf[s2][tb] = ld8h(Qc[0] + (16 * tb + li) * KP + 32 * s2 + 8 * g4);
       load_kf(0);
+      ec_next = __expf(gv[0].gam[kC - 1]);
 #pragma unroll
       for (int tb = 0; tb < 4; ++tb) Zt[tb] = f32x4{};
 #pragma unroll
@@ -375,7 +380,7 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
         bt[b] = ld4f(&G.bet[16 * b + 4 * g4]);
         bg[b] = ld4f(&G.begam[16 * b + 4 * g4]);
       }
-      const float ec = __expf(G.gam[kC - 1]);
+      const float ec = ec_next;
       phase();
       f32x4 D[4];
 #pragma unroll
@@ -467,9 +472,10 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
       }
       make_sb();
       phase();
-      // ---- 6: K reads for the next Y; O^T = scale e^gam Z^T + Delta^T (scale P)^T -> Ob[token][column];
-      //      Z^T = S^T Q^T of the next chunk
+      // ---- 6: K reads for the next Y and its e^{gam_c}; O^T = scale e^gam Z^T + Delta^T (scale P)^T
+      //      -> Ob[token][column]; Z^T = S^T Q^T of the next chunk
       load_kf(i + 1);
+      ec_next = __expf(gv[(i + 1) % 3].gam[kC - 1]);
       phase();
 #pragma unroll
       for (int tb = 0; tb < 4; ++tb) {
@@ -495,12 +501,13 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
     } else {  // T/V of chunk i+1, gates of chunk i+2, O of chunk i-1 out
       const int tq = thv_of(opaque_int(lane));
       bf16x8 pt[4], pv[2];
-      uint32_t graw = 0, braw = 0;
       fetch_tv(pt, pv, i + 1, tq);
-      if (w == 4) fetch_gates(i + 2, graw, braw);
+      if (w == 4) {  // gates of chunk i+2 (loaded a step ago), then the loads for chunk i+3
+        stage_gates(i + 2, ngraw, nbraw);
+        fetch_gates(i + 3, ngraw, nbraw);
+      }
       if (i > 0) store_o(i - 1, tq);
       stage_tv(pt, pv, (i + 1) & 1, tq);
-      if (w == 4) stage_gates(i + 2, graw, braw);
     }
     __syncthreads();
   }
