@@ -69,7 +69,12 @@ constexpr int kVP = kVB + 8;  // bf16 pitch of the V and O slices (80 B rows)
 template <int KD, int VD>
 __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p) {
   constexpr int NVB = VD / kVB;
-  constexpr int KP = KD + 8;                  // bf16 pitch of the q/k tiles
+  // q/k tiles in LDS: at KD = 128 rows are unpadded (256 B) and the 16-byte chunk c of row r sits
+  // at chunk c ^ kq_sw(r), which keeps both the row-fragment reads (16 rows, one chunk) and the
+  // transposed K^T reads (4 rows x 4 chunks per 16 lanes) free of bank conflicts; at KD = 64 rows
+  // are padded by 16 bytes instead.
+  constexpr bool SWZ = KD == 128;
+  constexpr int KP = SWZ ? KD : KD + 8;       // element pitch of the q/k tiles
   constexpr int KS = KD / 32;                 // MFMA k-steps over the key dim
   constexpr int KT = KD / 16;                 // 16-row state tiles
   constexpr int KCH = KD / 8;                 // 16-byte chunks per q/k row
@@ -85,6 +90,21 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
 
   // w is read back as a scalar: the compiler then treats the role branches as wave-uniform
   const int t = threadIdx.x, lane = t & 63, w = __builtin_amdgcn_readfirstlane(t >> 6), g4 = lane >> 4, li = lane & 15;
+
+  // q/k tile addressing (element offsets): the swizzle of row r, the column of the row fragment for
+  // key step s (lane row li, lane group g: keys 32s + 8g..+7), and the transposed K^T fragment of
+  // state tile a = 2s + h against token rows 32u + 4g + m and 32u + 16 + 4g + m (ld8_tr_pair's
+  // layout: lane 4m + q reads keys 32s + 8q + 4h..+3, i.e. chunk 4s + q, half h).
+  auto kq_sw = [](int r) { return SWZ ? (((r & 3) << 2) | ((r >> 2) & 3)) : 0; };
+  auto kq_col = [&](int s, int l_i, int l_g) { return (((4 * s + l_g) ^ kq_sw(l_i)) << 3); };
+  auto kt_pair = [&](const f16* tile, int u, int a) {
+    const int m = li >> 2, q = li & 3;
+    const int row = 32 * u + 4 * g4 + m;  // row & 3 = m, (row >> 2) & 3 = g4: the swizzle of both rows
+    const f16* p0 = tile + row * KP + ((((4 * (a >> 1) + q) ^ kq_sw(4 * g4 + m)) << 3) + 4 * (a & 1));
+    const bf16x4 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p0));
+    const bf16x4 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p0 + 16 * KP));
+    return __builtin_bit_cast(f16x8, bf16x8{x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]});
+  };
 
   // workgroup -> (chain rank k, slice vb) -> (sequence n, value head hv). Workgroups are dispatched
   // in blockIdx order and blockIdx b lands on XCD b % 8: XCD x takes chain ranks x, x + 8, ..., all
@@ -152,7 +172,7 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
     for (int u = 0; u < QKPT; ++u) dst[u] = buf_load16(rs, base + (uint32_t)(u * (256 / KCH)) * qk_row);
   };
   auto stage_rows = [&](const bf16x8 (&src)[QKPT], f16* dst, int tq) {  // bf16 rows (L2-normalised when asked) -> fp16
-    f16* const d0 = dst + (tq / KCH) * KP + (tq % KCH) * 8;
+    f16* const d0 = dst + (tq / KCH) * KP + (((tq % KCH) ^ kq_sw(tq / KCH)) << 3);  // rows tq/KCH + 16u: same swizzle
 #pragma unroll
     for (int u = 0; u < QKPT; ++u)
       *reinterpret_cast<f16x8*>(d0 + u * (256 / KCH) * KP) = bf16_to_f16x8(l2 ? l2norm_row_chunk<KCH>(src[u]) : src[u]);
@@ -223,9 +243,9 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
     for (int s = 0; s < KS; ++s) {
       f16x8 fk[JN], fq[TN];
 #pragma unroll
-      for (int a = 0; a < JN; ++a) fk[a] = ld8h(kb + (16 * (JA + a) + li) * KP + 32 * s + 8 * g4);
+      for (int a = 0; a < JN; ++a) fk[a] = ld8h(kb + (16 * (JA + a) + li) * KP + kq_col(s, li, g4));
 #pragma unroll
-      for (int b = 0; b < TN; ++b) fq[b] = ld8h(qb + (16 * (TA + b) + li) * KP + 32 * s + 8 * g4);
+      for (int b = 0; b < TN; ++b) fq[b] = ld8h(qb + (16 * (TA + b) + li) * KP + kq_col(s, li, g4));
 #pragma unroll
       for (int a = 0; a < JN; ++a)
 #pragma unroll
@@ -281,7 +301,7 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
 #pragma unroll
     for (int s = 0; s < KSH; ++s)
 #pragma unroll
-      for (int b = 0; b < 4; ++b) KF[4 * s + b] = __builtin_bit_cast(f32x4, ld8h(kb + (16 * b + li) * KP + 32 * s + 8 * g4));
+      for (int b = 0; b < 4; ++b) KF[4 * s + b] = __builtin_bit_cast(f32x4, ld8h(kb + (16 * b + li) * KP + kq_col(s, li, g4)));
   };
   // Each phase of the state step issues the LDS reads of the next phase before its own MFMAs, and
   // the scheduler may not move instructions across the phase boundaries: LDS reads complete in
@@ -332,7 +352,7 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
 #pragma unroll
       for (int s2 = 0; s2 < KS; ++s2)
 #pragma unroll
-        for (int tb = 0; tb < 4; ++tb) qf[s2][tb] = ld8h(Qc[0] + (16 * tb + li) * KP + 32 * s2 + 8 * g4);
+        for (int tb = 0; tb < 4; ++tb) qf[s2][tb] = ld8h(Qc[0] + (16 * tb + li) * KP + kq_col(s2, li, g4));
       load_kf(0);
       ec_next = __expf(gv[0].gam[kC - 1]);
 #pragma unroll
@@ -371,7 +391,7 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
 #pragma unroll
       for (int s2 = KSH; s2 < KS; ++s2)
 #pragma unroll
-        for (int b = 0; b < 4; ++b) kf2[s2 - KSH][b] = ld8h(kb + (16 * b + li) * KP + 32 * s2 + 8 * g4);
+        for (int b = 0; b < 4; ++b) kf2[s2 - KSH][b] = ld8h(kb + (16 * b + li) * KP + kq_col(s2, li, g4));
       bf16x4 vv[4];
       float4 bt[4], bg[4];
 #pragma unroll
@@ -424,7 +444,7 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
 #pragma unroll
       for (int a = 0; a < KH; ++a)
 #pragma unroll
-        for (int u = 0; u < 2; ++u) ktf[a][u] = ld8h_tr_pair(kb, KP, 32 * u, 32 * (a >> 1) + 4 * (a & 1), lane);
+        for (int u = 0; u < 2; ++u) ktf[a][u] = kt_pair(kb, u, a);
       phase();
       D[0] = mmah(tf[0], xb0, D[0]);
       D[1] = mmah(tf[1], xb0, D[1]);
@@ -446,7 +466,7 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
 #pragma unroll
       for (int a = KH; a < KT; ++a)
 #pragma unroll
-        for (int u = 0; u < 2; ++u) ktf[a][u] = ld8h_tr_pair(kb, KP, 32 * u, 32 * (a >> 1) + 4 * (a & 1), lane);
+        for (int u = 0; u < 2; ++u) ktf[a][u] = kt_pair(kb, u, a);
       f16x8 pf[6];
       float eg[4];
 #pragma unroll
@@ -468,7 +488,7 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
 #pragma unroll
         for (int s2 = 0; s2 < KS; ++s2)
 #pragma unroll
-          for (int tb = 0; tb < 4; ++tb) qf[s2][tb] = ld8h(qb + (16 * tb + li) * KP + 32 * s2 + 8 * g4);
+          for (int tb = 0; tb < 4; ++tb) qf[s2][tb] = ld8h(qb + (16 * tb + li) * KP + kq_col(s2, li, g4));
       }
       make_sb();
       phase();
