@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define GDN_ABI_VERSION 2
+#define GDN_ABI_VERSION 3
 
 #if defined(__GNUC__) || defined(__clang__)
 #define GDN_API __attribute__((visibility("default")))
@@ -83,6 +83,51 @@ GDN_API int gdn_chunk_fwd(const void* q, const void* k, const void* v, const voi
  * 0 for invalid sizes. No counterpart in the reference: FLA allocates its intermediates itself.
  */
 GDN_API size_t gdn_chunk_workspace_size(int64_t B, int64_t T, int64_t HV, int64_t N, int varlen);
+
+/*
+ * Training forward of the chunked rule: gdn_chunk_fwd plus the fp32 state entering every chunk,
+ * chunk_states [chunks][HV][K][V] (gdn_chunk_states_size bytes; chunk c of sequence n is
+ * n * ceil(T / 64) + c, or the running chunk count before n plus c with cu_seqlens), which
+ * gdn_chunk_bwd reads. The workspace must also be kept unchanged until gdn_chunk_bwd has run.
+ * Replaces the forward half of FLA's chunk_gated_delta_rule autograd function (the call at
+ * sore/model/gdn.py:166-169 when the inputs require grad).
+ */
+GDN_API int gdn_chunk_fwd_train(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                        const float* initial_state, void* o, float* final_state, const void* cu_seqlens,
+                        int64_t B, int64_t T, int64_t H, int64_t HV, int64_t K, int64_t V, int64_t N,
+                        int qkv_dtype, int g_dtype, int beta_dtype, float scale, unsigned flags,
+                        const float* A_log, const float* dt_bias, float* chunk_states, void* workspace,
+                        size_t workspace_bytes, void* stream);
+
+/* Bytes of chunk_states for gdn_chunk_fwd_train / gdn_chunk_bwd (0 for invalid sizes). */
+GDN_API size_t gdn_chunk_states_size(int64_t B, int64_t T, int64_t HV, int64_t K, int64_t V, int64_t N, int varlen);
+
+/*
+ * Backward of the chunked rule. Replaces the backward of FLA 0.5.2's chunk_gated_delta_rule
+ * autograd function (its kernels chunk_gated_delta_rule_bwd_kernel_dhu, chunk_bwd_kernel_dqkwg,
+ * prepare_wy_repr_bwd and the l2norm backward, named by the profiler at
+ * tests/train/test_profiling.py:25,29,31,32,35; gradients checked against autograd through the
+ * reference recurrence at tests/model/test_gdn.py:94-101,158-162).
+ * Inputs: the forward's q, k, v, g, beta, A_log, dt_bias, cu_seqlens, flags and scale; d_o
+ * [B,T,HV,V] bf16; d_final_state [N,HV,K,V] fp32 or NULL (zero); chunk_states and fwd_workspace
+ * as left by gdn_chunk_fwd_train.
+ * Outputs: dq, dk [B,T,H,K] and dv [B,T,HV,V] bf16 (value heads sharing a q/k head are summed);
+ * dg [B,T,HV] in g_dtype and dbeta in beta_dtype (with the flags set, the gradients of the raw
+ * gate input a and of the beta logits); d_initial_state [N,HV,K,V] fp32 or NULL (not written);
+ * with GDN_FLAG_GATE_IN_KERNEL, dA_log and ddt_bias [HV] fp32 (overwritten, not accumulated).
+ * workspace: gdn_chunk_bwd_workspace_size bytes, contents on entry irrelevant.
+ */
+GDN_API int gdn_chunk_bwd(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                  const void* d_o, const float* d_final_state, const float* chunk_states,
+                  const void* fwd_workspace, const void* cu_seqlens, int64_t B, int64_t T, int64_t H,
+                  int64_t HV, int64_t K, int64_t V, int64_t N, int qkv_dtype, int g_dtype, int beta_dtype,
+                  float scale, unsigned flags, const float* A_log, const float* dt_bias, void* dq, void* dk,
+                  void* dv, void* dg, void* dbeta, float* d_initial_state, float* dA_log, float* ddt_bias,
+                  void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace bytes gdn_chunk_bwd needs (0 for invalid sizes). No counterpart in the reference. */
+GDN_API size_t gdn_chunk_bwd_workspace_size(int64_t B, int64_t T, int64_t HV, int64_t K, int64_t V, int64_t N,
+                                            int varlen);
 
 /*
  * Recurrent gated delta rule forward: tokens in order, the state held on chip for the whole

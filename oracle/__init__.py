@@ -7,6 +7,7 @@ this package, and only as the checker or the timed CPU baseline. The product pat
 from oracle.gdn_oracle import (  # noqa: F401
     causal_conv1d_silu,
     causal_conv1d_varlen,
+    chunk_gated_delta_rule_bwd_ref,
     chunk_gated_delta_rule_ref,
     conv_state_from_sequence,
     decode_step_ref,

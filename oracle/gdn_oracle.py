@@ -35,6 +35,7 @@ from torch import Tensor
 __all__ = [
     "causal_conv1d_silu",
     "causal_conv1d_varlen",
+    "chunk_gated_delta_rule_bwd_ref",
     "chunk_gated_delta_rule_ref",
     "conv_state_from_sequence",
     "decode_step_ref",
@@ -262,6 +263,123 @@ def chunk_gated_delta_rule_ref(
         o[bi, a:e] = oo
         finals.append(s)
     return o.to(out_dtype), (torch.stack(finals) if output_final_state else None)
+
+
+def _chunk_segment_bwd(q, k, v, g, beta, do, scale, state, dstate, chunk):
+    """Backward of ``_chunk_segment`` for one document, all heads, fp64.
+
+    ``q,k [T,H,K]``, ``v,do [T,H,V]``, ``g,beta [T,H]``, ``state [H,K,V]`` (the initial state),
+    ``dstate [H,K,V]`` (the gradient of the final state). Returns ``(dq, dk, dv, dg, dbeta, dstate0)``.
+
+    A forward sweep keeps the state entering each chunk; a reverse sweep carries ``dS`` (the
+    gradient of the state leaving the chunk). Per chunk, with the forward's names
+    (``Y = K S``, ``X``, ``Delta``, ``P = (Q K^T) o M``, ``r = exp(gam_c - gam)``):
+    ``dDelta = scale P^T dO + r o (K dS')``, ``dX = T^T dDelta``, ``dV = diag(beta) dX``,
+    ``dY = -diag(beta exp(gam)) dX``, ``dA = -strict(dX Delta^T)``, and
+    ``dS = exp(gam_c) dS' + scale Q^T diag(exp(gam)) dO + K^T dY``. The gate gradient is the
+    reverse in-chunk cumsum of ``dgam``. This is the algebra of FLA's ``chunk_gated_delta_rule_bwd``
+    stages (``tests/train/test_profiling.py:25,29,31,32,35``); it is pinned against torch autograd
+    through the token recurrence.
+    """
+    t, h = q.shape[0], q.shape[1]
+    starts = list(range(0, t, chunk))
+    states = []
+    s = state
+    for c0 in starts:
+        states.append(s)
+        _, s = _chunk_segment(q[c0 : c0 + chunk], k[c0 : c0 + chunk], v[c0 : c0 + chunk], g[c0 : c0 + chunk],
+                              beta[c0 : c0 + chunk], scale, s, chunk)
+    dq, dk, dv = torch.zeros_like(q), torch.zeros_like(k), torch.zeros_like(v)
+    dg, db = torch.zeros_like(g), torch.zeros_like(beta)
+    ds_next = dstate.clone()
+    for ci in range(len(starts) - 1, -1, -1):
+        c0 = starts[ci]
+        sl = slice(c0, c0 + chunk)
+        qc, kc, vc, gc, bc, doc = q[sl], k[sl], v[sl], g[sl], beta[sl], do[sl]
+        s = states[ci]
+        c = qc.shape[0]
+        gam = torch.cumsum(gc, 0)  # [c,H]
+        idx = torch.arange(c)
+        strict = (idx[:, None] > idx[None, :])[..., None]
+        causal = (idx[:, None] >= idx[None, :])[..., None]
+        diff = gam[:, None, :] - gam[None, :, :]
+        e = torch.where(causal, diff, torch.full_like(diff, -float("inf"))).exp()  # [t,j,H]
+        a_vec, r_vec = gam.exp(), (gam[-1][None, :] - gam).exp()  # [c,H]
+        ac = gam[-1].exp()  # [H]
+        gram = torch.einsum("thk,jhk->tjh", kc, kc)
+        amat = torch.where(strict, bc[:, None, :] * e * gram, torch.zeros_like(gram))
+        eye = torch.eye(c, dtype=q.dtype)
+        tmat = torch.linalg.solve_triangular(
+            (eye[..., None] + amat).permute(2, 0, 1), eye.expand(h, c, c), upper=False, unitriangular=True
+        )  # [H,t,j]
+        y = torch.einsum("thk,hkv->thv", kc, s)
+        x = bc[..., None] * vc - (bc * a_vec)[..., None] * y
+        delta = torch.einsum("htj,jhv->thv", tmat, x)
+        qk = torch.einsum("thk,jhk->tjh", qc, kc)
+        p = torch.where(causal, qk * e, torch.zeros_like(qk))
+        # reverse
+        w1 = torch.einsum("thk,hkv->thv", kc, ds_next)
+        ddelta = scale * torch.einsum("tjh,thv->jhv", p, doc) + r_vec[..., None] * w1
+        dx = torch.einsum("htj,thv->jhv", tmat, ddelta)
+        dv[sl] = bc[..., None] * dx
+        dy = -(bc * a_vec)[..., None] * dx
+        da = -torch.where(strict, torch.einsum("thv,jhv->tjh", dx, delta), torch.zeros_like(gram))
+        dgram = bc[:, None, :] * da * e  # strict by construction
+        dp = torch.where(causal, scale * torch.einsum("thv,jhv->tjh", doc, delta), torch.zeros_like(qk))
+        dqk = dp * e
+        dq_s = scale * a_vec[..., None] * torch.einsum("thv,hkv->thk", doc, s)
+        dq[sl] = dq_s + torch.einsum("tjh,jhk->thk", dqk, kc)
+        dk_y = torch.einsum("thv,hkv->thk", dy, s)
+        dk_r = r_vec[..., None] * torch.einsum("thv,hkv->thk", delta, ds_next)
+        dk[sl] = (dk_r + torch.einsum("tjh,thk->jhk", dqk, qc) + torch.einsum("tjh,jhk->thk", dgram, kc)
+                  + torch.einsum("tjh,thk->jhk", dgram, kc) + dk_y)
+        db[sl] = (da * e * gram).sum(1) + ((vc - a_vec[..., None] * y) * dx).sum(-1)
+        pair = dgram * gram + dqk * qk  # [t,j,H]
+        dr = r_vec * (w1 * delta).sum(-1)  # r_t dr_t
+        dgam = (qc * dq_s).sum(-1) + (kc * dk_y).sum(-1) - dr + pair.sum(1) - pair.sum(0)
+        dgam[-1] = dgam[-1] + ac * (s * ds_next).sum((-2, -1)) + dr.sum(0)
+        dg[sl] = torch.flip(torch.cumsum(torch.flip(dgam, [0]), 0), [0])
+        ds_next = (ac[:, None, None] * ds_next + scale * torch.einsum("thk,thv->hkv", qc, a_vec[..., None] * doc)
+                   + torch.einsum("thk,thv->hkv", kc, dy))
+    return dq, dk, dv, dg, db, ds_next
+
+
+def chunk_gated_delta_rule_bwd_ref(
+    q, k, v, g, beta, do, scale=None, initial_state=None, dht=None, cu_seqlens=None, chunk_size=64
+):
+    """Gradients of ``chunk_gated_delta_rule_ref`` in fp64: ``(dq, dk, dv, dg, dbeta, dh0)``.
+
+    ``do [B,T,HV,V]`` is the gradient of ``o``; ``dht [N,HV,K,V]`` (or ``None``) that of the final
+    state. ``dq, dk`` come back in the q/k layout ``[B,T,H,K]`` (summed over the value heads that
+    share a q/k head, the adjoint of ``gva_expand``); ``dh0 [N,HV,K,V]``. All fp64. This is the
+    backward the reference gets from torch autograd through ``sore/model/gdn_ref.py:11-22``, written
+    in chunk form.
+    """
+    b, t, h, kd = q.shape
+    hv, vd = v.shape[2], v.shape[3]
+    if scale is None:
+        scale = kd**-0.5
+    qe, ke = gva_expand(q, hv), gva_expand(k, hv)
+    qe, ke, v, g, beta, do = (x.double() for x in (qe, ke, v, g, beta, do))
+    if cu_seqlens is None:
+        segs = [(bi, 0, t, bi) for bi in range(b)]
+    else:
+        bounds = _check_cu(cu_seqlens, b, t)
+        segs = [(0, a, e, n) for n, (a, e) in enumerate(zip(bounds[:-1], bounds[1:]))]
+    dq, dk = torch.zeros(b, t, hv, kd, dtype=torch.float64), torch.zeros(b, t, hv, kd, dtype=torch.float64)
+    dv = torch.zeros(b, t, hv, vd, dtype=torch.float64)
+    dg, db = torch.zeros(b, t, hv, dtype=torch.float64), torch.zeros(b, t, hv, dtype=torch.float64)
+    dh0 = torch.zeros(len(segs), hv, kd, vd, dtype=torch.float64)
+    for bi, a, e, n in segs:
+        s0 = torch.zeros(hv, kd, vd, dtype=torch.float64) if initial_state is None else initial_state[n].double()
+        ds = torch.zeros(hv, kd, vd, dtype=torch.float64) if dht is None else dht[n].double()
+        r = _chunk_segment_bwd(qe[bi, a:e], ke[bi, a:e], v[bi, a:e], g[bi, a:e], beta[bi, a:e], do[bi, a:e],
+                               scale, s0, ds, chunk_size)
+        dq[bi, a:e], dk[bi, a:e], dv[bi, a:e], dg[bi, a:e], db[bi, a:e], dh0[n] = r
+    rep = hv // h
+    dq = dq.view(b, t, h, rep, kd).sum(3)
+    dk = dk.view(b, t, h, rep, kd).sum(3)
+    return dq, dk, dv, dg, db, dh0
 
 
 # --------------------------------------------------------------------------------------------------

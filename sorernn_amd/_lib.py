@@ -20,7 +20,7 @@ FLAG_BETA_SIGMOID = 0x2
 FLAG_GATE_IN_KERNEL = 0x4
 FLAG_CU_INT32 = 0x8
 ACT_NONE, ACT_SILU = 0, 1
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -35,6 +35,10 @@ SIGNATURES = {
     "gdn_last_error": [],
     "gdn_chunk_fwd": [_P] * 9 + [_I64] * 7 + [_INT] * 3 + [_F, _U, _P, _P, _P, _SZ, _P],
     "gdn_chunk_workspace_size": [_I64] * 4 + [_INT],
+    "gdn_chunk_fwd_train": [_P] * 9 + [_I64] * 7 + [_INT] * 3 + [_F, _U, _P, _P, _P, _P, _SZ, _P],
+    "gdn_chunk_states_size": [_I64] * 6 + [_INT],
+    "gdn_chunk_bwd": [_P] * 10 + [_I64] * 7 + [_INT] * 3 + [_F, _U] + [_P] * 11 + [_SZ, _P],
+    "gdn_chunk_bwd_workspace_size": [_I64] * 6 + [_INT],
     "gdn_recurrent_fwd": [_P] * 9 + [_I64] * 7 + [_INT] * 3 + [_F, _U, _P, _P, _P],
     "gdn_decode_step": [_P] * 7 + [_I64] * 5 + [_INT] * 4 + [_F, _U, _P, _P, _P],
     "gdn_causal_conv1d_fwd": [_P] * 7 + [_I64] * 5 + [_INT, _INT, _U, _P],
@@ -42,7 +46,12 @@ SIGNATURES = {
     "gdn_rms_norm_gated_fwd": [_P] * 5 + [_I64, _I64, _INT, _F, _INT, _P],
 }
 
-RESTYPES = {"gdn_last_error": ctypes.c_char_p, "gdn_chunk_workspace_size": ctypes.c_size_t}
+RESTYPES = {
+    "gdn_last_error": ctypes.c_char_p,
+    "gdn_chunk_workspace_size": ctypes.c_size_t,
+    "gdn_chunk_states_size": ctypes.c_size_t,
+    "gdn_chunk_bwd_workspace_size": ctypes.c_size_t,
+}
 
 _lib = None
 

@@ -60,13 +60,17 @@ struct ChunkParams {
   float scale;
   unsigned flags;
   const float *A_log, *dt_bias;
+  float* hs;                 // SAVE only: the state entering each chunk, fp32 [chunks][HV][K][V]
+  const int* chunk_first;    // SAVE with cu: chunks before each sequence
 };
 
 constexpr int kVB = 32;       // value columns per workgroup (two state waves of 16)
 constexpr int kNT = 512;      // threads per workgroup (8 waves)
 constexpr int kVP = kVB + 8;  // bf16 pitch of the V and O slices (80 B rows)
 
-template <int KD, int VD>
+// SAVE (training forward): the state waves also store the fp32 state entering every chunk, the
+// input of the backward's per-chunk gradient kernel.
+template <int KD, int VD, bool SAVE>
 __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p) {
   constexpr int NVB = VD / kVB;
   // q/k tiles in LDS: at KD = 128 rows are unpadded (256 B) and the 16-byte chunk c of row r sits
@@ -373,6 +377,16 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
   // T_{i+1}, V_{i+1}, P_{i+1}, gates_{i+2}. No slot is written and read in the same step.
   for (int i = 0; i < nc; ++i) {
     if (w < 2) {
+      if constexpr (SAVE) {
+        const int64_t cg = (p.cu ? (int64_t)p.chunk_first[n] : n * ((p.T + kC - 1) / kC)) + i;
+        float* hp = p.hs + (cg * p.HV + hv) * (int64_t)KD * VD + vb * kVB + 16 * sw + li;
+#pragma unroll
+        for (int a = 0; a < KT; ++a) {
+          const int kd0 = 32 * (a >> 1) + 8 * g4 + 4 * (a & 1);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) hp[(int64_t)(kd0 + r) * VD] = S[a][r];
+        }
+      }
       const f16* kb = Kc[i % 3];
       const f16* tp = Tb[i & 1];
       const bf16* vp = Vc[i & 1];
@@ -554,12 +568,13 @@ extern "C" size_t gdn_chunk_workspace_size(int64_t B, int64_t T, int64_t HV, int
   return bytes;
 }
 
-extern "C" int gdn_chunk_fwd(const void* q, const void* k, const void* v, const void* g, const void* beta,
-                             const float* initial_state, void* o, float* final_state, const void* cu_seqlens,
-                             int64_t B, int64_t T, int64_t H, int64_t HV, int64_t K, int64_t V, int64_t N,
-                             int qkv_dtype, int g_dtype, int beta_dtype, float scale, unsigned flags,
-                             const float* A_log, const float* dt_bias, void* workspace, size_t workspace_bytes,
-                             void* stream) {
+namespace {
+
+int chunk_fwd_impl(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                   const float* initial_state, void* o, float* final_state, const void* cu_seqlens, int64_t B,
+                   int64_t T, int64_t H, int64_t HV, int64_t K, int64_t V, int64_t N, int qkv_dtype, int g_dtype,
+                   int beta_dtype, float scale, unsigned flags, const float* A_log, const float* dt_bias,
+                   float* chunk_states, void* workspace, size_t workspace_bytes, void* stream) {
   if (!q || !k || !v || !g || !beta || !o) {
     gdn_internal_set_error("gdn_chunk_fwd: null tensor pointer");
     return GDN_ERR_INVALID;
@@ -610,11 +625,45 @@ extern "C" int gdn_chunk_fwd(const void* q, const void* k, const void* v, const 
   const int rc = launch_chunk_prep(pp, B, K, s);
   if (rc != GDN_OK) return rc;
   ChunkParams p{q, k, v, g, beta, initial_state, o, final_state, tw, cu_seqlens, order, cu_i32, T, H, HV, N,
-                g_dtype, beta_dtype, scale, flags, A_log, dt_bias};
+                g_dtype, beta_dtype, scale, flags, A_log, dt_bias, chunk_states, chunk_first};
   dim3 grid((unsigned)blocks), block(kNT);
-  if (K == 128 && V == 128) hipLaunchKernelGGL((gated_delta_chunk_kernel<128, 128>), grid, block, 0, s, p);
-  else if (K == 64 && V == 64) hipLaunchKernelGGL((gated_delta_chunk_kernel<64, 64>), grid, block, 0, s, p);
-  else if (K == 128 && V == 64) hipLaunchKernelGGL((gated_delta_chunk_kernel<128, 64>), grid, block, 0, s, p);
-  else hipLaunchKernelGGL((gated_delta_chunk_kernel<64, 128>), grid, block, 0, s, p);
+  if (chunk_states) {
+    if (K == 128 && V == 128) hipLaunchKernelGGL((gated_delta_chunk_kernel<128, 128, true>), grid, block, 0, s, p);
+    else if (K == 64 && V == 64) hipLaunchKernelGGL((gated_delta_chunk_kernel<64, 64, true>), grid, block, 0, s, p);
+    else if (K == 128 && V == 64) hipLaunchKernelGGL((gated_delta_chunk_kernel<128, 64, true>), grid, block, 0, s, p);
+    else hipLaunchKernelGGL((gated_delta_chunk_kernel<64, 128, true>), grid, block, 0, s, p);
+  } else {
+    if (K == 128 && V == 128) hipLaunchKernelGGL((gated_delta_chunk_kernel<128, 128, false>), grid, block, 0, s, p);
+    else if (K == 64 && V == 64) hipLaunchKernelGGL((gated_delta_chunk_kernel<64, 64, false>), grid, block, 0, s, p);
+    else if (K == 128 && V == 64) hipLaunchKernelGGL((gated_delta_chunk_kernel<128, 64, false>), grid, block, 0, s, p);
+    else hipLaunchKernelGGL((gated_delta_chunk_kernel<64, 128, false>), grid, block, 0, s, p);
+  }
   return gdn_internal_check_launch("gated_delta_chunk_kernel");
+}
+
+}  // namespace
+
+extern "C" int gdn_chunk_fwd(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                             const float* initial_state, void* o, float* final_state, const void* cu_seqlens,
+                             int64_t B, int64_t T, int64_t H, int64_t HV, int64_t K, int64_t V, int64_t N,
+                             int qkv_dtype, int g_dtype, int beta_dtype, float scale, unsigned flags,
+                             const float* A_log, const float* dt_bias, void* workspace, size_t workspace_bytes,
+                             void* stream) {
+  return chunk_fwd_impl(q, k, v, g, beta, initial_state, o, final_state, cu_seqlens, B, T, H, HV, K, V, N, qkv_dtype,
+                        g_dtype, beta_dtype, scale, flags, A_log, dt_bias, nullptr, workspace, workspace_bytes, stream);
+}
+
+extern "C" int gdn_chunk_fwd_train(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                                   const float* initial_state, void* o, float* final_state, const void* cu_seqlens,
+                                   int64_t B, int64_t T, int64_t H, int64_t HV, int64_t K, int64_t V, int64_t N,
+                                   int qkv_dtype, int g_dtype, int beta_dtype, float scale, unsigned flags,
+                                   const float* A_log, const float* dt_bias, float* chunk_states, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
+  if (!chunk_states) {
+    gdn_internal_set_error("gdn_chunk_fwd_train: chunk_states is required");
+    return GDN_ERR_INVALID;
+  }
+  return chunk_fwd_impl(q, k, v, g, beta, initial_state, o, final_state, cu_seqlens, B, T, H, HV, K, V, N, qkv_dtype,
+                        g_dtype, beta_dtype, scale, flags, A_log, dt_bias, chunk_states, workspace, workspace_bytes,
+                        stream);
 }

@@ -1,0 +1,916 @@
+// Backward of the chunked gated delta rule for gfx950 (training through chunk_gated_delta_rule).
+//
+// Per chunk of c <= 64 tokens the forward computes (gam = in-chunk cumsum of g, a = e^gam,
+// r = e^{gam_c - gam}, E_tj = e^{gam_t - gam_j}, T = (I + A)^-1 with A_tj = beta_t E_tj k_t.k_j, j < t):
+//   Y = K S,  X = diag(beta) V - diag(beta a) Y,  Delta = T X,
+//   O = scale (diag(a) Q S + P Delta),  P = (Q K^T) o E (j <= t),  S' = e^{gam_c} S + K^T diag(r) Delta.
+// Given dO and dS' (the gradient of the state leaving the chunk), its backward is
+//   dDelta = scale P^T dO + diag(r) K dS',   dX = T^T dDelta,   dV = diag(beta) dX,
+//   dS     = e^{gam_c} dS' + scale Q^T diag(a) dO - K^T diag(beta a) dX            (to the previous chunk)
+//   dA     = -strict(dX Delta^T),  dG = diag(beta) dA o E,  dQK = scale (dO Delta^T) o E (j <= t)
+//   dQ     = scale diag(a) dO S^T + dQK K
+//   dK     = diag(r) Delta dS'^T - diag(beta a) dX S^T + dQK^T Q + (dG + dG^T) K
+//   dbeta  = rowsum(dA o E o KK^T) + rowsum((V - diag(a) Y) o dX)
+//   dgam   = rowsum(Q o dQ_S) - rowsum(diag(beta a) dX o Y) - diag(r) rowsum(K dS' o Delta)
+//            + rowsum(Pi) - colsum(Pi),  Pi = dG o KK^T + dQK o QK^T
+//            (+ e^{gam_c} <S, dS'> + sum_t r_t (K dS')_t . Delta_t at the chunk's last position),
+//   dg     = reverse in-chunk cumsum of dgam.
+// oracle/gdn_oracle.py::_chunk_segment_bwd restates the same algebra in fp64 (pinned there against
+// autograd through the token recurrence of sore/model/gdn_ref.py:11-22).
+//
+// Four launches on the caller's stream, after a forward that saved the state entering every chunk
+// (gdn_chunk_fwd_train):
+//   1. gated_delta_chunk_bwd_prep_kernel, per (chunk, value head): T - I in natural column order
+//      (bf16, for launches 2 and 3) and G1 = T^T (scale P^T dO) (fp32), the state-independent part
+//      of dX.
+//   2. gated_delta_chunk_bwd_state_kernel, per (sequence, value head, 32 value columns): the reverse
+//      recurrence dS <- e^{gam_c} dS + K^T (-beta a dX) + Q^T (scale a dO) with
+//      dX = G1 + T^T (r o K dS), over the chunks from last to first; it stores dS' of every chunk
+//      and the initial state's gradient.
+//   3. gated_delta_chunk_bwd_grad_kernel, per (chunk, q/k head): everything else, from the saved
+//      S, the stored dS' and the chunk's tiles; the value heads that share a q/k head are summed
+//      in registers (GVA), and the L2-norm, gate and sigmoid backwards are applied on the way out.
+//   4. gated_delta_gate_param_grad_kernel (in-kernel gate only): dA_log and ddt_bias per head from
+//      the per-chunk partial sums.
+// MFMA operands are bf16 (v_mfma_f32_16x16x32_bf16) with fp32 accumulation: gradients span a range
+// of magnitudes that fp16 cannot hold (a mean loss over 10^8 outputs gives dO ~ 1e-8).
+
+#include "gdn_chunk.h"
+
+namespace gdn {
+
+struct ChunkBwdParams {
+  const void *q, *k, *v, *g, *beta, *dout;
+  const float* dht;   // gradient of the final state [N][HV][K][V], or null
+  const float* hs;    // state entering each chunk, fp32 [chunks][HV][K][V] (forward output)
+  const f16* tw;      // the forward's T - I rows (fp16, tok_col columns)
+  bf16* tn;           // T - I rows, natural columns, bf16 [tokens][HV][64]      (workspace)
+  float* g1;          // G1 = T^T (scale P^T dO), fp32 [tokens][HV][V]           (workspace)
+  float* dhs;         // gradient of the state leaving each chunk [chunks][HV][K][V] (workspace)
+  float* gate_part;   // per-chunk partial sums of dA_log and ddt_bias [chunks][HV][2] (workspace)
+  const void* cu;
+  const int* chunk_first;
+  int cu_i32;
+  int64_t T, H, HV, N;
+  int dg, db;
+  float scale;
+  unsigned flags;
+  const float *A_log, *dt_bias;
+  void *dq, *dk, *dv, *dgate, *dbeta;
+  float *dh0, *dA_log, *ddt_bias;
+};
+
+constexpr int kCPb = 72;  // bf16 pitch of [*][64] tiles (144 B rows: row and transposed reads conflict-free)
+template <int D>
+constexpr int row_pitch() { return D == 128 ? D + 16 : D + 8; }  // bf16 pitch of [*][D] tiles
+
+// ---------------------------------------------------------------- fragments from row-major bf16 LDS tiles
+// frag_row: lane (g, i) reads M[r0 + i][c0 + 8g .. c0 + 8g + 7] -- the A operand for rows r0.. of M
+// with the contraction along M's rows, or the B operand of M^T.
+__device__ __forceinline__ bf16x8 frag_row(const bf16* M, int pitch, int r0, int c0, int lane) {
+  return ld8(M + (r0 + (lane & 15)) * pitch + c0 + 8 * (lane >> 4));
+}
+// frag_col: lane (g, i) gets M[r0 + 8g + j][c0 + i], j = 0..7 (two ds_read_b64_tr_b16: lane 4m + q
+// reads row r0 + 8g + m (then + 4) at columns c0 + 4q..+3) -- the B operand of M (contraction
+// along M's rows, output columns c0..) or the A operand of M^T.
+__device__ __forceinline__ bf16x8 frag_col(const bf16* M, int pitch, int r0, int c0, int lane) {
+  const int g = lane >> 4, li = lane & 15;
+  const bf16* p0 = M + (r0 + 8 * g + (li >> 2)) * pitch + c0 + 4 * (li & 3);
+  const bf16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p0));
+  const bf16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p0 + 4 * pitch));
+  return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+// An accumulator tile (rows r0 + 4g + r, column c0 + i) into a bf16 LDS tile.
+__device__ __forceinline__ void put_acc(bf16* M, int pitch, int r0, int c0, int lane, f32x4 x) {
+  const int g = lane >> 4, li = lane & 15;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) M[(r0 + 4 * g + r) * pitch + c0 + li] = static_cast<bf16>(x[r]);
+}
+__device__ __forceinline__ bf16x4 ld4b(const bf16* p) { return *reinterpret_cast<const bf16x4*>(p); }
+
+// ---------------------------------------------------------------- chunk -> sequence
+struct ChunkLoc {
+  int64_t n, c, c0;
+  int len;
+};
+// Item = global chunk index (sequence n's chunks are chunk_first[n] + c with cu_seqlens, n * ceil(T/64) + c
+// without); false for grid items past the last chunk.
+__device__ __forceinline__ bool locate_chunk(const ChunkBwdParams& p, int64_t item, ChunkLoc& L) {
+  int64_t bos, eos;
+  if (p.cu) {
+    if (item >= p.chunk_first[p.N]) return false;
+    int64_t lo = 0, hi = p.N - 1;
+    while (lo < hi) {
+      const int64_t mid = (lo + hi + 1) / 2;
+      if (p.chunk_first[mid] <= item) lo = mid;
+      else hi = mid - 1;
+    }
+    L.n = lo;
+    L.c = item - p.chunk_first[lo];
+    bos = load_index(p.cu, p.cu_i32, lo);
+    eos = load_index(p.cu, p.cu_i32, lo + 1);
+  } else {
+    const int64_t ncs = (p.T + kC - 1) / kC;
+    L.n = item / ncs;
+    L.c = item % ncs;
+    bos = L.n * p.T;
+    eos = bos + p.T;
+  }
+  L.c0 = bos + L.c * kC;
+  L.len = (int)((eos - L.c0) < kC ? (eos - L.c0) : kC);
+  return true;
+}
+
+// q/k rows of a chunk (bf16, L2-normalised and rounded to bf16 when asked, exactly as the forward
+// stages them) into a [64][pitch] LDS tile; rows past len read as zeros. NT threads, tid < NT.
+template <int KD, int NT>
+__device__ __forceinline__ void stage_qk_rows(bf16* dst, int pitch, const bf16* src, int64_t H, int len, bool l2, int tid) {
+  constexpr int KCH = KD / 8, RPP = NT / KCH;
+  const uint32_t rb = (uint32_t)(H * KD * 2);
+  const auto rs = make_rsrc(src, (uint32_t)len * rb);
+  const int row = tid / KCH, ch = tid % KCH;
+  bf16x8 x[kC / RPP];
+#pragma unroll
+  for (int u = 0; u < kC / RPP; ++u) x[u] = buf_load16(rs, (uint32_t)(row + u * RPP) * rb + ch * 16);
+#pragma unroll
+  for (int u = 0; u < kC / RPP; ++u)
+    *reinterpret_cast<bf16x8*>(dst + (row + u * RPP) * pitch + ch * 8) = l2 ? l2norm_row_chunk<KCH>(x[u]) : x[u];
+}
+// A bf16 [64][W] slice of a [tokens][heads][*] tensor (row stride rb bytes) into LDS; rows past len read as zeros.
+template <int W, int NT>
+__device__ __forceinline__ void stage_slice(bf16* dst, int pitch, const bf16* src, uint32_t rb, int len, int tid) {
+  constexpr int CH = W / 8, TOT = kC * CH;
+  const auto rs = make_rsrc(src, (uint32_t)len * rb);
+#pragma unroll
+  for (int e0 = 0; e0 < TOT; e0 += NT) {
+    const int e = e0 + tid;
+    if (TOT % NT == 0 || e < TOT) {
+      const int row = e / CH, ch = e % CH;
+      *reinterpret_cast<bf16x8*>(dst + row * pitch + ch * 8) = buf_load16(rs, (uint32_t)row * rb + ch * 16);
+    }
+  }
+}
+// Gate terms of a chunk (one wave, lane = token), as the forward computes them.
+__device__ __forceinline__ void stage_gates_bwd(ChunkGates& gs, const ChunkBwdParams& p, int64_t c0, int64_t hv, int len,
+                                                int lane) {
+  const uint32_t gb = (uint32_t)(p.HV * dtype_bytes(p.dg)), bb = (uint32_t)(p.HV * dtype_bytes(p.db));
+  const auto rg = make_rsrc(static_cast<const char*>(p.g) + (c0 * p.HV + hv) * dtype_bytes(p.dg), (uint32_t)len * gb);
+  const auto rb = make_rsrc(static_cast<const char*>(p.beta) + (c0 * p.HV + hv) * dtype_bytes(p.db), (uint32_t)len * bb);
+  const uint32_t graw = buf_load_raw32(rg, lane * gb, p.dg), braw = buf_load_raw32(rb, lane * bb, p.db);
+  chunk_gates_from_raw(gs, graw, braw, p.dg, p.db, len, p.flags, p.A_log ? p.A_log[hv] : 0.f,
+                       p.dt_bias ? p.dt_bias[hv] : 0.f, lane);
+}
+
+// ================================================================== 1. prep: T - I (natural) and G1
+// One workgroup of 4 waves per (chunk, value head); wave w owns the 16 tokens 16w..16w+15 of every
+// product it computes.
+template <int KD, int VD>
+__global__ __launch_bounds__(256) void gated_delta_chunk_bwd_prep_kernel(ChunkBwdParams p) {
+  constexpr int KPB = row_pitch<KD>(), VPB = row_pitch<VD>(), KS = KD / 32, VT = VD / 16;
+  __shared__ __align__(16) bf16 Kb[kC * KPB], Qb[kC * KPB], dOb[kC * VPB], Fb[kC * VPB];
+  __shared__ __align__(16) bf16 Pb[kC * kCPb], Tm[kC * kCPb];
+  __shared__ __align__(16) ChunkGates gs;
+  ChunkLoc L;
+  if (!locate_chunk(p, blockIdx.x, L)) return;
+  const int64_t hv = blockIdx.y, h = hv / (p.HV / p.H);
+  const int t = threadIdx.x, lane = t & 63, w = __builtin_amdgcn_readfirstlane(t >> 6), g4 = lane >> 4, li = lane & 15;
+  const bool l2 = p.flags & GDN_FLAG_QK_L2NORM;
+  const int len = L.len;
+  const int64_t c0 = L.c0;
+
+  stage_qk_rows<KD, 256>(Kb, KPB, static_cast<const bf16*>(p.k) + (c0 * p.H + h) * KD, p.H, len, l2, t);
+  stage_qk_rows<KD, 256>(Qb, KPB, static_cast<const bf16*>(p.q) + (c0 * p.H + h) * KD, p.H, len, l2, t);
+  stage_slice<VD, 256>(dOb, VPB, static_cast<const bf16*>(p.dout) + (c0 * p.HV + hv) * VD, (uint32_t)(p.HV * VD * 2), len, t);
+  {  // T - I: fp16 rows with tok_col columns -> bf16 natural columns (LDS and the workspace)
+    const uint32_t rb = (uint32_t)(p.HV * kC * 2);
+    const auto rs = make_rsrc(p.tw + (c0 * p.HV + hv) * kC, (uint32_t)len * rb);
+#pragma unroll
+    for (int e0 = 0; e0 < kC * 8; e0 += 256) {
+      const int e = e0 + t, row = e >> 3, ch = e & 7, u = ch >> 2, gq = ch & 3;
+      // columns 32u + 8gq + 4hh + r of the chunk hold tokens 32u + 16hh + 4gq + r
+      const f16x8 x = __builtin_bit_cast(f16x8, buf_load16(rs, (uint32_t)row * rb + ch * 16));
+      const bf16x4 lo = to_bf16x4((float)x[0], (float)x[1], (float)x[2], (float)x[3]);
+      const bf16x4 hi = to_bf16x4((float)x[4], (float)x[5], (float)x[6], (float)x[7]);
+      *reinterpret_cast<bf16x4*>(Tm + row * kCPb + 32 * u + 4 * gq) = lo;
+      *reinterpret_cast<bf16x4*>(Tm + row * kCPb + 32 * u + 16 + 4 * gq) = hi;
+      if (row < len) {
+        bf16* tn = p.tn + ((c0 + row) * p.HV + hv) * kC;
+        *reinterpret_cast<bf16x4*>(tn + 32 * u + 4 * gq) = lo;
+        *reinterpret_cast<bf16x4*>(tn + 32 * u + 16 + 4 * gq) = hi;
+      }
+    }
+  }
+  if (w == 0) stage_gates_bwd(gs, p, c0, hv, len, lane);
+  __syncthreads();
+
+  // scale P = scale (Q K^T) o E (j <= t), rows 16w..16w+15
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt) {
+    f32x4 acc = f32x4{};
+    if (jt <= w) {
+#pragma unroll
+      for (int s = 0; s < KS; ++s) acc = mma(frag_row(Qb, KPB, 16 * w, 32 * s, lane), frag_row(Kb, KPB, 16 * jt, 32 * s, lane), acc);
+    }
+    const int j = 16 * jt + li;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int tt = 16 * w + 4 * g4 + r;
+      acc[r] = j <= tt ? p.scale * __expf(gs.gam[tt] - gs.gam[j]) * acc[r] : 0.f;
+    }
+    put_acc(Pb, kCPb, 16 * w, 16 * jt, lane, acc);
+  }
+  __syncthreads();
+  // F = (scale P)^T dO, rows (key tokens j) 16w..16w+15
+  f32x4 F[VT];
+#pragma unroll
+  for (int ct = 0; ct < VT; ++ct) {
+    F[ct] = f32x4{};
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+      if (s == 1 || w <= 1) F[ct] = mma(frag_col(Pb, kCPb, 32 * s, 16 * w, lane), frag_col(dOb, VPB, 32 * s, 16 * ct, lane), F[ct]);
+    put_acc(Fb, VPB, 16 * w, 16 * ct, lane, F[ct]);
+  }
+  __syncthreads();
+  // G1 = F + (T - I)^T F  ((T - I)_{t'j} vanishes unless t' > j)
+#pragma unroll
+  for (int ct = 0; ct < VT; ++ct) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+      if (u == 1 || w <= 1) F[ct] = mma(frag_col(Tm, kCPb, 32 * u, 16 * w, lane), frag_col(Fb, VPB, 32 * u, 16 * ct, lane), F[ct]);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int tt = 16 * w + 4 * g4 + r;
+      if (tt < len) p.g1[((c0 + tt) * p.HV + hv) * VD + 16 * ct + li] = F[ct][r];
+    }
+  }
+}
+
+// ================================================================== 2. reverse state recurrence
+// One workgroup of 4 waves per (sequence, value head, 32 value columns). Waves 0 and 1 each hold 16
+// columns of dS [K x 16] in fp32 MFMA accumulators (tile a: keys 16a + 4g + r, column i) for the
+// whole sequence; waves 2 and 3 stage the next chunk's tiles into the other LDS slot meanwhile.
+template <int KD, int VD>
+__global__ __launch_bounds__(256, 1) void gated_delta_chunk_bwd_state_kernel(ChunkBwdParams p) {
+  constexpr int KPB = row_pitch<KD>(), KS = KD / 32, KT = KD / 16, NVB = VD / 32;
+  constexpr int GP = 36, OP = 40;  // fp32 pitch of the G1 slice, bf16 pitch of the dO slice
+  __shared__ __align__(16) bf16 Kb[2][kC * KPB], Qb[2][kC * KPB], Tm[2][kC * kCPb], dOs[2][kC * OP];
+  __shared__ __align__(16) float G1s[2][kC * GP];
+  __shared__ __align__(16) ChunkGates gv[2];
+
+  const int t = threadIdx.x, lane = t & 63, w = __builtin_amdgcn_readfirstlane(t >> 6), g4 = lane >> 4, li = lane & 15;
+  const int64_t chain = blockIdx.x / NVB;
+  const int vb = (int)(blockIdx.x % NVB);
+  const int64_t n = chain / p.HV, hv = chain % p.HV, h = hv / (p.HV / p.H);
+  int64_t bos, eos, cgb;
+  const int64_t ncs = (p.T + kC - 1) / kC;
+  if (p.cu) {
+    bos = load_index(p.cu, p.cu_i32, n);
+    eos = load_index(p.cu, p.cu_i32, n + 1);
+    cgb = p.chunk_first[n];
+  } else {
+    bos = n * p.T;
+    eos = bos + p.T;
+    cgb = n * ncs;
+  }
+  const int nc = (int)((eos - bos + kC - 1) / kC);
+  const bool l2 = p.flags & GDN_FLAG_QK_L2NORM;
+
+  auto load_chunk = [&](int c, int slot, int tl) {  // tl = 0..127 (waves 2, 3)
+    const int64_t c0 = bos + (int64_t)c * kC;
+    const int len = (int)((eos - c0) < kC ? (eos - c0) : kC);
+    stage_qk_rows<KD, 128>(Kb[slot], KPB, static_cast<const bf16*>(p.k) + (c0 * p.H + h) * KD, p.H, len, l2, tl);
+    stage_qk_rows<KD, 128>(Qb[slot], KPB, static_cast<const bf16*>(p.q) + (c0 * p.H + h) * KD, p.H, len, l2, tl);
+    stage_slice<kC, 128>(Tm[slot], kCPb, p.tn + (c0 * p.HV + hv) * kC, (uint32_t)(p.HV * kC * 2), len, tl);
+    stage_slice<32, 128>(dOs[slot], OP, static_cast<const bf16*>(p.dout) + (c0 * p.HV + hv) * VD + vb * 32,
+                         (uint32_t)(p.HV * VD * 2), len, tl);
+    {  // G1 slice: 64 rows x 8 chunks of 4 floats
+      const uint32_t rb = (uint32_t)(p.HV * VD * 4);
+      const auto rs = make_rsrc(p.g1 + (c0 * p.HV + hv) * VD + vb * 32, (uint32_t)len * rb);
+#pragma unroll
+      for (int e0 = 0; e0 < kC * 8; e0 += 128) {
+        const int e = e0 + tl, row = e >> 3, ch = e & 7;
+        *reinterpret_cast<u32x4*>(&G1s[slot][row * GP + ch * 4]) =
+            __builtin_bit_cast(u32x4, buf_load16(rs, (uint32_t)row * rb + ch * 16));
+      }
+    }
+    if (w == 2) stage_gates_bwd(gv[slot], p, c0, hv, len, lane);
+  };
+
+  const int sw = w & 1, col = vb * 32 + 16 * sw + li;  // state waves: value column of this lane
+  f32x4 dS[KT];
+  if (w < 2) {
+#pragma unroll
+    for (int a = 0; a < KT; ++a)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        dS[a][r] = p.dht ? p.dht[((n * p.HV + hv) * KD + 16 * a + 4 * g4 + r) * VD + col] : 0.f;
+  } else if (nc > 0) {
+    load_chunk(nc - 1, 0, t - 128);
+  }
+  __syncthreads();
+
+  for (int i = 0; i < nc; ++i) {
+    const int c = nc - 1 - i, slot = i & 1;
+    if (w < 2) {
+      // dS' of chunk c (the gradient of the state leaving it)
+      float* dp = p.dhs + ((cgb + c) * p.HV + hv) * (int64_t)KD * VD + col;
+#pragma unroll
+      for (int a = 0; a < KT; ++a)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dp[(int64_t)(16 * a + 4 * g4 + r) * VD] = dS[a][r];
+      const bf16* kb = Kb[slot];
+      const bf16* qb = Qb[slot];
+      const bf16* tm = Tm[slot];
+      const ChunkGates& G = gv[slot];
+      // W1 = K dS': contraction slots (g, j) hold keys 32s + 4g + j and 32s + 16 + 4g + j
+      f32x4 W[4];
+#pragma unroll
+      for (int b = 0; b < 4; ++b) W[b] = f32x4{};
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const bf16x8 sb = pack8(dS[2 * s], dS[2 * s + 1]);
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          const bf16* kr = kb + (16 * b + li) * KPB + 32 * s + 4 * g4;
+          const bf16x4 k0 = ld4b(kr), k1 = ld4b(kr + 16);
+          W[b] = mma(bf16x8{k0[0], k0[1], k0[2], k0[3], k1[0], k1[1], k1[2], k1[3]}, sb, W[b]);
+        }
+      }
+      // dX = G1 + Z + (T - I)^T Z, Z = r o W1 (token pairs 32u + 4g + r, 32u + 16 + 4g + r)
+      f32x4 X[4];
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int tok = 16 * b + 4 * g4 + r;
+          W[b][r] *= G.dlast[tok];
+          X[b][r] = G1s[slot][tok * GP + 16 * sw + li] + W[b][r];
+        }
+      const bf16x8 zb[2] = {pack8(W[0], W[1]), pack8(W[2], W[3])};
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+          if (u == 1 || b <= 1) {
+            const bf16x4 t0 = ld4_tr(tm, kCPb, 32 * u, 16 * b, lane), t1 = ld4_tr(tm, kCPb, 32 * u + 16, 16 * b, lane);
+            X[b] = mma(bf16x8{t0[0], t0[1], t0[2], t0[3], t1[0], t1[1], t1[2], t1[3]}, zb[u], X[b]);
+          }
+      // dY = -beta a dX; scale a dO
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) X[b][r] *= -G.begam[16 * b + 4 * g4 + r];
+      const bf16x8 yb[2] = {pack8(X[0], X[1]), pack8(X[2], X[3])};
+      bf16x8 qa[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const bf16x4 d0 = ld4_tr(dOs[slot], OP, 32 * u, 16 * sw, lane), d1 = ld4_tr(dOs[slot], OP, 32 * u + 16, 16 * sw, lane);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          qa[u][m] = static_cast<bf16>(p.scale * G.egam[32 * u + 4 * g4 + m] * (float)d0[m]);
+          qa[u][4 + m] = static_cast<bf16>(p.scale * G.egam[32 * u + 16 + 4 * g4 + m] * (float)d1[m]);
+        }
+      }
+      // dS = e^{gam_c} dS' + K^T dY + Q^T (scale a dO)
+      const float ac = G.egam[kC - 1];
+#pragma unroll
+      for (int a = 0; a < KT; ++a) {
+        dS[a] *= ac;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const bf16x4 k0 = ld4_tr(kb, KPB, 32 * u, 16 * a, lane), k1 = ld4_tr(kb, KPB, 32 * u + 16, 16 * a, lane);
+          dS[a] = mma(bf16x8{k0[0], k0[1], k0[2], k0[3], k1[0], k1[1], k1[2], k1[3]}, yb[u], dS[a]);
+          const bf16x4 q0 = ld4_tr(qb, KPB, 32 * u, 16 * a, lane), q1 = ld4_tr(qb, KPB, 32 * u + 16, 16 * a, lane);
+          dS[a] = mma(bf16x8{q0[0], q0[1], q0[2], q0[3], q1[0], q1[1], q1[2], q1[3]}, qa[u], dS[a]);
+        }
+      }
+    } else if (i + 1 < nc) {
+      load_chunk(c - 1, slot ^ 1, t - 128);
+    }
+    __syncthreads();
+  }
+  if (w < 2 && p.dh0) {
+#pragma unroll
+    for (int a = 0; a < KT; ++a)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) p.dh0[((n * p.HV + hv) * KD + 16 * a + 4 * g4 + r) * VD + col] = dS[a][r];
+  }
+}
+
+// ================================================================== 3. per-chunk gradients
+// One workgroup of 8 waves per (chunk, q/k head), looping over the value heads of the head. Wave w
+// owns the tokens 16bt..16bt+15 (bt = w / 2) and half hw = w % 2 of the columns of every product:
+// value columns 32hw..32hw+31 of a 64-column half of V, key tiles KD/32 * hw.., c x c tiles 2hw, 2hw+1.
+template <int KD, int VD>
+__global__ __launch_bounds__(512, 1) void gated_delta_chunk_bwd_grad_kernel(ChunkBwdParams p) {
+  constexpr int KPB = row_pitch<KD>(), KS = KD / 32, KTW = KD / 32, NVH = VD / 64;
+  constexpr int FP = KD + 4;  // fp32 pitch of the dq / dk rows at the end
+  // S and dS' halves [KD][64]; dO, scale a dO, V (then r Delta), X (then r o K dS'), Delta, dX and
+  // -beta a dX [64][64]. After the value loop the first two hold dG and dQK; at the end the region
+  // holds dq and dk in fp32. The row scalings of dQ and dK's state terms are folded into the staged
+  // operands (scale a dO, -beta a dX, r Delta), so one accumulator set per output covers all value
+  // heads of the q/k head.
+  constexpr int kSB = KD * kCPb, kTB = kC * kCPb;
+  constexpr int kBig = 2 * kSB + 7 * kTB, kFin = 2 * kC * FP * 4;
+  __shared__ __align__(16) bf16 Kb[kC * KPB], Qb[kC * KPB], Tm[kC * kCPb];
+  __shared__ __align__(16) char big_[kBig * 2 > kFin ? kBig * 2 : kFin];
+  bf16* const big = reinterpret_cast<bf16*>(big_);
+  __shared__ __align__(16) ChunkGates gs;
+  __shared__ float tb_[kC], tg_[kC], red_[2];
+  bf16* const Sb = big;
+  bf16* const dSb = big + kSB;
+  bf16* const dOb = big + 2 * kSB;
+  bf16* const dOab = dOb + kTB;
+  bf16* const Vb = dOab + kTB;   // V, then r o Delta
+  bf16* const Xb = Vb + kTB;     // X, then r o K dS'
+  bf16* const Db = Xb + kTB;
+  bf16* const dXb = Db + kTB;
+  bf16* const dYb = dXb + kTB;
+  bf16* const cc1 = big;         // dG (after the value loop)
+  bf16* const cc2 = big + kTB;   // dQK
+  float* const fq = reinterpret_cast<float*>(big_);
+  float* const fk = fq + kC * FP;
+
+  ChunkLoc L;
+  if (!locate_chunk(p, blockIdx.x, L)) return;
+  const int64_t h = blockIdx.y, rep = p.HV / p.H;
+  const int t = threadIdx.x, lane = t & 63, w = __builtin_amdgcn_readfirstlane(t >> 6), g4 = lane >> 4, li = lane & 15;
+  const int bt = w >> 1, hw = w & 1;
+  const bool l2 = p.flags & GDN_FLAG_QK_L2NORM;
+  const int len = L.len;
+  const int64_t c0 = L.c0, cg = blockIdx.x;
+
+  stage_qk_rows<KD, 512>(Kb, KPB, static_cast<const bf16*>(p.k) + (c0 * p.H + h) * KD, p.H, len, l2, t);
+  stage_qk_rows<KD, 512>(Qb, KPB, static_cast<const bf16*>(p.q) + (c0 * p.H + h) * KD, p.H, len, l2, t);
+
+  f32x4 dqa[KTW], dka[KTW];
+#pragma unroll
+  for (int j = 0; j < KTW; ++j) dqa[j] = dka[j] = f32x4{};
+
+  for (int64_t rr = 0; rr < rep; ++rr) {
+    const int64_t hv = h * rep + rr;
+    stage_slice<kC, 512>(Tm, kCPb, p.tn + (c0 * p.HV + hv) * kC, (uint32_t)(p.HV * kC * 2), len, t);
+    if (w == 0) stage_gates_bwd(gs, p, c0, hv, len, lane);
+    if (t < kC) {
+      tb_[t] = 0.f;
+      tg_[t] = 0.f;
+    }
+    if (t < 2) red_[t] = 0.f;
+
+    f32x4 dA[2], dP[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) dA[j] = dP[j] = f32x4{};
+    float pb[4] = {0.f, 0.f, 0.f, 0.f}, pg[4] = {0.f, 0.f, 0.f, 0.f}, pr[4] = {0.f, 0.f, 0.f, 0.f};
+    float sdot = 0.f;
+
+#pragma unroll 1
+    for (int vh = 0; vh < NVH; ++vh) {
+      {  // S and dS' of this chunk, columns 64vh..64vh+63, fp32 -> bf16; e^{gam_c}<S, dS'> partials
+        const float* hsrc = p.hs + (cg * p.HV + hv) * (int64_t)KD * VD + 64 * vh;
+        const float* dsrc = p.dhs + (cg * p.HV + hv) * (int64_t)KD * VD + 64 * vh;
+#pragma unroll
+        for (int e0 = 0; e0 < KD * 16; e0 += 512) {
+          const int e = e0 + t, row = e >> 4, c4 = (e & 15) * 4;
+          const float4 s = *reinterpret_cast<const float4*>(hsrc + (int64_t)row * VD + c4);
+          const float4 d = *reinterpret_cast<const float4*>(dsrc + (int64_t)row * VD + c4);
+          sdot += s.x * d.x + s.y * d.y + s.z * d.z + s.w * d.w;
+          *reinterpret_cast<bf16x4*>(Sb + row * kCPb + c4) = to_bf16x4(s.x, s.y, s.z, s.w);
+          *reinterpret_cast<bf16x4*>(dSb + row * kCPb + c4) = to_bf16x4(d.x, d.y, d.z, d.w);
+        }
+      }
+      stage_slice<64, 512>(dOb, kCPb, static_cast<const bf16*>(p.dout) + (c0 * p.HV + hv) * VD + 64 * vh,
+                           (uint32_t)(p.HV * VD * 2), len, t);
+      stage_slice<64, 512>(Vb, kCPb, static_cast<const bf16*>(p.v) + (c0 * p.HV + hv) * VD + 64 * vh,
+                           (uint32_t)(p.HV * VD * 2), len, t);
+      __syncthreads();
+      // Y = K S, W = K dS', QS = Q S (tiles (bt, 2hw + j))
+      f32x4 Y[2], W[2], QS[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) Y[j] = W[j] = QS[j] = f32x4{};
+#pragma unroll 1
+      for (int s = 0; s < KS; ++s) {
+        const bf16x8 a = frag_row(Kb, KPB, 16 * bt, 32 * s, lane);
+        const bf16x8 aq = frag_row(Qb, KPB, 16 * bt, 32 * s, lane);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int ct = 2 * hw + j;
+          const bf16x8 bs = frag_col(Sb, kCPb, 32 * s, 16 * ct, lane);
+          Y[j] = mma(a, bs, Y[j]);
+          QS[j] = mma(aq, bs, QS[j]);
+          W[j] = mma(a, frag_col(dSb, kCPb, 32 * s, 16 * ct, lane), W[j]);
+        }
+      }
+      // X = beta V - beta a Y; scale a dO; the a-term of dgam, scale a_t dO_t . (Q S)_t
+      f32x4 Vv[2], Dl[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int ct = 2 * hw + j;
+        const bf16x4 vv = ld4_tr(Vb, kCPb, 16 * bt, 16 * ct, lane);
+        const bf16x4 dd = ld4_tr(dOb, kCPb, 16 * bt, 16 * ct, lane);
+        f32x4 oa;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int tok = 16 * bt + 4 * g4 + r;
+          Vv[j][r] = (float)vv[r];
+          Dl[j][r] = gs.bet[tok] * Vv[j][r] - gs.begam[tok] * Y[j][r];
+          oa[r] = p.scale * gs.egam[tok] * (float)dd[r];
+          pg[r] += oa[r] * QS[j][r];
+        }
+        put_acc(Xb, kCPb, 16 * bt, 16 * ct, lane, Dl[j]);
+        put_acc(dOab, kCPb, 16 * bt, 16 * ct, lane, oa);
+      }
+      __syncthreads();
+      // Delta = X + (T - I) X  ((T - I)_{tj} vanishes unless j < t)
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+        if (u == 0 || bt >= 2) {
+          const bf16x8 a = frag_row(Tm, kCPb, 16 * bt, 32 * u, lane);
+#pragma unroll
+          for (int j = 0; j < 2; ++j) Dl[j] = mma(a, frag_col(Xb, kCPb, 32 * u, 16 * (2 * hw + j), lane), Dl[j]);
+        }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        put_acc(Db, kCPb, 16 * bt, 16 * (2 * hw + j), lane, Dl[j]);
+        f32x4 rd;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) rd[r] = gs.dlast[16 * bt + 4 * g4 + r] * Dl[j][r];
+        put_acc(Vb, kCPb, 16 * bt, 16 * (2 * hw + j), lane, rd);
+      }
+      __syncthreads();
+      // Z = r o (K dS') -> Xb
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) W[j][r] *= gs.dlast[16 * bt + 4 * g4 + r];
+        put_acc(Xb, kCPb, 16 * bt, 16 * (2 * hw + j), lane, W[j]);
+      }
+      __syncthreads();
+      // dX = G1 + Z + (T - I)^T Z
+      f32x4 dX[2];
+      {
+        const uint32_t rb = (uint32_t)(p.HV * VD * 4);
+        const auto rs = make_rsrc(p.g1 + (c0 * p.HV + hv) * VD + 64 * vh, (uint32_t)len * rb);
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int tok = 16 * bt + 4 * g4 + r, cc = 16 * (2 * hw + j) + li;
+            dX[j][r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, (int)((uint32_t)tok * rb + cc * 4), 0, 0)) + W[j][r];
+          }
+      }
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+        if (u == 1 || bt <= 1) {
+          const bf16x8 a = frag_col(Tm, kCPb, 32 * u, 16 * bt, lane);
+#pragma unroll
+          for (int j = 0; j < 2; ++j) dX[j] = mma(a, frag_col(Xb, kCPb, 32 * u, 16 * (2 * hw + j), lane), dX[j]);
+        }
+      // dV = beta dX; row partials of dbeta and dgam
+      bf16* const dvg = static_cast<bf16*>(p.dv);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int cc = 64 * vh + 16 * (2 * hw + j) + li;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int tok = 16 * bt + 4 * g4 + r;
+          if (tok < len) dvg[((c0 + tok) * p.HV + hv) * VD + cc] = static_cast<bf16>(gs.bet[tok] * dX[j][r]);
+          pb[r] += (Vv[j][r] - gs.egam[tok] * Y[j][r]) * dX[j][r];
+          pg[r] -= gs.begam[tok] * dX[j][r] * Y[j][r];
+          pr[r] += W[j][r] * Dl[j][r];
+        }
+        put_acc(dXb, kCPb, 16 * bt, 16 * (2 * hw + j), lane, dX[j]);
+        f32x4 dy;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dy[r] = -gs.begam[16 * bt + 4 * g4 + r] * dX[j][r];
+        put_acc(dYb, kCPb, 16 * bt, 16 * (2 * hw + j), lane, dy);
+      }
+      __syncthreads();
+      // c x c: dA' += dX Delta^T, dP' += dO Delta^T (tiles (bt, 2hw + j) on or below the diagonal)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int jt = 2 * hw + j;
+        if (jt <= bt) {
+#pragma unroll
+          for (int s = 0; s < 2; ++s) {
+            const bf16x8 bd = frag_row(Db, kCPb, 16 * jt, 32 * s, lane);
+            dA[j] = mma(frag_row(dXb, kCPb, 16 * bt, 32 * s, lane), bd, dA[j]);
+            dP[j] = mma(frag_row(dOb, kCPb, 16 * bt, 32 * s, lane), bd, dP[j]);
+          }
+        }
+      }
+      // c x K: dQ += (scale a dO) S^T, dK += (-beta a dX) S^T + (r Delta) dS'^T
+#pragma unroll 1
+      for (int s = 0; s < 2; ++s) {
+        const bf16x8 ao = frag_row(dOab, kCPb, 16 * bt, 32 * s, lane);
+        const bf16x8 ay = frag_row(dYb, kCPb, 16 * bt, 32 * s, lane);
+        const bf16x8 ad = frag_row(Vb, kCPb, 16 * bt, 32 * s, lane);
+#pragma unroll
+        for (int j = 0; j < KTW; ++j) {
+          const int kt = KTW * hw + j;
+          const bf16x8 bs = frag_row(Sb, kCPb, 16 * kt, 32 * s, lane);
+          dqa[j] = mma(ao, bs, dqa[j]);
+          dka[j] = mma(ay, bs, dka[j]);
+          dka[j] = mma(ad, frag_row(dSb, kCPb, 16 * kt, 32 * s, lane), dka[j]);
+        }
+      }
+      __syncthreads();
+    }
+
+    // e^{gam_c} <S, dS'> and sum_t r_t (K dS')_t . Delta_t go to the chunk's last position
+    sdot = wave_xor_sum(sdot, 1);
+    if (lane == 0) atomicAdd(&red_[0], sdot);
+    // c x c elementwise: G = K K^T, QK = Q K^T; dA, dG, dQK; their row and column sums
+    float colp[2] = {0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int jt = 2 * hw + j;
+      f32x4 Gm = f32x4{}, QKm = f32x4{};
+      if (jt <= bt) {
+#pragma unroll 1
+        for (int s = 0; s < KS; ++s) {
+          const bf16x8 bk = frag_row(Kb, KPB, 16 * jt, 32 * s, lane);
+          Gm = mma(frag_row(Kb, KPB, 16 * bt, 32 * s, lane), bk, Gm);
+          QKm = mma(frag_row(Qb, KPB, 16 * bt, 32 * s, lane), bk, QKm);
+        }
+      }
+      const int jj = 16 * jt + li;
+      f32x4 dG, dQK;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int tok = 16 * bt + 4 * g4 + r;
+        const float e = jj <= tok ? __expf(gs.gam[tok] - gs.gam[jj]) : 0.f;
+        const float dav = jj < tok ? -dA[j][r] : 0.f;
+        dG[r] = gs.bet[tok] * dav * e;
+        dQK[r] = p.scale * dP[j][r] * e;
+        pb[r] += dav * Gm[r] * e;
+        const float pair = dG[r] * Gm[r] + dQK[r] * QKm[r];
+        pg[r] += pair;
+        colp[j] += pair;
+      }
+      put_acc(cc1, kCPb, 16 * bt, 16 * jt, lane, dG);
+      put_acc(cc2, kCPb, 16 * bt, 16 * jt, lane, dQK);
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      float x = colp[j];
+      x += __shfl_xor(x, 16, kWave);
+      x += __shfl_xor(x, 32, kWave);
+      if (g4 == 0 && x != 0.f) atomicAdd(&tg_[16 * (2 * hw + j) + li], -x);
+    }
+    float rsum = 0.f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float b = group_sum<16>(pb[r]), gg = group_sum<16>(pg[r]), rr2 = group_sum<16>(pr[r]);
+      if (li == 0) {
+        const int tok = 16 * bt + 4 * g4 + r;
+        atomicAdd(&tb_[tok], b);
+        atomicAdd(&tg_[tok], gg - rr2);
+        rsum += rr2;
+      }
+    }
+    rsum = wave_xor_sum(rsum, 1);
+    if (lane == 0) atomicAdd(&red_[1], rsum);
+    __syncthreads();
+    // dQ += dQK K;  dK += dQK^T Q + dG K + dG^T K
+#pragma unroll
+    for (int j = 0; j < KTW; ++j) {
+      const int kt = KTW * hw + j;
+#pragma unroll 1
+      for (int u = 0; u < 2; ++u) {
+        const bf16x8 bk = frag_col(Kb, KPB, 32 * u, 16 * kt, lane);
+        dqa[j] = mma(frag_row(cc2, kCPb, 16 * bt, 32 * u, lane), bk, dqa[j]);
+        dka[j] = mma(frag_col(cc2, kCPb, 32 * u, 16 * bt, lane), frag_col(Qb, KPB, 32 * u, 16 * kt, lane), dka[j]);
+        dka[j] = mma(frag_row(cc1, kCPb, 16 * bt, 32 * u, lane), bk, dka[j]);
+        dka[j] = mma(frag_col(cc1, kCPb, 32 * u, 16 * bt, lane), bk, dka[j]);
+      }
+    }
+    // dg = reverse in-chunk cumsum of dgam; dbeta; the gate and sigmoid backwards
+    if (w == 0) {
+      const float ac = gs.egam[kC - 1];
+      float dgam = tg_[lane];
+      if (lane == kC - 1) dgam += ac * red_[0] + red_[1];
+      const float incl = wave_inclusive_sum(dgam);
+      const float tot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(incl), kWave - 1));
+      float dgv = tot - incl + dgam;
+      float dbv = tb_[lane];
+      const int64_t gi = (c0 + lane) * p.HV + hv;
+      float pa = 0.f, pd = 0.f;
+      if (lane < len) {
+        const float graw = load_as_f32(p.g, p.dg, gi);
+        if (p.flags & GDN_FLAG_GATE_IN_KERNEL) {
+          const float ea = __expf(p.A_log[hv]);
+          const float gval = -ea * softplus_f32(graw + p.dt_bias[hv]);
+          pa = dgv * gval;                                   // d/dA_log
+          dgv = dgv * (-ea) * sigmoid_f32(graw + p.dt_bias[hv]);  // d/da, a the raw gate input
+          pd = dgv;                                          // d/ddt_bias
+        }
+        if (p.flags & GDN_FLAG_BETA_SIGMOID) {
+          const float sb = sigmoid_f32(load_as_f32(p.beta, p.db, gi));
+          dbv *= sb * (1.f - sb);
+        }
+        store_from_f32(p.dgate, p.dg, gi, dgv);
+        store_from_f32(p.dbeta, p.db, gi, dbv);
+      }
+      if (p.flags & GDN_FLAG_GATE_IN_KERNEL) {
+        pa = wave_xor_sum(pa, 1);
+        pd = wave_xor_sum(pd, 1);
+        if (lane == 0) {
+          p.gate_part[(cg * p.HV + hv) * 2] = pa;
+          p.gate_part[(cg * p.HV + hv) * 2 + 1] = pd;
+        }
+      }
+    }
+    __syncthreads();
+  }
+
+  // dq, dk rows through LDS, then the L2-norm backward (x / max(|x|, eps)) on the raw rows
+#pragma unroll
+  for (int j = 0; j < KTW; ++j) {
+    const int kt = KTW * hw + j;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int tok = 16 * bt + 4 * g4 + r;
+      fq[tok * FP + 16 * kt + li] = dqa[j][r];
+      fk[tok * FP + 16 * kt + li] = dka[j][r];
+    }
+  }
+  __syncthreads();
+  {
+    constexpr int KCH = KD / 8, RPP = 512 / KCH;
+    const int row0 = t / KCH, ch = t % KCH;
+    const uint32_t rb = (uint32_t)(p.H * KD * 2);
+#pragma unroll
+    for (int x = 0; x < 2; ++x) {
+      const float* src = x == 0 ? fq : fk;
+      const bf16* raw = static_cast<const bf16*>(x == 0 ? p.q : p.k) + (c0 * p.H + h) * KD;
+      bf16* dst = static_cast<bf16*>(x == 0 ? p.dq : p.dk) + (c0 * p.H + h) * KD;
+      const auto rs = make_rsrc(raw, (uint32_t)len * rb);
+#pragma unroll
+      for (int u = 0; u < kC / RPP; ++u) {
+        const int row = row0 + u * RPP;
+        float d[8];
+        const float4 d0 = *reinterpret_cast<const float4*>(src + row * FP + ch * 8);
+        const float4 d1 = *reinterpret_cast<const float4*>(src + row * FP + ch * 8 + 4);
+        d[0] = d0.x; d[1] = d0.y; d[2] = d0.z; d[3] = d0.w;
+        d[4] = d1.x; d[5] = d1.y; d[6] = d1.z; d[7] = d1.w;
+        if (l2) {
+          const bf16x8 xr = buf_load16(rs, (uint32_t)row * rb + ch * 16);
+          float ss = 0.f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) ss += (float)xr[e] * (float)xr[e];
+          ss = group_sum<KCH>(ss);
+          const float nrm = sqrtf(ss);
+          const float inv = 1.f / fmaxf(nrm, 1e-12f);
+          float dot = 0.f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) dot += (float)xr[e] * inv * d[e];
+          dot = group_sum<KCH>(dot);
+          if (nrm <= 1e-12f) dot = 0.f;  // clamped norm: x / eps is linear in x
+#pragma unroll
+          for (int e = 0; e < 8; ++e) d[e] = (d[e] - (float)xr[e] * inv * dot) * inv;
+        }
+        if (row < len) {
+          bf16x8 o;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) o[e] = static_cast<bf16>(d[e]);
+          *reinterpret_cast<bf16x8*>(dst + (int64_t)row * p.H * KD + ch * 8) = o;
+        }
+      }
+    }
+  }
+}
+
+// ================================================================== 4. dA_log, ddt_bias per head
+__global__ __launch_bounds__(256) void gated_delta_gate_param_grad_kernel(const float* part, int64_t chunks,
+                                                                          const int* chunk_first, int64_t N, int64_t HV,
+                                                                          float* dA_log, float* ddt_bias) {
+  __shared__ float red[2][4];
+  const int64_t hv = blockIdx.x;
+  const int64_t nch = chunk_first ? chunk_first[N] : chunks;
+  float a = 0.f, d = 0.f;
+  for (int64_t c = threadIdx.x; c < nch; c += 256) {
+    a += part[(c * HV + hv) * 2];
+    d += part[(c * HV + hv) * 2 + 1];
+  }
+  a = wave_xor_sum(a, 1);
+  d = wave_xor_sum(d, 1);
+  if ((threadIdx.x & 63) == 0) {
+    red[0][threadIdx.x >> 6] = a;
+    red[1][threadIdx.x >> 6] = d;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    dA_log[hv] = red[0][0] + red[0][1] + red[0][2] + red[0][3];
+    ddt_bias[hv] = red[1][0] + red[1][1] + red[1][2] + red[1][3];
+  }
+}
+
+}  // namespace gdn
+
+using namespace gdn;
+
+namespace {
+
+int64_t chunk_bound(int64_t B, int64_t T, int64_t N, bool varlen) {
+  return varlen ? (T + kC - 1) / kC + N : B * ((T + kC - 1) / kC);
+}
+
+}  // namespace
+
+extern "C" size_t gdn_chunk_states_size(int64_t B, int64_t T, int64_t HV, int64_t K, int64_t V, int64_t N, int varlen) {
+  if (B <= 0 || T < 0 || HV <= 0 || K <= 0 || V <= 0 || N <= 0) return 0;
+  return (size_t)(chunk_bound(B, T, N, varlen != 0) * HV * K * V * 4);
+}
+
+extern "C" size_t gdn_chunk_bwd_workspace_size(int64_t B, int64_t T, int64_t HV, int64_t K, int64_t V, int64_t N,
+                                               int varlen) {
+  if (B <= 0 || T < 0 || HV <= 0 || K <= 0 || V <= 0 || N <= 0) return 0;
+  const int64_t tok = B * T, ch = chunk_bound(B, T, N, varlen != 0);
+  return (size_t)(align256(tok * HV * kC * 2) + align256(tok * HV * V * 4) + align256(ch * HV * K * V * 4) +
+                  align256(ch * HV * 2 * 4));
+}
+
+extern "C" int gdn_chunk_bwd(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                             const void* d_o, const float* d_final_state, const float* chunk_states,
+                             const void* fwd_workspace, const void* cu_seqlens, int64_t B, int64_t T, int64_t H,
+                             int64_t HV, int64_t K, int64_t V, int64_t N, int qkv_dtype, int g_dtype, int beta_dtype,
+                             float scale, unsigned flags, const float* A_log, const float* dt_bias, void* dq, void* dk,
+                             void* dv, void* dg, void* dbeta, float* d_initial_state, float* dA_log, float* ddt_bias,
+                             void* workspace, size_t workspace_bytes, void* stream) {
+  if (!q || !k || !v || !g || !beta || !d_o || !chunk_states || !fwd_workspace || !dq || !dk || !dv || !dg || !dbeta) {
+    gdn_internal_set_error("gdn_chunk_bwd: null tensor pointer");
+    return GDN_ERR_INVALID;
+  }
+  if (B <= 0 || T < 0 || H <= 0 || HV <= 0 || HV % H || N <= 0 || (cu_seqlens ? B != 1 : N != B)) {
+    gdn_internal_set_error("gdn_chunk_bwd: bad sizes B=%lld T=%lld H=%lld HV=%lld N=%lld", (long long)B, (long long)T,
+                           (long long)H, (long long)HV, (long long)N);
+    return GDN_ERR_INVALID;
+  }
+  if ((flags & GDN_FLAG_GATE_IN_KERNEL) && (!A_log || !dt_bias || !dA_log || !ddt_bias)) {
+    gdn_internal_set_error("gdn_chunk_bwd: gate in kernel needs A_log, dt_bias and their gradient outputs");
+    return GDN_ERR_INVALID;
+  }
+  if ((K != 64 && K != 128) || (V != 64 && V != 128) || qkv_dtype != GDN_DTYPE_BF16) {
+    gdn_internal_set_error("gdn_chunk_bwd: K=%lld V=%lld dtype %d unsupported (64/128, bf16)", (long long)K, (long long)V,
+                           qkv_dtype);
+    return GDN_ERR_UNSUPPORTED;
+  }
+  const bool varlen = cu_seqlens != nullptr;
+  const size_t need = gdn_chunk_bwd_workspace_size(B, T, HV, K, V, N, varlen);
+  if (!workspace || workspace_bytes < need) {
+    gdn_internal_set_error("gdn_chunk_bwd: workspace of %zu bytes needed (got %zu)", need, workspace ? workspace_bytes : (size_t)0);
+    return GDN_ERR_INVALID;
+  }
+  if (T == 0) return GDN_OK;
+  const int64_t tok = B * T, chunks = chunk_bound(B, T, N, varlen);
+  if (chunks > 0x7fffffff || HV > 65535 || N * HV * (V / 32) > 0x7fffffff) {
+    gdn_internal_set_error("gdn_chunk_bwd: grid too large");
+    return GDN_ERR_UNSUPPORTED;
+  }
+  char* ws = static_cast<char*>(workspace);
+  const char* fws = static_cast<const char*>(fwd_workspace);
+  ChunkBwdParams p{};
+  p.q = q; p.k = k; p.v = v; p.g = g; p.beta = beta; p.dout = d_o;
+  p.dht = d_final_state;
+  p.hs = chunk_states;
+  p.tw = reinterpret_cast<const f16*>(fws);
+  p.tn = reinterpret_cast<bf16*>(ws);
+  p.g1 = reinterpret_cast<float*>(ws + align256(tok * HV * kC * 2));
+  p.dhs = reinterpret_cast<float*>(ws + align256(tok * HV * kC * 2) + align256(tok * HV * V * 4));
+  p.gate_part = reinterpret_cast<float*>(ws + align256(tok * HV * kC * 2) + align256(tok * HV * V * 4) +
+                                         align256(chunks * HV * K * V * 4));
+  p.cu = cu_seqlens;
+  p.chunk_first = varlen ? reinterpret_cast<const int*>(fws + chunk_t_bytes(tok, HV)) : nullptr;
+  p.cu_i32 = (flags & GDN_FLAG_CU_INT32) ? 1 : 0;
+  p.T = T; p.H = H; p.HV = HV; p.N = N;
+  p.dg = g_dtype; p.db = beta_dtype;
+  p.scale = scale; p.flags = flags;
+  p.A_log = A_log; p.dt_bias = dt_bias;
+  p.dq = dq; p.dk = dk; p.dv = dv; p.dgate = dg; p.dbeta = dbeta;
+  p.dh0 = d_initial_state; p.dA_log = dA_log; p.ddt_bias = ddt_bias;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+
+#define GDN_BWD_DISPATCH(KERNEL, GRID, BLOCK)                                                          \
+  do {                                                                                                 \
+    if (K == 128 && V == 128) hipLaunchKernelGGL((KERNEL<128, 128>), GRID, BLOCK, 0, s, p);           \
+    else if (K == 64 && V == 64) hipLaunchKernelGGL((KERNEL<64, 64>), GRID, BLOCK, 0, s, p);          \
+    else if (K == 128 && V == 64) hipLaunchKernelGGL((KERNEL<128, 64>), GRID, BLOCK, 0, s, p);        \
+    else hipLaunchKernelGGL((KERNEL<64, 128>), GRID, BLOCK, 0, s, p);                                  \
+  } while (0)
+  GDN_BWD_DISPATCH(gated_delta_chunk_bwd_prep_kernel, dim3((unsigned)chunks, (unsigned)HV), dim3(256));
+  int rc = gdn_internal_check_launch("gated_delta_chunk_bwd_prep_kernel");
+  if (rc != GDN_OK) return rc;
+  GDN_BWD_DISPATCH(gated_delta_chunk_bwd_state_kernel, dim3((unsigned)(N * HV * (V / 32))), dim3(256));
+  rc = gdn_internal_check_launch("gated_delta_chunk_bwd_state_kernel");
+  if (rc != GDN_OK) return rc;
+  GDN_BWD_DISPATCH(gated_delta_chunk_bwd_grad_kernel, dim3((unsigned)chunks, (unsigned)H), dim3(512));
+  rc = gdn_internal_check_launch("gated_delta_chunk_bwd_grad_kernel");
+  if (rc != GDN_OK) return rc;
+#undef GDN_BWD_DISPATCH
+  if (flags & GDN_FLAG_GATE_IN_KERNEL) {
+    hipLaunchKernelGGL(gated_delta_gate_param_grad_kernel, dim3((unsigned)HV), dim3(256), 0, s, p.gate_part, chunks,
+                       p.chunk_first, N, HV, dA_log, ddt_bias);
+    rc = gdn_internal_check_launch("gated_delta_gate_param_grad_kernel");
+  }
+  return rc;
+}

@@ -11,9 +11,11 @@ its imports:
 - ``l2norm``                            <- ``F.normalize(x, dim=-1)`` / FLA ``l2norm`` (gdn.py:177)
 - ``gated_delta_decode_step``           (no reference counterpart: the fused decode step)
 
-Outputs are allocated here from torch's caching allocator; the C ABI never allocates. Everything
-is forward-only: a call that would need a backward raises ``NotImplementedError`` instead of
-silently detaching. Contract violations raise ``ValueError`` with the reference's wording
+Outputs are allocated here from torch's caching allocator; the C ABI never allocates.
+``chunk_gated_delta_rule`` is differentiable (bf16 q/k/v): with inputs that require grad it runs
+the training forward, which saves the state entering every chunk, and its backward launches the
+HIP backward kernels (``gdn_chunk_bwd``). The other operators are forward-only: a call that would
+need a backward raises ``NotImplementedError`` instead of silently detaching. Contract violations raise ``ValueError`` with the reference's wording
 ("B == 1", "cu_seqlens"; ``sore/model/gdn_ref.py:42-43,54-55``).
 """
 from __future__ import annotations
@@ -119,7 +121,7 @@ def _gdn_call(entry, name, q, k, v, g, beta, scale, initial_state, output_final_
               use_qk_l2norm_in_kernel, use_beta_sigmoid_in_kernel, use_gate_in_kernel, A_log, dt_bias,
               inplace_final_state=False):
     _check_cuda(name, q, k, v, g, beta, initial_state, cu_seqlens, A_log, dt_bias)
-    _no_grad_check(name, q, k, v, g, beta, initial_state, A_log, dt_bias)
+    a_log_in, dt_bias_in = A_log, dt_bias
     b, t, h, kd, hv, vd, n, flags, scale, A_log, dt_bias = _delta_rule_args(
         name, q, k, v, g, beta, scale, initial_state, cu_seqlens, cu_seqlens_cpu,
         use_qk_l2norm_in_kernel, use_beta_sigmoid_in_kernel, use_gate_in_kernel, A_log, dt_bias)
@@ -127,6 +129,18 @@ def _gdn_call(entry, name, q, k, v, g, beta, scale, initial_state, output_final_
         # The chunk kernels stage bf16 MFMA operands. fp32/fp16 q/k/v keep their precision on the
         # recurrent kernel, which computes the same recurrence token by token in fp32.
         entry = "gdn_recurrent_fwd"
+    grad_inputs = [q, k, v, g, beta, initial_state] + ([a_log_in, dt_bias_in] if use_gate_in_kernel else [])
+    if torch.is_grad_enabled() and any(x is not None and x.requires_grad for x in grad_inputs):
+        if entry != "gdn_chunk_fwd" or inplace_final_state:
+            raise NotImplementedError(
+                f"{name}: the backward exists for chunk_gated_delta_rule with bf16 q/k/v only (inputs "
+                "require grad); run under torch.no_grad() or detach the inputs"
+            )
+        cu = cu_seqlens.contiguous() if cu_seqlens is not None else None
+        meta = (b, t, h, kd, hv, vd, n, flags, scale, bool(output_final_state))
+        return _ChunkGatedDeltaRule.apply(q, k, v, g, beta, initial_state,
+                                          a_log_in if use_gate_in_kernel else None,
+                                          dt_bias_in if use_gate_in_kernel else None, cu, meta)
     q, k, v, g, beta = (x.contiguous() for x in (q, k, v, g, beta))
     h0 = None
     if initial_state is not None:
@@ -157,6 +171,80 @@ def _gdn_call(entry, name, q, k, v, g, beta, scale, initial_state, output_final_
 def chunk_workspace_bytes(batch: int, seqlen: int, num_v_heads: int, num_seqs: int, varlen: bool) -> int:
     """Bytes of device workspace ``gdn_chunk_fwd`` needs (the per-chunk ``(I + A)^-1`` rows)."""
     return int(_lib.load().gdn_chunk_workspace_size(batch, seqlen, num_v_heads, num_seqs, int(varlen)))
+
+
+class _ChunkGatedDeltaRule(torch.autograd.Function):
+    """``chunk_gated_delta_rule`` with a backward (the reference trains through FLA's autograd function).
+
+    Forward: ``gdn_chunk_fwd_train``, which also keeps the fp32 state entering every chunk and the
+    per-chunk ``(I + A)^-1`` rows for the backward. Backward: ``gdn_chunk_bwd`` (dq, dk, dv, dg,
+    dbeta, the initial state's gradient and, with the in-kernel gate, dA_log and ddt_bias).
+    """
+
+    @staticmethod
+    def forward(ctx, q, k, v, g, beta, initial_state, A_log, dt_bias, cu, meta):
+        b, t, h, kd, hv, vd, n, flags, scale, output_final_state = meta
+        qc, kc, vc, gc, bc = (x.detach().contiguous() for x in (q, k, v, g, beta))
+        h0 = None if initial_state is None else initial_state.detach().float().contiguous()
+        al = None if A_log is None else A_log.detach().float().contiguous()
+        dtb = None if dt_bias is None else dt_bias.detach().float().contiguous()
+        lib = _lib.load()
+        varlen = cu is not None
+        o = torch.empty(b, t, hv, vd, device=q.device, dtype=q.dtype)
+        final = torch.empty(n, hv, kd, vd, device=q.device, dtype=torch.float32) if output_final_state else None
+        ws = torch.empty(max(chunk_workspace_bytes(b, t, hv, n, varlen), 1), dtype=torch.uint8, device=q.device)
+        nstate = int(lib.gdn_chunk_states_size(b, t, hv, kd, vd, n, int(varlen))) // 4
+        states = torch.empty(max(nstate, 1), dtype=torch.float32, device=q.device)
+        if t > 0:
+            _lib.call("gdn_chunk_fwd_train", _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(vc), _lib.ptr(gc), _lib.ptr(bc),
+                      _lib.ptr(h0), _lib.ptr(o), _lib.ptr(final), _lib.ptr(cu), b, t, h, hv, kd, vd, n,
+                      _lib.dtype_code(qc.dtype), _lib.dtype_code(gc.dtype), _lib.dtype_code(bc.dtype), scale, flags,
+                      _lib.ptr(al), _lib.ptr(dtb), _lib.ptr(states), _lib.ptr(ws), ws.numel(), _lib.stream_of(qc))
+        elif final is not None:
+            final.copy_(h0 if h0 is not None else torch.zeros_like(final))
+        ctx.save_for_backward(qc, kc, vc, gc, bc, al, dtb, cu, states, ws)
+        ctx.meta = meta
+        ctx.h0_dtype = None if initial_state is None else initial_state.dtype
+        ctx.param_dtypes = (None if A_log is None else A_log.dtype, None if dt_bias is None else dt_bias.dtype)
+        return o, final
+
+    @staticmethod
+    def backward(ctx, do, dfinal):
+        qc, kc, vc, gc, bc, al, dtb, cu, states, ws = ctx.saved_tensors
+        b, t, h, kd, hv, vd, n, flags, scale, _ = ctx.meta
+        dev = qc.device
+        if do is None:
+            do = torch.zeros(b, t, hv, vd, device=dev, dtype=qc.dtype)
+        do = do.to(qc.dtype).contiguous()
+        dht = None if dfinal is None else dfinal.float().contiguous()
+        dq, dk, dv = torch.empty_like(qc), torch.empty_like(kc), torch.empty_like(vc)
+        dg, db = torch.empty_like(gc), torch.empty_like(bc)
+        want_h0 = ctx.h0_dtype is not None and ctx.needs_input_grad[5]
+        dh0 = torch.empty(n, hv, kd, vd, device=dev, dtype=torch.float32) if want_h0 else None
+        gate = bool(flags & _lib.FLAG_GATE_IN_KERNEL)
+        dal = torch.empty(hv, device=dev, dtype=torch.float32) if gate else None
+        ddt = torch.empty(hv, device=dev, dtype=torch.float32) if gate else None
+        if t > 0:
+            lib = _lib.load()
+            nbytes = int(lib.gdn_chunk_bwd_workspace_size(b, t, hv, kd, vd, n, int(cu is not None)))
+            bws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+            _lib.call("gdn_chunk_bwd", _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(vc), _lib.ptr(gc), _lib.ptr(bc),
+                      _lib.ptr(do), _lib.ptr(dht), _lib.ptr(states), _lib.ptr(ws), _lib.ptr(cu), b, t, h, hv, kd, vd,
+                      n, _lib.dtype_code(qc.dtype), _lib.dtype_code(gc.dtype), _lib.dtype_code(bc.dtype), scale,
+                      flags, _lib.ptr(al), _lib.ptr(dtb), _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(dg),
+                      _lib.ptr(db), _lib.ptr(dh0), _lib.ptr(dal), _lib.ptr(ddt), _lib.ptr(bws), bws.numel(),
+                      _lib.stream_of(qc))
+        else:
+            if dh0 is not None:
+                dh0.copy_(dht if dht is not None else torch.zeros_like(dh0))
+            if gate:
+                dal.zero_()
+                ddt.zero_()
+        if dh0 is not None:
+            dh0 = dh0.to(ctx.h0_dtype)
+        if gate:
+            dal, ddt = dal.to(ctx.param_dtypes[0]), ddt.to(ctx.param_dtypes[1])
+        return dq, dk, dv, dg, db, dh0, dal, ddt, None, None
 
 
 def chunk_gated_delta_rule(

@@ -14,6 +14,7 @@ import torch.nn.functional as F
 from oracle import (
     causal_conv1d_silu,
     causal_conv1d_varlen,
+    chunk_gated_delta_rule_bwd_ref,
     chunk_gated_delta_rule_ref,
     conv_state_from_sequence,
     decode_step_ref,
@@ -395,3 +396,62 @@ def test_decode_step_equals_last_token_of_sequence():
     torch.testing.assert_close(o[:, 0], o_full[:, -1], atol=1e-5, rtol=0)
     torch.testing.assert_close(s, s_full, atol=1e-5, rtol=0)
     torch.testing.assert_close(new_cache, conv_state_from_sequence(x, width))
+
+
+# ---------------------------------------------------------------- backward of the chunked rule
+def _bwd_case(t, h, hv, kd, vd, seed, cu=None):
+    gen = torch.Generator().manual_seed(seed)
+    q = F.normalize(torch.randn(1, t, h, kd, generator=gen, dtype=torch.float64), dim=-1)
+    k = F.normalize(torch.randn(1, t, h, kd, generator=gen, dtype=torch.float64), dim=-1)
+    v = torch.randn(1, t, hv, vd, generator=gen, dtype=torch.float64)
+    g = -torch.rand(1, t, hv, generator=gen, dtype=torch.float64) * 0.3
+    beta = torch.rand(1, t, hv, generator=gen, dtype=torch.float64)
+    n = 1 if cu is None else len(cu) - 1
+    h0 = torch.randn(n, hv, kd, vd, generator=gen, dtype=torch.float64) * 0.1
+    do = torch.randn(1, t, hv, vd, generator=gen, dtype=torch.float64)
+    dht = torch.randn(n, hv, kd, vd, generator=gen, dtype=torch.float64)
+    return q, k, v, g, beta, h0, do, dht
+
+
+@pytest.mark.parametrize("case", [
+    dict(t=150, h=2, hv=4, kd=8, vd=6, chunk=16, cu=[0, 40, 41, 150]),  # GVA, varlen, partial chunks
+    dict(t=70, h=1, hv=1, kd=5, vd=3, chunk=64, cu=None),
+    dict(t=33, h=2, hv=2, kd=4, vd=4, chunk=8, cu=[0, 1, 2, 33]),        # single-token documents
+], ids=["gva_varlen", "plain", "short_docs"])
+def test_chunk_bwd_equals_autograd_through_recurrence(case):
+    """The chunk-form backward against torch autograd through the token recurrence (fp64)."""
+    cu = None if case["cu"] is None else torch.tensor(case["cu"])
+    q, k, v, g, beta, h0, do, dht = _bwd_case(case["t"], case["h"], case["hv"], case["kd"], case["vd"], 11, case["cu"])
+    leaves = [x.clone().requires_grad_(True) for x in (q, k, v, g, beta, h0)]
+    o, ht = recurrent_gated_delta_rule(*leaves[:5], scale=0.3, initial_state=leaves[5], output_final_state=True,
+                                       cu_seqlens=cu)
+    ref = torch.autograd.grad((o * do).sum() + (ht * dht).sum(), leaves)
+    mine = chunk_gated_delta_rule_bwd_ref(q, k, v, g, beta, do, scale=0.3, initial_state=h0, dht=dht, cu_seqlens=cu,
+                                          chunk_size=case["chunk"])
+    for name, a, b in zip(("dq", "dk", "dv", "dg", "dbeta", "dh0"), mine, ref):
+        torch.testing.assert_close(a, b, rtol=0, atol=1e-10, msg=lambda m, n=name: f"{n}: {m}")
+
+
+def test_chunk_bwd_plausible_mistakes_are_caught():
+    """Each plausible slip in the backward (a dropped term, a sign) moves some gradient by O(1)."""
+    q, k, v, g, beta, h0, do, dht = _bwd_case(40, 1, 1, 6, 5, 12)
+    good = chunk_gated_delta_rule_bwd_ref(q, k, v, g, beta, do, 0.4, h0, dht, chunk_size=16)
+    variants = {
+        "no_dht": chunk_gated_delta_rule_bwd_ref(q, k, v, g, beta, do, 0.4, h0, None, chunk_size=16),
+        "gate_sign": chunk_gated_delta_rule_bwd_ref(q, k, v, -g, beta, do, 0.4, h0, dht, chunk_size=16),
+        "beta_off": chunk_gated_delta_rule_bwd_ref(q, k, v, g, beta * 0.5, do, 0.4, h0, dht, chunk_size=16),
+    }
+    for name, bad in variants.items():
+        assert any(float((a - b).abs().max()) > 1e-3 for a, b in zip(good, bad)), name
+    # the finite difference of the loss matches the analytic gradient in each input direction
+    gen = torch.Generator().manual_seed(13)
+    loss = lambda *xs: (recurrent_gated_delta_rule(*xs[:5], scale=0.4, initial_state=xs[5], output_final_state=True)[0] * do).sum() \
+        + (recurrent_gated_delta_rule(*xs[:5], scale=0.4, initial_state=xs[5], output_final_state=True)[1] * dht).sum()  # noqa: E731
+    base = [q, k, v, g, beta, h0]
+    for i, grad in enumerate(good):
+        d = torch.randn(base[i].shape, generator=gen, dtype=torch.float64)
+        eps = 1e-6
+        plus = [x + eps * d if j == i else x for j, x in enumerate(base)]
+        minus = [x - eps * d if j == i else x for j, x in enumerate(base)]
+        fd = (loss(*plus) - loss(*minus)) / (2 * eps)
+        torch.testing.assert_close(fd, (grad * d).sum(), rtol=1e-6, atol=1e-8)
