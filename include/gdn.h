@@ -85,8 +85,9 @@ GDN_API int gdn_chunk_fwd(const void* q, const void* k, const void* v, const voi
 GDN_API size_t gdn_chunk_workspace_size(int64_t B, int64_t T, int64_t HV, int64_t N, int varlen);
 
 /*
- * Training forward of the chunked rule: gdn_chunk_fwd plus the fp32 state entering every chunk,
- * chunk_states [chunks][HV][K][V] (gdn_chunk_states_size bytes; chunk c of sequence n is
+ * Training forward of the chunked rule: gdn_chunk_fwd plus the state entering every chunk, rounded
+ * to bf16 and stored transposed, chunk_states [chunks][HV][V][K] (gdn_chunk_states_size bytes; the
+ * backward uses it only as a bf16 MFMA operand; chunk c of sequence n is
  * n * ceil(T / 64) + c, or the running chunk count before n plus c with cu_seqlens), which
  * gdn_chunk_bwd reads. The workspace must also be kept unchanged until gdn_chunk_bwd has run.
  * Replaces the forward half of FLA's chunk_gated_delta_rule autograd function (the call at
@@ -96,7 +97,7 @@ GDN_API int gdn_chunk_fwd_train(const void* q, const void* k, const void* v, con
                         const float* initial_state, void* o, float* final_state, const void* cu_seqlens,
                         int64_t B, int64_t T, int64_t H, int64_t HV, int64_t K, int64_t V, int64_t N,
                         int qkv_dtype, int g_dtype, int beta_dtype, float scale, unsigned flags,
-                        const float* A_log, const float* dt_bias, float* chunk_states, void* workspace,
+                        const float* A_log, const float* dt_bias, void* chunk_states, void* workspace,
                         size_t workspace_bytes, void* stream);
 
 /* Bytes of chunk_states for gdn_chunk_fwd_train / gdn_chunk_bwd (0 for invalid sizes). */
@@ -118,7 +119,7 @@ GDN_API size_t gdn_chunk_states_size(int64_t B, int64_t T, int64_t HV, int64_t K
  * workspace: gdn_chunk_bwd_workspace_size bytes, contents on entry irrelevant.
  */
 GDN_API int gdn_chunk_bwd(const void* q, const void* k, const void* v, const void* g, const void* beta,
-                  const void* d_o, const float* d_final_state, const float* chunk_states,
+                  const void* d_o, const float* d_final_state, const void* chunk_states,
                   const void* fwd_workspace, const void* cu_seqlens, int64_t B, int64_t T, int64_t H,
                   int64_t HV, int64_t K, int64_t V, int64_t N, int qkv_dtype, int g_dtype, int beta_dtype,
                   float scale, unsigned flags, const float* A_log, const float* dt_bias, void* dq, void* dk,

@@ -60,7 +60,7 @@ struct ChunkParams {
   float scale;
   unsigned flags;
   const float *A_log, *dt_bias;
-  float* hs;                 // SAVE only: the state entering each chunk, fp32 [chunks][HV][K][V]
+  bf16* hs;                  // SAVE only: the state entering each chunk, bf16 [chunks][HV][V][K] (transposed)
   const int* chunk_first;    // SAVE with cu: chunks before each sequence
 };
 
@@ -68,8 +68,9 @@ constexpr int kVB = 32;       // value columns per workgroup (two state waves of
 constexpr int kNT = 512;      // threads per workgroup (8 waves)
 constexpr int kVP = kVB + 8;  // bf16 pitch of the V and O slices (80 B rows)
 
-// SAVE (training forward): the state waves also store the fp32 state entering every chunk, the
-// input of the backward's per-chunk gradient kernel.
+// SAVE (training forward): the state waves also store the state entering every chunk, rounded to
+// bf16 and transposed ([V][K]: a lane's four consecutive keys are one 8-byte store), the input of
+// the backward's per-chunk gradient kernel, which uses it only as a bf16 MFMA operand.
 template <int KD, int VD, bool SAVE>
 __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p) {
   constexpr int NVB = VD / kVB;
@@ -379,13 +380,10 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
     if (w < 2) {
       if constexpr (SAVE) {
         const int64_t cg = (p.cu ? (int64_t)p.chunk_first[n] : n * ((p.T + kC - 1) / kC)) + i;
-        float* hp = p.hs + (cg * p.HV + hv) * (int64_t)KD * VD + vb * kVB + 16 * sw + li;
+        bf16* hp = p.hs + ((cg * p.HV + hv) * VD + vb * kVB + 16 * sw + li) * (int64_t)KD;
 #pragma unroll
-        for (int a = 0; a < KT; ++a) {
-          const int kd0 = 32 * (a >> 1) + 8 * g4 + 4 * (a & 1);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) hp[(int64_t)(kd0 + r) * VD] = S[a][r];
-        }
+        for (int a = 0; a < KT; ++a)
+          *reinterpret_cast<bf16x4*>(hp + 32 * (a >> 1) + 8 * g4 + 4 * (a & 1)) = to_bf16x4(S[a][0], S[a][1], S[a][2], S[a][3]);
       }
       const f16* kb = Kc[i % 3];
       const f16* tp = Tb[i & 1];
@@ -574,7 +572,7 @@ int chunk_fwd_impl(const void* q, const void* k, const void* v, const void* g, c
                    const float* initial_state, void* o, float* final_state, const void* cu_seqlens, int64_t B,
                    int64_t T, int64_t H, int64_t HV, int64_t K, int64_t V, int64_t N, int qkv_dtype, int g_dtype,
                    int beta_dtype, float scale, unsigned flags, const float* A_log, const float* dt_bias,
-                   float* chunk_states, void* workspace, size_t workspace_bytes, void* stream) {
+                   void* chunk_states, void* workspace, size_t workspace_bytes, void* stream) {
   if (!q || !k || !v || !g || !beta || !o) {
     gdn_internal_set_error("gdn_chunk_fwd: null tensor pointer");
     return GDN_ERR_INVALID;
@@ -625,7 +623,7 @@ int chunk_fwd_impl(const void* q, const void* k, const void* v, const void* g, c
   const int rc = launch_chunk_prep(pp, B, K, s);
   if (rc != GDN_OK) return rc;
   ChunkParams p{q, k, v, g, beta, initial_state, o, final_state, tw, cu_seqlens, order, cu_i32, T, H, HV, N,
-                g_dtype, beta_dtype, scale, flags, A_log, dt_bias, chunk_states, chunk_first};
+                g_dtype, beta_dtype, scale, flags, A_log, dt_bias, static_cast<bf16*>(chunk_states), chunk_first};
   dim3 grid((unsigned)blocks), block(kNT);
   if (chunk_states) {
     if (K == 128 && V == 128) hipLaunchKernelGGL((gated_delta_chunk_kernel<128, 128, true>), grid, block, 0, s, p);
@@ -657,7 +655,7 @@ extern "C" int gdn_chunk_fwd_train(const void* q, const void* k, const void* v, 
                                    const float* initial_state, void* o, float* final_state, const void* cu_seqlens,
                                    int64_t B, int64_t T, int64_t H, int64_t HV, int64_t K, int64_t V, int64_t N,
                                    int qkv_dtype, int g_dtype, int beta_dtype, float scale, unsigned flags,
-                                   const float* A_log, const float* dt_bias, float* chunk_states, void* workspace,
+                                   const float* A_log, const float* dt_bias, void* chunk_states, void* workspace,
                                    size_t workspace_bytes, void* stream) {
   if (!chunk_states) {
     gdn_internal_set_error("gdn_chunk_fwd_train: chunk_states is required");

@@ -42,11 +42,11 @@ namespace gdn {
 struct ChunkBwdParams {
   const void *q, *k, *v, *g, *beta, *dout;
   const float* dht;   // gradient of the final state [N][HV][K][V], or null
-  const float* hs;    // state entering each chunk, fp32 [chunks][HV][K][V] (forward output)
+  const bf16* hs;     // state entering each chunk, bf16 [chunks][HV][V][K] (forward output, transposed)
   const f16* tw;      // the forward's T - I rows (fp16, tok_col columns)
   bf16* tn;           // T - I rows, natural columns, bf16 [tokens][HV][64]      (workspace)
   float* g1;          // G1 = T^T (scale P^T dO), fp32 [tokens][HV][V]           (workspace)
-  float* dhs;         // gradient of the state leaving each chunk [chunks][HV][K][V] (workspace)
+  bf16* dhs;          // gradient of the state leaving each chunk, bf16 [chunks][HV][V][K]   (workspace)
   float* gate_part;   // per-chunk partial sums of dA_log and ddt_bias [chunks][HV][2] (workspace)
   const void* cu;
   const int* chunk_first;
@@ -312,12 +312,11 @@ __global__ __launch_bounds__(256, 1) void gated_delta_chunk_bwd_state_kernel(Chu
   for (int i = 0; i < nc; ++i) {
     const int c = nc - 1 - i, slot = i & 1;
     if (w < 2) {
-      // dS' of chunk c (the gradient of the state leaving it)
-      float* dp = p.dhs + ((cgb + c) * p.HV + hv) * (int64_t)KD * VD + col;
+      // dS' of chunk c (the gradient of the state leaving it), bf16, transposed: keys 16a + 4g..+3 of column col
+      bf16* dp = p.dhs + (((cgb + c) * p.HV + hv) * VD + col) * (int64_t)KD + 4 * g4;
 #pragma unroll
       for (int a = 0; a < KT; ++a)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) dp[(int64_t)(16 * a + 4 * g4 + r) * VD] = dS[a][r];
+        *reinterpret_cast<bf16x4*>(dp + 16 * a) = to_bf16x4(dS[a][0], dS[a][1], dS[a][2], dS[a][3]);
       const bf16* kb = Kb[slot];
       const bf16* qb = Qb[slot];
       const bf16* tm = Tm[slot];
@@ -405,12 +404,12 @@ template <int KD, int VD>
 __global__ __launch_bounds__(512, 1) void gated_delta_chunk_bwd_grad_kernel(ChunkBwdParams p) {
   constexpr int KPB = row_pitch<KD>(), KS = KD / 32, KTW = KD / 32, NVH = VD / 64;
   constexpr int FP = KD + 4;  // fp32 pitch of the dq / dk rows at the end
-  // S and dS' halves [KD][64]; dO, scale a dO, V (then r Delta), X (then r o K dS'), Delta, dX and
+  // S^T and dS'^T halves [64][KD]; dO, scale a dO, V (then r Delta), X (then r o K dS'), Delta, dX and
   // -beta a dX [64][64]. After the value loop the first two hold dG and dQK; at the end the region
   // holds dq and dk in fp32. The row scalings of dQ and dK's state terms are folded into the staged
   // operands (scale a dO, -beta a dX, r Delta), so one accumulator set per output covers all value
   // heads of the q/k head.
-  constexpr int kSB = KD * kCPb, kTB = kC * kCPb;
+  constexpr int kSB = kC * KPB, kTB = kC * kCPb;
   constexpr int kBig = 2 * kSB + 7 * kTB, kFin = 2 * kC * FP * 4;
   __shared__ __align__(16) bf16 Kb[kC * KPB], Qb[kC * KPB], Tm[kC * kCPb];
   __shared__ __align__(16) char big_[kBig * 2 > kFin ? kBig * 2 : kFin];
@@ -465,17 +464,24 @@ __global__ __launch_bounds__(512, 1) void gated_delta_chunk_bwd_grad_kernel(Chun
 
 #pragma unroll 1
     for (int vh = 0; vh < NVH; ++vh) {
-      {  // S and dS' of this chunk, columns 64vh..64vh+63, fp32 -> bf16; e^{gam_c}<S, dS'> partials
-        const float* hsrc = p.hs + (cg * p.HV + hv) * (int64_t)KD * VD + 64 * vh;
-        const float* dsrc = p.dhs + (cg * p.HV + hv) * (int64_t)KD * VD + 64 * vh;
+      {  // S^T and dS'^T rows (value columns 64vh..64vh+63, all keys); e^{gam_c}<S, dS'> partials
+        constexpr int CH = KD / 8;
+        const bf16* hsrc = p.hs + ((cg * p.HV + hv) * VD + 64 * vh) * (int64_t)KD;
+        const bf16* dsrc = p.dhs + ((cg * p.HV + hv) * VD + 64 * vh) * (int64_t)KD;
+        bf16x8 sv[kC * CH / 512], dv8[kC * CH / 512];
 #pragma unroll
-        for (int e0 = 0; e0 < KD * 16; e0 += 512) {
-          const int e = e0 + t, row = e >> 4, c4 = (e & 15) * 4;
-          const float4 s = *reinterpret_cast<const float4*>(hsrc + (int64_t)row * VD + c4);
-          const float4 d = *reinterpret_cast<const float4*>(dsrc + (int64_t)row * VD + c4);
-          sdot += s.x * d.x + s.y * d.y + s.z * d.z + s.w * d.w;
-          *reinterpret_cast<bf16x4*>(Sb + row * kCPb + c4) = to_bf16x4(s.x, s.y, s.z, s.w);
-          *reinterpret_cast<bf16x4*>(dSb + row * kCPb + c4) = to_bf16x4(d.x, d.y, d.z, d.w);
+        for (int u = 0; u < kC * CH / 512; ++u) {
+          const int e = u * 512 + t;
+          sv[u] = ld8(hsrc + (int64_t)e * 8);
+          dv8[u] = ld8(dsrc + (int64_t)e * 8);
+        }
+#pragma unroll
+        for (int u = 0; u < kC * CH / 512; ++u) {
+          const int e = u * 512 + t, row = e / CH, c8 = (e % CH) * 8;
+#pragma unroll
+          for (int x = 0; x < 8; ++x) sdot += (float)sv[u][x] * (float)dv8[u][x];
+          *reinterpret_cast<bf16x8*>(Sb + row * KPB + c8) = sv[u];
+          *reinterpret_cast<bf16x8*>(dSb + row * KPB + c8) = dv8[u];
         }
       }
       stage_slice<64, 512>(dOb, kCPb, static_cast<const bf16*>(p.dout) + (c0 * p.HV + hv) * VD + 64 * vh,
@@ -494,10 +500,10 @@ __global__ __launch_bounds__(512, 1) void gated_delta_chunk_bwd_grad_kernel(Chun
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
           const int ct = 2 * hw + j;
-          const bf16x8 bs = frag_col(Sb, kCPb, 32 * s, 16 * ct, lane);
+          const bf16x8 bs = frag_row(Sb, KPB, 16 * ct, 32 * s, lane);
           Y[j] = mma(a, bs, Y[j]);
           QS[j] = mma(aq, bs, QS[j]);
-          W[j] = mma(a, frag_col(dSb, kCPb, 32 * s, 16 * ct, lane), W[j]);
+          W[j] = mma(a, frag_row(dSb, KPB, 16 * ct, 32 * s, lane), W[j]);
         }
       }
       // X = beta V - beta a Y; scale a dO; the a-term of dgam, scale a_t dO_t . (Q S)_t
@@ -607,10 +613,10 @@ __global__ __launch_bounds__(512, 1) void gated_delta_chunk_bwd_grad_kernel(Chun
 #pragma unroll
         for (int j = 0; j < KTW; ++j) {
           const int kt = KTW * hw + j;
-          const bf16x8 bs = frag_row(Sb, kCPb, 16 * kt, 32 * s, lane);
+          const bf16x8 bs = frag_col(Sb, KPB, 32 * s, 16 * kt, lane);
           dqa[j] = mma(ao, bs, dqa[j]);
           dka[j] = mma(ay, bs, dka[j]);
-          dka[j] = mma(ad, frag_row(dSb, kCPb, 16 * kt, 32 * s, lane), dka[j]);
+          dka[j] = mma(ad, frag_col(dSb, KPB, 32 * s, 16 * kt, lane), dka[j]);
         }
       }
       __syncthreads();
@@ -819,19 +825,19 @@ int64_t chunk_bound(int64_t B, int64_t T, int64_t N, bool varlen) {
 
 extern "C" size_t gdn_chunk_states_size(int64_t B, int64_t T, int64_t HV, int64_t K, int64_t V, int64_t N, int varlen) {
   if (B <= 0 || T < 0 || HV <= 0 || K <= 0 || V <= 0 || N <= 0) return 0;
-  return (size_t)(chunk_bound(B, T, N, varlen != 0) * HV * K * V * 4);
+  return (size_t)(chunk_bound(B, T, N, varlen != 0) * HV * K * V * 2);
 }
 
 extern "C" size_t gdn_chunk_bwd_workspace_size(int64_t B, int64_t T, int64_t HV, int64_t K, int64_t V, int64_t N,
                                                int varlen) {
   if (B <= 0 || T < 0 || HV <= 0 || K <= 0 || V <= 0 || N <= 0) return 0;
   const int64_t tok = B * T, ch = chunk_bound(B, T, N, varlen != 0);
-  return (size_t)(align256(tok * HV * kC * 2) + align256(tok * HV * V * 4) + align256(ch * HV * K * V * 4) +
+  return (size_t)(align256(tok * HV * kC * 2) + align256(tok * HV * V * 4) + align256(ch * HV * K * V * 2) +
                   align256(ch * HV * 2 * 4));
 }
 
 extern "C" int gdn_chunk_bwd(const void* q, const void* k, const void* v, const void* g, const void* beta,
-                             const void* d_o, const float* d_final_state, const float* chunk_states,
+                             const void* d_o, const float* d_final_state, const void* chunk_states,
                              const void* fwd_workspace, const void* cu_seqlens, int64_t B, int64_t T, int64_t H,
                              int64_t HV, int64_t K, int64_t V, int64_t N, int qkv_dtype, int g_dtype, int beta_dtype,
                              float scale, unsigned flags, const float* A_log, const float* dt_bias, void* dq, void* dk,
@@ -872,13 +878,13 @@ extern "C" int gdn_chunk_bwd(const void* q, const void* k, const void* v, const 
   ChunkBwdParams p{};
   p.q = q; p.k = k; p.v = v; p.g = g; p.beta = beta; p.dout = d_o;
   p.dht = d_final_state;
-  p.hs = chunk_states;
+  p.hs = static_cast<const bf16*>(chunk_states);
   p.tw = reinterpret_cast<const f16*>(fws);
   p.tn = reinterpret_cast<bf16*>(ws);
   p.g1 = reinterpret_cast<float*>(ws + align256(tok * HV * kC * 2));
-  p.dhs = reinterpret_cast<float*>(ws + align256(tok * HV * kC * 2) + align256(tok * HV * V * 4));
+  p.dhs = reinterpret_cast<bf16*>(ws + align256(tok * HV * kC * 2) + align256(tok * HV * V * 4));
   p.gate_part = reinterpret_cast<float*>(ws + align256(tok * HV * kC * 2) + align256(tok * HV * V * 4) +
-                                         align256(chunks * HV * K * V * 4));
+                                         align256(chunks * HV * K * V * 2));
   p.cu = cu_seqlens;
   p.chunk_first = varlen ? reinterpret_cast<const int*>(fws + chunk_t_bytes(tok, HV)) : nullptr;
   p.cu_i32 = (flags & GDN_FLAG_CU_INT32) ? 1 : 0;

@@ -176,7 +176,7 @@ def chunk_workspace_bytes(batch: int, seqlen: int, num_v_heads: int, num_seqs: i
 class _ChunkGatedDeltaRule(torch.autograd.Function):
     """``chunk_gated_delta_rule`` with a backward (the reference trains through FLA's autograd function).
 
-    Forward: ``gdn_chunk_fwd_train``, which also keeps the fp32 state entering every chunk and the
+    Forward: ``gdn_chunk_fwd_train``, which also keeps the state entering every chunk (bf16) and the
     per-chunk ``(I + A)^-1`` rows for the backward. Backward: ``gdn_chunk_bwd`` (dq, dk, dv, dg,
     dbeta, the initial state's gradient and, with the in-kernel gate, dA_log and ddt_bias).
     """
@@ -193,8 +193,8 @@ class _ChunkGatedDeltaRule(torch.autograd.Function):
         o = torch.empty(b, t, hv, vd, device=q.device, dtype=q.dtype)
         final = torch.empty(n, hv, kd, vd, device=q.device, dtype=torch.float32) if output_final_state else None
         ws = torch.empty(max(chunk_workspace_bytes(b, t, hv, n, varlen), 1), dtype=torch.uint8, device=q.device)
-        nstate = int(lib.gdn_chunk_states_size(b, t, hv, kd, vd, n, int(varlen))) // 4
-        states = torch.empty(max(nstate, 1), dtype=torch.float32, device=q.device)
+        nstate = int(lib.gdn_chunk_states_size(b, t, hv, kd, vd, n, int(varlen)))
+        states = torch.empty(max(nstate, 1), dtype=torch.uint8, device=q.device)
         if t > 0:
             _lib.call("gdn_chunk_fwd_train", _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(vc), _lib.ptr(gc), _lib.ptr(bc),
                       _lib.ptr(h0), _lib.ptr(o), _lib.ptr(final), _lib.ptr(cu), b, t, h, hv, kd, vd, n,
