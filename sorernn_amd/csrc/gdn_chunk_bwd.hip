@@ -121,44 +121,92 @@ __device__ __forceinline__ bool locate_chunk(const ChunkBwdParams& p, int64_t it
   return true;
 }
 
-// q/k rows of a chunk (bf16, L2-normalised and rounded to bf16 when asked, exactly as the forward
-// stages them) into a [64][pitch] LDS tile; rows past len read as zeros. NT threads, tid < NT.
+// Staging of a chunk's tiles into LDS, split into fetch (the global loads, into registers) and put
+// (the LDS writes): a caller issues every fetch of a step before the first put, so the loads are in
+// flight together instead of one round trip per tile. Rows past len read as zeros (buffer range).
+//
+// q/k rows [64][KD] (bf16; L2-normalised and rounded to bf16 at the put when asked, exactly as the
+// forward stages them); NT threads, tid < NT.
 template <int KD, int NT>
-__device__ __forceinline__ void stage_qk_rows(bf16* dst, int pitch, const bf16* src, int64_t H, int len, bool l2, int tid) {
-  constexpr int KCH = KD / 8, RPP = NT / KCH;
+struct QKRows {
+  static constexpr int KCH = KD / 8, RPP = NT / KCH, N = kC / RPP;
+  bf16x8 x[N];
+};
+template <int KD, int NT>
+__device__ __forceinline__ void fetch_qk(QKRows<KD, NT>& r, const bf16* src, int64_t H, int len, int tid) {
+  using R = QKRows<KD, NT>;
   const uint32_t rb = (uint32_t)(H * KD * 2);
   const auto rs = make_rsrc(src, (uint32_t)len * rb);
-  const int row = tid / KCH, ch = tid % KCH;
-  bf16x8 x[kC / RPP];
+  const int row = tid / R::KCH, ch = tid % R::KCH;
 #pragma unroll
-  for (int u = 0; u < kC / RPP; ++u) x[u] = buf_load16(rs, (uint32_t)(row + u * RPP) * rb + ch * 16);
-#pragma unroll
-  for (int u = 0; u < kC / RPP; ++u)
-    *reinterpret_cast<bf16x8*>(dst + (row + u * RPP) * pitch + ch * 8) = l2 ? l2norm_row_chunk<KCH>(x[u]) : x[u];
+  for (int u = 0; u < R::N; ++u) r.x[u] = buf_load16(rs, (uint32_t)(row + u * R::RPP) * rb + ch * 16);
 }
-// A bf16 [64][W] slice of a [tokens][heads][*] tensor (row stride rb bytes) into LDS; rows past len read as zeros.
+template <int KD, int NT>
+__device__ __forceinline__ void put_qk(const QKRows<KD, NT>& r, bf16* dst, int pitch, bool l2, int tid) {
+  using R = QKRows<KD, NT>;
+  const int row = tid / R::KCH, ch = tid % R::KCH;
+#pragma unroll
+  for (int u = 0; u < R::N; ++u)
+    *reinterpret_cast<bf16x8*>(dst + (row + u * R::RPP) * pitch + ch * 8) = l2 ? l2norm_row_chunk<R::KCH>(r.x[u]) : r.x[u];
+}
+// A [64][W] slice (16-byte pieces) of a [tokens][heads][*] tensor with row stride rb bytes.
 template <int W, int NT>
-__device__ __forceinline__ void stage_slice(bf16* dst, int pitch, const bf16* src, uint32_t rb, int len, int tid) {
-  constexpr int CH = W / 8, TOT = kC * CH;
+struct Slice {
+  static constexpr int CH = W / 8, N = kC * CH / NT;
+  static_assert(kC * CH % NT == 0, "slice pieces must divide among the threads");
+  u32x4 x[N];
+};
+template <int W, int NT>
+__device__ __forceinline__ void fetch_slice(Slice<W, NT>& r, const void* src, uint32_t rb, int len, int tid) {
+  using R = Slice<W, NT>;
   const auto rs = make_rsrc(src, (uint32_t)len * rb);
 #pragma unroll
-  for (int e0 = 0; e0 < TOT; e0 += NT) {
-    const int e = e0 + tid;
-    if (TOT % NT == 0 || e < TOT) {
-      const int row = e / CH, ch = e % CH;
-      *reinterpret_cast<bf16x8*>(dst + row * pitch + ch * 8) = buf_load16(rs, (uint32_t)row * rb + ch * 16);
-    }
+  for (int u = 0; u < R::N; ++u) {
+    const int e = u * NT + tid, row = e / R::CH, ch = e % R::CH;
+    r.x[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)((uint32_t)row * rb + ch * 16), 0, 0);
   }
 }
-// Gate terms of a chunk (one wave, lane = token), as the forward computes them.
-__device__ __forceinline__ void stage_gates_bwd(ChunkGates& gs, const ChunkBwdParams& p, int64_t c0, int64_t hv, int len,
-                                                int lane) {
+template <int W, int NT, typename E>
+__device__ __forceinline__ void put_slice(const Slice<W, NT>& r, E* dst, int pitch, int tid) {
+  using R = Slice<W, NT>;
+  constexpr int EPC = 16 / sizeof(E);  // elements per 16-byte piece
+#pragma unroll
+  for (int u = 0; u < R::N; ++u) {
+    const int e = u * NT + tid, row = e / R::CH, ch = e % R::CH;
+    *reinterpret_cast<u32x4*>(dst + row * pitch + ch * EPC) = r.x[u];
+  }
+}
+template <int KD, int NT>
+__device__ __forceinline__ void stage_qk_rows(bf16* dst, int pitch, const bf16* src, int64_t H, int len, bool l2, int tid) {
+  QKRows<KD, NT> r;
+  fetch_qk(r, src, H, len, tid);
+  put_qk(r, dst, pitch, l2, tid);
+}
+template <int W, int NT>
+__device__ __forceinline__ void stage_slice(bf16* dst, int pitch, const bf16* src, uint32_t rb, int len, int tid) {
+  Slice<W, NT> r;
+  fetch_slice(r, src, rb, len, tid);
+  put_slice(r, dst, pitch, tid);
+}
+// Gate terms of a chunk (one wave, lane = token), as the forward computes them: raw loads, then the put.
+__device__ __forceinline__ void fetch_gates_bwd(uint32_t& graw, uint32_t& braw, const ChunkBwdParams& p, int64_t c0,
+                                                int64_t hv, int len, int lane) {
   const uint32_t gb = (uint32_t)(p.HV * dtype_bytes(p.dg)), bb = (uint32_t)(p.HV * dtype_bytes(p.db));
   const auto rg = make_rsrc(static_cast<const char*>(p.g) + (c0 * p.HV + hv) * dtype_bytes(p.dg), (uint32_t)len * gb);
   const auto rb = make_rsrc(static_cast<const char*>(p.beta) + (c0 * p.HV + hv) * dtype_bytes(p.db), (uint32_t)len * bb);
-  const uint32_t graw = buf_load_raw32(rg, lane * gb, p.dg), braw = buf_load_raw32(rb, lane * bb, p.db);
+  graw = buf_load_raw32(rg, lane * gb, p.dg);
+  braw = buf_load_raw32(rb, lane * bb, p.db);
+}
+__device__ __forceinline__ void put_gates_bwd(ChunkGates& gs, uint32_t graw, uint32_t braw, const ChunkBwdParams& p,
+                                              int64_t hv, int len, int lane) {
   chunk_gates_from_raw(gs, graw, braw, p.dg, p.db, len, p.flags, p.A_log ? p.A_log[hv] : 0.f,
                        p.dt_bias ? p.dt_bias[hv] : 0.f, lane);
+}
+__device__ __forceinline__ void stage_gates_bwd(ChunkGates& gs, const ChunkBwdParams& p, int64_t c0, int64_t hv, int len,
+                                                int lane) {
+  uint32_t graw, braw;
+  fetch_gates_bwd(graw, braw, p, c0, hv, len, lane);
+  put_gates_bwd(gs, graw, braw, p, hv, len, lane);
 }
 
 // ================================================================== 1. prep: T - I (natural) and G1
@@ -167,8 +215,12 @@ __device__ __forceinline__ void stage_gates_bwd(ChunkGates& gs, const ChunkBwdPa
 template <int KD, int VD>
 __global__ __launch_bounds__(256) void gated_delta_chunk_bwd_prep_kernel(ChunkBwdParams p) {
   constexpr int KPB = row_pitch<KD>(), VPB = row_pitch<VD>(), KS = KD / 32, VT = VD / 16;
-  __shared__ __align__(16) bf16 Kb[kC * KPB], Qb[kC * KPB], dOb[kC * VPB], Fb[kC * VPB];
+  // F reuses K's space: K is dead once P is computed. 72 KB at K = V = 128, two workgroups per CU.
+  constexpr int kKF = kC * (KPB > VPB ? KPB : VPB);
+  __shared__ __align__(16) bf16 KFb[kKF], Qb[kC * KPB], dOb[kC * VPB];
   __shared__ __align__(16) bf16 Pb[kC * kCPb], Tm[kC * kCPb];
+  bf16* const Kb = KFb;
+  bf16* const Fb = KFb;
   __shared__ __align__(16) ChunkGates gs;
   ChunkLoc L;
   if (!locate_chunk(p, blockIdx.x, L)) return;
@@ -178,17 +230,25 @@ __global__ __launch_bounds__(256) void gated_delta_chunk_bwd_prep_kernel(ChunkBw
   const int len = L.len;
   const int64_t c0 = L.c0;
 
-  stage_qk_rows<KD, 256>(Kb, KPB, static_cast<const bf16*>(p.k) + (c0 * p.H + h) * KD, p.H, len, l2, t);
-  stage_qk_rows<KD, 256>(Qb, KPB, static_cast<const bf16*>(p.q) + (c0 * p.H + h) * KD, p.H, len, l2, t);
-  stage_slice<VD, 256>(dOb, VPB, static_cast<const bf16*>(p.dout) + (c0 * p.HV + hv) * VD, (uint32_t)(p.HV * VD * 2), len, t);
+  // every global load of the chunk in flight together, then the LDS writes
+  QKRows<KD, 256> xk, xq;
+  Slice<VD, 256> xo;
+  Slice<kC, 256> xt;
+  fetch_qk(xk, static_cast<const bf16*>(p.k) + (c0 * p.H + h) * KD, p.H, len, t);
+  fetch_qk(xq, static_cast<const bf16*>(p.q) + (c0 * p.H + h) * KD, p.H, len, t);
+  fetch_slice(xo, static_cast<const bf16*>(p.dout) + (c0 * p.HV + hv) * VD, (uint32_t)(p.HV * VD * 2), len, t);
+  fetch_slice(xt, p.tw + (c0 * p.HV + hv) * kC, (uint32_t)(p.HV * kC * 2), len, t);
+  uint32_t graw = 0, braw = 0;
+  if (w == 0) fetch_gates_bwd(graw, braw, p, c0, hv, len, lane);
+  put_qk(xk, Kb, KPB, l2, t);
+  put_qk(xq, Qb, KPB, l2, t);
+  put_slice(xo, dOb, VPB, t);
   {  // T - I: fp16 rows with tok_col columns -> bf16 natural columns (LDS and the workspace)
-    const uint32_t rb = (uint32_t)(p.HV * kC * 2);
-    const auto rs = make_rsrc(p.tw + (c0 * p.HV + hv) * kC, (uint32_t)len * rb);
 #pragma unroll
-    for (int e0 = 0; e0 < kC * 8; e0 += 256) {
-      const int e = e0 + t, row = e >> 3, ch = e & 7, u = ch >> 2, gq = ch & 3;
+    for (int u8 = 0; u8 < Slice<kC, 256>::N; ++u8) {
+      const int e = u8 * 256 + t, row = e >> 3, ch = e & 7, u = ch >> 2, gq = ch & 3;
       // columns 32u + 8gq + 4hh + r of the chunk hold tokens 32u + 16hh + 4gq + r
-      const f16x8 x = __builtin_bit_cast(f16x8, buf_load16(rs, (uint32_t)row * rb + ch * 16));
+      const f16x8 x = __builtin_bit_cast(f16x8, xt.x[u8]);
       const bf16x4 lo = to_bf16x4((float)x[0], (float)x[1], (float)x[2], (float)x[3]);
       const bf16x4 hi = to_bf16x4((float)x[4], (float)x[5], (float)x[6], (float)x[7]);
       *reinterpret_cast<bf16x4*>(Tm + row * kCPb + 32 * u + 4 * gq) = lo;
@@ -200,7 +260,7 @@ __global__ __launch_bounds__(256) void gated_delta_chunk_bwd_prep_kernel(ChunkBw
       }
     }
   }
-  if (w == 0) stage_gates_bwd(gs, p, c0, hv, len, lane);
+  if (w == 0) put_gates_bwd(gs, graw, braw, p, hv, len, lane);
   __syncthreads();
 
   // scale P = scale (Q K^T) o E (j <= t), rows 16w..16w+15
@@ -220,7 +280,7 @@ __global__ __launch_bounds__(256) void gated_delta_chunk_bwd_prep_kernel(ChunkBw
     put_acc(Pb, kCPb, 16 * w, 16 * jt, lane, acc);
   }
   __syncthreads();
-  // F = (scale P)^T dO, rows (key tokens j) 16w..16w+15
+  // F = (scale P)^T dO, rows (key tokens j) 16w..16w+15 (into K's space: K is dead now)
   f32x4 F[VT];
 #pragma unroll
   for (int ct = 0; ct < VT; ++ct) {
@@ -228,8 +288,9 @@ __global__ __launch_bounds__(256) void gated_delta_chunk_bwd_prep_kernel(ChunkBw
 #pragma unroll
     for (int s = 0; s < 2; ++s)
       if (s == 1 || w <= 1) F[ct] = mma(frag_col(Pb, kCPb, 32 * s, 16 * w, lane), frag_col(dOb, VPB, 32 * s, 16 * ct, lane), F[ct]);
-    put_acc(Fb, VPB, 16 * w, 16 * ct, lane, F[ct]);
   }
+#pragma unroll
+  for (int ct = 0; ct < VT; ++ct) put_acc(Fb, VPB, 16 * w, 16 * ct, lane, F[ct]);
   __syncthreads();
   // G1 = F + (T - I)^T F  ((T - I)_{t'j} vanishes unless t' > j)
 #pragma unroll
@@ -275,25 +336,26 @@ __global__ __launch_bounds__(256, 1) void gated_delta_chunk_bwd_state_kernel(Chu
   const int nc = (int)((eos - bos + kC - 1) / kC);
   const bool l2 = p.flags & GDN_FLAG_QK_L2NORM;
 
-  auto load_chunk = [&](int c, int slot, int tl) {  // tl = 0..127 (waves 2, 3)
+  auto load_chunk = [&](int c, int slot, int tl) {  // tl = 0..127 (waves 2, 3): all loads, then the LDS writes
     const int64_t c0 = bos + (int64_t)c * kC;
     const int len = (int)((eos - c0) < kC ? (eos - c0) : kC);
-    stage_qk_rows<KD, 128>(Kb[slot], KPB, static_cast<const bf16*>(p.k) + (c0 * p.H + h) * KD, p.H, len, l2, tl);
-    stage_qk_rows<KD, 128>(Qb[slot], KPB, static_cast<const bf16*>(p.q) + (c0 * p.H + h) * KD, p.H, len, l2, tl);
-    stage_slice<kC, 128>(Tm[slot], kCPb, p.tn + (c0 * p.HV + hv) * kC, (uint32_t)(p.HV * kC * 2), len, tl);
-    stage_slice<32, 128>(dOs[slot], OP, static_cast<const bf16*>(p.dout) + (c0 * p.HV + hv) * VD + vb * 32,
-                         (uint32_t)(p.HV * VD * 2), len, tl);
-    {  // G1 slice: 64 rows x 8 chunks of 4 floats
-      const uint32_t rb = (uint32_t)(p.HV * VD * 4);
-      const auto rs = make_rsrc(p.g1 + (c0 * p.HV + hv) * VD + vb * 32, (uint32_t)len * rb);
-#pragma unroll
-      for (int e0 = 0; e0 < kC * 8; e0 += 128) {
-        const int e = e0 + tl, row = e >> 3, ch = e & 7;
-        *reinterpret_cast<u32x4*>(&G1s[slot][row * GP + ch * 4]) =
-            __builtin_bit_cast(u32x4, buf_load16(rs, (uint32_t)row * rb + ch * 16));
-      }
-    }
-    if (w == 2) stage_gates_bwd(gv[slot], p, c0, hv, len, lane);
+    QKRows<KD, 128> xk, xq;
+    Slice<kC, 128> xt;
+    Slice<32, 128> xo;
+    Slice<64, 128> xg;  // the G1 slice: 32 fp32 = 128 bytes per row, handled as 64 16-bit columns
+    fetch_qk(xk, static_cast<const bf16*>(p.k) + (c0 * p.H + h) * KD, p.H, len, tl);
+    fetch_qk(xq, static_cast<const bf16*>(p.q) + (c0 * p.H + h) * KD, p.H, len, tl);
+    fetch_slice(xt, p.tn + (c0 * p.HV + hv) * kC, (uint32_t)(p.HV * kC * 2), len, tl);
+    fetch_slice(xo, static_cast<const bf16*>(p.dout) + (c0 * p.HV + hv) * VD + vb * 32, (uint32_t)(p.HV * VD * 2), len, tl);
+    fetch_slice(xg, p.g1 + (c0 * p.HV + hv) * VD + vb * 32, (uint32_t)(p.HV * VD * 4), len, tl);
+    uint32_t graw = 0, braw = 0;
+    if (w == 2) fetch_gates_bwd(graw, braw, p, c0, hv, len, lane);
+    put_qk(xk, Kb[slot], KPB, l2, tl);
+    put_qk(xq, Qb[slot], KPB, l2, tl);
+    put_slice(xt, Tm[slot], kCPb, tl);
+    put_slice(xo, dOs[slot], OP, tl);
+    put_slice(xg, G1s[slot], GP, tl);
+    if (w == 2) put_gates_bwd(gv[slot], graw, braw, p, hv, len, lane);
   };
 
   const int sw = w & 1, col = vb * 32 + 16 * sw + li;  // state waves: value column of this lane
