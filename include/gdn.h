@@ -189,6 +189,44 @@ GDN_API int gdn_l2norm_fwd(const void* x, void* y, int64_t rows, int64_t D, int 
 GDN_API int gdn_rms_norm_gated_fwd(const void* x, const void* gate, const float* weight, const float* bias, void* y,
                            int64_t rows, int64_t D, int dtype, float eps, int activation, void* stream);
 
+/*
+ * Backward of gdn_causal_conv1d_fwd (the reference trains through FLA causal_conv1d's backward, or
+ * autograd through sore/model/conv.py:6-23 + F.silu, gdn.py:199-209). Inputs as the forward plus
+ * dy [B, T, C] (x_dtype). Outputs: dx [B, T, C] (x_dtype); dweight [C, W] and dbias [C] fp32
+ * (dbias may be NULL); d_initial_state [N, C, W] fp32 or NULL (written only with initial_state).
+ * workspace: gdn_causal_conv1d_bwd_workspace_size bytes (per-block partial sums of dweight/dbias).
+ */
+GDN_API int gdn_causal_conv1d_bwd(const void* x, const float* weight, const float* bias, const void* dy,
+                          const void* initial_state, const void* cu_seqlens, int64_t B, int64_t T, int64_t C,
+                          int64_t W, int64_t N, int x_dtype, int activation, unsigned flags, void* dx,
+                          float* dweight, float* dbias, float* d_initial_state, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
+/* Workspace bytes gdn_causal_conv1d_bwd needs (0 for invalid sizes). No counterpart in the reference. */
+GDN_API size_t gdn_causal_conv1d_bwd_workspace_size(int64_t B, int64_t T, int64_t C, int64_t W);
+
+/*
+ * Backward of gdn_l2norm_fwd: dx = (dy - y (y . dy)) / max(|x|, eps) per row (dy / eps where the
+ * norm is clamped). Replaces the autograd of F.normalize (sore/model/gdn.py:177) and FLA's
+ * l2norm backward (tests/train/test_profiling.py:30).
+ */
+GDN_API int gdn_l2norm_bwd(const void* x, const void* dy, void* dx, int64_t rows, int64_t D, int dtype, float eps,
+                   void* stream);
+
+/*
+ * Backward of gdn_rms_norm_gated_fwd (FLA rms_norm_gated's backward, sore/model/gdn.py:182-186, or
+ * autograd through RMSNorm * silu(gate), gdn.py:188 and layers.py:7-18). Outputs: dx, dgate
+ * (dtype; dgate only with a gate), dweight and dbias [D] fp32 (either may be NULL).
+ * workspace: gdn_rms_norm_gated_bwd_workspace_size bytes.
+ */
+GDN_API int gdn_rms_norm_gated_bwd(const void* x, const void* gate, const float* weight, const float* bias,
+                           const void* dy, void* dx, void* dgate, float* dweight, float* dbias, int64_t rows,
+                           int64_t D, int dtype, float eps, int activation, void* workspace,
+                           size_t workspace_bytes, void* stream);
+
+/* Workspace bytes gdn_rms_norm_gated_bwd needs. No counterpart in the reference. */
+GDN_API size_t gdn_rms_norm_gated_bwd_workspace_size(int64_t rows, int64_t D);
+
 #ifdef __cplusplus
 }
 #endif

@@ -44,6 +44,11 @@ SIGNATURES = {
     "gdn_causal_conv1d_fwd": [_P] * 7 + [_I64] * 5 + [_INT, _INT, _U, _P],
     "gdn_l2norm_fwd": [_P, _P, _I64, _I64, _INT, _F, _P],
     "gdn_rms_norm_gated_fwd": [_P] * 5 + [_I64, _I64, _INT, _F, _INT, _P],
+    "gdn_causal_conv1d_bwd": [_P] * 6 + [_I64] * 5 + [_INT, _INT, _U] + [_P] * 5 + [_SZ, _P],
+    "gdn_causal_conv1d_bwd_workspace_size": [_I64] * 4,
+    "gdn_l2norm_bwd": [_P, _P, _P, _I64, _I64, _INT, _F, _P],
+    "gdn_rms_norm_gated_bwd": [_P] * 9 + [_I64, _I64, _INT, _F, _INT, _P, _SZ, _P],
+    "gdn_rms_norm_gated_bwd_workspace_size": [_I64, _I64],
 }
 
 RESTYPES = {
@@ -51,6 +56,8 @@ RESTYPES = {
     "gdn_chunk_workspace_size": ctypes.c_size_t,
     "gdn_chunk_states_size": ctypes.c_size_t,
     "gdn_chunk_bwd_workspace_size": ctypes.c_size_t,
+    "gdn_causal_conv1d_bwd_workspace_size": ctypes.c_size_t,
+    "gdn_rms_norm_gated_bwd_workspace_size": ctypes.c_size_t,
 }
 
 _lib = None

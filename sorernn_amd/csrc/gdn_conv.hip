@@ -93,6 +93,141 @@ __global__ __launch_bounds__(256) void gated_delta_conv1d_kernel(ConvParams p) {
   }
 }
 
+// Backward (the reference trains through it: FLA causal_conv1d's backward, or autograd through
+// sore/model/conv.py:6-23 + F.silu). With z_t = bias + sum_j w[W-1-j] x_{t-j} and dz_t = dy_t act'(z_t):
+//   dx_s = sum_j w[W-1-j] dz_{s+j}   (s + j in s's document),
+//   dw[W-1-j] = sum_t dz_t x_{t-j},  dbias = sum_t dz_t,
+//   d initial_state[n, W-m] = sum over the first tokens t of document n of w[W-1-j] dz_t, t - j = start - m.
+// Same walk as the forward (thread = channel, 64 tokens per block, the window of inputs in registers)
+// over the block's tokens plus the W-1 that follow it; the dx of a position is final once the W
+// tokens that read it are done (a ring of W pending sums). dw and dbias leave as per-block partial
+// sums (reduced by gated_delta_conv1d_param_grad_kernel); the initial-state gradient is added with
+// atomics (a document's first tokens can span two blocks).
+struct ConvBwdParams {
+  const void* x;
+  const float* w;
+  const float* bias;
+  const void* dy;
+  const void* init;
+  const void* cu;
+  int cu_i32;
+  int64_t T, C, N;
+  int dx_t, act;
+  void* dx;
+  float* part;   // [blocks][C][W + 1]
+  float* dinit;  // [N][C][W] fp32, zeroed first, or null
+};
+
+template <int W>
+__global__ __launch_bounds__(256) void gated_delta_conv1d_bwd_kernel(ConvBwdParams p) {
+  const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= p.C) return;
+  const int64_t bb = blockIdx.z;
+  const int64_t t0 = (int64_t)blockIdx.y * kConvTokens;
+  if (t0 >= p.T) return;
+  const int64_t t1 = t0 + kConvTokens < p.T ? t0 + kConvTokens : p.T;
+  const int64_t tend = t1 + W - 1 < p.T ? t1 + W - 1 : p.T;
+  float w[W];
+#pragma unroll
+  for (int i = 0; i < W; ++i) w[i] = p.w[c * W + i];
+  const float bias = p.bias ? p.bias[c] : 0.f;
+  int64_t d = bb, ds = 0, de = p.T;
+  if (p.cu) {
+    int64_t lo = 0, hi = p.N - 1;
+    while (lo < hi) {
+      const int64_t mid = (lo + hi + 1) / 2;
+      if (load_index(p.cu, p.cu_i32, mid) <= t0) lo = mid;
+      else hi = mid - 1;
+    }
+    d = lo;
+    ds = load_index(p.cu, p.cu_i32, d);
+    de = load_index(p.cu, p.cu_i32, d + 1);
+  }
+  const int64_t row = bb * p.T;
+  float win[W > 1 ? W - 1 : 1];  // inputs at t - (W-1) + i
+#pragma unroll
+  for (int i = 0; i < W - 1; ++i) {
+    const int64_t pos = t0 - (W - 1) + i;
+    if (pos >= ds) win[i] = load_as_f32(p.x, p.dx_t, (row + pos) * p.C + c);
+    else if (p.init) win[i] = load_as_f32(p.init, p.dx_t, (d * p.C + c) * W + (W - (ds - pos)));
+    else win[i] = 0.f;
+  }
+  float pend[W];  // pending dx of positions t - (W-1) + i
+#pragma unroll
+  for (int i = 0; i < W; ++i) pend[i] = 0.f;
+  float dw[W], db = 0.f;
+#pragma unroll
+  for (int i = 0; i < W; ++i) dw[i] = 0.f;
+  for (int64_t t = t0; t < tend; ++t) {
+    // position t - W is complete: store it if this block owns it
+    if (t - W >= t0) store_from_f32(p.dx, p.dx_t, (row + t - W) * p.C + c, pend[0]);
+#pragma unroll
+    for (int i = 0; i + 1 < W; ++i) pend[i] = pend[i + 1];
+    pend[W - 1] = 0.f;
+    while (t >= de) {
+      ++d;
+      ds = de;
+      de = load_index(p.cu, p.cu_i32, d + 1);
+#pragma unroll
+      for (int i = 0; i < W - 1; ++i)
+        win[i] = p.init ? load_as_f32(p.init, p.dx_t, (d * p.C + c) * W + i + 1) : 0.f;
+    }
+    const float xt = load_as_f32(p.x, p.dx_t, (row + t) * p.C + c);
+    float z = bias + w[W - 1] * xt;
+#pragma unroll
+    for (int i = 0; i < W - 1; ++i) z += w[i] * win[i];
+    float dz = load_as_f32(p.dy, p.dx_t, (row + t) * p.C + c);
+    if (p.act == GDN_ACT_SILU) {
+      const float sg = sigmoid_f32(z);
+      dz *= sg * (1.f + z * (1.f - sg));
+    }
+    const bool own = t < t1;
+#pragma unroll
+    for (int j = 0; j < W; ++j) {
+      const int64_t pos = t - j;
+      const float xin = j == 0 ? xt : win[W - 1 - j];
+      if (pos >= ds) {
+        pend[W - 1 - j] += w[W - 1 - j] * dz;
+      } else if (own && p.dinit) {
+        atomicAdd(&p.dinit[(d * p.C + c) * W + (W - (ds - pos))], w[W - 1 - j] * dz);
+      }
+      if (own) dw[W - 1 - j] += dz * xin;
+    }
+    if (own) db += dz;
+#pragma unroll
+    for (int i = 0; i + 1 < W - 1; ++i) win[i] = win[i + 1];
+    if (W > 1) win[W - 2] = xt;
+  }
+  // flush: pend[i] is position tend - W + i
+#pragma unroll
+  for (int i = 0; i < W; ++i) {
+    const int64_t pos = tend - W + i;
+    if (pos >= t0 && pos < t1) store_from_f32(p.dx, p.dx_t, (row + pos) * p.C + c, pend[i]);
+  }
+  const int64_t blk = bb * gridDim.y + blockIdx.y;
+  float* pp = p.part + (blk * p.C + c) * (W + 1);
+#pragma unroll
+  for (int i = 0; i < W; ++i) pp[i] = dw[i];
+  pp[W] = db;
+}
+
+// dweight [C][W] and dbias [C] (fp32) from the per-block partial sums [blocks][C][W + 1].
+__global__ __launch_bounds__(256) void gated_delta_conv1d_param_grad_kernel(const float* part, int64_t blocks, int64_t C,
+                                                                            int W, float* dw, float* dbias) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // = c * (W + 1) + i
+  if (e >= C * (W + 1)) return;
+  float acc = 0.f;
+  for (int64_t b = 0; b < blocks; ++b) acc += part[b * C * (W + 1) + e];
+  const int64_t c = e / (W + 1), i = e % (W + 1);
+  if (i < W) dw[c * W + i] = acc;
+  else if (dbias) dbias[c] = acc;
+}
+
+__global__ void gated_delta_fill_zero_kernel(float* p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0.f;
+}
+
 }  // namespace gdn
 
 using namespace gdn;
@@ -139,4 +274,73 @@ extern "C" int gdn_causal_conv1d_fwd(const void* x, const float* weight, const f
     default: hipLaunchKernelGGL(gated_delta_conv1d_kernel<8>, grid, block, 0, s, p); break;
   }
   return gdn_internal_check_launch("gated_delta_conv1d_kernel");
+}
+
+extern "C" size_t gdn_causal_conv1d_bwd_workspace_size(int64_t B, int64_t T, int64_t C, int64_t W) {
+  if (B <= 0 || T < 0 || C <= 0 || W < 1) return 0;
+  return (size_t)(B * ((T + kConvTokens - 1) / kConvTokens) * C * (W + 1) * 4);
+}
+
+extern "C" int gdn_causal_conv1d_bwd(const void* x, const float* weight, const float* bias, const void* dy,
+                                     const void* initial_state, const void* cu_seqlens, int64_t B, int64_t T, int64_t C,
+                                     int64_t W, int64_t N, int x_dtype, int activation, unsigned flags, void* dx,
+                                     float* dweight, float* dbias, float* d_initial_state, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
+  if (!x || !weight || !dy || !dx || !dweight) {
+    gdn_internal_set_error("gdn_causal_conv1d_bwd: null tensor pointer");
+    return GDN_ERR_INVALID;
+  }
+  if (B <= 0 || T < 0 || C <= 0 || N <= 0 || (cu_seqlens ? B != 1 : N != B)) {
+    gdn_internal_set_error("gdn_causal_conv1d_bwd: bad sizes B=%lld T=%lld C=%lld N=%lld (cu_seqlens needs B == 1)",
+                           (long long)B, (long long)T, (long long)C, (long long)N);
+    return GDN_ERR_INVALID;
+  }
+  if (W < 1 || W > 8) {
+    gdn_internal_set_error("gdn_causal_conv1d_bwd: kernel width %lld unsupported (1..8)", (long long)W);
+    return GDN_ERR_UNSUPPORTED;
+  }
+  if (activation != GDN_ACT_NONE && activation != GDN_ACT_SILU) {
+    gdn_internal_set_error("gdn_causal_conv1d_bwd: unknown activation %d", activation);
+    return GDN_ERR_INVALID;
+  }
+  const size_t need = gdn_causal_conv1d_bwd_workspace_size(B, T, C, W);
+  if (need > 0 && (!workspace || workspace_bytes < need)) {
+    gdn_internal_set_error("gdn_causal_conv1d_bwd: workspace of %zu bytes needed", need);
+    return GDN_ERR_INVALID;
+  }
+  const int64_t tb = (T + kConvTokens - 1) / kConvTokens;
+  if (tb > 65535 || B > 65535) {
+    gdn_internal_set_error("gdn_causal_conv1d_bwd: T=%lld B=%lld exceed the grid limits", (long long)T, (long long)B);
+    return GDN_ERR_UNSUPPORTED;
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (d_initial_state) {
+    const int64_t n = N * C * W;
+    hipLaunchKernelGGL(gated_delta_fill_zero_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, d_initial_state, n);
+  }
+  if (T == 0) {
+    const int64_t n = C * W;  // no tokens: zero parameter gradients
+    hipLaunchKernelGGL(gated_delta_fill_zero_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, dweight, n);
+    if (dbias) hipLaunchKernelGGL(gated_delta_fill_zero_kernel, dim3((unsigned)((C + 255) / 256)), dim3(256), 0, s, dbias, C);
+    return gdn_internal_check_launch("gated_delta_fill_zero_kernel");
+  }
+  ConvBwdParams p{x, weight, bias, dy, initial_state, cu_seqlens, (flags & GDN_FLAG_CU_INT32) ? 1 : 0, T, C, N,
+                  x_dtype, activation, dx, static_cast<float*>(workspace), initial_state ? d_initial_state : nullptr};
+  dim3 grid((unsigned)((C + 255) / 256), (unsigned)tb, (unsigned)B), block(256);
+  switch (W) {
+    case 1: hipLaunchKernelGGL(gated_delta_conv1d_bwd_kernel<1>, grid, block, 0, s, p); break;
+    case 2: hipLaunchKernelGGL(gated_delta_conv1d_bwd_kernel<2>, grid, block, 0, s, p); break;
+    case 3: hipLaunchKernelGGL(gated_delta_conv1d_bwd_kernel<3>, grid, block, 0, s, p); break;
+    case 4: hipLaunchKernelGGL(gated_delta_conv1d_bwd_kernel<4>, grid, block, 0, s, p); break;
+    case 5: hipLaunchKernelGGL(gated_delta_conv1d_bwd_kernel<5>, grid, block, 0, s, p); break;
+    case 6: hipLaunchKernelGGL(gated_delta_conv1d_bwd_kernel<6>, grid, block, 0, s, p); break;
+    case 7: hipLaunchKernelGGL(gated_delta_conv1d_bwd_kernel<7>, grid, block, 0, s, p); break;
+    default: hipLaunchKernelGGL(gated_delta_conv1d_bwd_kernel<8>, grid, block, 0, s, p); break;
+  }
+  int rc = gdn_internal_check_launch("gated_delta_conv1d_bwd_kernel");
+  if (rc != GDN_OK) return rc;
+  const int64_t ne = C * (W + 1);
+  hipLaunchKernelGGL(gated_delta_conv1d_param_grad_kernel, dim3((unsigned)((ne + 255) / 256)), dim3(256), 0, s,
+                     static_cast<const float*>(workspace), B * tb, C, (int)W, dweight, dbias);
+  return gdn_internal_check_launch("gated_delta_conv1d_param_grad_kernel");
 }

@@ -58,6 +58,119 @@ __global__ __launch_bounds__(256) void gated_delta_norm_kernel(NormParams p) {
   }
 }
 
+// Backward of both norms, one wave per row (the reference trains through F.normalize and through
+// RMSNorm * silu(gate) by autograd, sore/model/gdn.py:177,180-188; FLA's fused l2norm and
+// rms_norm_gated kernels have their own backward):
+//   L2:  y = x / max(|x|, eps):          dx = (dy - y (y . dy)) / |x|   (dy / eps where |x| <= eps)
+//   RMS: n = x r, r = rsqrt(mean(x^2) + eps), u = n w + b, y = u act(g):
+//        du = dy act(g), dg = dy u act'(g), dx = r (du w) - x r^3 mean((du w) x),
+//        dw = sum_rows du n, db = sum_rows du  (per-wave partial sums, reduced by a second kernel).
+struct NormBwdParams {
+  const void* x;
+  const void* gate;
+  const float* w;
+  const float* bias;
+  const void* dy;
+  void* dx;
+  void* dgate;
+  float* part;  // [waves][2][D] partial dw, db (RMS mode)
+  int64_t rows, D;
+  int dt, act;
+  float eps;
+  int mode;
+};
+
+__global__ __launch_bounds__(256) void gated_delta_norm_bwd_kernel(NormBwdParams p) {
+  const int lane = threadIdx.x % kWave;
+  const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+  const int64_t nwaves = ((int64_t)gridDim.x * blockDim.x) / kWave;
+  float pw[kNormMaxPerLane], pb[kNormMaxPerLane];
+#pragma unroll
+  for (int j = 0; j < kNormMaxPerLane; ++j) pw[j] = pb[j] = 0.f;
+  for (int64_t r = wave; r < p.rows; r += nwaves) {
+    const int64_t base = r * p.D;
+    float xv[kNormMaxPerLane], dv[kNormMaxPerLane];
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < kNormMaxPerLane; ++j) {
+      const int64_t e = lane + (int64_t)j * kWave;
+      xv[j] = e < p.D ? load_as_f32(p.x, p.dt, base + e) : 0.f;
+      dv[j] = e < p.D ? load_as_f32(p.dy, p.dt, base + e) : 0.f;
+      ss += xv[j] * xv[j];
+    }
+    ss = wave_xor_sum(ss, 1);
+    if (p.mode == 0) {
+      const float nrm = sqrtf(ss), inv = 1.f / fmaxf(nrm, p.eps);
+      float dot = 0.f;
+#pragma unroll
+      for (int j = 0; j < kNormMaxPerLane; ++j) dot += xv[j] * inv * dv[j];
+      dot = nrm > p.eps ? wave_xor_sum(dot, 1) : 0.f;
+#pragma unroll
+      for (int j = 0; j < kNormMaxPerLane; ++j) {
+        const int64_t e = lane + (int64_t)j * kWave;
+        if (e >= p.D) break;
+        store_from_f32(p.dx, p.dt, base + e, (dv[j] - xv[j] * inv * dot) * inv);
+      }
+    } else {
+      const float rr = 1.f / sqrtf(ss / (float)p.D + p.eps);
+      float dot = 0.f;
+#pragma unroll
+      for (int j = 0; j < kNormMaxPerLane; ++j) {
+        const int64_t e = lane + (int64_t)j * kWave;
+        if (e >= p.D) break;
+        const float n = xv[j] * rr, wv = p.w ? p.w[e] : 1.f;
+        float du = dv[j];
+        if (p.gate) {
+          const float gv = load_as_f32(p.gate, p.dt, base + e);
+          const float u = n * wv + (p.bias ? p.bias[e] : 0.f);
+          float act = gv, dact = 1.f;
+          if (p.act == GDN_ACT_SILU) {
+            const float sg = sigmoid_f32(gv);
+            act = gv * sg;
+            dact = sg * (1.f + gv * (1.f - sg));
+          }
+          store_from_f32(p.dgate, p.dt, base + e, du * u * dact);
+          du *= act;
+        }
+        pw[j] += du * n;
+        pb[j] += du;
+        dv[j] = du * wv;  // dn
+        dot += dv[j] * xv[j];
+      }
+      dot = wave_xor_sum(dot, 1) / (float)p.D;
+#pragma unroll
+      for (int j = 0; j < kNormMaxPerLane; ++j) {
+        const int64_t e = lane + (int64_t)j * kWave;
+        if (e >= p.D) break;
+        store_from_f32(p.dx, p.dt, base + e, rr * dv[j] - xv[j] * rr * rr * rr * dot);
+      }
+    }
+  }
+  if (p.mode == 1) {
+#pragma unroll
+    for (int j = 0; j < kNormMaxPerLane; ++j) {
+      const int64_t e = lane + (int64_t)j * kWave;
+      if (e >= p.D) break;
+      p.part[(wave * 2) * p.D + e] = pw[j];
+      p.part[(wave * 2 + 1) * p.D + e] = pb[j];
+    }
+  }
+}
+
+// dweight, dbias [D] from the per-wave partial sums [waves][2][D].
+__global__ __launch_bounds__(256) void gated_delta_norm_param_grad_kernel(const float* part, int64_t waves, int64_t D,
+                                                                          float* dw, float* db) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // = k * D + col, k = 0 (dw), 1 (db)
+  if (e >= 2 * D) return;
+  const int64_t k = e / D, col = e % D;
+  float acc = 0.f;
+  for (int64_t wv = 0; wv < waves; ++wv) acc += part[(wv * 2 + k) * D + col];
+  float* out = k == 0 ? dw : db;
+  if (out) out[col] = acc;
+}
+
+constexpr int64_t kNormBwdBlocks = 1024;  // the RMS backward's grid: 4096 waves of partial sums
+
 static int launch_norm(const NormParams& p, void* stream, const char* what) {
   if (p.rows == 0) return GDN_OK;
   int64_t blocks = (p.rows + 3) / 4;
@@ -99,4 +212,58 @@ extern "C" int gdn_rms_norm_gated_fwd(const void* x, const void* gate, const flo
   }
   NormParams p{x, gate, weight, bias, y, rows, D, dtype, activation, eps, 1};
   return launch_norm(p, stream, "gated_delta_norm_kernel(rms)");
+}
+
+extern "C" int gdn_l2norm_bwd(const void* x, const void* dy, void* dx, int64_t rows, int64_t D, int dtype, float eps,
+                              void* stream) {
+  if (!x || !dy || !dx || rows < 0 || D <= 0) {
+    gdn_internal_set_error("gdn_l2norm_bwd: bad arguments (rows=%lld D=%lld)", (long long)rows, (long long)D);
+    return GDN_ERR_INVALID;
+  }
+  if (D > kNormMaxPerLane * kWave) {
+    gdn_internal_set_error("gdn_l2norm_bwd: D=%lld exceeds %d", (long long)D, kNormMaxPerLane * kWave);
+    return GDN_ERR_UNSUPPORTED;
+  }
+  if (rows == 0) return GDN_OK;
+  NormBwdParams p{x, nullptr, nullptr, nullptr, dy, dx, nullptr, nullptr, rows, D, dtype, GDN_ACT_NONE, eps, 0};
+  int64_t blocks = (rows + 3) / 4;
+  if (blocks > 65536) blocks = 65536;
+  hipLaunchKernelGGL(gated_delta_norm_bwd_kernel, dim3((unsigned)blocks), dim3(256), 0, static_cast<hipStream_t>(stream), p);
+  return gdn_internal_check_launch("gated_delta_norm_bwd_kernel(l2)");
+}
+
+extern "C" size_t gdn_rms_norm_gated_bwd_workspace_size(int64_t rows, int64_t D) {
+  if (rows < 0 || D <= 0) return 0;
+  return (size_t)(kNormBwdBlocks * 4 * 2 * D * 4);
+}
+
+extern "C" int gdn_rms_norm_gated_bwd(const void* x, const void* gate, const float* weight, const float* bias,
+                                      const void* dy, void* dx, void* dgate, float* dweight, float* dbias, int64_t rows,
+                                      int64_t D, int dtype, float eps, int activation, void* workspace,
+                                      size_t workspace_bytes, void* stream) {
+  if (!x || !dy || !dx || rows < 0 || D <= 0 || (gate && !dgate)) {
+    gdn_internal_set_error("gdn_rms_norm_gated_bwd: bad arguments (rows=%lld D=%lld)", (long long)rows, (long long)D);
+    return GDN_ERR_INVALID;
+  }
+  if (D > kNormMaxPerLane * kWave) {
+    gdn_internal_set_error("gdn_rms_norm_gated_bwd: D=%lld exceeds %d", (long long)D, kNormMaxPerLane * kWave);
+    return GDN_ERR_UNSUPPORTED;
+  }
+  if (activation != GDN_ACT_NONE && activation != GDN_ACT_SILU) {
+    gdn_internal_set_error("gdn_rms_norm_gated_bwd: unknown activation %d", activation);
+    return GDN_ERR_INVALID;
+  }
+  const size_t need = gdn_rms_norm_gated_bwd_workspace_size(rows, D);
+  if (!workspace || workspace_bytes < need) {
+    gdn_internal_set_error("gdn_rms_norm_gated_bwd: workspace of %zu bytes needed", need);
+    return GDN_ERR_INVALID;
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  NormBwdParams p{x, gate, weight, bias, dy, dx, dgate, static_cast<float*>(workspace), rows, D, dtype, activation, eps, 1};
+  hipLaunchKernelGGL(gated_delta_norm_bwd_kernel, dim3((unsigned)kNormBwdBlocks), dim3(256), 0, s, p);
+  int rc = gdn_internal_check_launch("gated_delta_norm_bwd_kernel(rms)");
+  if (rc != GDN_OK) return rc;
+  hipLaunchKernelGGL(gated_delta_norm_param_grad_kernel, dim3((unsigned)((2 * D + 255) / 256)), dim3(256), 0, s,
+                     static_cast<const float*>(workspace), (int64_t)kNormBwdBlocks * 4, D, dweight, dbias);
+  return gdn_internal_check_launch("gated_delta_norm_param_grad_kernel");
 }

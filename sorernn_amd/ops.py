@@ -12,10 +12,12 @@ its imports:
 - ``gated_delta_decode_step``           (no reference counterpart: the fused decode step)
 
 Outputs are allocated here from torch's caching allocator; the C ABI never allocates.
-``chunk_gated_delta_rule`` is differentiable (bf16 q/k/v): with inputs that require grad it runs
-the training forward, which saves the state entering every chunk, and its backward launches the
-HIP backward kernels (``gdn_chunk_bwd``). The other operators are forward-only: a call that would
-need a backward raises ``NotImplementedError`` instead of silently detaching. Contract violations raise ``ValueError`` with the reference's wording
+``chunk_gated_delta_rule`` (bf16 q/k/v), ``causal_conv1d``, ``l2norm`` and ``rms_norm_gated`` are
+differentiable: with inputs that require grad they run as autograd functions whose backward
+launches the HIP backward kernels (``gdn_chunk_bwd``, ``gdn_causal_conv1d_bwd``, ``gdn_l2norm_bwd``,
+``gdn_rms_norm_gated_bwd``); the chunk forward then also saves the state entering every chunk. The
+recurrent/decode operators are forward-only: a call that would need their backward raises
+``NotImplementedError`` instead of silently detaching. Contract violations raise ``ValueError`` with the reference's wording
 ("B == 1", "cu_seqlens"; ``sore/model/gdn_ref.py:42-43,54-55``).
 """
 from __future__ import annotations
@@ -203,6 +205,7 @@ class _ChunkGatedDeltaRule(torch.autograd.Function):
         elif final is not None:
             final.copy_(h0 if h0 is not None else torch.zeros_like(final))
         ctx.save_for_backward(qc, kc, vc, gc, bc, al, dtb, cu, states, ws)
+        ctx.set_materialize_grads(False)
         ctx.meta = meta
         ctx.h0_dtype = None if initial_state is None else initial_state.dtype
         ctx.param_dtypes = (None if A_log is None else A_log.dtype, None if dt_bias is None else dt_bias.dtype)
@@ -413,7 +416,6 @@ def causal_conv1d(
     if residual is not None:
         raise NotImplementedError(f"{name}: residual is not supported")
     _check_cuda(name, x, weight, bias, initial_state, cu_seqlens)
-    _no_grad_check(name, x, weight, bias, initial_state)
     if x.dim() != 3 or weight.dim() != 2 or weight.shape[0] != x.shape[2]:
         raise ValueError(f"{name}: expected x [B,T,C] and weight [C,W], got {tuple(x.shape)}, {tuple(weight.shape)}")
     b, t, c = x.shape
@@ -425,16 +427,18 @@ def causal_conv1d(
         act = _lib.ACT_NONE
     else:
         raise NotImplementedError(f"{name}: activation {activation!r} is not supported")
+    if initial_state is not None and tuple(initial_state.shape) != (n, c, w):
+        raise ValueError(f"{name}: initial_state must be [N,C,W] = {(n, c, w)}")
+    cu = cu_seqlens.contiguous() if cu_seqlens is not None else None
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (x, weight, bias, initial_state)):
+        return _CausalConv1d.apply(x, weight, bias, initial_state, cu, (b, t, c, w, n, flags, act, bool(output_final_state)))
     x = x.contiguous()
     if initial_state is not None:
-        if tuple(initial_state.shape) != (n, c, w):
-            raise ValueError(f"{name}: initial_state must be [N,C,W] = {(n, c, w)}")
         initial_state = initial_state.to(x.dtype).contiguous()
     wgt = weight.detach().float().contiguous()
     bs = None if bias is None else bias.detach().float().contiguous()
     y = torch.empty_like(x)
     fin = torch.empty(n, c, w, device=x.device, dtype=x.dtype) if output_final_state else None
-    cu = cu_seqlens.contiguous() if cu_seqlens is not None else None
     _lib.call("gdn_causal_conv1d_fwd", _lib.ptr(x), _lib.ptr(wgt), _lib.ptr(bs), _lib.ptr(y), _lib.ptr(initial_state),
               _lib.ptr(fin), _lib.ptr(cu), b, t, c, w, n, _lib.dtype_code(x.dtype), act, flags, _lib.stream_of(x))
     return y, fin
@@ -443,7 +447,8 @@ def causal_conv1d(
 def l2norm(x: Tensor, eps: float = 1e-12) -> Tensor:
     """``x / max(||x||_2, eps)`` over the last axis (``F.normalize`` semantics, fp32 math, one rounding)."""
     _check_cuda("l2norm", x)
-    _no_grad_check("l2norm", x)
+    if torch.is_grad_enabled() and x.requires_grad:
+        return _L2Norm.apply(x, float(eps))
     xc = x.contiguous()
     y = torch.empty_like(xc)
     d = xc.shape[-1]
@@ -477,19 +482,132 @@ def rms_norm_gated(
     else:
         raise NotImplementedError(f"{name}: activation {activation!r} is not supported")
     _check_cuda(name, x, g, weight, bias)
-    _no_grad_check(name, x, g, weight, bias)
+    if g is not None and g.shape != x.shape:
+        raise ValueError(f"{name}: gate shape {tuple(g.shape)} != x shape {tuple(x.shape)}")
+    d = x.shape[-1]
+    if (weight is not None and weight.numel() != d) or (bias is not None and bias.numel() != d):
+        raise ValueError(f"{name}: weight/bias must have {d} entries")
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (x, g, weight, bias)):
+        return _RMSNormGated.apply(x, g, weight, bias, float(eps), act)
     xc = x.contiguous()
-    d = xc.shape[-1]
     gc = None
     if g is not None:
-        if g.shape != x.shape:
-            raise ValueError(f"{name}: gate shape {tuple(g.shape)} != x shape {tuple(x.shape)}")
         gc = g.to(xc.dtype).contiguous()
     wc = None if weight is None else weight.detach().float().contiguous()
     bc = None if bias is None else bias.detach().float().contiguous()
-    if (wc is not None and wc.numel() != d) or (bc is not None and bc.numel() != d):
-        raise ValueError(f"{name}: weight/bias must have {d} entries")
     y = torch.empty_like(xc)
     _lib.call("gdn_rms_norm_gated_fwd", _lib.ptr(xc), _lib.ptr(gc), _lib.ptr(wc), _lib.ptr(bc), _lib.ptr(y),
               xc.numel() // max(d, 1), d, _lib.dtype_code(xc.dtype), float(eps), act, _lib.stream_of(xc))
     return y
+
+
+class _CausalConv1d(torch.autograd.Function):
+    """``causal_conv1d`` with a backward (``gdn_causal_conv1d_bwd``).
+
+    The conv cache output (``final_state``) is the decode path's state: a gradient through it is not
+    supported and raises in the backward.
+    """
+
+    @staticmethod
+    def forward(ctx, x, weight, bias, initial_state, cu, meta):
+        b, t, c, w, n, flags, act, output_final_state = meta
+        xc = x.detach().contiguous()
+        init = None if initial_state is None else initial_state.detach().to(x.dtype).contiguous()
+        wgt = weight.detach().float().contiguous()
+        bs = None if bias is None else bias.detach().float().contiguous()
+        y = torch.empty_like(xc)
+        fin = torch.empty(n, c, w, device=x.device, dtype=x.dtype) if output_final_state else None
+        _lib.call("gdn_causal_conv1d_fwd", _lib.ptr(xc), _lib.ptr(wgt), _lib.ptr(bs), _lib.ptr(y), _lib.ptr(init),
+                  _lib.ptr(fin), _lib.ptr(cu), b, t, c, w, n, _lib.dtype_code(xc.dtype), act, flags, _lib.stream_of(xc))
+        ctx.save_for_backward(xc, wgt, bs, init, cu)
+        ctx.set_materialize_grads(False)
+        ctx.meta = meta
+        ctx.dtypes = (weight.dtype, None if bias is None else bias.dtype,
+                      None if initial_state is None else initial_state.dtype)
+        return y, fin
+
+    @staticmethod
+    def backward(ctx, dy, dfin):
+        if dfin is not None:
+            raise NotImplementedError("causal_conv1d: no gradient through final_state (the decode cache)")
+        xc, wgt, bs, init, cu = ctx.saved_tensors
+        b, t, c, w, n, flags, act, _ = ctx.meta
+        dy = torch.zeros_like(xc) if dy is None else dy.to(xc.dtype).contiguous()
+        dx = torch.empty_like(xc)
+        dw = torch.empty(c, w, device=xc.device, dtype=torch.float32)
+        db = None if bs is None else torch.empty(c, device=xc.device, dtype=torch.float32)
+        dinit = None if init is None else torch.empty(n, c, w, device=xc.device, dtype=torch.float32)
+        lib = _lib.load()
+        ws = torch.empty(max(int(lib.gdn_causal_conv1d_bwd_workspace_size(b, t, c, w)), 1), dtype=torch.uint8,
+                         device=xc.device)
+        _lib.call("gdn_causal_conv1d_bwd", _lib.ptr(xc), _lib.ptr(wgt), _lib.ptr(bs), _lib.ptr(dy), _lib.ptr(init),
+                  _lib.ptr(cu), b, t, c, w, n, _lib.dtype_code(xc.dtype), act, flags, _lib.ptr(dx), _lib.ptr(dw),
+                  _lib.ptr(db), _lib.ptr(dinit), _lib.ptr(ws), ws.numel(), _lib.stream_of(xc))
+        wdt, bdt, idt = ctx.dtypes
+        return (dx, dw.to(wdt), None if db is None else db.to(bdt), None if dinit is None else dinit.to(idt), None, None)
+
+
+class _L2Norm(torch.autograd.Function):
+    """``l2norm`` with a backward (``gdn_l2norm_bwd``)."""
+
+    @staticmethod
+    def forward(ctx, x, eps):
+        xc = x.detach().contiguous()
+        y = torch.empty_like(xc)
+        d = xc.shape[-1]
+        rows = xc.numel() // max(d, 1)
+        _lib.call("gdn_l2norm_fwd", _lib.ptr(xc), _lib.ptr(y), rows, d, _lib.dtype_code(xc.dtype), eps, _lib.stream_of(xc))
+        ctx.save_for_backward(xc)
+        ctx.eps = eps
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        (xc,) = ctx.saved_tensors
+        dy = dy.to(xc.dtype).contiguous()
+        dx = torch.empty_like(xc)
+        d = xc.shape[-1]
+        _lib.call("gdn_l2norm_bwd", _lib.ptr(xc), _lib.ptr(dy), _lib.ptr(dx), xc.numel() // max(d, 1), d,
+                  _lib.dtype_code(xc.dtype), ctx.eps, _lib.stream_of(xc))
+        return dx, None
+
+
+class _RMSNormGated(torch.autograd.Function):
+    """``rms_norm_gated`` with a backward (``gdn_rms_norm_gated_bwd``)."""
+
+    @staticmethod
+    def forward(ctx, x, g, weight, bias, eps, act):
+        xc = x.detach().contiguous()
+        gc = None if g is None else g.detach().to(xc.dtype).contiguous()
+        wc = None if weight is None else weight.detach().float().contiguous()
+        bc = None if bias is None else bias.detach().float().contiguous()
+        y = torch.empty_like(xc)
+        d = xc.shape[-1]
+        rows = xc.numel() // max(d, 1)
+        _lib.call("gdn_rms_norm_gated_fwd", _lib.ptr(xc), _lib.ptr(gc), _lib.ptr(wc), _lib.ptr(bc), _lib.ptr(y), rows,
+                  d, _lib.dtype_code(xc.dtype), eps, act, _lib.stream_of(xc))
+        ctx.save_for_backward(xc, gc, wc, bc)
+        ctx.eps, ctx.act = eps, act
+        ctx.dtypes = (None if g is None else g.dtype, None if weight is None else weight.dtype,
+                      None if bias is None else bias.dtype)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        xc, gc, wc, bc = ctx.saved_tensors
+        dy = dy.to(xc.dtype).contiguous()
+        d = xc.shape[-1]
+        rows = xc.numel() // max(d, 1)
+        dx = torch.empty_like(xc)
+        dg = None if gc is None else torch.empty_like(gc)
+        dw = None if wc is None else torch.empty(d, device=xc.device, dtype=torch.float32)
+        db = None if bc is None else torch.empty(d, device=xc.device, dtype=torch.float32)
+        lib = _lib.load()
+        ws = torch.empty(max(int(lib.gdn_rms_norm_gated_bwd_workspace_size(rows, d)), 1), dtype=torch.uint8,
+                         device=xc.device)
+        _lib.call("gdn_rms_norm_gated_bwd", _lib.ptr(xc), _lib.ptr(gc), _lib.ptr(wc), _lib.ptr(bc), _lib.ptr(dy),
+                  _lib.ptr(dx), _lib.ptr(dg), _lib.ptr(dw), _lib.ptr(db), rows, d, _lib.dtype_code(xc.dtype), ctx.eps,
+                  ctx.act, _lib.ptr(ws), ws.numel(), _lib.stream_of(xc))
+        gdt, wdt, bdt = ctx.dtypes
+        return (dx, None if dg is None else dg.to(gdt), None if dw is None else dw.to(wdt),
+                None if db is None else db.to(bdt), None, None)
