@@ -16,6 +16,9 @@ The same line carries
   update, state updated in place) with HBM bytes/step = 141,664,256, plus a run rotating over
   5 state copies (335 MB > the 256 MB Infinity Cache) that forces DRAM traffic;
 - ``varlen``: config 3 (8 packed documents, 32768 tokens);
+- ``train``: config 1 under autograd -- the training forward (which also saves the bf16 state
+  entering every chunk) and the backward (dq, dk, dv, dg, dbeta, dh0), timed separately with HIP
+  events; backward algorithmic FLOPs = (22 C^2 d + 14 C d^2) per (chunk, head);
 - ``cpu_baseline``: the CPU oracle (``oracle/``, torch fp32 recurrence) on the GPU box's host
   cores over the full config-1 input, plus 100 decode steps of config 2.
 """
@@ -46,6 +49,50 @@ def chunk_flops(lengths, heads: int, d: int) -> int:
         if rem:
             total += 10 * rem * rem * d + 6 * rem * d * d
     return total * heads
+
+
+def chunk_bwd_flops(lengths, heads: int, d: int) -> int:
+    """Algorithmic backward FLOPs: per chunk (c tokens) 22 c^2 d + 14 c d^2 (the recomputed Y and Delta,
+    the seven c x d x d products with S or dS' and the eleven c x c x d products), times heads."""
+    total = 0
+    for L in lengths:
+        full, rem = divmod(L, C)
+        total += full * (22 * C * C * d + 14 * C * d * d)
+        if rem:
+            total += 22 * rem * rem * d + 14 * rem * d * d
+    return total * heads
+
+
+def train_step_times(torch, inp, steps: int):
+    """(training forward ms, backward ms) of chunk_gated_delta_rule under autograd, HIP events per step."""
+    from sorernn_amd import chunk_gated_delta_rule
+
+    leaves = [x.detach().clone().requires_grad_(True) for x in (inp.q, inp.k, inp.v, inp.g, inp.beta, inp.h0)]
+    gen = torch.Generator().manual_seed(5)
+    do = torch.randn(inp.v.shape, generator=gen).to(torch.bfloat16).to(inp.q.device)
+    dht = (torch.randn(inp.h0.shape, generator=gen) * 0.1).to(inp.q.device)
+
+    def fwd():
+        return chunk_gated_delta_rule(*leaves[:5], scale=inp.scale, initial_state=leaves[5], output_final_state=True)
+
+    def bwd(o, st):
+        torch.autograd.grad([o, st], leaves, [do, dht])
+
+    for _ in range(2):
+        bwd(*fwd())
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    tf = tb = 0.0
+    for _ in range(steps):
+        ev[0].record()
+        o, st = fwd()
+        ev[1].record()
+        bwd(o, st)
+        ev[2].record()
+        torch.cuda.synchronize()
+        tf += ev[0].elapsed_time(ev[1])
+        tb += ev[1].elapsed_time(ev[2])
+    return tf / steps, tb / steps
 
 
 def decode_bytes(B=64, H=16, HV=16, D=128, W=4) -> int:
@@ -161,6 +208,10 @@ def run_only(torch, args) -> int:
     from sorernn_amd import chunk_gated_delta_rule, gated_delta_decode_step
     from sorernn_amd.synthetic import config_inputs, decode_inputs
 
+    if args.only == "train":
+        tf, tb = train_step_times(torch, config_inputs(1).to("cuda"), args.steps)
+        print(f"ran train: {args.steps} steps, forward {tf:.3f} ms, backward {tb:.3f} ms", flush=True)
+        return 0
     if args.only in ("prefill", "varlen"):
         idx = 1 if args.only == "prefill" else 3
         inp = config_inputs(idx)
@@ -188,7 +239,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 256 MiB device copy (the reference kernel for PMC byte counters)")
-    ap.add_argument("--only", choices=["prefill", "decode", "varlen"], default=None,
+    ap.add_argument("--only", choices=["prefill", "decode", "varlen", "train"], default=None,
                     help="run one workload only (for profiler runs); prints no JSON line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -286,6 +337,11 @@ def main() -> int:
     v_ms, v_launch = time_launches(torch, vstep, max(5, args.steps // 5))
     lens = (cu_cpu[1:] - cu_cpu[:-1]).tolist()
     v_flops = chunk_flops(lens, 16, 128)
+    del v3
+
+    # ------------------------------------------------------------------ config 1 under autograd
+    tr_f, tr_b = train_step_times(torch, inp, max(5, args.steps // 5))
+    b_flops = chunk_bwd_flops([T] * B, H, K)
 
     result = {
         "metric": "GDN prefill tokens/s & decode-step µs (H=16,d=128); % of MI355X roofline",
@@ -339,6 +395,18 @@ def main() -> int:
             "ms_per_launch": round(v_launch, 4),
             "tflops": round(v_flops / (v_launch * 1e-3) / 1e12, 2),
             "frac_mfma_peak": round(v_flops / (v_launch * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+        },
+        "train": {
+            "workload": "config1 under autograd: training forward (saves bf16 per-chunk states) + backward "
+                        "(dq, dk, dv, dg, dbeta, dh0) of chunk_gated_delta_rule",
+            "fwd_ms": round(tr_f, 4),
+            "bwd_ms": round(tr_b, 4),
+            "tokens_per_s_fwd_bwd": round(B * T / ((tr_f + tr_b) * 1e-3), 1),
+            "bwd_flops": b_flops,
+            "bwd_tflops": round(b_flops / (tr_b * 1e-3) / 1e12, 2),
+            "bwd_frac_mfma_peak": round(b_flops / (tr_b * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+            "kernels": "gated_delta_chunk_kernel<SAVE>; gated_delta_chunk_bwd_prep_kernel, "
+                       "gated_delta_chunk_bwd_state_kernel, gated_delta_chunk_bwd_grad_kernel",
         },
     }
     if not args.no_cpu_baseline:
