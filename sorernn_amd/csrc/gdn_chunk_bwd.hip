@@ -45,6 +45,7 @@ struct ChunkBwdParams {
   const bf16* hs;     // state entering each chunk, bf16 [chunks][HV][V][K] (forward output, transposed)
   const f16* tw;      // the forward's T - I rows (fp16, tok_col columns)
   bf16* tn;           // T - I rows, natural columns, bf16 [tokens][HV][64]      (workspace)
+  bf16* tnt;          // (T - I)^T rows, bf16 [tokens][HV][64]                   (workspace)
   float* g1;          // G1 = T^T (scale P^T dO), fp32 [tokens][HV][V]           (workspace)
   bf16* dhs;          // gradient of the state leaving each chunk, bf16 [chunks][HV][V][K]   (workspace)
   float* gate_part;   // per-chunk partial sums of dA_log and ddt_bias [chunks][HV][2] (workspace)
@@ -262,6 +263,16 @@ __global__ __launch_bounds__(256) void gated_delta_chunk_bwd_prep_kernel(ChunkBw
   }
   if (w == 0) put_gates_bwd(gs, graw, braw, p, hv, len, lane);
   __syncthreads();
+  {  // (T - I)^T rows for the gradient kernel: row t holds (T - I)[j][t], j = 0..63
+#pragma unroll
+    for (int u8 = 0; u8 < 2; ++u8) {
+      const int e = u8 * 256 + t, row = e >> 3, j0 = (e & 7) * 8;
+      bf16x8 x;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) x[j] = Tm[(j0 + j) * kCPb + row];
+      if (row < len) *reinterpret_cast<bf16x8*>(p.tnt + ((c0 + row) * p.HV + hv) * kC + j0) = x;
+    }
+  }
 
   // scale P = scale (Q K^T) o E (j <= t), rows 16w..16w+15
 #pragma unroll
@@ -459,278 +470,288 @@ __global__ __launch_bounds__(256, 1) void gated_delta_chunk_bwd_state_kernel(Chu
 }
 
 // ================================================================== 3. per-chunk gradients
-// One workgroup of 8 waves per (chunk, q/k head), looping over the value heads of the head. Wave w
-// owns the tokens 16bt..16bt+15 (bt = w / 2) and half hw = w % 2 of the columns of every product:
-// value columns 32hw..32hw+31 of a 64-column half of V, key tiles KD/32 * hw.., c x c tiles 2hw, 2hw+1.
+// One workgroup of 4 waves per (chunk, q/k head), looping over the value heads of the head (GVA:
+// dq and dk are summed in registers) and, per value head, over 32-column passes of V. Wave w owns
+// the tokens 16w..16w+15 of every product: the pass's two 16-column tiles, the c x c tiles (w, jt)
+// with jt <= w, and all key tiles of dq and dk, so per-token sums stay inside a wave. 77 KB of LDS
+// and at most 256 VGPRs: two workgroups share a CU, so one's loads and barriers overlap the
+// other's MFMAs. The row
+// scalings of the state terms (scale e^gam of dQ_S, -beta e^gam of dY, r of Delta) are applied to
+// the A fragments per lane (a lane's A row is one token).
 template <int KD, int VD>
-__global__ __launch_bounds__(512, 1) void gated_delta_chunk_bwd_grad_kernel(ChunkBwdParams p) {
-  constexpr int KPB = row_pitch<KD>(), KS = KD / 32, KTW = KD / 32, NVH = VD / 64;
+__global__ __launch_bounds__(256, 2) void gated_delta_chunk_bwd_grad_kernel(ChunkBwdParams p) {
+  constexpr int KPB = KD + 8, KS = KD / 32, KT = KD / 16, NP = VD / 32;
+  constexpr int XP = 48;      // bf16 pitch of the [64][32] pass tiles (96 B rows)
   constexpr int FP = KD + 4;  // fp32 pitch of the dq / dk rows at the end
-  // S^T and dS'^T halves [64][KD]; dO, scale a dO, V (then r Delta), X (then r o K dS'), Delta, dX and
-  // -beta a dX [64][64]. After the value loop the first two hold dG and dQK; at the end the region
-  // holds dq and dk in fp32. The row scalings of dQ and dK's state terms are folded into the staged
-  // operands (scale a dO, -beta a dX, r Delta), so one accumulator set per output covers all value
-  // heads of the q/k head.
-  constexpr int kSB = kC * KPB, kTB = kC * kCPb;
-  constexpr int kBig = 2 * kSB + 7 * kTB, kFin = 2 * kC * FP * 4;
-  __shared__ __align__(16) bf16 Kb[kC * KPB], Qb[kC * KPB], Tm[kC * kCPb];
-  __shared__ __align__(16) char big_[kBig * 2 > kFin ? kBig * 2 : kFin];
-  bf16* const big = reinterpret_cast<bf16*>(big_);
+  constexpr int NSP = KD / 64;  // 16-byte pieces per thread of a [32][KD] S^T tile
+  constexpr int kSB = 32 * KPB, kPB = kC * XP;
+  constexpr int kBig = 2 * kSB + 4 * kPB;  // bf16 elements
+  static_assert(2 * kC * kCPb <= kBig && kC * FP * 2 <= kBig, "LDS reuse");
+  __shared__ __align__(16) bf16 Kb[kC * KPB], Qb[kC * KPB];
+  __shared__ __align__(16) bf16 big[kBig];
   __shared__ __align__(16) ChunkGates gs;
   __shared__ float tb_[kC], tg_[kC], red_[2];
-  bf16* const Sb = big;
-  bf16* const dSb = big + kSB;
-  bf16* const dOb = big + 2 * kSB;
-  bf16* const dOab = dOb + kTB;
-  bf16* const Vb = dOab + kTB;   // V, then r o Delta
-  bf16* const Xb = Vb + kTB;     // X, then r o K dS'
-  bf16* const Db = Xb + kTB;
-  bf16* const dXb = Db + kTB;
-  bf16* const dYb = dXb + kTB;
-  bf16* const cc1 = big;         // dG (after the value loop)
-  bf16* const cc2 = big + kTB;   // dQK
-  float* const fq = reinterpret_cast<float*>(big_);
-  float* const fk = fq + kC * FP;
+  bf16* const SbT = big;             // S^T of the pass: [32 value columns][KD keys]
+  bf16* const dSbT = big + kSB;      // dS'^T of the pass
+  bf16* const dOb = big + 2 * kSB;   // [64 tokens][32 value columns]
+  bf16* const Xb = dOb + kPB;        // V, then X, then r o K dS'
+  bf16* const Db = Xb + kPB;         // Delta
+  bf16* const dXb = Db + kPB;
+  bf16* const cc1 = big;             // dG (after the passes)
+  bf16* const cc2 = big + kC * kCPb; // dQK
+  float* const fr = reinterpret_cast<float*>(big);  // dq or dk rows at the end
 
   ChunkLoc L;
   if (!locate_chunk(p, blockIdx.x, L)) return;
   const int64_t h = blockIdx.y, rep = p.HV / p.H;
   const int t = threadIdx.x, lane = t & 63, w = __builtin_amdgcn_readfirstlane(t >> 6), g4 = lane >> 4, li = lane & 15;
-  const int bt = w >> 1, hw = w & 1;
+  const int tok0 = 16 * w;
   const bool l2 = p.flags & GDN_FLAG_QK_L2NORM;
   const int len = L.len;
   const int64_t c0 = L.c0, cg = blockIdx.x;
+  const uint32_t vrow = (uint32_t)(p.HV * VD * 2), trow = (uint32_t)(p.HV * kC * 2), grow = (uint32_t)(p.HV * VD * 4);
 
-  stage_qk_rows<KD, 512>(Kb, KPB, static_cast<const bf16*>(p.k) + (c0 * p.H + h) * KD, p.H, len, l2, t);
-  stage_qk_rows<KD, 512>(Qb, KPB, static_cast<const bf16*>(p.q) + (c0 * p.H + h) * KD, p.H, len, l2, t);
+  stage_qk_rows<KD, 256>(Kb, KPB, static_cast<const bf16*>(p.k) + (c0 * p.H + h) * KD, p.H, len, l2, t);
+  stage_qk_rows<KD, 256>(Qb, KPB, static_cast<const bf16*>(p.q) + (c0 * p.H + h) * KD, p.H, len, l2, t);
 
-  f32x4 dqa[KTW], dka[KTW];
+  f32x4 dqa[KT], dka[KT];
 #pragma unroll
-  for (int j = 0; j < KTW; ++j) dqa[j] = dka[j] = f32x4{};
+  for (int j = 0; j < KT; ++j) dqa[j] = dka[j] = f32x4{};
+
+  // the global loads of a pass: S^T and dS'^T rows (all rows valid), dO and V [64][32] (rows past
+  // len read as zeros), G1 in accumulator layout (tiles ct = 0, 1 of the pass)
+  bf16x8 ps[NSP], pd[NSP];
+  u32x4 po, pv;
+  float g1c[8];
+  auto fetch_pass = [&](int64_t hv, int ps_i, float (&g1)[8]) {
+    const bf16* hsrc = p.hs + ((cg * p.HV + hv) * VD + 32 * ps_i) * (int64_t)KD;
+    const bf16* dsrc = p.dhs + ((cg * p.HV + hv) * VD + 32 * ps_i) * (int64_t)KD;
+#pragma unroll
+    for (int u = 0; u < NSP; ++u) {
+      ps[u] = ld8(hsrc + (int64_t)(u * 256 + t) * 8);
+      pd[u] = ld8(dsrc + (int64_t)(u * 256 + t) * 8);
+    }
+    const int row = t >> 2, ch = t & 3;
+    const auto ro = make_rsrc(static_cast<const bf16*>(p.dout) + (c0 * p.HV + hv) * VD + 32 * ps_i, (uint32_t)len * vrow);
+    const auto rv = make_rsrc(static_cast<const bf16*>(p.v) + (c0 * p.HV + hv) * VD + 32 * ps_i, (uint32_t)len * vrow);
+    po = __builtin_amdgcn_raw_buffer_load_b128(ro, (int)((uint32_t)row * vrow + ch * 16), 0, 0);
+    pv = __builtin_amdgcn_raw_buffer_load_b128(rv, (int)((uint32_t)row * vrow + ch * 16), 0, 0);
+    const auto rg = make_rsrc(p.g1 + (c0 * p.HV + hv) * VD + 32 * ps_i, (uint32_t)len * grow);
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        g1[4 * ct + r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+            rg, (int)((uint32_t)(tok0 + 4 * g4 + r) * grow + (16 * ct + li) * 4), 0, 0));
+  };
 
   for (int64_t rr = 0; rr < rep; ++rr) {
     const int64_t hv = h * rep + rr;
-    stage_slice<kC, 512>(Tm, kCPb, p.tn + (c0 * p.HV + hv) * kC, (uint32_t)(p.HV * kC * 2), len, t);
-    if (w == 0) stage_gates_bwd(gs, p, c0, hv, len, lane);
+    // T - I fragments of this wave's rows: (T - I) rows (Delta) and (T - I)^T rows (dX)
+    bf16x8 tfr[2], tft[2];
+    {
+      const auto rn = make_rsrc(p.tn + (c0 * p.HV + hv) * kC, (uint32_t)len * trow);
+      const auto rt = make_rsrc(p.tnt + (c0 * p.HV + hv) * kC, (uint32_t)len * trow);
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        tfr[u] = buf_load16(rn, (uint32_t)(tok0 + li) * trow + (32 * u + 8 * g4) * 2);
+        tft[u] = buf_load16(rt, (uint32_t)(tok0 + li) * trow + (32 * u + 8 * g4) * 2);
+      }
+    }
+    uint32_t graw = 0, braw = 0;
+    if (w == 0) fetch_gates_bwd(graw, braw, p, c0, hv, len, lane);
     if (t < kC) {
       tb_[t] = 0.f;
       tg_[t] = 0.f;
     }
     if (t < 2) red_[t] = 0.f;
+    if (w == 0) put_gates_bwd(gs, graw, braw, p, hv, len, lane);
 
-    f32x4 dA[2], dP[2];
+    f32x4 dA[4], dP[4];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) dA[j] = dP[j] = f32x4{};
+    for (int j = 0; j < 4; ++j) dA[j] = dP[j] = f32x4{};
     float pb[4] = {0.f, 0.f, 0.f, 0.f}, pg[4] = {0.f, 0.f, 0.f, 0.f}, pr[4] = {0.f, 0.f, 0.f, 0.f};
     float sdot = 0.f;
 
 #pragma unroll 1
-    for (int vh = 0; vh < NVH; ++vh) {
-      {  // S^T and dS'^T rows (value columns 64vh..64vh+63, all keys); e^{gam_c}<S, dS'> partials
-        constexpr int CH = KD / 8;
-        const bf16* hsrc = p.hs + ((cg * p.HV + hv) * VD + 64 * vh) * (int64_t)KD;
-        const bf16* dsrc = p.dhs + ((cg * p.HV + hv) * VD + 64 * vh) * (int64_t)KD;
-        bf16x8 sv[kC * CH / 512], dv8[kC * CH / 512];
+    for (int pi = 0; pi < NP; ++pi) {
+      fetch_pass(hv, pi, g1c);
+      __syncthreads();  // the previous pass (or value head) is done with the LDS tiles
 #pragma unroll
-        for (int u = 0; u < kC * CH / 512; ++u) {
-          const int e = u * 512 + t;
-          sv[u] = ld8(hsrc + (int64_t)e * 8);
-          dv8[u] = ld8(dsrc + (int64_t)e * 8);
-        }
+      for (int u = 0; u < NSP; ++u) {
+        const int e = u * 256 + t, row = e / (KD / 8), c8 = (e % (KD / 8)) * 8;
 #pragma unroll
-        for (int u = 0; u < kC * CH / 512; ++u) {
-          const int e = u * 512 + t, row = e / CH, c8 = (e % CH) * 8;
-#pragma unroll
-          for (int x = 0; x < 8; ++x) sdot += (float)sv[u][x] * (float)dv8[u][x];
-          *reinterpret_cast<bf16x8*>(Sb + row * KPB + c8) = sv[u];
-          *reinterpret_cast<bf16x8*>(dSb + row * KPB + c8) = dv8[u];
-        }
+        for (int x = 0; x < 8; ++x) sdot += (float)ps[u][x] * (float)pd[u][x];
+        *reinterpret_cast<bf16x8*>(SbT + row * KPB + c8) = ps[u];
+        *reinterpret_cast<bf16x8*>(dSbT + row * KPB + c8) = pd[u];
       }
-      stage_slice<64, 512>(dOb, kCPb, static_cast<const bf16*>(p.dout) + (c0 * p.HV + hv) * VD + 64 * vh,
-                           (uint32_t)(p.HV * VD * 2), len, t);
-      stage_slice<64, 512>(Vb, kCPb, static_cast<const bf16*>(p.v) + (c0 * p.HV + hv) * VD + 64 * vh,
-                           (uint32_t)(p.HV * VD * 2), len, t);
+      *reinterpret_cast<u32x4*>(dOb + (t >> 2) * XP + (t & 3) * 8) = po;
+      *reinterpret_cast<u32x4*>(Xb + (t >> 2) * XP + (t & 3) * 8) = pv;
       __syncthreads();
-      // Y = K S, W = K dS', QS = Q S (tiles (bt, 2hw + j))
+      // Y = K S, W = K dS', QS = Q S on the tiles (w, ct). (Fragment addresses derive from lane ids
+      // passed through an empty asm per phase, so they are rebuilt where used instead of being
+      // hoisted out of the loops into registers that stay live across them.)
+      int ln = opaque_int(lane);
       f32x4 Y[2], W[2], QS[2];
 #pragma unroll
-      for (int j = 0; j < 2; ++j) Y[j] = W[j] = QS[j] = f32x4{};
-#pragma unroll 1
-      for (int s = 0; s < KS; ++s) {
-        const bf16x8 a = frag_row(Kb, KPB, 16 * bt, 32 * s, lane);
-        const bf16x8 aq = frag_row(Qb, KPB, 16 * bt, 32 * s, lane);
+      for (int ct = 0; ct < 2; ++ct) Y[ct] = W[ct] = QS[ct] = f32x4{};
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const int ct = 2 * hw + j;
-          const bf16x8 bs = frag_row(Sb, KPB, 16 * ct, 32 * s, lane);
-          Y[j] = mma(a, bs, Y[j]);
-          QS[j] = mma(aq, bs, QS[j]);
-          W[j] = mma(a, frag_row(dSb, KPB, 16 * ct, 32 * s, lane), W[j]);
+      for (int s = 0; s < KS; ++s) {
+        const bf16x8 ak = frag_row(Kb, KPB, tok0, 32 * s, ln), aq = frag_row(Qb, KPB, tok0, 32 * s, ln);
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+          const bf16x8 bs = frag_row(SbT, KPB, 16 * ct, 32 * s, ln);
+          Y[ct] = mma(ak, bs, Y[ct]);
+          QS[ct] = mma(aq, bs, QS[ct]);
+          W[ct] = mma(ak, frag_row(dSbT, KPB, 16 * ct, 32 * s, ln), W[ct]);
         }
+        __builtin_amdgcn_sched_barrier(0);  // one k-step's fragments live at a time
       }
-      // X = beta V - beta a Y; scale a dO; the a-term of dgam, scale a_t dO_t . (Q S)_t
+      // X = beta V - beta a Y (V read from Xb, X written over it: each wave touches only its rows);
+      // the a-term of dgam, scale a_t dO_t . (Q S)_t
       f32x4 Vv[2], Dl[2];
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int ct = 2 * hw + j;
-        const bf16x4 vv = ld4_tr(Vb, kCPb, 16 * bt, 16 * ct, lane);
-        const bf16x4 dd = ld4_tr(dOb, kCPb, 16 * bt, 16 * ct, lane);
-        f32x4 oa;
+      for (int ct = 0; ct < 2; ++ct) {
+        const bf16x4 vv = ld4_tr(Xb, XP, tok0, 16 * ct, ln);
+        const bf16x4 dd = ld4_tr(dOb, XP, tok0, 16 * ct, ln);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int tok = 16 * bt + 4 * g4 + r;
-          Vv[j][r] = (float)vv[r];
-          Dl[j][r] = gs.bet[tok] * Vv[j][r] - gs.begam[tok] * Y[j][r];
-          oa[r] = p.scale * gs.egam[tok] * (float)dd[r];
-          pg[r] += oa[r] * QS[j][r];
+          const int tok = tok0 + 4 * (ln >> 4) + r;
+          Vv[ct][r] = (float)vv[r];
+          Dl[ct][r] = gs.bet[tok] * Vv[ct][r] - gs.begam[tok] * Y[ct][r];
+          pg[r] += p.scale * gs.egam[tok] * (float)dd[r] * QS[ct][r];
         }
-        put_acc(Xb, kCPb, 16 * bt, 16 * ct, lane, Dl[j]);
-        put_acc(dOab, kCPb, 16 * bt, 16 * ct, lane, oa);
+        put_acc(Xb, XP, tok0, 16 * ct, lane, Dl[ct]);
       }
       __syncthreads();
       // Delta = X + (T - I) X  ((T - I)_{tj} vanishes unless j < t)
+      ln = opaque_int(lane);
 #pragma unroll
       for (int u = 0; u < 2; ++u)
-        if (u == 0 || bt >= 2) {
-          const bf16x8 a = frag_row(Tm, kCPb, 16 * bt, 32 * u, lane);
+        if (u == 0 || w >= 2) {
 #pragma unroll
-          for (int j = 0; j < 2; ++j) Dl[j] = mma(a, frag_col(Xb, kCPb, 32 * u, 16 * (2 * hw + j), lane), Dl[j]);
+          for (int ct = 0; ct < 2; ++ct) Dl[ct] = mma(tfr[u], frag_col(Xb, XP, 32 * u, 16 * ct, ln), Dl[ct]);
         }
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        put_acc(Db, kCPb, 16 * bt, 16 * (2 * hw + j), lane, Dl[j]);
-        f32x4 rd;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) rd[r] = gs.dlast[16 * bt + 4 * g4 + r] * Dl[j][r];
-        put_acc(Vb, kCPb, 16 * bt, 16 * (2 * hw + j), lane, rd);
-      }
+      for (int ct = 0; ct < 2; ++ct) put_acc(Db, XP, tok0, 16 * ct, lane, Dl[ct]);
       __syncthreads();
       // Z = r o (K dS') -> Xb
+      ln = opaque_int(lane);
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
+      for (int ct = 0; ct < 2; ++ct) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) W[j][r] *= gs.dlast[16 * bt + 4 * g4 + r];
-        put_acc(Xb, kCPb, 16 * bt, 16 * (2 * hw + j), lane, W[j]);
+        for (int r = 0; r < 4; ++r) W[ct][r] *= gs.dlast[tok0 + 4 * (ln >> 4) + r];
+        put_acc(Xb, XP, tok0, 16 * ct, lane, W[ct]);
       }
       __syncthreads();
       // dX = G1 + Z + (T - I)^T Z
+      ln = opaque_int(lane);
       f32x4 dX[2];
-      {
-        const uint32_t rb = (uint32_t)(p.HV * VD * 4);
-        const auto rs = make_rsrc(p.g1 + (c0 * p.HV + hv) * VD + 64 * vh, (uint32_t)len * rb);
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+      for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int tok = 16 * bt + 4 * g4 + r, cc = 16 * (2 * hw + j) + li;
-            dX[j][r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, (int)((uint32_t)tok * rb + cc * 4), 0, 0)) + W[j][r];
-          }
-      }
+        for (int r = 0; r < 4; ++r) dX[ct][r] = g1c[4 * ct + r] + W[ct][r];
 #pragma unroll
       for (int u = 0; u < 2; ++u)
-        if (u == 1 || bt <= 1) {
-          const bf16x8 a = frag_col(Tm, kCPb, 32 * u, 16 * bt, lane);
+        if (u == 1 || w <= 1) {
 #pragma unroll
-          for (int j = 0; j < 2; ++j) dX[j] = mma(a, frag_col(Xb, kCPb, 32 * u, 16 * (2 * hw + j), lane), dX[j]);
+          for (int ct = 0; ct < 2; ++ct) dX[ct] = mma(tft[u], frag_col(Xb, XP, 32 * u, 16 * ct, ln), dX[ct]);
         }
       // dV = beta dX; row partials of dbeta and dgam
       bf16* const dvg = static_cast<bf16*>(p.dv);
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int cc = 64 * vh + 16 * (2 * hw + j) + li;
+      for (int ct = 0; ct < 2; ++ct) {
+        const int cc = 32 * pi + 16 * ct + (ln & 15);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int tok = 16 * bt + 4 * g4 + r;
-          if (tok < len) dvg[((c0 + tok) * p.HV + hv) * VD + cc] = static_cast<bf16>(gs.bet[tok] * dX[j][r]);
-          pb[r] += (Vv[j][r] - gs.egam[tok] * Y[j][r]) * dX[j][r];
-          pg[r] -= gs.begam[tok] * dX[j][r] * Y[j][r];
-          pr[r] += W[j][r] * Dl[j][r];
+          const int tok = tok0 + 4 * (ln >> 4) + r;
+          if (tok < len) dvg[((c0 + tok) * p.HV + hv) * VD + cc] = static_cast<bf16>(gs.bet[tok] * dX[ct][r]);
+          pb[r] += (Vv[ct][r] - gs.egam[tok] * Y[ct][r]) * dX[ct][r];
+          pg[r] -= gs.begam[tok] * dX[ct][r] * Y[ct][r];
+          pr[r] += W[ct][r] * Dl[ct][r];
         }
-        put_acc(dXb, kCPb, 16 * bt, 16 * (2 * hw + j), lane, dX[j]);
-        f32x4 dy;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) dy[r] = -gs.begam[16 * bt + 4 * g4 + r] * dX[j][r];
-        put_acc(dYb, kCPb, 16 * bt, 16 * (2 * hw + j), lane, dy);
+        put_acc(dXb, XP, tok0, 16 * ct, lane, dX[ct]);
       }
       __syncthreads();
-      // c x c: dA' += dX Delta^T, dP' += dO Delta^T (tiles (bt, 2hw + j) on or below the diagonal)
+      // c x c: dA' += dX Delta^T, dP' += dO Delta^T on the tiles (w, jt <= w)
+      ln = opaque_int(lane);
+      const bf16x8 ax = frag_row(dXb, XP, tok0, 0, ln), ao = frag_row(dOb, XP, tok0, 0, ln);
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int jt = 2 * hw + j;
-        if (jt <= bt) {
-#pragma unroll
-          for (int s = 0; s < 2; ++s) {
-            const bf16x8 bd = frag_row(Db, kCPb, 16 * jt, 32 * s, lane);
-            dA[j] = mma(frag_row(dXb, kCPb, 16 * bt, 32 * s, lane), bd, dA[j]);
-            dP[j] = mma(frag_row(dOb, kCPb, 16 * bt, 32 * s, lane), bd, dP[j]);
-          }
+      for (int jt = 0; jt < 4; ++jt)
+        if (jt <= w) {
+          const bf16x8 bd = frag_row(Db, XP, 16 * jt, 0, ln);
+          dA[jt] = mma(ax, bd, dA[jt]);
+          dP[jt] = mma(ao, bd, dP[jt]);
         }
-      }
       // c x K: dQ += (scale a dO) S^T, dK += (-beta a dX) S^T + (r Delta) dS'^T
-#pragma unroll 1
-      for (int s = 0; s < 2; ++s) {
-        const bf16x8 ao = frag_row(dOab, kCPb, 16 * bt, 32 * s, lane);
-        const bf16x8 ay = frag_row(dYb, kCPb, 16 * bt, 32 * s, lane);
-        const bf16x8 ad = frag_row(Vb, kCPb, 16 * bt, 32 * s, lane);
+      {
+        const int rowt = tok0 + (ln & 15);  // the token of this lane's A row
+        const float fo = p.scale * gs.egam[rowt], fy = -gs.begam[rowt], fd = gs.dlast[rowt];
+        const bf16x8 ad = frag_row(Db, XP, tok0, 0, ln);
+        bf16x8 so, sy, sd;
 #pragma unroll
-        for (int j = 0; j < KTW; ++j) {
-          const int kt = KTW * hw + j;
-          const bf16x8 bs = frag_col(Sb, KPB, 32 * s, 16 * kt, lane);
-          dqa[j] = mma(ao, bs, dqa[j]);
-          dka[j] = mma(ay, bs, dka[j]);
-          dka[j] = mma(ad, frag_col(dSb, KPB, 32 * s, 16 * kt, lane), dka[j]);
+        for (int x = 0; x < 8; ++x) {
+          so[x] = static_cast<bf16>(fo * (float)ao[x]);
+          sy[x] = static_cast<bf16>(fy * (float)ax[x]);
+          sd[x] = static_cast<bf16>(fd * (float)ad[x]);
+        }
+#pragma unroll
+        for (int kt = 0; kt < KT; ++kt) {
+          const bf16x8 bs = frag_col(SbT, KPB, 0, 16 * kt, ln);
+          dqa[kt] = mma(so, bs, dqa[kt]);
+          dka[kt] = mma(sy, bs, dka[kt]);
+          dka[kt] = mma(sd, frag_col(dSbT, KPB, 0, 16 * kt, ln), dka[kt]);
+          if (kt & 1) __builtin_amdgcn_sched_barrier(0);
         }
       }
-      __syncthreads();
     }
 
     // e^{gam_c} <S, dS'> and sum_t r_t (K dS')_t . Delta_t go to the chunk's last position
     sdot = wave_xor_sum(sdot, 1);
     if (lane == 0) atomicAdd(&red_[0], sdot);
+    __syncthreads();  // the passes are done with the LDS tiles: dG and dQK go over them
     // c x c elementwise: G = K K^T, QK = Q K^T; dA, dG, dQK; their row and column sums
-    float colp[2] = {0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int jt = 2 * hw + j;
+    for (int jt = 0; jt < 4; ++jt) {
+      const int ln = opaque_int(lane);
       f32x4 Gm = f32x4{}, QKm = f32x4{};
-      if (jt <= bt) {
-#pragma unroll 1
+      if (jt <= w) {
+#pragma unroll
         for (int s = 0; s < KS; ++s) {
-          const bf16x8 bk = frag_row(Kb, KPB, 16 * jt, 32 * s, lane);
-          Gm = mma(frag_row(Kb, KPB, 16 * bt, 32 * s, lane), bk, Gm);
-          QKm = mma(frag_row(Qb, KPB, 16 * bt, 32 * s, lane), bk, QKm);
+          const bf16x8 bk = frag_row(Kb, KPB, 16 * jt, 32 * s, ln);
+          Gm = mma(frag_row(Kb, KPB, tok0, 32 * s, ln), bk, Gm);
+          QKm = mma(frag_row(Qb, KPB, tok0, 32 * s, ln), bk, QKm);
+          __builtin_amdgcn_sched_barrier(0);
         }
       }
-      const int jj = 16 * jt + li;
+      const int jj = 16 * jt + (ln & 15);
       f32x4 dG, dQK;
+      float colp = 0.f;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int tok = 16 * bt + 4 * g4 + r;
+        const int tok = tok0 + 4 * (ln >> 4) + r;
         const float e = jj <= tok ? __expf(gs.gam[tok] - gs.gam[jj]) : 0.f;
-        const float dav = jj < tok ? -dA[j][r] : 0.f;
+        const float dav = jj < tok ? -dA[jt][r] : 0.f;
         dG[r] = gs.bet[tok] * dav * e;
-        dQK[r] = p.scale * dP[j][r] * e;
+        dQK[r] = p.scale * dP[jt][r] * e;
         pb[r] += dav * Gm[r] * e;
         const float pair = dG[r] * Gm[r] + dQK[r] * QKm[r];
         pg[r] += pair;
-        colp[j] += pair;
+        colp += pair;
       }
-      put_acc(cc1, kCPb, 16 * bt, 16 * jt, lane, dG);
-      put_acc(cc2, kCPb, 16 * bt, 16 * jt, lane, dQK);
-    }
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      float x = colp[j];
-      x += __shfl_xor(x, 16, kWave);
-      x += __shfl_xor(x, 32, kWave);
-      if (g4 == 0 && x != 0.f) atomicAdd(&tg_[16 * (2 * hw + j) + li], -x);
+      put_acc(cc1, kCPb, tok0, 16 * jt, lane, dG);
+      put_acc(cc2, kCPb, tok0, 16 * jt, lane, dQK);
+      colp += __shfl_xor(colp, 16, kWave);
+      colp += __shfl_xor(colp, 32, kWave);
+      if ((ln >> 4) == 0 && jt <= w) atomicAdd(&tg_[jj], -colp);
+      __builtin_amdgcn_sched_barrier(0);  // one c x c tile at a time
     }
     float rsum = 0.f;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const float b = group_sum<16>(pb[r]), gg = group_sum<16>(pg[r]), rr2 = group_sum<16>(pr[r]);
       if (li == 0) {
-        const int tok = 16 * bt + 4 * g4 + r;
+        const int tok = tok0 + 4 * g4 + r;
         atomicAdd(&tb_[tok], b);
         atomicAdd(&tg_[tok], gg - rr2);
         rsum += rr2;
@@ -741,15 +762,16 @@ __global__ __launch_bounds__(512, 1) void gated_delta_chunk_bwd_grad_kernel(Chun
     __syncthreads();
     // dQ += dQK K;  dK += dQK^T Q + dG K + dG^T K
 #pragma unroll
-    for (int j = 0; j < KTW; ++j) {
-      const int kt = KTW * hw + j;
-#pragma unroll 1
+    for (int kt = 0; kt < KT; ++kt) {
+      const int ln = opaque_int(lane);
+#pragma unroll
       for (int u = 0; u < 2; ++u) {
-        const bf16x8 bk = frag_col(Kb, KPB, 32 * u, 16 * kt, lane);
-        dqa[j] = mma(frag_row(cc2, kCPb, 16 * bt, 32 * u, lane), bk, dqa[j]);
-        dka[j] = mma(frag_col(cc2, kCPb, 32 * u, 16 * bt, lane), frag_col(Qb, KPB, 32 * u, 16 * kt, lane), dka[j]);
-        dka[j] = mma(frag_row(cc1, kCPb, 16 * bt, 32 * u, lane), bk, dka[j]);
-        dka[j] = mma(frag_col(cc1, kCPb, 32 * u, 16 * bt, lane), bk, dka[j]);
+        const bf16x8 bk = frag_col(Kb, KPB, 32 * u, 16 * kt, ln);
+        dqa[kt] = mma(frag_row(cc2, kCPb, tok0, 32 * u, ln), bk, dqa[kt]);
+        dka[kt] = mma(frag_col(cc2, kCPb, 32 * u, tok0, ln), frag_col(Qb, KPB, 32 * u, 16 * kt, ln), dka[kt]);
+        dka[kt] = mma(frag_row(cc1, kCPb, tok0, 32 * u, ln), bk, dka[kt]);
+        dka[kt] = mma(frag_col(cc1, kCPb, 32 * u, tok0, ln), bk, dka[kt]);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
     // dg = reverse in-chunk cumsum of dgam; dbeta; the gate and sigmoid backwards
@@ -764,13 +786,13 @@ __global__ __launch_bounds__(512, 1) void gated_delta_chunk_bwd_grad_kernel(Chun
       const int64_t gi = (c0 + lane) * p.HV + hv;
       float pa = 0.f, pd = 0.f;
       if (lane < len) {
-        const float graw = load_as_f32(p.g, p.dg, gi);
+        const float graw2 = load_as_f32(p.g, p.dg, gi);
         if (p.flags & GDN_FLAG_GATE_IN_KERNEL) {
           const float ea = __expf(p.A_log[hv]);
-          const float gval = -ea * softplus_f32(graw + p.dt_bias[hv]);
-          pa = dgv * gval;                                   // d/dA_log
-          dgv = dgv * (-ea) * sigmoid_f32(graw + p.dt_bias[hv]);  // d/da, a the raw gate input
-          pd = dgv;                                          // d/ddt_bias
+          const float gval = -ea * softplus_f32(graw2 + p.dt_bias[hv]);
+          pa = dgv * gval;                                         // d/dA_log
+          dgv = dgv * (-ea) * sigmoid_f32(graw2 + p.dt_bias[hv]);  // d/da, a the raw gate input
+          pd = dgv;                                                // d/ddt_bias
         }
         if (p.flags & GDN_FLAG_BETA_SIGMOID) {
           const float sb = sigmoid_f32(load_as_f32(p.beta, p.db, gi));
@@ -788,61 +810,56 @@ __global__ __launch_bounds__(512, 1) void gated_delta_chunk_bwd_grad_kernel(Chun
         }
       }
     }
-    __syncthreads();
   }
 
-  // dq, dk rows through LDS, then the L2-norm backward (x / max(|x|, eps)) on the raw rows
+  // dq, then dk: rows through LDS, the L2-norm backward (x / max(|x|, eps)) on the raw rows, store
+#pragma unroll 1
+  for (int x = 0; x < 2; ++x) {
+    __syncthreads();
 #pragma unroll
-  for (int j = 0; j < KTW; ++j) {
-    const int kt = KTW * hw + j;
+    for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int tok = 16 * bt + 4 * g4 + r;
-      fq[tok * FP + 16 * kt + li] = dqa[j][r];
-      fk[tok * FP + 16 * kt + li] = dka[j][r];
-    }
-  }
-  __syncthreads();
-  {
-    constexpr int KCH = KD / 8, RPP = 512 / KCH;
+      for (int r = 0; r < 4; ++r) fr[(tok0 + 4 * g4 + r) * FP + 16 * kt + li] = x == 0 ? dqa[kt][r] : dka[kt][r];
+    __syncthreads();
+    constexpr int KCH = KD / 8, RPP = 256 / KCH;
     const int row0 = t / KCH, ch = t % KCH;
     const uint32_t rb = (uint32_t)(p.H * KD * 2);
+    const bf16* raw = static_cast<const bf16*>(x == 0 ? p.q : p.k) + (c0 * p.H + h) * KD;
+    bf16* dst = static_cast<bf16*>(x == 0 ? p.dq : p.dk) + (c0 * p.H + h) * KD;
+    const auto rs = make_rsrc(raw, (uint32_t)len * rb);
+    bf16x8 xr[kC / RPP];
+    if (l2) {
 #pragma unroll
-    for (int x = 0; x < 2; ++x) {
-      const float* src = x == 0 ? fq : fk;
-      const bf16* raw = static_cast<const bf16*>(x == 0 ? p.q : p.k) + (c0 * p.H + h) * KD;
-      bf16* dst = static_cast<bf16*>(x == 0 ? p.dq : p.dk) + (c0 * p.H + h) * KD;
-      const auto rs = make_rsrc(raw, (uint32_t)len * rb);
+      for (int u = 0; u < kC / RPP; ++u) xr[u] = buf_load16(rs, (uint32_t)(row0 + u * RPP) * rb + ch * 16);
+    }
 #pragma unroll
-      for (int u = 0; u < kC / RPP; ++u) {
-        const int row = row0 + u * RPP;
-        float d[8];
-        const float4 d0 = *reinterpret_cast<const float4*>(src + row * FP + ch * 8);
-        const float4 d1 = *reinterpret_cast<const float4*>(src + row * FP + ch * 8 + 4);
-        d[0] = d0.x; d[1] = d0.y; d[2] = d0.z; d[3] = d0.w;
-        d[4] = d1.x; d[5] = d1.y; d[6] = d1.z; d[7] = d1.w;
-        if (l2) {
-          const bf16x8 xr = buf_load16(rs, (uint32_t)row * rb + ch * 16);
-          float ss = 0.f;
+    for (int u = 0; u < kC / RPP; ++u) {
+      const int row = row0 + u * RPP;
+      float d[8];
+      const float4 d0 = *reinterpret_cast<const float4*>(fr + row * FP + ch * 8);
+      const float4 d1 = *reinterpret_cast<const float4*>(fr + row * FP + ch * 8 + 4);
+      d[0] = d0.x; d[1] = d0.y; d[2] = d0.z; d[3] = d0.w;
+      d[4] = d1.x; d[5] = d1.y; d[6] = d1.z; d[7] = d1.w;
+      if (l2) {
+        float ss = 0.f;
 #pragma unroll
-          for (int e = 0; e < 8; ++e) ss += (float)xr[e] * (float)xr[e];
-          ss = group_sum<KCH>(ss);
-          const float nrm = sqrtf(ss);
-          const float inv = 1.f / fmaxf(nrm, 1e-12f);
-          float dot = 0.f;
+        for (int e = 0; e < 8; ++e) ss += (float)xr[u][e] * (float)xr[u][e];
+        ss = group_sum<KCH>(ss);
+        const float nrm = sqrtf(ss);
+        const float inv = 1.f / fmaxf(nrm, 1e-12f);
+        float dot = 0.f;
 #pragma unroll
-          for (int e = 0; e < 8; ++e) dot += (float)xr[e] * inv * d[e];
-          dot = group_sum<KCH>(dot);
-          if (nrm <= 1e-12f) dot = 0.f;  // clamped norm: x / eps is linear in x
+        for (int e = 0; e < 8; ++e) dot += (float)xr[u][e] * inv * d[e];
+        dot = group_sum<KCH>(dot);
+        if (nrm <= 1e-12f) dot = 0.f;  // clamped norm: x / eps is linear in x
 #pragma unroll
-          for (int e = 0; e < 8; ++e) d[e] = (d[e] - (float)xr[e] * inv * dot) * inv;
-        }
-        if (row < len) {
-          bf16x8 o;
+        for (int e = 0; e < 8; ++e) d[e] = (d[e] - (float)xr[u][e] * inv * dot) * inv;
+      }
+      if (row < len) {
+        bf16x8 o;
 #pragma unroll
-          for (int e = 0; e < 8; ++e) o[e] = static_cast<bf16>(d[e]);
-          *reinterpret_cast<bf16x8*>(dst + (int64_t)row * p.H * KD + ch * 8) = o;
-        }
+        for (int e = 0; e < 8; ++e) o[e] = static_cast<bf16>(d[e]);
+        *reinterpret_cast<bf16x8*>(dst + (int64_t)row * p.H * KD + ch * 8) = o;
       }
     }
   }
@@ -894,7 +911,7 @@ extern "C" size_t gdn_chunk_bwd_workspace_size(int64_t B, int64_t T, int64_t HV,
                                                int varlen) {
   if (B <= 0 || T < 0 || HV <= 0 || K <= 0 || V <= 0 || N <= 0) return 0;
   const int64_t tok = B * T, ch = chunk_bound(B, T, N, varlen != 0);
-  return (size_t)(align256(tok * HV * kC * 2) + align256(tok * HV * V * 4) + align256(ch * HV * K * V * 2) +
+  return (size_t)(2 * align256(tok * HV * kC * 2) + align256(tok * HV * V * 4) + align256(ch * HV * K * V * 2) +
                   align256(ch * HV * 2 * 4));
 }
 
@@ -942,11 +959,12 @@ extern "C" int gdn_chunk_bwd(const void* q, const void* k, const void* v, const 
   p.dht = d_final_state;
   p.hs = static_cast<const bf16*>(chunk_states);
   p.tw = reinterpret_cast<const f16*>(fws);
+  const int64_t tnb = align256(tok * HV * kC * 2);
   p.tn = reinterpret_cast<bf16*>(ws);
-  p.g1 = reinterpret_cast<float*>(ws + align256(tok * HV * kC * 2));
-  p.dhs = reinterpret_cast<bf16*>(ws + align256(tok * HV * kC * 2) + align256(tok * HV * V * 4));
-  p.gate_part = reinterpret_cast<float*>(ws + align256(tok * HV * kC * 2) + align256(tok * HV * V * 4) +
-                                         align256(chunks * HV * K * V * 2));
+  p.tnt = reinterpret_cast<bf16*>(ws + tnb);
+  p.g1 = reinterpret_cast<float*>(ws + 2 * tnb);
+  p.dhs = reinterpret_cast<bf16*>(ws + 2 * tnb + align256(tok * HV * V * 4));
+  p.gate_part = reinterpret_cast<float*>(ws + 2 * tnb + align256(tok * HV * V * 4) + align256(chunks * HV * K * V * 2));
   p.cu = cu_seqlens;
   p.chunk_first = varlen ? reinterpret_cast<const int*>(fws + chunk_t_bytes(tok, HV)) : nullptr;
   p.cu_i32 = (flags & GDN_FLAG_CU_INT32) ? 1 : 0;
@@ -971,7 +989,7 @@ extern "C" int gdn_chunk_bwd(const void* q, const void* k, const void* v, const 
   GDN_BWD_DISPATCH(gated_delta_chunk_bwd_state_kernel, dim3((unsigned)(N * HV * (V / 32))), dim3(256));
   rc = gdn_internal_check_launch("gated_delta_chunk_bwd_state_kernel");
   if (rc != GDN_OK) return rc;
-  GDN_BWD_DISPATCH(gated_delta_chunk_bwd_grad_kernel, dim3((unsigned)chunks, (unsigned)H), dim3(512));
+  GDN_BWD_DISPATCH(gated_delta_chunk_bwd_grad_kernel, dim3((unsigned)chunks, (unsigned)H), dim3(256));
   rc = gdn_internal_check_launch("gated_delta_chunk_bwd_grad_kernel");
   if (rc != GDN_OK) return rc;
 #undef GDN_BWD_DISPATCH
