@@ -330,8 +330,19 @@ __global__ __launch_bounds__(256, 1) void gated_delta_chunk_bwd_state_kernel(Chu
   __shared__ __align__(16) ChunkGates gv[2];
 
   const int t = threadIdx.x, lane = t & 63, w = __builtin_amdgcn_readfirstlane(t >> 6), g4 = lane >> 4, li = lane & 15;
-  const int64_t chain = blockIdx.x / NVB;
-  const int vb = (int)(blockIdx.x % NVB);
+  // blockIdx b lands on XCD b % 8: XCD x takes chains x, x + 8, ..., all V/32 slices of a chain on
+  // one XCD, so the K, Q and T - I tiles its slices all read come from one L2 (as in the forward)
+  const int64_t chains = p.N * p.HV;
+  int64_t chain;
+  int vb;
+  if (chains % 8 == 0) {
+    const int64_t x = blockIdx.x % 8, j = blockIdx.x / 8;
+    chain = 8 * (j / NVB) + x;
+    vb = (int)(j % NVB);
+  } else {
+    chain = blockIdx.x / NVB;
+    vb = (int)(blockIdx.x % NVB);
+  }
   const int64_t n = chain / p.HV, hv = chain % p.HV, h = hv / (p.HV / p.H);
   int64_t bos, eos, cgb;
   const int64_t ncs = (p.T + kC - 1) / kC;
@@ -547,17 +558,6 @@ __global__ __launch_bounds__(256, 2) void gated_delta_chunk_bwd_grad_kernel(Chun
 
   for (int64_t rr = 0; rr < rep; ++rr) {
     const int64_t hv = h * rep + rr;
-    // T - I fragments of this wave's rows: (T - I) rows (Delta) and (T - I)^T rows (dX)
-    bf16x8 tfr[2], tft[2];
-    {
-      const auto rn = make_rsrc(p.tn + (c0 * p.HV + hv) * kC, (uint32_t)len * trow);
-      const auto rt = make_rsrc(p.tnt + (c0 * p.HV + hv) * kC, (uint32_t)len * trow);
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        tfr[u] = buf_load16(rn, (uint32_t)(tok0 + li) * trow + (32 * u + 8 * g4) * 2);
-        tft[u] = buf_load16(rt, (uint32_t)(tok0 + li) * trow + (32 * u + 8 * g4) * 2);
-      }
-    }
     uint32_t graw = 0, braw = 0;
     if (w == 0) fetch_gates_bwd(graw, braw, p, c0, hv, len, lane);
     if (t < kC) {
@@ -576,6 +576,19 @@ __global__ __launch_bounds__(256, 2) void gated_delta_chunk_bwd_grad_kernel(Chun
 #pragma unroll 1
     for (int pi = 0; pi < NP; ++pi) {
       fetch_pass(hv, pi, g1c);
+      // T - I fragments of this wave's rows, (T - I) rows (Delta) and (T - I)^T rows (dX): loaded
+      // with each pass (L2 hits after the first) so they are not live through the c x K products
+      bf16x8 tfr[2], tft[2];
+      {
+        const int lq = opaque_int(lane);
+        const auto rn = make_rsrc(p.tn + (c0 * p.HV + hv) * kC, (uint32_t)len * trow);
+        const auto rt = make_rsrc(p.tnt + (c0 * p.HV + hv) * kC, (uint32_t)len * trow);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          tfr[u] = buf_load16(rn, (uint32_t)(tok0 + (lq & 15)) * trow + (32 * u + 8 * (lq >> 4)) * 2);
+          tft[u] = buf_load16(rt, (uint32_t)(tok0 + (lq & 15)) * trow + (32 * u + 8 * (lq >> 4)) * 2);
+        }
+      }
       __syncthreads();  // the previous pass (or value head) is done with the LDS tiles
 #pragma unroll
       for (int u = 0; u < NSP; ++u) {
@@ -609,19 +622,19 @@ __global__ __launch_bounds__(256, 2) void gated_delta_chunk_bwd_grad_kernel(Chun
       }
       // X = beta V - beta a Y (V read from Xb, X written over it: each wave touches only its rows);
       // the a-term of dgam, scale a_t dO_t . (Q S)_t
-      f32x4 Vv[2], Dl[2];
+      bf16x4 Vv[2];  // V is bf16: kept as loaded
+      f32x4 Dl[2];
 #pragma unroll
       for (int ct = 0; ct < 2; ++ct) {
-        const bf16x4 vv = ld4_tr(Xb, XP, tok0, 16 * ct, ln);
+        Vv[ct] = ld4_tr(Xb, XP, tok0, 16 * ct, ln);
         const bf16x4 dd = ld4_tr(dOb, XP, tok0, 16 * ct, ln);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int tok = tok0 + 4 * (ln >> 4) + r;
-          Vv[ct][r] = (float)vv[r];
-          Dl[ct][r] = gs.bet[tok] * Vv[ct][r] - gs.begam[tok] * Y[ct][r];
+          Dl[ct][r] = gs.bet[tok] * (float)Vv[ct][r] - gs.begam[tok] * Y[ct][r];
           pg[r] += p.scale * gs.egam[tok] * (float)dd[r] * QS[ct][r];
         }
-        put_acc(Xb, XP, tok0, 16 * ct, lane, Dl[ct]);
+        put_acc(Xb, XP, tok0, 16 * ct, ln, Dl[ct]);
       }
       __syncthreads();
       // Delta = X + (T - I) X  ((T - I)_{tj} vanishes unless j < t)
@@ -633,15 +646,18 @@ __global__ __launch_bounds__(256, 2) void gated_delta_chunk_bwd_grad_kernel(Chun
           for (int ct = 0; ct < 2; ++ct) Dl[ct] = mma(tfr[u], frag_col(Xb, XP, 32 * u, 16 * ct, ln), Dl[ct]);
         }
 #pragma unroll
-      for (int ct = 0; ct < 2; ++ct) put_acc(Db, XP, tok0, 16 * ct, lane, Dl[ct]);
+      for (int ct = 0; ct < 2; ++ct) put_acc(Db, XP, tok0, 16 * ct, ln, Dl[ct]);
       __syncthreads();
-      // Z = r o (K dS') -> Xb
+      // Z = r o (K dS') -> Xb; the r-term of dgam, r_t (K dS')_t . Delta_t
       ln = opaque_int(lane);
 #pragma unroll
       for (int ct = 0; ct < 2; ++ct) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) W[ct][r] *= gs.dlast[tok0 + 4 * (ln >> 4) + r];
-        put_acc(Xb, XP, tok0, 16 * ct, lane, W[ct]);
+        for (int r = 0; r < 4; ++r) {
+          W[ct][r] *= gs.dlast[tok0 + 4 * (ln >> 4) + r];
+          pr[r] += W[ct][r] * Dl[ct][r];
+        }
+        put_acc(Xb, XP, tok0, 16 * ct, ln, W[ct]);
       }
       __syncthreads();
       // dX = G1 + Z + (T - I)^T Z
@@ -666,11 +682,10 @@ __global__ __launch_bounds__(256, 2) void gated_delta_chunk_bwd_grad_kernel(Chun
         for (int r = 0; r < 4; ++r) {
           const int tok = tok0 + 4 * (ln >> 4) + r;
           if (tok < len) dvg[((c0 + tok) * p.HV + hv) * VD + cc] = static_cast<bf16>(gs.bet[tok] * dX[ct][r]);
-          pb[r] += (Vv[ct][r] - gs.egam[tok] * Y[ct][r]) * dX[ct][r];
+          pb[r] += ((float)Vv[ct][r] - gs.egam[tok] * Y[ct][r]) * dX[ct][r];
           pg[r] -= gs.begam[tok] * dX[ct][r] * Y[ct][r];
-          pr[r] += W[ct][r] * Dl[ct][r];
         }
-        put_acc(dXb, XP, tok0, 16 * ct, lane, dX[ct]);
+        put_acc(dXb, XP, tok0, 16 * ct, ln, dX[ct]);
       }
       __syncthreads();
       // c x c: dA' += dX Delta^T, dP' += dO Delta^T on the tiles (w, jt <= w)
@@ -739,8 +754,8 @@ __global__ __launch_bounds__(256, 2) void gated_delta_chunk_bwd_grad_kernel(Chun
         pg[r] += pair;
         colp += pair;
       }
-      put_acc(cc1, kCPb, tok0, 16 * jt, lane, dG);
-      put_acc(cc2, kCPb, tok0, 16 * jt, lane, dQK);
+      put_acc(cc1, kCPb, tok0, 16 * jt, ln, dG);
+      put_acc(cc2, kCPb, tok0, 16 * jt, ln, dQK);
       colp += __shfl_xor(colp, 16, kWave);
       colp += __shfl_xor(colp, 32, kWave);
       if ((ln >> 4) == 0 && jt <= w) atomicAdd(&tg_[jj], -colp);
