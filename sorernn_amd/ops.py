@@ -13,9 +13,11 @@ its imports:
 
 Outputs are allocated here from torch's caching allocator; the C ABI never allocates.
 ``chunk_gated_delta_rule`` (bf16 q/k/v), ``causal_conv1d``, ``l2norm`` and ``rms_norm_gated`` are
-differentiable: with inputs that require grad they run as autograd functions whose backward
-launches the HIP backward kernels (``gdn_chunk_bwd``, ``gdn_causal_conv1d_bwd``, ``gdn_l2norm_bwd``,
-``gdn_rms_norm_gated_bwd``); the chunk forward then also saves the state entering every chunk. The
+differentiable: their backward launches the HIP backward kernels (``gdn_chunk_bwd``,
+``gdn_causal_conv1d_bwd``, ``gdn_l2norm_bwd``, ``gdn_rms_norm_gated_bwd``). The chunk op is a
+``torch.library`` custom op (``sorernn_amd/library.py``) with a fake implementation and a
+registered autograd formula, so ``torch.compile`` traces through it without a graph break; with
+grad, its forward also saves the state entering every chunk. The
 recurrent/decode operators are forward-only: a call that would need their backward raises
 ``NotImplementedError`` instead of silently detaching. Contract violations raise ``ValueError`` with the reference's wording
 ("B == 1", "cu_seqlens"; ``sore/model/gdn_ref.py:42-43,54-55``).
@@ -26,6 +28,7 @@ import torch
 from torch import Tensor
 
 from sorernn_amd import _lib
+from sorernn_amd import library as _library
 
 __all__ = [
     "causal_conv1d",
@@ -73,6 +76,11 @@ def _cu_info(name: str, cu_seqlens: Tensor | None, cu_seqlens_cpu: Tensor | None
         raise ValueError(f"{name}: cu_seqlens must be 1-D with at least 2 entries")
     if cu_seqlens.dtype not in (torch.int32, torch.int64):
         raise ValueError(f"{name}: cu_seqlens must be int32 or int64, got {cu_seqlens.dtype}")
+    flags = _lib.FLAG_CU_INT32 if cu_seqlens.dtype == torch.int32 else 0
+    if torch.compiler.is_compiling():
+        # under torch.compile the values are not read (no host sync, no graph break); the kernels
+        # need only N, and cu_seqlens_cpu is checked when the same call runs eagerly
+        return cu_seqlens.numel() - 1, flags
     host = cu_seqlens_cpu if cu_seqlens_cpu is not None else cu_seqlens.detach().cpu()
     if host.numel() != cu_seqlens.numel():
         raise ValueError(f"{name}: cu_seqlens_cpu has {host.numel()} entries, cu_seqlens {cu_seqlens.numel()}")
@@ -81,7 +89,7 @@ def _cu_info(name: str, cu_seqlens: Tensor | None, cu_seqlens_cpu: Tensor | None
         raise ValueError(f"{name}: cu_seqlens must go from 0 to T = {t}, got {b[0]}..{b[-1]}")
     if any(y <= x for x, y in zip(b[:-1], b[1:])):
         raise ValueError(f"{name}: cu_seqlens must be strictly increasing")
-    return len(b) - 1, (_lib.FLAG_CU_INT32 if cu_seqlens.dtype == torch.int32 else 0)
+    return len(b) - 1, flags
 
 
 def _delta_rule_args(name, q, k, v, g, beta, scale, initial_state, cu_seqlens, cu_seqlens_cpu,
@@ -132,17 +140,20 @@ def _gdn_call(entry, name, q, k, v, g, beta, scale, initial_state, output_final_
         # recurrent kernel, which computes the same recurrence token by token in fp32.
         entry = "gdn_recurrent_fwd"
     grad_inputs = [q, k, v, g, beta, initial_state] + ([a_log_in, dt_bias_in] if use_gate_in_kernel else [])
-    if torch.is_grad_enabled() and any(x is not None and x.requires_grad for x in grad_inputs):
-        if entry != "gdn_chunk_fwd" or inplace_final_state:
-            raise NotImplementedError(
-                f"{name}: the backward exists for chunk_gated_delta_rule with bf16 q/k/v only (inputs "
-                "require grad); run under torch.no_grad() or detach the inputs"
-            )
-        cu = cu_seqlens.contiguous() if cu_seqlens is not None else None
-        meta = (b, t, h, kd, hv, vd, n, flags, scale, bool(output_final_state))
-        return _ChunkGatedDeltaRule.apply(q, k, v, g, beta, initial_state,
-                                          a_log_in if use_gate_in_kernel else None,
-                                          dt_bias_in if use_gate_in_kernel else None, cu, meta)
+    needs_grad = torch.is_grad_enabled() and any(x is not None and x.requires_grad for x in grad_inputs)
+    if needs_grad and (entry != "gdn_chunk_fwd" or inplace_final_state):
+        raise NotImplementedError(
+            f"{name}: the backward exists for chunk_gated_delta_rule with bf16 q/k/v only (inputs "
+            "require grad); run under torch.no_grad() or detach the inputs"
+        )
+    if entry == "gdn_chunk_fwd":
+        # the torch.library op (sorernn::chunk_gated_delta_rule_fwd): traceable by torch.compile, with
+        # the backward registered on it; with grad it also keeps the per-chunk states for the backward
+        o, final, _, _ = _library.chunk_fwd(q, k, v, g, beta, initial_state,
+                                            a_log_in if use_gate_in_kernel else None,
+                                            dt_bias_in if use_gate_in_kernel else None, cu_seqlens, scale, flags, n,
+                                            bool(output_final_state), needs_grad)
+        return o, (final if output_final_state else None)
     q, k, v, g, beta = (x.contiguous() for x in (q, k, v, g, beta))
     h0 = None
     if initial_state is not None:
@@ -173,81 +184,6 @@ def _gdn_call(entry, name, q, k, v, g, beta, scale, initial_state, output_final_
 def chunk_workspace_bytes(batch: int, seqlen: int, num_v_heads: int, num_seqs: int, varlen: bool) -> int:
     """Bytes of device workspace ``gdn_chunk_fwd`` needs (the per-chunk ``(I + A)^-1`` rows)."""
     return int(_lib.load().gdn_chunk_workspace_size(batch, seqlen, num_v_heads, num_seqs, int(varlen)))
-
-
-class _ChunkGatedDeltaRule(torch.autograd.Function):
-    """``chunk_gated_delta_rule`` with a backward (the reference trains through FLA's autograd function).
-
-    Forward: ``gdn_chunk_fwd_train``, which also keeps the state entering every chunk (bf16) and the
-    per-chunk ``(I + A)^-1`` rows for the backward. Backward: ``gdn_chunk_bwd`` (dq, dk, dv, dg,
-    dbeta, the initial state's gradient and, with the in-kernel gate, dA_log and ddt_bias).
-    """
-
-    @staticmethod
-    def forward(ctx, q, k, v, g, beta, initial_state, A_log, dt_bias, cu, meta):
-        b, t, h, kd, hv, vd, n, flags, scale, output_final_state = meta
-        qc, kc, vc, gc, bc = (x.detach().contiguous() for x in (q, k, v, g, beta))
-        h0 = None if initial_state is None else initial_state.detach().float().contiguous()
-        al = None if A_log is None else A_log.detach().float().contiguous()
-        dtb = None if dt_bias is None else dt_bias.detach().float().contiguous()
-        lib = _lib.load()
-        varlen = cu is not None
-        o = torch.empty(b, t, hv, vd, device=q.device, dtype=q.dtype)
-        final = torch.empty(n, hv, kd, vd, device=q.device, dtype=torch.float32) if output_final_state else None
-        ws = torch.empty(max(chunk_workspace_bytes(b, t, hv, n, varlen), 1), dtype=torch.uint8, device=q.device)
-        nstate = int(lib.gdn_chunk_states_size(b, t, hv, kd, vd, n, int(varlen)))
-        states = torch.empty(max(nstate, 1), dtype=torch.uint8, device=q.device)
-        if t > 0:
-            _lib.call("gdn_chunk_fwd_train", _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(vc), _lib.ptr(gc), _lib.ptr(bc),
-                      _lib.ptr(h0), _lib.ptr(o), _lib.ptr(final), _lib.ptr(cu), b, t, h, hv, kd, vd, n,
-                      _lib.dtype_code(qc.dtype), _lib.dtype_code(gc.dtype), _lib.dtype_code(bc.dtype), scale, flags,
-                      _lib.ptr(al), _lib.ptr(dtb), _lib.ptr(states), _lib.ptr(ws), ws.numel(), _lib.stream_of(qc))
-        elif final is not None:
-            final.copy_(h0 if h0 is not None else torch.zeros_like(final))
-        ctx.save_for_backward(qc, kc, vc, gc, bc, al, dtb, cu, states, ws)
-        ctx.set_materialize_grads(False)
-        ctx.meta = meta
-        ctx.h0_dtype = None if initial_state is None else initial_state.dtype
-        ctx.param_dtypes = (None if A_log is None else A_log.dtype, None if dt_bias is None else dt_bias.dtype)
-        return o, final
-
-    @staticmethod
-    def backward(ctx, do, dfinal):
-        qc, kc, vc, gc, bc, al, dtb, cu, states, ws = ctx.saved_tensors
-        b, t, h, kd, hv, vd, n, flags, scale, _ = ctx.meta
-        dev = qc.device
-        if do is None:
-            do = torch.zeros(b, t, hv, vd, device=dev, dtype=qc.dtype)
-        do = do.to(qc.dtype).contiguous()
-        dht = None if dfinal is None else dfinal.float().contiguous()
-        dq, dk, dv = torch.empty_like(qc), torch.empty_like(kc), torch.empty_like(vc)
-        dg, db = torch.empty_like(gc), torch.empty_like(bc)
-        want_h0 = ctx.h0_dtype is not None and ctx.needs_input_grad[5]
-        dh0 = torch.empty(n, hv, kd, vd, device=dev, dtype=torch.float32) if want_h0 else None
-        gate = bool(flags & _lib.FLAG_GATE_IN_KERNEL)
-        dal = torch.empty(hv, device=dev, dtype=torch.float32) if gate else None
-        ddt = torch.empty(hv, device=dev, dtype=torch.float32) if gate else None
-        if t > 0:
-            lib = _lib.load()
-            nbytes = int(lib.gdn_chunk_bwd_workspace_size(b, t, hv, kd, vd, n, int(cu is not None)))
-            bws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
-            _lib.call("gdn_chunk_bwd", _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(vc), _lib.ptr(gc), _lib.ptr(bc),
-                      _lib.ptr(do), _lib.ptr(dht), _lib.ptr(states), _lib.ptr(ws), _lib.ptr(cu), b, t, h, hv, kd, vd,
-                      n, _lib.dtype_code(qc.dtype), _lib.dtype_code(gc.dtype), _lib.dtype_code(bc.dtype), scale,
-                      flags, _lib.ptr(al), _lib.ptr(dtb), _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(dg),
-                      _lib.ptr(db), _lib.ptr(dh0), _lib.ptr(dal), _lib.ptr(ddt), _lib.ptr(bws), bws.numel(),
-                      _lib.stream_of(qc))
-        else:
-            if dh0 is not None:
-                dh0.copy_(dht if dht is not None else torch.zeros_like(dh0))
-            if gate:
-                dal.zero_()
-                ddt.zero_()
-        if dh0 is not None:
-            dh0 = dh0.to(ctx.h0_dtype)
-        if gate:
-            dal, ddt = dal.to(ctx.param_dtypes[0]), ddt.to(ctx.param_dtypes[1])
-        return dq, dk, dv, dg, db, dh0, dal, ddt, None, None
 
 
 def chunk_gated_delta_rule(
@@ -430,31 +366,14 @@ def causal_conv1d(
     if initial_state is not None and tuple(initial_state.shape) != (n, c, w):
         raise ValueError(f"{name}: initial_state must be [N,C,W] = {(n, c, w)}")
     cu = cu_seqlens.contiguous() if cu_seqlens is not None else None
-    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (x, weight, bias, initial_state)):
-        return _CausalConv1d.apply(x, weight, bias, initial_state, cu, (b, t, c, w, n, flags, act, bool(output_final_state)))
-    x = x.contiguous()
-    if initial_state is not None:
-        initial_state = initial_state.to(x.dtype).contiguous()
-    wgt = weight.detach().float().contiguous()
-    bs = None if bias is None else bias.detach().float().contiguous()
-    y = torch.empty_like(x)
-    fin = torch.empty(n, c, w, device=x.device, dtype=x.dtype) if output_final_state else None
-    _lib.call("gdn_causal_conv1d_fwd", _lib.ptr(x), _lib.ptr(wgt), _lib.ptr(bs), _lib.ptr(y), _lib.ptr(initial_state),
-              _lib.ptr(fin), _lib.ptr(cu), b, t, c, w, n, _lib.dtype_code(x.dtype), act, flags, _lib.stream_of(x))
-    return y, fin
+    y, fin = _library.conv_fwd(x, weight, bias, initial_state, cu, act, flags, n, bool(output_final_state))
+    return y, (fin if output_final_state else None)
 
 
 def l2norm(x: Tensor, eps: float = 1e-12) -> Tensor:
     """``x / max(||x||_2, eps)`` over the last axis (``F.normalize`` semantics, fp32 math, one rounding)."""
     _check_cuda("l2norm", x)
-    if torch.is_grad_enabled() and x.requires_grad:
-        return _L2Norm.apply(x, float(eps))
-    xc = x.contiguous()
-    y = torch.empty_like(xc)
-    d = xc.shape[-1]
-    _lib.call("gdn_l2norm_fwd", _lib.ptr(xc), _lib.ptr(y), xc.numel() // max(d, 1), d, _lib.dtype_code(xc.dtype),
-              float(eps), _lib.stream_of(xc))
-    return y
+    return _library.l2norm_fwd(x, float(eps))
 
 
 def rms_norm_gated(
@@ -487,127 +406,4 @@ def rms_norm_gated(
     d = x.shape[-1]
     if (weight is not None and weight.numel() != d) or (bias is not None and bias.numel() != d):
         raise ValueError(f"{name}: weight/bias must have {d} entries")
-    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (x, g, weight, bias)):
-        return _RMSNormGated.apply(x, g, weight, bias, float(eps), act)
-    xc = x.contiguous()
-    gc = None
-    if g is not None:
-        gc = g.to(xc.dtype).contiguous()
-    wc = None if weight is None else weight.detach().float().contiguous()
-    bc = None if bias is None else bias.detach().float().contiguous()
-    y = torch.empty_like(xc)
-    _lib.call("gdn_rms_norm_gated_fwd", _lib.ptr(xc), _lib.ptr(gc), _lib.ptr(wc), _lib.ptr(bc), _lib.ptr(y),
-              xc.numel() // max(d, 1), d, _lib.dtype_code(xc.dtype), float(eps), act, _lib.stream_of(xc))
-    return y
-
-
-class _CausalConv1d(torch.autograd.Function):
-    """``causal_conv1d`` with a backward (``gdn_causal_conv1d_bwd``).
-
-    The conv cache output (``final_state``) is the decode path's state: a gradient through it is not
-    supported and raises in the backward.
-    """
-
-    @staticmethod
-    def forward(ctx, x, weight, bias, initial_state, cu, meta):
-        b, t, c, w, n, flags, act, output_final_state = meta
-        xc = x.detach().contiguous()
-        init = None if initial_state is None else initial_state.detach().to(x.dtype).contiguous()
-        wgt = weight.detach().float().contiguous()
-        bs = None if bias is None else bias.detach().float().contiguous()
-        y = torch.empty_like(xc)
-        fin = torch.empty(n, c, w, device=x.device, dtype=x.dtype) if output_final_state else None
-        _lib.call("gdn_causal_conv1d_fwd", _lib.ptr(xc), _lib.ptr(wgt), _lib.ptr(bs), _lib.ptr(y), _lib.ptr(init),
-                  _lib.ptr(fin), _lib.ptr(cu), b, t, c, w, n, _lib.dtype_code(xc.dtype), act, flags, _lib.stream_of(xc))
-        ctx.save_for_backward(xc, wgt, bs, init, cu)
-        ctx.set_materialize_grads(False)
-        ctx.meta = meta
-        ctx.dtypes = (weight.dtype, None if bias is None else bias.dtype,
-                      None if initial_state is None else initial_state.dtype)
-        return y, fin
-
-    @staticmethod
-    def backward(ctx, dy, dfin):
-        if dfin is not None:
-            raise NotImplementedError("causal_conv1d: no gradient through final_state (the decode cache)")
-        xc, wgt, bs, init, cu = ctx.saved_tensors
-        b, t, c, w, n, flags, act, _ = ctx.meta
-        dy = torch.zeros_like(xc) if dy is None else dy.to(xc.dtype).contiguous()
-        dx = torch.empty_like(xc)
-        dw = torch.empty(c, w, device=xc.device, dtype=torch.float32)
-        db = None if bs is None else torch.empty(c, device=xc.device, dtype=torch.float32)
-        dinit = None if init is None else torch.empty(n, c, w, device=xc.device, dtype=torch.float32)
-        lib = _lib.load()
-        ws = torch.empty(max(int(lib.gdn_causal_conv1d_bwd_workspace_size(b, t, c, w)), 1), dtype=torch.uint8,
-                         device=xc.device)
-        _lib.call("gdn_causal_conv1d_bwd", _lib.ptr(xc), _lib.ptr(wgt), _lib.ptr(bs), _lib.ptr(dy), _lib.ptr(init),
-                  _lib.ptr(cu), b, t, c, w, n, _lib.dtype_code(xc.dtype), act, flags, _lib.ptr(dx), _lib.ptr(dw),
-                  _lib.ptr(db), _lib.ptr(dinit), _lib.ptr(ws), ws.numel(), _lib.stream_of(xc))
-        wdt, bdt, idt = ctx.dtypes
-        return (dx, dw.to(wdt), None if db is None else db.to(bdt), None if dinit is None else dinit.to(idt), None, None)
-
-
-class _L2Norm(torch.autograd.Function):
-    """``l2norm`` with a backward (``gdn_l2norm_bwd``)."""
-
-    @staticmethod
-    def forward(ctx, x, eps):
-        xc = x.detach().contiguous()
-        y = torch.empty_like(xc)
-        d = xc.shape[-1]
-        rows = xc.numel() // max(d, 1)
-        _lib.call("gdn_l2norm_fwd", _lib.ptr(xc), _lib.ptr(y), rows, d, _lib.dtype_code(xc.dtype), eps, _lib.stream_of(xc))
-        ctx.save_for_backward(xc)
-        ctx.eps = eps
-        return y
-
-    @staticmethod
-    def backward(ctx, dy):
-        (xc,) = ctx.saved_tensors
-        dy = dy.to(xc.dtype).contiguous()
-        dx = torch.empty_like(xc)
-        d = xc.shape[-1]
-        _lib.call("gdn_l2norm_bwd", _lib.ptr(xc), _lib.ptr(dy), _lib.ptr(dx), xc.numel() // max(d, 1), d,
-                  _lib.dtype_code(xc.dtype), ctx.eps, _lib.stream_of(xc))
-        return dx, None
-
-
-class _RMSNormGated(torch.autograd.Function):
-    """``rms_norm_gated`` with a backward (``gdn_rms_norm_gated_bwd``)."""
-
-    @staticmethod
-    def forward(ctx, x, g, weight, bias, eps, act):
-        xc = x.detach().contiguous()
-        gc = None if g is None else g.detach().to(xc.dtype).contiguous()
-        wc = None if weight is None else weight.detach().float().contiguous()
-        bc = None if bias is None else bias.detach().float().contiguous()
-        y = torch.empty_like(xc)
-        d = xc.shape[-1]
-        rows = xc.numel() // max(d, 1)
-        _lib.call("gdn_rms_norm_gated_fwd", _lib.ptr(xc), _lib.ptr(gc), _lib.ptr(wc), _lib.ptr(bc), _lib.ptr(y), rows,
-                  d, _lib.dtype_code(xc.dtype), eps, act, _lib.stream_of(xc))
-        ctx.save_for_backward(xc, gc, wc, bc)
-        ctx.eps, ctx.act = eps, act
-        ctx.dtypes = (None if g is None else g.dtype, None if weight is None else weight.dtype,
-                      None if bias is None else bias.dtype)
-        return y
-
-    @staticmethod
-    def backward(ctx, dy):
-        xc, gc, wc, bc = ctx.saved_tensors
-        dy = dy.to(xc.dtype).contiguous()
-        d = xc.shape[-1]
-        rows = xc.numel() // max(d, 1)
-        dx = torch.empty_like(xc)
-        dg = None if gc is None else torch.empty_like(gc)
-        dw = None if wc is None else torch.empty(d, device=xc.device, dtype=torch.float32)
-        db = None if bc is None else torch.empty(d, device=xc.device, dtype=torch.float32)
-        lib = _lib.load()
-        ws = torch.empty(max(int(lib.gdn_rms_norm_gated_bwd_workspace_size(rows, d)), 1), dtype=torch.uint8,
-                         device=xc.device)
-        _lib.call("gdn_rms_norm_gated_bwd", _lib.ptr(xc), _lib.ptr(gc), _lib.ptr(wc), _lib.ptr(bc), _lib.ptr(dy),
-                  _lib.ptr(dx), _lib.ptr(dg), _lib.ptr(dw), _lib.ptr(db), rows, d, _lib.dtype_code(xc.dtype), ctx.eps,
-                  ctx.act, _lib.ptr(ws), ws.numel(), _lib.stream_of(xc))
-        gdt, wdt, bdt = ctx.dtypes
-        return (dx, None if dg is None else dg.to(gdt), None if dw is None else dw.to(wdt),
-                None if db is None else db.to(bdt), None, None)
+    return _library.rms_fwd(x, g, weight, bias, float(eps), act)

@@ -74,3 +74,20 @@ def test_chunk_backward_buffer_sizes_match_layout():
     assert lib.gdn_chunk_bwd_workspace_size(4, 4096, 16, 128, 128, 4, 0) == (
         2 * a(tok * 16 * 128) + a(tok * 16 * 128 * 4) + a(ch * 16 * 128 * 128 * 2) + a(ch * 16 * 8))
     assert lib.gdn_chunk_bwd_workspace_size(0, 4096, 16, 128, 128, 4, 0) == 0
+
+
+def test_every_kernel_name_matches_the_reference_profiler_gdn_rule():
+    """The reference's profiler files kernels into its "gdn" category with
+    ``^(chunk_|recompute_w_u|prepare_wy_repr|l2norm_|fused_recurrent|fused_gdn|solve_tril|merge_16x16|causal_conv1d)|gated_delta``
+    searched over the kernel name (sore/train/profiling.py:35); every kernel of this build must land there."""
+    import re
+    rule = re.compile(r"^(chunk_|recompute_w_u|prepare_wy_repr|l2norm_|fused_recurrent|fused_gdn|solve_tril|merge_16x16|causal_conv1d)|gated_delta")
+    csrc = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "sorernn_amd", "csrc")
+    names = []
+    for f in sorted(os.listdir(csrc)):
+        if f.endswith(".hip"):
+            src = open(os.path.join(csrc, f)).read()
+            names += re.findall(r"__global__\s+(?:__launch_bounds__\([^)]*\)\s+)?void\s+(\w+)", src)
+    assert len(names) >= 15, names
+    for n in names:
+        assert rule.search(f"void gdn::{n}<128, 128>(gdn::Params)"), n

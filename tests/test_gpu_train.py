@@ -147,3 +147,32 @@ def test_layer_backward_matches_oracle(cu):
     print("  rel L2:", {k: f"{v:.1e}" for k, v in errs.items()}, flush=True)
     bad = {k: v for k, v in errs.items() if v > 3e-2}
     assert not bad, f"gradients off: {bad}"
+
+
+@pytest.mark.parametrize("cu", [None, [0, 1, 3, 4, 70, 200, 256]], ids=["rows", "short_docs"])
+def test_layer_step_compiles_without_graph_breaks(cu):
+    """``torch.compile(fullgraph=True)`` of a layer's forward + backward (a graph break raises); the
+    compiled step's gradients match the eager step's."""
+    torch.manual_seed(0)
+    cfg = GDNLayerConfig(d_model=128, gdn_qk_heads=2, gdn_v_heads=4, gdn_head_dim=64, gdn_kernel_gate=True)
+    layer = GatedDeltaNet(cfg).to(DEV)
+    b = 2 if cu is None else 1
+    x = torch.randn(b, 256, 128, generator=torch.Generator().manual_seed(3)).to(DEV)
+    cu_t = None if cu is None else torch.tensor(cu)
+    cu_d = None if cu_t is None else cu_t.to(DEV)
+
+    def step(xx):
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            out = layer(xx, cu_seqlens=cu_d, cu_seqlens_cpu=cu_t)
+        return out.float().square().mean()
+
+    grads = []
+    for fn in (step, torch.compile(step, fullgraph=True, backend="aot_eager")):
+        layer.zero_grad(set_to_none=True)
+        xx = x.clone().requires_grad_(True)
+        fn(xx).backward()
+        torch.cuda.synchronize()
+        grads.append([xx.grad] + [p.grad for p in layer.parameters()])
+    # the traced graph may place autocast's bf16 casts differently: equal to bf16 rounding, not bit-exact
+    for a, b_ in zip(*grads):
+        assert rel_l2(a, b_) <= 2e-2, rel_l2(a, b_)
