@@ -176,3 +176,45 @@ def test_layer_step_compiles_without_graph_breaks(cu):
     # the traced graph may place autocast's bf16 casts differently: equal to bf16 rounding, not bit-exact
     for a, b_ in zip(*grads):
         assert rel_l2(a, b_) <= 2e-2, rel_l2(a, b_)
+
+
+def test_selective_checkpoint_policy_sees_the_gdn_ops():
+    """The ops go through the dispatcher (``torch.ops.sorernn.*``), so a selective activation-checkpoint
+    policy can save them. The reference notes that FLA's autograd functions bypass the dispatcher and
+    are always recomputed (``sore/model/checkpointing.py:10-17``). With MUST_SAVE on the chunk op
+    the checkpointed step equals the plain one."""
+    import functools
+    from torch.utils.checkpoint import CheckpointPolicy, checkpoint, create_selective_checkpoint_contexts
+
+    torch.manual_seed(0)
+    cfg = GDNLayerConfig(d_model=128, gdn_qk_heads=2, gdn_v_heads=4, gdn_head_dim=64, gdn_kernel_gate=True)
+    layer = GatedDeltaNet(cfg).to(DEV)
+    x = torch.randn(2, 192, 128, generator=torch.Generator().manual_seed(4)).to(DEV)
+    seen = set()
+    saved_ops = {torch.ops.sorernn.chunk_gated_delta_rule_fwd.default, torch.ops.sorernn.causal_conv1d_fwd.default}
+
+    def policy(ctx, op, *args, **kwargs):
+        if str(op).startswith("sorernn."):
+            seen.add(str(op))
+        return CheckpointPolicy.MUST_SAVE if op in saved_ops else CheckpointPolicy.PREFER_RECOMPUTE
+
+    def fwd(xx):
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            return layer(xx).float().square().mean()
+
+    grads = []
+    for use_ckpt in (False, True):
+        layer.zero_grad(set_to_none=True)
+        xx = x.clone().requires_grad_(True)
+        if use_ckpt:
+            loss = checkpoint(fwd, xx, use_reentrant=False,
+                              context_fn=functools.partial(create_selective_checkpoint_contexts, policy))
+        else:
+            loss = fwd(xx)
+        loss.backward()
+        torch.cuda.synchronize()
+        grads.append([xx.grad] + [p.grad for p in layer.parameters()])
+    assert {"sorernn.chunk_gated_delta_rule_fwd.default", "sorernn.causal_conv1d_fwd.default",
+            "sorernn.rms_norm_gated_fwd.default"} <= seen, seen
+    for a, b_ in zip(*grads):
+        assert rel_l2(a, b_) <= 2e-2, rel_l2(a, b_)
