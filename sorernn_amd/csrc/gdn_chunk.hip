@@ -204,18 +204,28 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
 #pragma unroll
     for (int u = 0; u < 2; ++u) *reinterpret_cast<bf16x8*>(v0 + 32 * u * kVP) = pv[u];
   };
-  auto fetch_gates = [&](int c, uint32_t& graw, uint32_t& braw) {  // wave 4, lane = token
+  // The gate bits of a chunk are loaded as both a 32-bit and a 16-bit word (each range-checked) and
+  // the dtype picks one at the use: a load whose width depends on the dtype would be two
+  // instructions on two paths, and the loop-carried register they share would then be copied at
+  // the loop's join under a wait for every load and store in flight.
+  struct GateBits {
+    uint32_t g32, g16, b32, b16;
+  };
+  auto fetch_gates = [&](int c, GateBits& r) {  // wave 4, lane = token
     const int64_t c0 = bos + (int64_t)c * kC;
     const uint32_t gb = (uint32_t)(p.HV * dtype_bytes(p.dg)), bb = (uint32_t)(p.HV * dtype_bytes(p.db));
     const uint32_t len = (uint32_t)chunk_len(c);
     const auto rg = make_rsrc(static_cast<const char*>(p.g) + (c0 * p.HV + hv) * dtype_bytes(p.dg), len * gb);
     const auto rb = make_rsrc(static_cast<const char*>(p.beta) + (c0 * p.HV + hv) * dtype_bytes(p.db), len * bb);
-    graw = buf_load_raw32(rg, lane * gb, p.dg);
-    braw = buf_load_raw32(rb, lane * bb, p.db);
+    r.g32 = __builtin_amdgcn_raw_buffer_load_b32(rg, (int)(lane * gb), 0, 0);
+    r.g16 = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rg, (int)(lane * gb), 0, 0);
+    r.b32 = __builtin_amdgcn_raw_buffer_load_b32(rb, (int)(lane * bb), 0, 0);
+    r.b16 = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rb, (int)(lane * bb), 0, 0);
   };
-  auto stage_gates = [&](int c, uint32_t graw, uint32_t braw) {
+  auto stage_gates = [&](int c, const GateBits& r) {
     // (A_log through opaque_int: its exp is recomputed here, not held in a register)
     const float al = __int_as_float(opaque_int(__float_as_int(a_log)));
+    const uint32_t graw = p.dg == GDN_DTYPE_F32 ? r.g32 : r.g16, braw = p.db == GDN_DTYPE_F32 ? r.b32 : r.b16;
     chunk_gates_from_raw(gv[c % 3], graw, braw, p.dg, p.db, chunk_len(c), p.flags, al, dt_b, lane);
   };
   auto store_o = [&](int c, int tq) {  // waves 4-5: O of chunk c from Ob to HBM, rows tq / 4 + 32u
@@ -296,9 +306,22 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
   float ec_next = 1.f;  // e^{gam_c} of the chunk the next step processes
   auto sb = [&](int s) { return __builtin_bit_cast(f16x8, SB[s]); };
   const int64_t sbase = (n * p.HV + hv) * (int64_t)KD * VD + vb * kVB + 16 * sw;
+  // SAVE: global index of the sequence's first chunk (chunks before it with cu_seqlens)
+  const int64_t cg_first = SAVE ? (p.cu ? (int64_t)p.chunk_first[n] : n * ((p.T + kC - 1) / kC)) : 0;
   auto make_sb = [&]() {
 #pragma unroll
     for (int s = 0; s < KS; ++s) SB[s] = __builtin_bit_cast(f32x4, pack8h(S[2 * s], S[2 * s + 1]));
+  };
+  // SAVE: S (the state entering chunk c) as bf16 into its [V][K] slot: a buffer resource over the
+  // chunk-head's state (uniform base), lane offsets from an opaque lane id
+  auto save_state = [&](int c) {
+    const auto rs = make_rsrc(p.hs + ((cg_first + c) * p.HV + hv) * (int64_t)(KD * VD), (uint32_t)(KD * VD * 2));
+    const int ls = opaque_int(lane);
+    const uint32_t off = (uint32_t)(((vb * kVB + 16 * sw + (ls & 15)) * KD + 8 * (ls >> 4)) * 2);
+#pragma unroll
+    for (int a = 0; a < KT; ++a)
+      __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, to_bf16x4(S[a][0], S[a][1], S[a][2], S[a][3])), rs,
+                                            (int)(off + (32 * (a >> 1) + 4 * (a & 1)) * 2), 0, 0);
   };
   // K row fragments of Y = K S for chunk c, key steps s < KSH (row tile b), read ahead
   auto load_kf = [&](int c) {
@@ -313,7 +336,7 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
   // order, so every phase finds its operands arrived or in flight instead of starting a round trip.
   auto phase = [] { __builtin_amdgcn_sched_barrier(0); };
 
-  uint32_t ngraw = 0, nbraw = 0;  // wave 4: raw gate bits of the chunk two steps ahead, in flight
+  GateBits ngate{0, 0, 0, 0};  // wave 4: raw gate bits of the chunk two steps ahead, in flight
 
   // ------------------------------------------------------------------ prologue
   // P is causally lower: its tiles above the diagonal stay zero for the whole run
@@ -329,6 +352,9 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
       for (int r = 0; r < 4; ++r) S[a][r] = p.h0 ? p.h0[sbase + (int64_t)(kd0 + r) * VD + li] : 0.f;
     }
     make_sb();
+    if constexpr (SAVE) {
+      if (nc > 0) save_state(0);
+    }
   } else if (qk_wave) {  // K/Q of chunks 0 and 1
     bf16x8 pk[QKPT], pq[QKPT];
     for (int c = 0; c < 2; ++c) {
@@ -343,11 +369,11 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
     stage_tv(pt, pv, 0, thv);
     if (w == 4) {
       for (int c = 0; c < 2; ++c) {
-        uint32_t graw, braw;
-        fetch_gates(c, graw, braw);
-        stage_gates(c, graw, braw);
+        GateBits gb0;
+        fetch_gates(c, gb0);
+        stage_gates(c, gb0);
       }
-      fetch_gates(2, ngraw, nbraw);
+      fetch_gates(2, ngate);
     }
   }
   __syncthreads();
@@ -378,13 +404,6 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
   // T_{i+1}, V_{i+1}, P_{i+1}, gates_{i+2}. No slot is written and read in the same step.
   for (int i = 0; i < nc; ++i) {
     if (w < 2) {
-      if constexpr (SAVE) {
-        const int64_t cg = (p.cu ? (int64_t)p.chunk_first[n] : n * ((p.T + kC - 1) / kC)) + i;
-        bf16* hp = p.hs + ((cg * p.HV + hv) * VD + vb * kVB + 16 * sw + li) * (int64_t)KD;
-#pragma unroll
-        for (int a = 0; a < KT; ++a)
-          *reinterpret_cast<bf16x4*>(hp + 32 * (a >> 1) + 8 * g4 + 4 * (a & 1)) = to_bf16x4(S[a][0], S[a][1], S[a][2], S[a][3]);
-      }
       const f16* kb = Kc[i % 3];
       const f16* tp = Tb[i & 1];
       const bf16* vp = Vc[i & 1];
@@ -522,6 +541,11 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
       for (int s2 = 0; s2 < KS; ++s2)
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb) Zt[tb] = mmah(sb(s2), qf[s2][tb], Zt[tb]);
+      if constexpr (SAVE) {
+        // S' (updated in phase 4) is the state entering chunk i + 1; stored at the step's end, away
+        // from the helpers' load burst at its start
+        if (i + 1 < nc) save_state(i + 1);
+      }
     } else if (qk_wave) {  // K/Q of chunk i+2 (loads first, P of chunk i+1 while they land)
       const int tq = thq_of(opaque_int(lane));
       bf16x8 pk[QKPT], pq[QKPT];
@@ -535,8 +559,8 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
       bf16x8 pt[4], pv[2];
       fetch_tv(pt, pv, i + 1, tq);
       if (w == 4) {  // gates of chunk i+2 (loaded a step ago), then the loads for chunk i+3
-        stage_gates(i + 2, ngraw, nbraw);
-        fetch_gates(i + 3, ngraw, nbraw);
+        stage_gates(i + 2, ngate);
+        fetch_gates(i + 3, ngate);
       }
       if (i > 0) store_o(i - 1, tq);
       stage_tv(pt, pv, (i + 1) & 1, tq);

@@ -108,7 +108,7 @@ __global__ __launch_bounds__(256) void gated_delta_norm_bwd_kernel(NormBwdParams
 #pragma unroll
       for (int j = 0; j < kNormMaxPerLane; ++j) {
         const int64_t e = lane + (int64_t)j * kWave;
-        if (e >= p.D) break;
+        if (e >= p.D) continue;
         store_from_f32(p.dx, p.dt, base + e, (dv[j] - xv[j] * inv * dot) * inv);
       }
     } else {
@@ -117,7 +117,7 @@ __global__ __launch_bounds__(256) void gated_delta_norm_bwd_kernel(NormBwdParams
 #pragma unroll
       for (int j = 0; j < kNormMaxPerLane; ++j) {
         const int64_t e = lane + (int64_t)j * kWave;
-        if (e >= p.D) break;
+        if (e >= p.D) continue;
         const float n = xv[j] * rr, wv = p.w ? p.w[e] : 1.f;
         float du = dv[j];
         if (p.gate) {
@@ -141,7 +141,7 @@ __global__ __launch_bounds__(256) void gated_delta_norm_bwd_kernel(NormBwdParams
 #pragma unroll
       for (int j = 0; j < kNormMaxPerLane; ++j) {
         const int64_t e = lane + (int64_t)j * kWave;
-        if (e >= p.D) break;
+        if (e >= p.D) continue;
         store_from_f32(p.dx, p.dt, base + e, rr * dv[j] - xv[j] * rr * rr * rr * dot);
       }
     }
@@ -150,7 +150,7 @@ __global__ __launch_bounds__(256) void gated_delta_norm_bwd_kernel(NormBwdParams
 #pragma unroll
     for (int j = 0; j < kNormMaxPerLane; ++j) {
       const int64_t e = lane + (int64_t)j * kWave;
-      if (e >= p.D) break;
+      if (e >= p.D) continue;
       p.part[(wave * 2) * p.D + e] = pw[j];
       p.part[(wave * 2 + 1) * p.D + e] = pb[j];
     }
