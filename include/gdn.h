@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define GDN_ABI_VERSION 3
+#define GDN_ABI_VERSION 4
 
 #if defined(__GNUC__) || defined(__clang__)
 #define GDN_API __attribute__((visibility("default")))
@@ -226,6 +226,35 @@ GDN_API int gdn_rms_norm_gated_bwd(const void* x, const void* gate, const float*
 
 /* Workspace bytes gdn_rms_norm_gated_bwd needs. No counterpart in the reference. */
 GDN_API size_t gdn_rms_norm_gated_bwd_workspace_size(int64_t rows, int64_t D);
+
+/*
+ * Gated attention prologue: per (token, head) row of q_in [B, T, HQ*D] and k_in [B, T, HKV*D]
+ * (row strides q_row_stride / k_row_stride elements, e.g. column slices of one fused projection
+ * output), RMSNorm over D with weights q_weight / k_weight [D] (w_dtype fp32 or bf16), then the
+ * GPT-NeoX rotary embedding on the first rot_dim dims at the token's position (restarting at 0 in
+ * every document with cu_seqlens). Writes q_out [B, T, HQ, D] and k_out [B, T, HKV, D] contiguous.
+ * bf16 activations. Replaces q_norm(q_proj(x)), k_norm(k_proj(x)) and self.rotary(q, k, positions)
+ * in GatedAttention.forward (sore/model/attention.py:105-116; RMSNorm sore/model/layers.py:7-18;
+ * PartialRotary sore/model/rope.py:24-41) with the same rounding points.
+ */
+GDN_API int gdn_attn_qk_norm_rope_fwd(const void* q_in, int64_t q_row_stride, const void* k_in, int64_t k_row_stride,
+                              const void* q_weight, const void* k_weight, int w_dtype, void* q_out, void* k_out,
+                              const void* cu_seqlens, int64_t B, int64_t T, int64_t HQ, int64_t HKV, int64_t D,
+                              int64_t N, int rot_dim, float theta, float eps, unsigned flags, void* stream);
+
+/*
+ * Causal GQA attention with the sigmoid output gate: o = softmax(scale q k^T + causal mask) v *
+ * sigmoid(gate), q head i reading kv head i / (HQ / HKV). q [B, T, HQ, D], k [B, T, HKV, D]
+ * contiguous; v [B, T, HKV*D] and gate [B, T, HQ*D] with row strides v_row_stride /
+ * gate_row_stride elements; o [B, T, HQ*D] contiguous. With cu_seqlens (B == 1) a query attends only
+ * to keys of its own document. bf16, fp32 softmax and accumulation; D = 64 or 128.
+ * Replaces F.scaled_dot_product_attention(q, k, v, is_causal=True, enable_gqa=True) and its
+ * document-causal mask variant (sore/model/attention.py:124-135; flex_attention with
+ * doc_causal_block_mask, :28-50,131-135) followed by o * torch.sigmoid(gate_proj(x)) (:122).
+ */
+GDN_API int gdn_attn_fwd(const void* q, const void* k, const void* v, int64_t v_row_stride, const void* gate,
+                 int64_t gate_row_stride, void* o, const void* cu_seqlens, int64_t B, int64_t T, int64_t HQ,
+                 int64_t HKV, int64_t D, int64_t N, float scale, unsigned flags, void* stream);
 
 #ifdef __cplusplus
 }

@@ -20,7 +20,7 @@ FLAG_BETA_SIGMOID = 0x2
 FLAG_GATE_IN_KERNEL = 0x4
 FLAG_CU_INT32 = 0x8
 ACT_NONE, ACT_SILU = 0, 1
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -49,6 +49,8 @@ SIGNATURES = {
     "gdn_l2norm_bwd": [_P, _P, _P, _I64, _I64, _INT, _F, _P],
     "gdn_rms_norm_gated_bwd": [_P] * 9 + [_I64, _I64, _INT, _F, _INT, _P, _SZ, _P],
     "gdn_rms_norm_gated_bwd_workspace_size": [_I64, _I64],
+    "gdn_attn_qk_norm_rope_fwd": [_P, _I64, _P, _I64, _P, _P, _INT, _P, _P, _P] + [_I64] * 6 + [_INT, _F, _F, _U, _P],
+    "gdn_attn_fwd": [_P, _P, _P, _I64, _P, _I64, _P, _P] + [_I64] * 6 + [_F, _U, _P],
 }
 
 RESTYPES = {

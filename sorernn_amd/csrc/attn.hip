@@ -1,0 +1,389 @@
+// Gated global attention layer of the hybrid block pair for gfx950: the q/k RMSNorm + partial RoPE
+// prologue and a causal GQA flash-attention forward with the sigmoid output gate fused into its
+// store. Counterpart of GatedAttention.forward (sore/model/attention.py:98-135) between its
+// projections: q_norm / k_norm (layers.py:7-18), PartialRotary (rope.py:24-41), then
+// F.scaled_dot_product_attention(is_causal, enable_gqa) or the document-causal mask with
+// cu_seqlens (attention.py:124-135), then o * sigmoid(gate) (attention.py:122).
+//
+// gated_attn_flash_fwd_kernel: one workgroup of 4 waves per (128-query tile, q head, batch row);
+// wave w owns queries 32w..32w+31 of the tile. Per 64-key block (K and V staged through LDS, double
+// buffered, the next block's global loads in flight during the current block's math):
+//   S^T = K Q^T   v_mfma_f32_32x32x16_bf16, A = K rows from LDS, B = the wave's Q rows held in
+//                 registers for the whole loop. The transposed product puts one query in each
+//                 lane's accumulator column (lane (h, i): query i, keys 8j + 4h + r of a 32-key
+//                 tile), so the online-softmax row max is an in-lane max plus one lane^32 exchange
+//                 and the rescale of O^T is a per-lane scalar.
+//   O^T += V^T P^T  A = V^T through ds_read_b64_tr_b16 (4 consecutive keys of one d column per
+//                 read), B = P^T straight from the S^T accumulators rounded to bf16: the contraction
+//                 over the block's keys runs in the order {16s + 4h + r, 16s + 8 + 4h + r}, which is
+//                 the accumulator's own key order, so P never passes through LDS.
+// Scores are scaled by scale * log2(e) and exponentiated with exp2; the running max starts at -inf
+// and a row whose keys are all masked so far uses 0 as its max (no inf - inf).
+// Tiles are dispatched longest first (the last query tiles have the most keys under the causal
+// mask); with cu_seqlens a tile may straddle documents and every query masks keys before its own
+// document's start.
+
+#include "gdn_mfma.h"
+
+namespace gdn {
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// Start of the document holding token t (t in [0, T)): the largest cu[n] <= t.
+__device__ __forceinline__ int64_t doc_start_of(const void* cu, int cu_i32, int64_t n_docs, int64_t t) {
+  int64_t lo = 0, hi = n_docs - 1;  // invariant: cu[lo] <= t
+  while (lo < hi) {
+    const int64_t mid = (lo + hi + 1) >> 1;
+    if (load_index(cu, cu_i32, mid) <= t) lo = mid;
+    else hi = mid - 1;
+  }
+  return load_index(cu, cu_i32, lo);
+}
+
+// ------------------------------------------------------------------------------------------------
+// q/k RMSNorm + partial rotary embedding (GPT-NeoX rotate_half on the first `rot` dims).
+// One wave per (token, head) row, two elements per lane. The reference's rounding points are kept:
+// RMSNorm in fp32 rounded to the activation dtype (layers.py:15-17), cos/sin computed in fp32 and
+// rounded to the activation dtype (rope.py:29-34), then x*cos and rotate_half(x)*sin each rounded
+// before their sum is rounded (rope.py:36-40, bf16 tensor arithmetic).
+struct RopeParams {
+  const bf16 *q_in, *k_in;
+  int64_t q_stride, k_stride;  // elements between consecutive tokens of q_in / k_in
+  const void *qw, *kw;         // RMSNorm weights [D]
+  int w_dtype;
+  bf16 *q_out, *k_out;         // [B, T, H, D] contiguous
+  const void* cu;
+  int cu_i32;
+  int64_t B, T, HQ, HKV, N;
+  int D, rot;
+  float theta, eps;
+};
+
+__global__ __launch_bounds__(256) void gated_attn_qk_norm_rope_elementwise_kernel(RopeParams p) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t hs = p.HQ + p.HKV;
+  if (row >= p.B * p.T * hs) return;
+  const int64_t bt = row / hs;
+  const int hh = (int)(row % hs);
+  const bool is_q = hh < p.HQ;
+  const int head = is_q ? hh : hh - (int)p.HQ;
+  const bf16* src = is_q ? p.q_in + bt * p.q_stride + (int64_t)head * p.D : p.k_in + bt * p.k_stride + (int64_t)head * p.D;
+  bf16* dst = is_q ? p.q_out + (bt * p.HQ + head) * p.D : p.k_out + (bt * p.HKV + head) * p.D;
+  const void* w = is_q ? p.qw : p.kw;
+  const int d0 = 2 * lane;
+  const bool act = d0 < p.D;
+  float x0 = 0.f, x1 = 0.f;
+  if (act) {
+    const bf16x2 xv = *reinterpret_cast<const bf16x2*>(src + d0);
+    x0 = (float)xv[0];
+    x1 = (float)xv[1];
+  }
+  const float ss = wave_xor_sum(x0 * x0 + x1 * x1, 1);
+  const float r = 1.f / sqrtf(ss / (float)p.D + p.eps);
+  // y = (x r w) rounded to bf16 (the RMSNorm output the rotary reads)
+  const float y0 = act ? (float)(bf16)(x0 * r * load_as_f32(w, p.w_dtype, d0)) : 0.f;
+  const float y1 = act ? (float)(bf16)(x1 * r * load_as_f32(w, p.w_dtype, d0 + 1)) : 0.f;
+  // rotate_half partner: element d < half pairs with d + half (half = rot / 2, a multiple of 2, so
+  // a pair of elements moves as one lane)
+  const int half = p.rot >> 1, lsh = half >> 1;
+  const bool lo = d0 < half, in_rot = d0 < p.rot;
+  const int src_lane = lo ? lane + lsh : lane - lsh;
+  const float py0 = __shfl(y0, in_rot ? src_lane : lane, kWave);
+  const float py1 = __shfl(y1, in_rot ? src_lane : lane, kWave);
+  float o0 = y0, o1 = y1;
+  if (act && in_rot) {
+    int64_t pos = bt % p.T;
+    if (p.cu) pos = bt - doc_start_of(p.cu, p.cu_i32, p.N, bt);
+    const float pf = (float)pos;
+    const int f0 = lo ? d0 : d0 - half;  // frequency index of element d0 (d0 + 1 uses f0 + 1)
+    float c[2], s[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const float ex = (float)(2 * (f0 + e)) / (float)p.rot;
+      const float inv = 1.f / powf(p.theta, ex);
+      float sv, cv;
+      sincosf(pf * inv, &sv, &cv);
+      c[e] = (float)(bf16)cv;
+      s[e] = (float)(bf16)sv;
+    }
+    // rotate_half(x) = cat(-x[half:rot], x[:half])
+    const float r0 = lo ? -py0 : py0, r1 = lo ? -py1 : py1;
+    o0 = (float)(bf16)((float)(bf16)(y0 * c[0]) + (float)(bf16)(r0 * s[0]));
+    o1 = (float)(bf16)((float)(bf16)(y1 * c[1]) + (float)(bf16)(r1 * s[1]));
+  }
+  if (act) *reinterpret_cast<bf16x2*>(dst + d0) = bf16x2{(bf16)o0, (bf16)o1};
+}
+
+// ------------------------------------------------------------------------------------------------
+struct AttnParams {
+  const bf16 *q, *k, *v, *gate;
+  bf16* o;
+  const void* cu;
+  int cu_i32;
+  int64_t T, HQ, HKV, N;
+  int64_t v_stride, gate_stride;  // elements between consecutive tokens of v / gate
+  float scale_log2;               // softmax scale * log2(e)
+};
+
+constexpr int kAttnBM = 128;  // queries per workgroup
+constexpr int kAttnBN = 64;   // keys per block
+constexpr int kAttnNT = 256;
+
+template <int D>
+__global__ __launch_bounds__(kAttnNT, 2) void gated_attn_flash_fwd_kernel(AttnParams p) {
+  constexpr int KP = D + 8;   // K row pitch: 16 consecutive rows of one 16-byte column hit distinct banks
+  constexpr int VP = D + 32;  // V row pitch: the 4 rows of a transposed read sit 64 bytes apart in the banks
+  constexpr int DS = D / 16;  // k-steps of S^T over the head dim
+  constexpr int DT = D / 32;  // 32-row d tiles of O^T
+  constexpr int LPT = kAttnBN * D / 8 / kAttnNT;  // 16-byte loads per thread per K (or V) block
+  __shared__ __align__(16) bf16 Ks[2][kAttnBN * KP];
+  __shared__ __align__(16) bf16 Vs[2][kAttnBN * VP];
+
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6, hh = lane >> 5, li = lane & 31;
+  const int64_t n_tiles = (p.T + kAttnBM - 1) / kAttnBM;
+  const int64_t tile = n_tiles - 1 - (int64_t)blockIdx.x;  // longest first
+  const int hq = blockIdx.y, hkv = hq / (int)(p.HQ / p.HKV);
+  const int64_t b = blockIdx.z;
+  const int64_t q0 = tile * kAttnBM;
+  const int64_t q_last = (q0 + kAttnBM < p.T ? q0 + kAttnBM : p.T) - 1;
+
+  // this lane's query and the start of its document
+  const int64_t qi = q0 + 32 * w + li;
+  const bool q_ok = qi < p.T;
+  const int64_t qi_c = q_ok ? qi : p.T - 1;
+  const int64_t ds_q = p.cu ? doc_start_of(p.cu, p.cu_i32, p.N, qi_c) : 0;
+  // the wave's query range and the smallest / largest document start in it (monotone in the query)
+  const int64_t wq0 = q0 + 32 * w, wq1 = (wq0 + 31 < q_last ? wq0 + 31 : q_last);
+  const bool wave_live = wq0 <= q_last;
+  const int64_t wds0 = p.cu && wave_live ? doc_start_of(p.cu, p.cu_i32, p.N, wq0) : 0;
+  const int64_t wds1 = p.cu && wave_live ? doc_start_of(p.cu, p.cu_i32, p.N, wq1) : 0;
+  const int64_t kv_lo = p.cu ? doc_start_of(p.cu, p.cu_i32, p.N, q0) : 0;
+  const int64_t jb0 = kv_lo / kAttnBN, jb1 = q_last / kAttnBN + 1;
+
+  // Q^T fragments (B operand of S^T): lane (hh, li) holds query qi, d = 16s + 8hh .. +7
+  const int64_t rowq = p.HQ * D, rowk = p.HKV * D;
+  bf16x8 qf[DS];
+  {
+    const auto rq = make_rsrc(p.q + (b * p.T * p.HQ + hq) * D, (uint32_t)(p.T * rowq * 2));
+#pragma unroll
+    for (int s = 0; s < DS; ++s) qf[s] = buf_load16(rq, (uint32_t)((qi * rowq + 16 * s + 8 * hh) * 2));
+    if (!q_ok) {
+#pragma unroll
+      for (int s = 0; s < DS; ++s) qf[s] = bf16x8{};
+    }
+  }
+
+  // cooperative K/V block loads: thread t handles 16-byte chunks t + 256u (row (t + 256u) / (D/8))
+  const auto rk = make_rsrc(p.k + (b * p.T * p.HKV + hkv) * D, (uint32_t)(p.T * rowk * 2));
+  const auto rv = make_rsrc(p.v + b * p.T * p.v_stride + (int64_t)hkv * D, (uint32_t)(p.T * p.v_stride * 2));
+  auto fetch = [&](int64_t jb, bf16x8 (&kr)[LPT], bf16x8 (&vr)[LPT]) {
+#pragma unroll
+    for (int u = 0; u < LPT; ++u) {
+      const int c = t + kAttnNT * u, r = c / (D / 8), col = (c % (D / 8)) * 8;
+      const int64_t key = jb * kAttnBN + r;
+      kr[u] = buf_load16(rk, (uint32_t)((key * rowk + col) * 2));
+      vr[u] = buf_load16(rv, (uint32_t)((key * p.v_stride + col) * 2));
+    }
+  };
+  auto stage = [&](int buf, const bf16x8 (&kr)[LPT], const bf16x8 (&vr)[LPT]) {
+#pragma unroll
+    for (int u = 0; u < LPT; ++u) {
+      const int c = t + kAttnNT * u, r = c / (D / 8), col = (c % (D / 8)) * 8;
+      *reinterpret_cast<bf16x8*>(&Ks[buf][r * KP + col]) = kr[u];
+      *reinterpret_cast<bf16x8*>(&Vs[buf][r * VP + col]) = vr[u];
+    }
+  };
+
+  f32x16 acc[DT];
+#pragma unroll
+  for (int d = 0; d < DT; ++d) acc[d] = f32x16{};
+  float m_run = -INFINITY, l_run = 0.f;
+
+  {
+    bf16x8 kr[LPT], vr[LPT];
+    fetch(jb0, kr, vr);
+    stage(0, kr, vr);
+  }
+  __syncthreads();
+  for (int64_t jb = jb0; jb < jb1; ++jb) {
+    const int buf = (int)((jb - jb0) & 1);
+    bf16x8 kr[LPT], vr[LPT];
+    const bool more = jb + 1 < jb1;
+    if (more) fetch(jb + 1, kr, vr);
+    const int64_t k0 = jb * kAttnBN;
+    // keys of the block beyond every query of the wave, or before every query's document: skip
+    const bool work = wave_live && k0 <= wq1 && k0 + kAttnBN > wds0;
+    if (work) {
+      const bf16* kb = Ks[buf];
+      f32x16 s[2];
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        s[kt] = f32x16{};
+#pragma unroll
+        for (int st = 0; st < DS; ++st)
+          s[kt] = mfma32(ld8(kb + (32 * kt + li) * KP + 16 * st + 8 * hh), qf[st], s[kt]);
+      }
+      // mask where some key of the block lies after some query or before some query's document
+      const bool masked = (k0 + kAttnBN - 1 > wq0) || (k0 < wds1);
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          float x = s[kt][e] * p.scale_log2;
+          if (masked) {
+            const int64_t key = k0 + 32 * kt + 8 * (e >> 2) + 4 * hh + (e & 3);
+            if (key > qi || key < ds_q) x = -INFINITY;
+          }
+          s[kt][e] = x;
+          mx = fmaxf(mx, x);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+      const float m_new = fmaxf(m_run, mx);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = exp2f(m_run - m_use);
+      m_run = m_new;
+      float rs = 0.f;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const float pv = exp2f(s[kt][e] - m_use);
+          s[kt][e] = pv;
+          rs += pv;
+        }
+      l_run = l_run * alpha + rs;
+#pragma unroll
+      for (int d = 0; d < DT; ++d) acc[d] *= alpha;
+      // P^T as B operands: k-step ks covers keys 16ks + {4hh + r, 8 + 4hh + r}
+      bf16x8 pb[4];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const int kt = ks >> 1, j0 = 2 * (ks & 1);
+        pb[ks] = bf16x8{(bf16)s[kt][4 * j0], (bf16)s[kt][4 * j0 + 1], (bf16)s[kt][4 * j0 + 2], (bf16)s[kt][4 * j0 + 3],
+                        (bf16)s[kt][4 * j0 + 4], (bf16)s[kt][4 * j0 + 5], (bf16)s[kt][4 * j0 + 6], (bf16)s[kt][4 * j0 + 7]};
+      }
+      // V^T A operands: lane 4m + q of 16-lane group G reads row 16ks + 4hh + m (then + 8) at
+      // columns 32d + 16(G & 1) + 4q, and receives V[16ks + 4hh + m'][32d + li], m' = 0..3
+      const bf16* vb = Vs[buf];
+      const int gsub = (lane >> 4) & 1, lm = (lane & 15) >> 2, lq = lane & 3;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int d = 0; d < DT; ++d) {
+          const bf16* p0 = vb + (16 * ks + 4 * hh + lm) * VP + 32 * d + 16 * gsub + 4 * lq;
+          const bf16x4 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p0));
+          const bf16x4 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p0 + 8 * VP));
+          acc[d] = mfma32(bf16x8{x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]}, pb[ks], acc[d]);
+        }
+    }
+    if (more) stage(buf ^ 1, kr, vr);
+    __syncthreads();
+  }
+
+  // epilogue: O = O^T / l * sigmoid(gate); lane (hh, li) holds query qi, d = 32d + 8j + 4hh + r
+  if (!q_ok) return;
+  const float l = l_run + __shfl_xor(l_run, 32, kWave);
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  const bf16* gp = p.gate + (b * p.T + qi) * p.gate_stride + (int64_t)hq * D;
+  bf16* op = p.o + ((b * p.T + qi) * p.HQ + hq) * D;
+#pragma unroll
+  for (int d = 0; d < DT; ++d)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = 32 * d + 8 * j + 4 * hh;
+      const bf16x4 gv = *reinterpret_cast<const bf16x4*>(gp + c);
+      float ov[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ov[r] = acc[d][4 * j + r] * inv * sigmoid_f32((float)gv[r]);
+      *reinterpret_cast<bf16x4*>(op + c) = to_bf16x4(ov[0], ov[1], ov[2], ov[3]);
+    }
+}
+
+}  // namespace gdn
+
+using namespace gdn;
+
+extern "C" int gdn_attn_qk_norm_rope_fwd(const void* q_in, int64_t q_row_stride, const void* k_in,
+                                         int64_t k_row_stride, const void* q_weight, const void* k_weight,
+                                         int w_dtype, void* q_out, void* k_out, const void* cu_seqlens, int64_t B,
+                                         int64_t T, int64_t HQ, int64_t HKV, int64_t D, int64_t N, int rot_dim,
+                                         float theta, float eps, unsigned flags, void* stream) {
+  if (!q_in || !k_in || !q_weight || !k_weight || !q_out || !k_out) {
+    gdn_internal_set_error("gdn_attn_qk_norm_rope_fwd: null pointer");
+    return GDN_ERR_INVALID;
+  }
+  if (B <= 0 || T < 0 || HQ <= 0 || HKV <= 0 || N <= 0 || (cu_seqlens ? B != 1 : N != B)) {
+    gdn_internal_set_error("gdn_attn_qk_norm_rope_fwd: bad sizes B=%lld T=%lld HQ=%lld HKV=%lld N=%lld "
+                           "(cu_seqlens requires B == 1)", (long long)B, (long long)T, (long long)HQ,
+                           (long long)HKV, (long long)N);
+    return GDN_ERR_INVALID;
+  }
+  if (D % 2 || D > 128 || D <= 0 || rot_dim <= 0 || rot_dim > D || rot_dim % 4) {
+    gdn_internal_set_error("gdn_attn_qk_norm_rope_fwd: D=%lld rot_dim=%d unsupported (even D <= 128, rot_dim a "
+                           "positive multiple of 4 <= D)", (long long)D, rot_dim);
+    return GDN_ERR_UNSUPPORTED;
+  }
+  if (q_row_stride < HQ * D || k_row_stride < HKV * D || q_row_stride % 2 || k_row_stride % 2) {
+    gdn_internal_set_error("gdn_attn_qk_norm_rope_fwd: row strides %lld/%lld too small or odd",
+                           (long long)q_row_stride, (long long)k_row_stride);
+    return GDN_ERR_INVALID;
+  }
+  if (w_dtype != GDN_DTYPE_F32 && w_dtype != GDN_DTYPE_BF16) {
+    gdn_internal_set_error("gdn_attn_qk_norm_rope_fwd: weight dtype %d unsupported (fp32 or bf16)", w_dtype);
+    return GDN_ERR_UNSUPPORTED;
+  }
+  const int64_t rows = B * T * (HQ + HKV);
+  if (rows == 0) return GDN_OK;
+  RopeParams p{static_cast<const bf16*>(q_in), static_cast<const bf16*>(k_in), q_row_stride, k_row_stride,
+               q_weight, k_weight, w_dtype, static_cast<bf16*>(q_out), static_cast<bf16*>(k_out), cu_seqlens,
+               (flags & GDN_FLAG_CU_INT32) ? 1 : 0, B, T, HQ, HKV, N, (int)D, rot_dim, theta, eps};
+  hipLaunchKernelGGL(gated_attn_qk_norm_rope_elementwise_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), p);
+  return gdn_internal_check_launch("gated_attn_qk_norm_rope_elementwise_kernel");
+}
+
+extern "C" int gdn_attn_fwd(const void* q, const void* k, const void* v, int64_t v_row_stride, const void* gate,
+                            int64_t gate_row_stride, void* o, const void* cu_seqlens, int64_t B, int64_t T,
+                            int64_t HQ, int64_t HKV, int64_t D, int64_t N, float scale, unsigned flags,
+                            void* stream) {
+  if (!q || !k || !v || !gate || !o) {
+    gdn_internal_set_error("gdn_attn_fwd: null pointer");
+    return GDN_ERR_INVALID;
+  }
+  if (B <= 0 || T < 0 || HQ <= 0 || HKV <= 0 || HQ % HKV || N <= 0 || (cu_seqlens ? B != 1 : N != B)) {
+    gdn_internal_set_error("gdn_attn_fwd: bad sizes B=%lld T=%lld HQ=%lld HKV=%lld N=%lld (HQ a multiple of HKV; "
+                           "cu_seqlens requires B == 1)", (long long)B, (long long)T, (long long)HQ, (long long)HKV,
+                           (long long)N);
+    return GDN_ERR_INVALID;
+  }
+  if (D != 64 && D != 128) {
+    gdn_internal_set_error("gdn_attn_fwd: head dim %lld unsupported (64 or 128)", (long long)D);
+    return GDN_ERR_UNSUPPORTED;
+  }
+  if (v_row_stride < HKV * D || gate_row_stride < HQ * D || v_row_stride % 8 || gate_row_stride % 4) {
+    gdn_internal_set_error("gdn_attn_fwd: v/gate row strides %lld/%lld too small or misaligned",
+                           (long long)v_row_stride, (long long)gate_row_stride);
+    return GDN_ERR_INVALID;
+  }
+  // buffer resources address each (batch row, head) slab with 32-bit byte offsets
+  if (T * (HQ > HKV ? HQ : HKV) * D * 2 > 0x7fffffffLL || T * v_row_stride * 2 > 0x7fffffffLL) {
+    gdn_internal_set_error("gdn_attn_fwd: sequence too long for 32-bit offsets (T=%lld)", (long long)T);
+    return GDN_ERR_UNSUPPORTED;
+  }
+  if (T == 0) return GDN_OK;
+  AttnParams p{static_cast<const bf16*>(q), static_cast<const bf16*>(k), static_cast<const bf16*>(v),
+               static_cast<const bf16*>(gate), static_cast<bf16*>(o), cu_seqlens,
+               (flags & GDN_FLAG_CU_INT32) ? 1 : 0, T, HQ, HKV, N, v_row_stride, gate_row_stride,
+               scale * 1.4426950408889634f};
+  const dim3 grid((unsigned)((T + kAttnBM - 1) / kAttnBM), (unsigned)HQ, (unsigned)B);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (D == 128) hipLaunchKernelGGL(gated_attn_flash_fwd_kernel<128>, grid, dim3(kAttnNT), 0, s, p);
+  else hipLaunchKernelGGL(gated_attn_flash_fwd_kernel<64>, grid, dim3(kAttnNT), 0, s, p);
+  return gdn_internal_check_launch("gated_attn_flash_fwd_kernel");
+}

@@ -7,7 +7,7 @@ no binary fixtures for this path. Two cases:
 - ``c0_*``: BASELINE config 0 exactly (B=1, T=256, H=4, d_k=d_v=64, fp32 inputs from
   ``sorernn_amd.synthetic.config_inputs(0)``, zero initial state, chunk 64) -> ``o`` and the final
   state, computed by the token recurrence (``sore/model/gdn_ref.py:11-22`` order) in fp64;
-- ``vl_*``: a small varlen case (3 documents of 37, 64 and 27 tokens, GVA 2, d_k=32, d_v=16,
+- ``vl_*``: a small varlen case (3 documents of 37, 64 and 27 tokens, GVA 2, d_k=d_v=64,
   per-document initial states) -> ``o`` and the three final states.
 
 Inputs are stored in fp32 (what the kernels read), outputs in fp64.
@@ -34,7 +34,7 @@ VARLEN_CU = [0, 37, 101, 128]
 
 def varlen_inputs():
     cu = torch.tensor(VARLEN_CU, dtype=torch.long)
-    return gdn_inputs(1, VARLEN_CU[-1], 2, 32, V=16, HV=4, dtype=torch.float32, seed=2024, h0=True, cu_seqlens=cu)
+    return gdn_inputs(1, VARLEN_CU[-1], 2, 64, V=64, HV=4, dtype=torch.float32, seed=2024, h0=True, cu_seqlens=cu)
 
 
 def _run(inp):

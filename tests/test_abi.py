@@ -76,18 +76,60 @@ def test_chunk_backward_buffer_sizes_match_layout():
     assert lib.gdn_chunk_bwd_workspace_size(0, 4096, 16, 128, 128, 4, 0) == 0
 
 
-def test_every_kernel_name_matches_the_reference_profiler_gdn_rule():
-    """The reference's profiler files kernels into its "gdn" category with
-    ``^(chunk_|recompute_w_u|prepare_wy_repr|l2norm_|fused_recurrent|fused_gdn|solve_tril|merge_16x16|causal_conv1d)|gated_delta``
-    searched over the kernel name (sore/train/profiling.py:35); every kernel of this build must land there."""
-    import re
-    rule = re.compile(r"^(chunk_|recompute_w_u|prepare_wy_repr|l2norm_|fused_recurrent|fused_gdn|solve_tril|merge_16x16|causal_conv1d)|gated_delta")
+def _kernel_names(files):
     csrc = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "sorernn_amd", "csrc")
     names = []
     for f in sorted(os.listdir(csrc)):
-        if f.endswith(".hip"):
+        if f.endswith(".hip") and files(f):
             src = open(os.path.join(csrc, f)).read()
             names += re.findall(r"__global__\s+(?:__launch_bounds__\([^)]*\)\s+)?void\s+(\w+)", src)
-    assert len(names) >= 15, names
-    for n in names:
-        assert rule.search(f"void gdn::{n}<128, 128>(gdn::Params)"), n
+    return names
+
+
+# The reference profiler's rules in precedence order (sore/train/profiling.py:33-40): a kernel name
+# lands in the first category whose regex it matches.
+_PROFILER_RULES = (
+    ("gdn", r"^(chunk_|recompute_w_u|prepare_wy_repr|l2norm_|fused_recurrent|fused_gdn|solve_tril|merge_16x16|causal_conv1d)|gated_delta"),
+    ("attention", r"flex_attention|fmha_|flash_(fwd|bwd)|pytorch_flash|efficient_attention"),
+    ("loss", r"nll_loss|log_softmax|LogSoftMax|SoftMax(Forward|Backward)|softmax_warp|cross_entropy"),
+    ("matmul", r"gemm|gemv|cutlass|cublas|xmma|nvjet|^triton_tem_"),
+    ("elementwise", r"^triton_(poi|red|per)_|elementwise_kernel|reduce_kernel|multi_tensor_apply|CatArrayBatchedCopy|index_elementwise|gather_kernel|indexSelect|lpnorm|embedding_backward"),
+)
+
+
+def _category(name: str) -> str:
+    for cat, pat in _PROFILER_RULES:
+        if re.search(pat, name):
+            return cat
+    return "other"
+
+
+def test_every_kernel_name_matches_the_reference_profiler_gdn_rule():
+    """The reference's profiler files kernels by name (sore/train/profiling.py:33-40). Every kernel of
+    the GDN path lands in "gdn"; the attention layer's flash kernel in "attention" and its q/k
+    norm + rotary prologue in "elementwise" (where the reference's torch ops for it land)."""
+    gdn = _kernel_names(lambda f: not f.startswith("attn"))
+    assert len(gdn) >= 15, gdn
+    for n in gdn:
+        assert _category(f"void gdn::{n}<128, 128>(gdn::Params)") == "gdn", n
+    attn = _kernel_names(lambda f: f.startswith("attn"))
+    cats = {n: _category(f"void gdn::{n}<128>(gdn::AttnParams)") for n in attn}
+    assert cats == {"gated_attn_qk_norm_rope_elementwise_kernel": "elementwise",
+                    "gated_attn_flash_fwd_kernel": "attention"}, cats
+
+
+def test_gated_attention_layer_keeps_the_reference_parameter_names():
+    """GatedAttention's state_dict keys and shapes (sore/model/attention.py:83-91)."""
+    from sorernn_amd.attention import AttnLayerConfig, GatedAttention
+
+    layer = GatedAttention(AttnLayerConfig(d_model=256, attn_heads=4, attn_kv_heads=2, attn_head_dim=64))
+    shapes = {n: tuple(p.shape) for n, p in layer.state_dict().items()}
+    assert shapes == {"q_proj.weight": (256, 256), "gate_proj.weight": (256, 256), "k_proj.weight": (128, 256),
+                      "v_proj.weight": (128, 256), "q_norm.weight": (64,), "k_norm.weight": (64,),
+                      "o_proj.weight": (256, 256)}
+    assert layer.rotary.rot_dim == 16
+    with pytest.raises(ValueError, match="rot_dim"):
+        GatedAttention(AttnLayerConfig(d_model=64, attn_head_dim=6, rope_partial=0.5))
+    with pytest.raises(ValueError, match="B == 1"):
+        with torch.no_grad():
+            layer(torch.zeros(2, 3, 256), torch.tensor([0, 3]))
