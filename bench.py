@@ -19,6 +19,9 @@ The same line carries
 - ``train``: config 1 under autograd -- the training forward (which also saves the bf16 state
   entering every chunk) and the backward (dq, dk, dv, dg, dbeta, dh0), timed separately with HIP
   events; backward algorithmic FLOPs = (22 C^2 d + 14 C d^2) per (chunk, head);
+- ``block_pair``: config 4 -- the GDN layer and the gated attention layer (B=2, T=8192, hidden 2048)
+  forward, each timed whole, plus the flash-attention kernel alone against bf16 peak (causal FLOPs
+  4 d T (T + 1) / 2 per head and batch row);
 - ``cpu_baseline``: the CPU oracle (``oracle/``, torch fp32 recurrence) on the GPU box's host
   cores over the full config-1 input, plus 100 decode steps of config 2.
 """
@@ -103,6 +106,64 @@ def decode_bytes(B=64, H=16, HV=16, D=128, W=4) -> int:
     gates = B * HV * 4 * 2
     conv = B * ch * W * 2 * 2 + ch * W * 4  # cache read + write, fp32 weight
     return state + qkv + out + gates + conv
+
+
+def attn_flops(B: int, T: int, HQ: int, D: int) -> int:
+    """Causal attention FLOPs: QK^T and PV over the (T (T + 1) / 2) allowed pairs, 2 x 2 D each, per head."""
+    return 4 * D * HQ * B * (T * (T + 1) // 2)
+
+
+def block_pair(torch, steps: int) -> dict:
+    """the GDN layer and the gated attention layer at B=2, T=8192, hidden 2048, bf16,
+    random-init weights ~N(0, 0.02); forward of each layer timed with HIP events, plus the attention
+    kernel alone (its causal FLOPs against bf16 peak) and the chunked GDN op alone."""
+    from sorernn_amd.attention import AttnLayerConfig, GatedAttention, attn_qk_norm_rope, gated_attention
+    from sorernn_amd.gdn_layer import GatedDeltaNet, GDNLayerConfig
+
+    B, T, Dm, H, Dh, HKV = 2, 8192, 2048, 16, 128, 4
+    torch.manual_seed(1004)
+    gdn = GatedDeltaNet(GDNLayerConfig(d_model=Dm, gdn_qk_heads=H, gdn_v_heads=H, gdn_head_dim=Dh, gdn_kernel_gate=True))
+    attn = GatedAttention(AttnLayerConfig(d_model=Dm, attn_heads=H, attn_kv_heads=HKV, attn_head_dim=Dh,
+                                          rope_theta=1e6, rope_partial=0.25))
+    with torch.no_grad():
+        for mod in (gdn, attn):
+            for name, prm in mod.named_parameters():
+                if name.endswith("proj.weight"):
+                    prm.normal_(0, 0.02)
+    gdn = gdn.to("cuda", torch.bfloat16)
+    attn = attn.to("cuda", torch.bfloat16)
+    gen = torch.Generator().manual_seed(1004)
+    x = torch.randn(B, T, Dm, generator=gen).to(torch.bfloat16).to("cuda")
+    out = {"workload": "config4: B=2, T=8192, hidden 2048, bf16 weights ~N(0,0.02); GDN layer (H=16, d=128, "
+                       "in-kernel gate) and gated attention layer (16 q / 4 kv heads, d=128, RoPE theta=1e6 on "
+                       "25% of dims, sigmoid output gate), forward"}
+    with torch.no_grad():
+        for name, fn in (("gdn_layer", lambda: gdn(x)), ("attn_layer", lambda: attn(x))):
+            for _ in range(2):
+                fn()
+            ms, _ = time_launches(torch, fn, steps)
+            out[f"{name}_ms"] = round(ms, 4)
+        # the attention kernel alone on the layer's own q, k, v, gate
+        proj = torch.nn.functional.linear(x, attn._fused_weight(torch.bfloat16))
+        nq, nkv = H * Dh, HKV * Dh
+        q, k = attn_qk_norm_rope(proj[..., :nq], proj[..., 2 * nq:2 * nq + nkv], attn.q_norm.weight,
+                                 attn.k_norm.weight, H, HKV, attn.rotary.rot_dim, 1e6)
+        v, gate = proj[..., 2 * nq + nkv:], proj[..., nq:2 * nq]
+        fa = lambda: gated_attention(q, k, v, gate)  # noqa: E731
+        fa()
+        _, fa_ms = time_launches(torch, fa, steps)
+        fl = attn_flops(B, T, H, Dh)
+    pair_ms = out["gdn_layer_ms"] + out["attn_layer_ms"]
+    out.update({
+        "pair_ms": round(pair_ms, 4),
+        "pair_tokens_per_s": round(B * T / (pair_ms * 1e-3), 1),
+        "attn_kernel": "gated_attn_flash_fwd_kernel",
+        "attn_kernel_ms": round(fa_ms, 4),
+        "attn_flops": fl,
+        "attn_tflops": round(fl / (fa_ms * 1e-3) / 1e12, 2),
+        "attn_frac_mfma_peak": round(fl / (fa_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+    })
+    return out
 
 
 def time_launches(torch, fn, steps: int) -> tuple[float, float]:
@@ -208,6 +269,11 @@ def run_only(torch, args) -> int:
     from sorernn_amd import chunk_gated_delta_rule, gated_delta_decode_step
     from sorernn_amd.synthetic import config_inputs, decode_inputs
 
+    if args.only == "block_pair":
+        bp = block_pair(torch, args.steps)
+        print(f"ran block_pair: gdn {bp['gdn_layer_ms']} ms, attn {bp['attn_layer_ms']} ms, "
+              f"attention kernel {bp['attn_kernel_ms']} ms", flush=True)
+        return 0
     if args.only == "train":
         tf, tb = train_step_times(torch, config_inputs(1).to("cuda"), args.steps)
         print(f"ran train: {args.steps} steps, forward {tf:.3f} ms, backward {tb:.3f} ms", flush=True)
@@ -239,7 +305,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 256 MiB device copy (the reference kernel for PMC byte counters)")
-    ap.add_argument("--only", choices=["prefill", "decode", "varlen", "train"], default=None,
+    ap.add_argument("--only", choices=["prefill", "decode", "varlen", "train", "block_pair"], default=None,
                     help="run one workload only (for profiler runs); prints no JSON line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -343,6 +409,9 @@ def main() -> int:
     tr_f, tr_b = train_step_times(torch, inp, max(5, args.steps // 5))
     b_flops = chunk_bwd_flops([T] * B, H, K)
 
+    # ------------------------------------------------------------------ config 4: block pair
+    bp = block_pair(torch, max(5, args.steps // 5))
+
     result = {
         "metric": "GDN prefill tokens/s & decode-step µs (H=16,d=128); % of MI355X roofline",
         "value": round(tok_s, 1),
@@ -408,6 +477,7 @@ def main() -> int:
             "kernels": "gated_delta_chunk_kernel<SAVE>; gated_delta_chunk_bwd_prep_kernel, "
                        "gated_delta_chunk_bwd_state_kernel, gated_delta_chunk_bwd_grad_kernel",
         },
+        "block_pair": bp,
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(torch)

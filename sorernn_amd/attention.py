@@ -173,11 +173,11 @@ class GatedAttention(nn.Module):
         self._wcat_key = None
         self._wcat = None
 
-    def _fused_weight(self) -> Tensor:
+    def _fused_weight(self, dtype: torch.dtype) -> Tensor:
         ws = (self.q_proj.weight, self.gate_proj.weight, self.k_proj.weight, self.v_proj.weight)
-        key = tuple((w.data_ptr(), w._version, w.dtype, w.device) for w in ws)
+        key = tuple((w.data_ptr(), w._version, w.dtype, w.device) for w in ws) + (dtype,)
         if key != self._wcat_key:
-            self._wcat = torch.cat([w.detach() for w in ws], dim=0)
+            self._wcat = torch.cat([w.detach().to(dtype) for w in ws], dim=0)
             self._wcat_key = key
         return self._wcat
 
@@ -188,10 +188,11 @@ class GatedAttention(nn.Module):
             raise ValueError(f"cu_seqlens requires B == 1 (packed [1, N] layout); got B={b}")
         _no_grad_check("GatedAttention", x, *self.parameters())
         hq, hkv, dh = self.heads, self.kv_heads, self.head_dim
-        w = self._fused_weight()
-        if x.dtype != w.dtype:
-            raise ValueError(f"GatedAttention: activations ({x.dtype}) and weights ({w.dtype}) must share a dtype")
-        proj = F.linear(x, w)  # [B, T, q | gate | k | v]
+        # under autocast the projections run in the autocast dtype, as nn.Linear's would
+        dt = torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda") else self.q_proj.weight.dtype
+        if x.dtype != dt:
+            raise ValueError(f"GatedAttention: activations ({x.dtype}) and projections ({dt}) must share a dtype")
+        proj = F.linear(x, self._fused_weight(dt))  # [B, T, q | gate | k | v]
         nq, nkv = hq * dh, hkv * dh
         q_in, gate = proj[..., :nq], proj[..., nq:2 * nq]
         k_in, v = proj[..., 2 * nq:2 * nq + nkv], proj[..., 2 * nq + nkv:]

@@ -46,10 +46,12 @@ __device__ __forceinline__ int64_t doc_start_of(const void* cu, int cu_i32, int6
 
 // ------------------------------------------------------------------------------------------------
 // q/k RMSNorm + partial rotary embedding (GPT-NeoX rotate_half on the first `rot` dims).
-// One wave per (token, head) row, two elements per lane. The reference's rounding points are kept:
-// RMSNorm in fp32 rounded to the activation dtype (layers.py:15-17), cos/sin computed in fp32 and
-// rounded to the activation dtype (rope.py:29-34), then x*cos and rotate_half(x)*sin each rounded
-// before their sum is rounded (rope.py:36-40, bf16 tensor arithmetic).
+// One workgroup per token: its rot/2 cos/sin pairs are computed once into LDS, then every q and k
+// head row of the token is normalised and rotated, D/8 lanes per row (one 16-byte chunk each).
+// The reference's rounding points are kept: RMSNorm in fp32 rounded to the activation dtype
+// (layers.py:15-17), cos/sin computed in fp32 and rounded to the activation dtype (rope.py:29-34),
+// then x*cos and rotate_half(x)*sin each rounded before their sum is rounded (rope.py:36-40, bf16
+// tensor arithmetic).
 struct RopeParams {
   const bf16 *q_in, *k_in;
   int64_t q_stride, k_stride;  // elements between consecutive tokens of q_in / k_in
@@ -59,64 +61,68 @@ struct RopeParams {
   const void* cu;
   int cu_i32;
   int64_t B, T, HQ, HKV, N;
-  int D, rot;
+  int rot;
   float theta, eps;
 };
 
+template <int D>
 __global__ __launch_bounds__(256) void gated_attn_qk_norm_rope_elementwise_kernel(RopeParams p) {
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int64_t hs = p.HQ + p.HKV;
-  if (row >= p.B * p.T * hs) return;
-  const int64_t bt = row / hs;
-  const int hh = (int)(row % hs);
-  const bool is_q = hh < p.HQ;
-  const int head = is_q ? hh : hh - (int)p.HQ;
-  const bf16* src = is_q ? p.q_in + bt * p.q_stride + (int64_t)head * p.D : p.k_in + bt * p.k_stride + (int64_t)head * p.D;
-  bf16* dst = is_q ? p.q_out + (bt * p.HQ + head) * p.D : p.k_out + (bt * p.HKV + head) * p.D;
-  const void* w = is_q ? p.qw : p.kw;
-  const int d0 = 2 * lane;
-  const bool act = d0 < p.D;
-  float x0 = 0.f, x1 = 0.f;
-  if (act) {
-    const bf16x2 xv = *reinterpret_cast<const bf16x2*>(src + d0);
-    x0 = (float)xv[0];
-    x1 = (float)xv[1];
-  }
-  const float ss = wave_xor_sum(x0 * x0 + x1 * x1, 1);
-  const float r = 1.f / sqrtf(ss / (float)p.D + p.eps);
-  // y = (x r w) rounded to bf16 (the RMSNorm output the rotary reads)
-  const float y0 = act ? (float)(bf16)(x0 * r * load_as_f32(w, p.w_dtype, d0)) : 0.f;
-  const float y1 = act ? (float)(bf16)(x1 * r * load_as_f32(w, p.w_dtype, d0 + 1)) : 0.f;
-  // rotate_half partner: element d < half pairs with d + half (half = rot / 2, a multiple of 2, so
-  // a pair of elements moves as one lane)
-  const int half = p.rot >> 1, lsh = half >> 1;
-  const bool lo = d0 < half, in_rot = d0 < p.rot;
-  const int src_lane = lo ? lane + lsh : lane - lsh;
-  const float py0 = __shfl(y0, in_rot ? src_lane : lane, kWave);
-  const float py1 = __shfl(y1, in_rot ? src_lane : lane, kWave);
-  float o0 = y0, o1 = y1;
-  if (act && in_rot) {
+  constexpr int LPR = D / 8;        // lanes per row
+  constexpr int RPP = 256 / LPR;    // rows per pass of the workgroup
+  __shared__ float cs[2][D / 2];    // bf16-rounded cos / sin of each frequency
+  const int64_t bt = blockIdx.x;    // flat token (batch row * T + t)
+  const int half = p.rot >> 1;
+  if ((int)threadIdx.x < half) {
     int64_t pos = bt % p.T;
     if (p.cu) pos = bt - doc_start_of(p.cu, p.cu_i32, p.N, bt);
-    const float pf = (float)pos;
-    const int f0 = lo ? d0 : d0 - half;  // frequency index of element d0 (d0 + 1 uses f0 + 1)
-    float c[2], s[2];
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const float ex = (float)(2 * (f0 + e)) / (float)p.rot;
-      const float inv = 1.f / powf(p.theta, ex);
-      float sv, cv;
-      sincosf(pf * inv, &sv, &cv);
-      c[e] = (float)(bf16)cv;
-      s[e] = (float)(bf16)sv;
-    }
-    // rotate_half(x) = cat(-x[half:rot], x[:half])
-    const float r0 = lo ? -py0 : py0, r1 = lo ? -py1 : py1;
-    o0 = (float)(bf16)((float)(bf16)(y0 * c[0]) + (float)(bf16)(r0 * s[0]));
-    o1 = (float)(bf16)((float)(bf16)(y1 * c[1]) + (float)(bf16)(r1 * s[1]));
+    const int f = threadIdx.x;
+    const float inv = 1.f / powf(p.theta, (float)(2 * f) / (float)p.rot);
+    float sv, cv;
+    sincosf((float)pos * inv, &sv, &cv);
+    cs[0][f] = (float)(bf16)cv;
+    cs[1][f] = (float)(bf16)sv;
   }
-  if (act) *reinterpret_cast<bf16x2*>(dst + d0) = bf16x2{(bf16)o0, (bf16)o1};
+  __syncthreads();
+  const int li = threadIdx.x % LPR, d0 = 8 * li;
+  const int64_t rows = p.HQ + p.HKV;
+  for (int64_t r = threadIdx.x / LPR; r < rows; r += RPP) {  // uniform inside a row's lane group
+    const bool is_q = r < p.HQ;
+    const int64_t head = is_q ? r : r - p.HQ;
+    const bf16* src = is_q ? p.q_in + bt * p.q_stride + head * D : p.k_in + bt * p.k_stride + head * D;
+    bf16* dst = is_q ? p.q_out + (bt * p.HQ + head) * D : p.k_out + (bt * p.HKV + head) * D;
+    const void* w = is_q ? p.qw : p.kw;
+    const bf16x8 xv = *reinterpret_cast<const bf16x8*>(src + d0);
+    float x[8], ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      x[e] = (float)xv[e];
+      ss += x[e] * x[e];
+    }
+    ss = group_sum<LPR>(ss);
+    const float rr = 1.f / sqrtf(ss / (float)D + p.eps);
+    float y[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) y[e] = (float)(bf16)(x[e] * rr * load_as_f32(w, p.w_dtype, d0 + e));
+    // rotate_half partner: element d < half pairs with d + half, i.e. lane li with li +- half/8
+    const bool lo = d0 < half, in_rot = d0 < p.rot;
+    const int lane = threadIdx.x % kWave;
+    const int src_lane = in_rot ? (lo ? lane + (half >> 3) : lane - (half >> 3)) : lane;
+    float py[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) py[e] = __shfl(y[e], src_lane, kWave);
+    bf16x8 ov;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float o = y[e];
+      if (in_rot) {
+        const int f = (lo ? d0 : d0 - half) + e;
+        const float rv = lo ? -py[e] : py[e];  // rotate_half(x) = cat(-x[half:rot], x[:half])
+        o = (float)(bf16)((float)(bf16)(y[e] * cs[0][f]) + (float)(bf16)(rv * cs[1][f]));
+      }
+      ov[e] = (bf16)o;
+    }
+    *reinterpret_cast<bf16x8*>(dst + d0) = ov;
+  }
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -324,13 +330,14 @@ extern "C" int gdn_attn_qk_norm_rope_fwd(const void* q_in, int64_t q_row_stride,
                            (long long)HKV, (long long)N);
     return GDN_ERR_INVALID;
   }
-  if (D % 2 || D > 128 || D <= 0 || rot_dim <= 0 || rot_dim > D || rot_dim % 4) {
-    gdn_internal_set_error("gdn_attn_qk_norm_rope_fwd: D=%lld rot_dim=%d unsupported (even D <= 128, rot_dim a "
-                           "positive multiple of 4 <= D)", (long long)D, rot_dim);
+  if ((D != 64 && D != 128) || rot_dim <= 0 || rot_dim > D || rot_dim % 16) {
+    gdn_internal_set_error("gdn_attn_qk_norm_rope_fwd: D=%lld rot_dim=%d unsupported (D = 64 or 128, rot_dim a "
+                           "positive multiple of 16 <= D)", (long long)D, rot_dim);
     return GDN_ERR_UNSUPPORTED;
   }
-  if (q_row_stride < HQ * D || k_row_stride < HKV * D || q_row_stride % 2 || k_row_stride % 2) {
-    gdn_internal_set_error("gdn_attn_qk_norm_rope_fwd: row strides %lld/%lld too small or odd",
+  if (q_row_stride < HQ * D || k_row_stride < HKV * D || q_row_stride % 8 || k_row_stride % 8 ||
+      ((reinterpret_cast<uintptr_t>(q_in) | reinterpret_cast<uintptr_t>(k_in)) & 15)) {
+    gdn_internal_set_error("gdn_attn_qk_norm_rope_fwd: row strides %lld/%lld too small or not 16-byte aligned",
                            (long long)q_row_stride, (long long)k_row_stride);
     return GDN_ERR_INVALID;
   }
@@ -338,13 +345,17 @@ extern "C" int gdn_attn_qk_norm_rope_fwd(const void* q_in, int64_t q_row_stride,
     gdn_internal_set_error("gdn_attn_qk_norm_rope_fwd: weight dtype %d unsupported (fp32 or bf16)", w_dtype);
     return GDN_ERR_UNSUPPORTED;
   }
-  const int64_t rows = B * T * (HQ + HKV);
-  if (rows == 0) return GDN_OK;
+  if (B * T == 0) return GDN_OK;
+  if (B * T > 0x7fffffffLL) {
+    gdn_internal_set_error("gdn_attn_qk_norm_rope_fwd: B*T=%lld exceeds the grid", (long long)(B * T));
+    return GDN_ERR_UNSUPPORTED;
+  }
   RopeParams p{static_cast<const bf16*>(q_in), static_cast<const bf16*>(k_in), q_row_stride, k_row_stride,
                q_weight, k_weight, w_dtype, static_cast<bf16*>(q_out), static_cast<bf16*>(k_out), cu_seqlens,
-               (flags & GDN_FLAG_CU_INT32) ? 1 : 0, B, T, HQ, HKV, N, (int)D, rot_dim, theta, eps};
-  hipLaunchKernelGGL(gated_attn_qk_norm_rope_elementwise_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), p);
+               (flags & GDN_FLAG_CU_INT32) ? 1 : 0, B, T, HQ, HKV, N, rot_dim, theta, eps};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (D == 128) hipLaunchKernelGGL(gated_attn_qk_norm_rope_elementwise_kernel<128>, dim3((unsigned)(B * T)), dim3(256), 0, s, p);
+  else hipLaunchKernelGGL(gated_attn_qk_norm_rope_elementwise_kernel<64>, dim3((unsigned)(B * T)), dim3(256), 0, s, p);
   return gdn_internal_check_launch("gated_attn_qk_norm_rope_elementwise_kernel");
 }
 

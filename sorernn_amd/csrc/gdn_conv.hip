@@ -93,6 +93,111 @@ __global__ __launch_bounds__(256) void gated_delta_conv1d_kernel(ConvParams p) {
   }
 }
 
+// Vector path for 16-bit activations with C % 8 == 0: each thread owns 8 consecutive channels
+// (16-byte loads and stores of a token row; a wave covers 512 channels, 1 KB per token) and walks
+// kConvV8Tokens tokens, issuing the loads of 8 token rows before it uses the first. Same
+// semantics and document handling as gated_delta_conv1d_kernel.
+constexpr int kConvV8Tokens = 32;
+
+template <int W, typename E>
+__global__ __launch_bounds__(256) void gated_delta_conv1d_v8_kernel(ConvParams p) {
+  typedef E V8 __attribute__((ext_vector_type(8)));
+  const int64_t c0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+  if (c0 >= p.C) return;
+  const int64_t bb = blockIdx.z;
+  const int64_t t0 = (int64_t)blockIdx.y * kConvV8Tokens;
+  if (t0 >= p.T) return;
+  const int64_t t1 = t0 + kConvV8Tokens < p.T ? t0 + kConvV8Tokens : p.T;
+  const E* __restrict__ xs = static_cast<const E*>(p.x) + bb * p.T * p.C + c0;
+  E* __restrict__ ys = static_cast<E*>(p.y) + bb * p.T * p.C + c0;
+  const E* init = static_cast<const E*>(p.init);
+  float w[8][W], bias[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+#pragma unroll
+    for (int i = 0; i < W; ++i) w[e][i] = p.w[(c0 + e) * W + i];
+    bias[e] = p.bias ? p.bias[c0 + e] : 0.f;
+  }
+  int64_t d = bb, ds = 0, de = p.T;
+  if (p.cu) {
+    int64_t lo = 0, hi = p.N - 1;  // largest d with cu[d] <= t0
+    while (lo < hi) {
+      const int64_t mid = (lo + hi + 1) / 2;
+      if (load_index(p.cu, p.cu_i32, mid) <= t0) lo = mid;
+      else hi = mid - 1;
+    }
+    d = lo;
+    ds = load_index(p.cu, p.cu_i32, d);
+    de = load_index(p.cu, p.cu_i32, d + 1);
+  }
+  // win[i][e]: input at position t - (W-1) + i of channel c0 + e for the next token t
+  float win[W > 1 ? W - 1 : 1][8];
+#pragma unroll
+  for (int i = 0; i < W - 1; ++i) {
+    const int64_t pos = t0 - (W - 1) + i;
+    if (pos >= ds) {
+      const V8 v = *reinterpret_cast<const V8*>(xs + pos * p.C);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) win[i][e] = (float)v[e];
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) win[i][e] = init ? (float)init[(d * p.C + c0 + e) * W + (W - (ds - pos))] : 0.f;
+    }
+  }
+  for (int64_t tg = t0; tg < t1; tg += 8) {
+    V8 xv[8];
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {  // rows past t1 re-read the last valid row (never used)
+      const int64_t tt = tg + g < t1 ? tg + g : t1 - 1;
+      xv[g] = *reinterpret_cast<const V8*>(xs + tt * p.C);
+    }
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      const int64_t t = tg + g;
+      if (t >= t1) break;
+      while (t >= de) {  // next document: restart the window from its initial state
+        ++d;
+        ds = de;
+        de = load_index(p.cu, p.cu_i32, d + 1);
+#pragma unroll
+        for (int i = 0; i < W - 1; ++i)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) win[i][e] = init ? (float)init[(d * p.C + c0 + e) * W + i + 1] : 0.f;
+      }
+      V8 yv;
+      float xt[8], dropped[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        xt[e] = (float)xv[g][e];
+        float acc = bias[e] + w[e][W - 1] * xt[e];
+#pragma unroll
+        for (int i = 0; i < W - 1; ++i) acc += w[e][i] * win[i][e];
+        if (p.act == GDN_ACT_SILU) acc = silu_f32(acc);
+        yv[e] = (E)acc;
+        dropped[e] = W > 1 ? win[0][e] : xt[e];
+#pragma unroll
+        for (int i = 0; i + 1 < W - 1; ++i) win[i][e] = win[i + 1][e];
+        if (W > 1) win[W - 2][e] = xt[e];
+      }
+      *reinterpret_cast<V8*>(ys + t * p.C) = yv;
+      if (p.fin && t == de - 1) {  // last token of document d: the cache is its last W inputs
+        E* fin = static_cast<E*>(p.fin);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int64_t fb = (d * p.C + c0 + e) * W;
+          if (W > 1) {
+            fin[fb] = (E)dropped[e];
+#pragma unroll
+            for (int i = 0; i < W - 1; ++i) fin[fb + 1 + i] = (E)win[i][e];
+          } else {
+            fin[fb] = (E)xt[e];
+          }
+        }
+      }
+    }
+  }
+}
+
 // Backward (the reference trains through it: FLA causal_conv1d's backward, or autograd through
 // sore/model/conv.py:6-23 + F.silu). With z_t = bias + sum_j w[W-1-j] x_{t-j} and dz_t = dy_t act'(z_t):
 //   dx_s = sum_j w[W-1-j] dz_{s+j}   (s + j in s's document),
@@ -261,8 +366,16 @@ extern "C" int gdn_causal_conv1d_fwd(const void* x, const float* weight, const f
   }
   ConvParams p{x, weight, bias, y, initial_state, final_state, cu_seqlens, (flags & GDN_FLAG_CU_INT32) ? 1 : 0,
                T, C, N, x_dtype, activation};
-  dim3 grid((unsigned)((C + 255) / 256), (unsigned)tb, (unsigned)B), block(256);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t tb8 = (T + kConvV8Tokens - 1) / kConvV8Tokens;
+  const bool aligned = ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) & 15) == 0;
+  if (aligned && C % 8 == 0 && W == 4 && tb8 <= 65535 && (x_dtype == GDN_DTYPE_BF16 || x_dtype == GDN_DTYPE_F16)) {
+    const dim3 g8((unsigned)((C / 8 + 255) / 256), (unsigned)tb8, (unsigned)B), b8(256);
+    if (x_dtype == GDN_DTYPE_BF16) hipLaunchKernelGGL((gated_delta_conv1d_v8_kernel<4, bf16>), g8, b8, 0, s, p);
+    else hipLaunchKernelGGL((gated_delta_conv1d_v8_kernel<4, f16>), g8, b8, 0, s, p);
+    return gdn_internal_check_launch("gated_delta_conv1d_v8_kernel");
+  }
+  dim3 grid((unsigned)((C + 255) / 256), (unsigned)tb, (unsigned)B), block(256);
   switch (W) {
     case 1: hipLaunchKernelGGL(gated_delta_conv1d_kernel<1>, grid, block, 0, s, p); break;
     case 2: hipLaunchKernelGGL(gated_delta_conv1d_kernel<2>, grid, block, 0, s, p); break;

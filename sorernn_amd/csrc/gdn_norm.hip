@@ -58,6 +58,55 @@ __global__ __launch_bounds__(256) void gated_delta_norm_kernel(NormParams p) {
   }
 }
 
+// Vector path of the same two norms for 16-bit rows of D = 64 or 128: LPR = D / 8 lanes per row,
+// each lane one 16-byte chunk of x (and of the gate), so a wave covers 64 / LPR rows with
+// 16-byte loads and stores; the sum of squares is reduced inside the row's lane group by DPP.
+// Same math as gated_delta_norm_kernel (fp32, one rounding).
+template <typename E, int LPR>
+__global__ __launch_bounds__(256) void gated_delta_norm_v8_kernel(NormParams p) {
+  typedef E V8 __attribute__((ext_vector_type(8)));
+  constexpr int RPW = kWave / LPR;
+  const int lane = threadIdx.x % kWave, sub = lane / LPR, li = lane % LPR;
+  const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+  const int64_t nwaves = ((int64_t)gridDim.x * blockDim.x) / kWave;
+  float wv[8], bv[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    wv[e] = (p.mode == 1 && p.w) ? p.w[li * 8 + e] : 1.f;
+    bv[e] = (p.mode == 1 && p.bias) ? p.bias[li * 8 + e] : 0.f;
+  }
+  for (int64_t r0 = wave * RPW; r0 < p.rows; r0 += nwaves * RPW) {
+    const int64_t r = r0 + sub;
+    const bool ok = r < p.rows;
+    const int64_t base = (ok ? r : p.rows - 1) * p.D + li * 8;  // every lane loads: the reduction needs all
+    const V8 xv = *reinterpret_cast<const V8*>(static_cast<const E*>(p.x) + base);
+    V8 gv{};
+    if (p.mode == 1 && p.gate) gv = *reinterpret_cast<const V8*>(static_cast<const E*>(p.gate) + base);
+    float xf[8], ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      xf[e] = (float)xv[e];
+      ss += xf[e] * xf[e];
+    }
+    ss = group_sum<LPR>(ss);
+    const float scale = p.mode == 0 ? 1.f / fmaxf(sqrtf(ss), p.eps) : 1.f / sqrtf(ss / (float)p.D + p.eps);
+    V8 yv;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float out = xf[e] * scale;
+      if (p.mode == 1) {
+        out = out * wv[e] + bv[e];
+        if (p.gate) {
+          const float g = (float)gv[e];
+          out *= (p.act == GDN_ACT_SILU) ? silu_f32(g) : g;
+        }
+      }
+      yv[e] = (E)out;
+    }
+    if (ok) *reinterpret_cast<V8*>(static_cast<E*>(p.y) + base) = yv;
+  }
+}
+
 // Backward of both norms, one wave per row (the reference trains through F.normalize and through
 // RMSNorm * silu(gate) by autograd, sore/model/gdn.py:177,180-188; FLA's fused l2norm and
 // rms_norm_gated kernels have their own backward):
@@ -173,9 +222,26 @@ constexpr int64_t kNormBwdBlocks = 1024;  // the RMS backward's grid: 4096 waves
 
 static int launch_norm(const NormParams& p, void* stream, const char* what) {
   if (p.rows == 0) return GDN_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool aligned = ((reinterpret_cast<uintptr_t>(p.x) | reinterpret_cast<uintptr_t>(p.y) |
+                         reinterpret_cast<uintptr_t>(p.gate)) & 15) == 0;
+  if (aligned && (p.D == 64 || p.D == 128) && (p.dt == GDN_DTYPE_BF16 || p.dt == GDN_DTYPE_F16)) {
+    const int64_t rpb = 4 * (kWave / (p.D / 8));  // rows per 256-thread block
+    int64_t vb = (p.rows + rpb - 1) / rpb;
+    if (vb > 65536) vb = 65536;
+    const dim3 g((unsigned)vb), b(256);
+    if (p.dt == GDN_DTYPE_BF16) {
+      if (p.D == 128) hipLaunchKernelGGL((gated_delta_norm_v8_kernel<bf16, 16>), g, b, 0, s, p);
+      else hipLaunchKernelGGL((gated_delta_norm_v8_kernel<bf16, 8>), g, b, 0, s, p);
+    } else {
+      if (p.D == 128) hipLaunchKernelGGL((gated_delta_norm_v8_kernel<f16, 16>), g, b, 0, s, p);
+      else hipLaunchKernelGGL((gated_delta_norm_v8_kernel<f16, 8>), g, b, 0, s, p);
+    }
+    return gdn_internal_check_launch(what);
+  }
   int64_t blocks = (p.rows + 3) / 4;
   if (blocks > 65536) blocks = 65536;
-  hipLaunchKernelGGL(gated_delta_norm_kernel, dim3((unsigned)blocks), dim3(256), 0, static_cast<hipStream_t>(stream), p);
+  hipLaunchKernelGGL(gated_delta_norm_kernel, dim3((unsigned)blocks), dim3(256), 0, s, p);
   return gdn_internal_check_launch(what);
 }
 

@@ -41,14 +41,37 @@ def test_conv_tap_order_and_no_activation():
     assert y[0, :, 0].cpu().tolist() == [0.0, 0.0, 100.0, 10.0, 1.0]
 
 
-def test_conv_initial_state_continues_sequence():
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_conv_initial_state_continues_sequence(dtype):
     gen = torch.Generator().manual_seed(2)
-    x = torch.randn(1, 50, 128, generator=gen)
+    x = torch.randn(2, 50, 128, generator=gen).to(dtype)
     w = torch.randn(128, 4, generator=gen)
     full, _ = causal_conv1d(x.to(DEV), w.to(DEV), activation="silu")
     _, cache = causal_conv1d(x[:, :20].to(DEV), w.to(DEV), activation="silu", output_final_state=True)
-    tail, _ = causal_conv1d(x[:, 20:].to(DEV), w.to(DEV), activation="silu", initial_state=cache)
-    assert_output_close(tail.cpu(), full[:, 20:].cpu(), tol=1e-5)
+    tail, _ = causal_conv1d(x[:, 20:].contiguous().to(DEV), w.to(DEV), activation="silu", initial_state=cache)
+    # the same fp32 sums of the same inputs: bit-identical
+    assert torch.equal(tail.cpu(), full[:, 20:].cpu())
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_conv_varlen_initial_states_match_oracle(dtype):
+    """Per-document initial conv caches (documents of 1, 2, 1, 66 and 30 tokens; the 16-bit path
+    walks 32-token blocks, so documents start inside and at the edges of blocks)."""
+    gen = torch.Generator().manual_seed(4)
+    bounds = [0, 1, 3, 4, 70, 100]
+    t, c, wd = bounds[-1], 256, 4
+    x = torch.randn(1, t, c, generator=gen).to(dtype)
+    init = torch.randn(len(bounds) - 1, c, wd, generator=gen).to(dtype)
+    w = torch.randn(c, wd, generator=gen) * 0.5
+    cu = torch.tensor(bounds)
+    y, fin = causal_conv1d(x.to(DEV), w.to(DEV), activation="silu", initial_state=init.to(DEV),
+                           output_final_state=True, cu_seqlens=cu.to(DEV), cu_seqlens_cpu=cu)
+    for n, (a, e) in enumerate(zip(bounds[:-1], bounds[1:])):
+        # the cache's last W-1 inputs (newest last) precede the document
+        seq = torch.cat([init[n, :, 1:].T[None], x[:, a:e]], dim=1)
+        ref = causal_conv1d_silu(seq, w, None)[:, wd - 1:]
+        assert_output_close(y[:, a:e].cpu(), ref, tol=1e-2 if dtype == torch.bfloat16 else 1e-5)
+        assert torch.equal(fin[n].cpu(), seq[0, -wd:].T)
 
 
 def test_conv_nan_does_not_leak_across_documents():
