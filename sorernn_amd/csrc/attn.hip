@@ -17,8 +17,9 @@
 //                 read), B = P^T straight from the S^T accumulators rounded to bf16: the contraction
 //                 over the block's keys runs in the order {16s + 4h + r, 16s + 8 + 4h + r}, which is
 //                 the accumulator's own key order, so P never passes through LDS.
-// Scores are scaled by scale * log2(e) and exponentiated with exp2; the running max starts at -inf
-// and a row whose keys are all masked so far uses 0 as its max (no inf - inf).
+// The softmax runs on raw scores: p = 2^(s c - m c), c = scale log2(e), one FMA and one v_exp_f32 per
+// score; the running max starts at -inf and a row whose keys are all masked so far uses 0 as its max
+// (no inf - inf); O^T is rescaled only in blocks where some row's max moved.
 // Tiles are dispatched longest first (the last query tiles have the most keys under the causal
 // mask); with cu_seqlens a tile may straddle documents and every query masks keys before its own
 // document's start.
@@ -235,37 +236,46 @@ __global__ __launch_bounds__(kAttnNT, 2) void gated_attn_flash_fwd_kernel(AttnPa
           s[kt] = mfma32(ld8(kb + (32 * kt + li) * KP + 16 * st + 8 * hh), qf[st], s[kt]);
       }
       // mask where some key of the block lies after some query or before some query's document
-      const bool masked = (k0 + kAttnBN - 1 > wq0) || (k0 < wds1);
+      // (32-bit key offsets inside the block against this lane's limits)
+      if ((k0 + kAttnBN - 1 > wq0) || (k0 < wds1)) {
+        const int hi_lim = (int)(qi - k0), lo_lim = (int)(ds_q - k0);
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int ko = 32 * kt + 8 * (e >> 2) + 4 * hh + (e & 3);
+            if (ko > hi_lim || ko < lo_lim) s[kt][e] = -INFINITY;
+          }
+      }
+      // online softmax on the raw scores (scale > 0 commutes with the max): p = 2^(s c - m c) with
+      // c = scale log2(e), one FMA and one v_exp_f32 per score
       float mx = -INFINITY;
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          float x = s[kt][e] * p.scale_log2;
-          if (masked) {
-            const int64_t key = k0 + 32 * kt + 8 * (e >> 2) + 4 * hh + (e & 3);
-            if (key > qi || key < ds_q) x = -INFINITY;
-          }
-          s[kt][e] = x;
-          mx = fmaxf(mx, x);
-        }
+        for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[kt][e]);
       mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
       const float m_new = fmaxf(m_run, mx);
       const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = exp2f(m_run - m_use);
+      const float c = p.scale_log2, nmc = -m_use * c;
+      const float alpha = __builtin_amdgcn_exp2f((m_run - m_use) * c);  // 0 while no key was seen
       m_run = m_new;
       float rs = 0.f;
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-          const float pv = exp2f(s[kt][e] - m_use);
+          const float pv = __builtin_amdgcn_exp2f(fmaf(s[kt][e], c, nmc));
           s[kt][e] = pv;
           rs += pv;
         }
       l_run = l_run * alpha + rs;
+      // the running max of most rows stops moving after the first blocks: rescale O^T only when
+      // some lane's max moved (alpha != 1)
+      if (!__all(alpha == 1.f)) {
 #pragma unroll
-      for (int d = 0; d < DT; ++d) acc[d] *= alpha;
+        for (int d = 0; d < DT; ++d) acc[d] *= alpha;
+      }
       // P^T as B operands: k-step ks covers keys 16ks + {4hh + r, 8 + 4hh + r}
       bf16x8 pb[4];
 #pragma unroll
@@ -295,7 +305,7 @@ __global__ __launch_bounds__(kAttnNT, 2) void gated_attn_flash_fwd_kernel(AttnPa
   // epilogue: O = O^T / l * sigmoid(gate); lane (hh, li) holds query qi, d = 32d + 8j + 4hh + r
   if (!q_ok) return;
   const float l = l_run + __shfl_xor(l_run, 32, kWave);
-  const float inv = l > 0.f ? 1.f / l : 0.f;
+  const float inv = l > 0.f ? __builtin_amdgcn_rcpf(l) : 0.f;
   const bf16* gp = p.gate + (b * p.T + qi) * p.gate_stride + (int64_t)hq * D;
   bf16* op = p.o + ((b * p.T + qi) * p.HQ + hq) * D;
 #pragma unroll
@@ -306,7 +316,7 @@ __global__ __launch_bounds__(kAttnNT, 2) void gated_attn_flash_fwd_kernel(AttnPa
       const bf16x4 gv = *reinterpret_cast<const bf16x4*>(gp + c);
       float ov[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) ov[r] = acc[d][4 * j + r] * inv * sigmoid_f32((float)gv[r]);
+      for (int r = 0; r < 4; ++r) ov[r] = acc[d][4 * j + r] * inv * __builtin_amdgcn_rcpf(1.f + __expf(-(float)gv[r]));
       *reinterpret_cast<bf16x4*>(op + c) = to_bf16x4(ov[0], ov[1], ov[2], ov[3]);
     }
 }
