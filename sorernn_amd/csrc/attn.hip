@@ -20,9 +20,11 @@
 // The softmax runs on raw scores: p = 2^(s c - m c), c = scale log2(e), one FMA and one v_exp_f32 per
 // score; the running max starts at -inf and a row whose keys are all masked so far uses 0 as its max
 // (no inf - inf); O^T is rescaled only in blocks where some row's max moved.
-// Tiles are dispatched longest first (the last query tiles have the most keys under the causal
-// mask); with cu_seqlens a tile may straddle documents and every query masks keys before its own
-// document's start.
+// Tiles are dispatched longest first over all heads (the last query tiles have the most keys under
+// the causal mask), the q heads of one kv head on one XCD; with cu_seqlens a tile may straddle
+// documents and every query masks keys before its own document's start.
+
+#include <type_traits>
 
 #include "gdn_mfma.h"
 
@@ -132,7 +134,7 @@ struct AttnParams {
   bf16* o;
   const void* cu;
   int cu_i32;
-  int64_t T, HQ, HKV, N;
+  int64_t B, T, HQ, HKV, N;
   int64_t v_stride, gate_stride;  // elements between consecutive tokens of v / gate
   float scale_log2;               // softmax scale * log2(e)
 };
@@ -151,11 +153,33 @@ __global__ __launch_bounds__(kAttnNT, 2) void gated_attn_flash_fwd_kernel(AttnPa
   __shared__ __align__(16) bf16 Ks[2][kAttnBN * KP];
   __shared__ __align__(16) bf16 Vs[2][kAttnBN * VP];
 
-  const int t = threadIdx.x, lane = t & 63, w = t >> 6, hh = lane >> 5, li = lane & 31;
+  // w is read back as a scalar, so everything derived from it (the wave's query range, its masks
+  // and skips) is wave-uniform and its branches are scalar
+  const int t = threadIdx.x, lane = t & 63, w = __builtin_amdgcn_readfirstlane(t >> 6), hh = lane >> 5, li = lane & 31;
+  // Flat grid, longest query tiles first across all heads: workgroup rank = tile rank (slow) x
+  // (q head, batch row) (fast). Workgroup i runs on XCD i % 8; when the (kv head, batch row) groups
+  // divide evenly over the 8 XCDs, the q heads of one group (which read the same K/V) share an XCD
+  // and its L2.
   const int64_t n_tiles = (p.T + kAttnBM - 1) / kAttnBM;
-  const int64_t tile = n_tiles - 1 - (int64_t)blockIdx.x;  // longest first
-  const int hq = blockIdx.y, hkv = hq / (int)(p.HQ / p.HKV);
-  const int64_t b = blockIdx.z;
+  const int rep = (int)(p.HQ / p.HKV);
+  const int64_t groups = p.HKV * p.B, idx = blockIdx.x;
+  int64_t rank, grp;
+  int hm;
+  if (groups % 8 == 0) {
+    const int64_t x = idx % 8, j = idx / 8, per_xcd = (groups / 8) * rep;
+    rank = j / per_xcd;
+    const int64_t m = j % per_xcd;
+    grp = x + 8 * (m / rep);
+    hm = (int)(m % rep);
+  } else {
+    rank = idx / (groups * rep);
+    const int64_t m = idx % (groups * rep);
+    grp = m / rep;
+    hm = (int)(m % rep);
+  }
+  const int64_t tile = n_tiles - 1 - rank;
+  const int64_t b = grp / p.HKV;
+  const int hkv = (int)(grp % p.HKV), hq = hkv * rep + hm;
   const int64_t q0 = tile * kAttnBM;
   const int64_t q_last = (q0 + kAttnBM < p.T ? q0 + kAttnBM : p.T) - 1;
 
@@ -185,16 +209,25 @@ __global__ __launch_bounds__(kAttnNT, 2) void gated_attn_flash_fwd_kernel(AttnPa
     }
   }
 
-  // cooperative K/V block loads: thread t handles 16-byte chunks t + 256u (row (t + 256u) / (D/8))
-  const auto rk = make_rsrc(p.k + (b * p.T * p.HKV + hkv) * D, (uint32_t)(p.T * rowk * 2));
-  const auto rv = make_rsrc(p.v + b * p.T * p.v_stride + (int64_t)hkv * D, (uint32_t)(p.T * p.v_stride * 2));
+  // cooperative K/V block loads: thread t handles 16-byte chunks t + 256u (row (t + 256u) / (D/8)).
+  // The per-lane byte offsets inside a block are loop constants; each block gets buffer resources
+  // based at its first key and sized to the keys left in the sequence, so keys past the end read as
+  // zeros and no offset is recomputed per block.
+  const bf16* const kbase = p.k + (b * p.T * p.HKV + hkv) * D;
+  const bf16* const vbase = p.v + b * p.T * p.v_stride + (int64_t)hkv * D;
+  // thread t's chunks u sit (2048 / D) rows apart: one per-lane offset plus a scalar step
+  constexpr int RSTEP = kAttnNT / (D / 8);
+  const uint32_t koff = (uint32_t)(((t / (D / 8)) * rowk + (t % (D / 8)) * 8) * 2);
+  const uint32_t voff = (uint32_t)(((t / (D / 8)) * p.v_stride + (t % (D / 8)) * 8) * 2);
+  const uint32_t kstep = (uint32_t)(RSTEP * rowk * 2), vstep = (uint32_t)(RSTEP * p.v_stride * 2);
   auto fetch = [&](int64_t jb, bf16x8 (&kr)[LPT], bf16x8 (&vr)[LPT]) {
+    const int64_t key0 = jb * kAttnBN, left = p.T - key0 > 0 ? p.T - key0 : 0;
+    const auto rk = make_rsrc(kbase + key0 * rowk, (uint32_t)(left * rowk * 2));
+    const auto rv = make_rsrc(vbase + key0 * p.v_stride, (uint32_t)(left * p.v_stride * 2));
 #pragma unroll
     for (int u = 0; u < LPT; ++u) {
-      const int c = t + kAttnNT * u, r = c / (D / 8), col = (c % (D / 8)) * 8;
-      const int64_t key = jb * kAttnBN + r;
-      kr[u] = buf_load16(rk, (uint32_t)((key * rowk + col) * 2));
-      vr[u] = buf_load16(rv, (uint32_t)((key * p.v_stride + col) * 2));
+      kr[u] = buf_load16(rk, koff + u * kstep);
+      vr[u] = buf_load16(rv, voff + u * vstep);
     }
   };
   auto stage = [&](int buf, const bf16x8 (&kr)[LPT], const bf16x8 (&vr)[LPT]) {
@@ -211,6 +244,79 @@ __global__ __launch_bounds__(kAttnNT, 2) void gated_attn_flash_fwd_kernel(AttnPa
   for (int d = 0; d < DT; ++d) acc[d] = f32x16{};
   float m_run = -INFINITY, l_run = 0.f;
 
+  // One 64-key block of the wave's 32 queries. `masked` (wave-uniform, a scalar branch) applies the
+  // causal / document mask; blocks strictly below every query of the wave and inside every query's
+  // document skip it.
+  auto block = [&](bool masked, const bf16* kb, const bf16* vb, int64_t k0) {
+    f32x16 s[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      s[kt] = f32x16{};
+#pragma unroll
+      for (int st = 0; st < DS; ++st)
+        s[kt] = mfma32(ld8(kb + (32 * kt + li) * KP + 16 * st + 8 * hh), qf[st], s[kt]);
+    }
+    if (masked) {  // 32-bit key offsets inside the block against this lane's limits
+      const int hi_lim = (int)(qi - k0), lo_lim = (int)(ds_q - k0);
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int ko = 32 * kt + 8 * (e >> 2) + 4 * hh + (e & 3);
+          if (ko > hi_lim || ko < lo_lim) s[kt][e] = -INFINITY;
+        }
+    }
+    // online softmax on the raw scores (scale > 0 commutes with the max): p = 2^(s c - m c) with
+    // c = scale log2(e), one FMA and one v_exp_f32 per score
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[kt][e]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float c = p.scale_log2, nmc = -m_use * c;
+    const float alpha = __builtin_amdgcn_exp2f((m_run - m_use) * c);  // 0 while no key was seen
+    m_run = m_new;
+    float rs = 0.f;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float pv = __builtin_amdgcn_exp2f(fmaf(s[kt][e], c, nmc));
+        s[kt][e] = pv;
+        rs += pv;
+      }
+    l_run = l_run * alpha + rs;
+    // the running max of most rows stops moving after the first blocks: rescale O^T only when
+    // some lane's max moved (alpha != 1)
+    if (!__all(alpha == 1.f)) {
+#pragma unroll
+      for (int d = 0; d < DT; ++d) acc[d] *= alpha;
+    }
+    // P^T as B operands: k-step ks covers keys 16ks + {4hh + r, 8 + 4hh + r}
+    bf16x8 pb[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int kt = ks >> 1, j0 = 2 * (ks & 1);
+      pb[ks] = bf16x8{(bf16)s[kt][4 * j0], (bf16)s[kt][4 * j0 + 1], (bf16)s[kt][4 * j0 + 2], (bf16)s[kt][4 * j0 + 3],
+                      (bf16)s[kt][4 * j0 + 4], (bf16)s[kt][4 * j0 + 5], (bf16)s[kt][4 * j0 + 6], (bf16)s[kt][4 * j0 + 7]};
+    }
+    // V^T A operands: lane 4m + q of 16-lane group G reads row 16ks + 4hh + m (then + 8) at
+    // columns 32d + 16(G & 1) + 4q, and receives V[16ks + 4hh + m'][32d + li], m' = 0..3
+    const int gsub = (lane >> 4) & 1, lm = (lane & 15) >> 2, lq = lane & 3;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int d = 0; d < DT; ++d) {
+        const bf16* p0 = vb + (16 * ks + 4 * hh + lm) * VP + 32 * d + 16 * gsub + 4 * lq;
+        const bf16x4 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p0));
+        const bf16x4 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p0 + 8 * VP));
+        acc[d] = mfma32(bf16x8{x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]}, pb[ks], acc[d]);
+      }
+  };
+
   {
     bf16x8 kr[LPT], vr[LPT];
     fetch(jb0, kr, vr);
@@ -223,80 +329,10 @@ __global__ __launch_bounds__(kAttnNT, 2) void gated_attn_flash_fwd_kernel(AttnPa
     const bool more = jb + 1 < jb1;
     if (more) fetch(jb + 1, kr, vr);
     const int64_t k0 = jb * kAttnBN;
-    // keys of the block beyond every query of the wave, or before every query's document: skip
-    const bool work = wave_live && k0 <= wq1 && k0 + kAttnBN > wds0;
-    if (work) {
-      const bf16* kb = Ks[buf];
-      f32x16 s[2];
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        s[kt] = f32x16{};
-#pragma unroll
-        for (int st = 0; st < DS; ++st)
-          s[kt] = mfma32(ld8(kb + (32 * kt + li) * KP + 16 * st + 8 * hh), qf[st], s[kt]);
-      }
-      // mask where some key of the block lies after some query or before some query's document
-      // (32-bit key offsets inside the block against this lane's limits)
-      if ((k0 + kAttnBN - 1 > wq0) || (k0 < wds1)) {
-        const int hi_lim = (int)(qi - k0), lo_lim = (int)(ds_q - k0);
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-          for (int e = 0; e < 16; ++e) {
-            const int ko = 32 * kt + 8 * (e >> 2) + 4 * hh + (e & 3);
-            if (ko > hi_lim || ko < lo_lim) s[kt][e] = -INFINITY;
-          }
-      }
-      // online softmax on the raw scores (scale > 0 commutes with the max): p = 2^(s c - m c) with
-      // c = scale log2(e), one FMA and one v_exp_f32 per score
-      float mx = -INFINITY;
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[kt][e]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-      const float m_new = fmaxf(m_run, mx);
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      const float c = p.scale_log2, nmc = -m_use * c;
-      const float alpha = __builtin_amdgcn_exp2f((m_run - m_use) * c);  // 0 while no key was seen
-      m_run = m_new;
-      float rs = 0.f;
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const float pv = __builtin_amdgcn_exp2f(fmaf(s[kt][e], c, nmc));
-          s[kt][e] = pv;
-          rs += pv;
-        }
-      l_run = l_run * alpha + rs;
-      // the running max of most rows stops moving after the first blocks: rescale O^T only when
-      // some lane's max moved (alpha != 1)
-      if (!__all(alpha == 1.f)) {
-#pragma unroll
-        for (int d = 0; d < DT; ++d) acc[d] *= alpha;
-      }
-      // P^T as B operands: k-step ks covers keys 16ks + {4hh + r, 8 + 4hh + r}
-      bf16x8 pb[4];
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const int kt = ks >> 1, j0 = 2 * (ks & 1);
-        pb[ks] = bf16x8{(bf16)s[kt][4 * j0], (bf16)s[kt][4 * j0 + 1], (bf16)s[kt][4 * j0 + 2], (bf16)s[kt][4 * j0 + 3],
-                        (bf16)s[kt][4 * j0 + 4], (bf16)s[kt][4 * j0 + 5], (bf16)s[kt][4 * j0 + 6], (bf16)s[kt][4 * j0 + 7]};
-      }
-      // V^T A operands: lane 4m + q of 16-lane group G reads row 16ks + 4hh + m (then + 8) at
-      // columns 32d + 16(G & 1) + 4q, and receives V[16ks + 4hh + m'][32d + li], m' = 0..3
-      const bf16* vb = Vs[buf];
-      const int gsub = (lane >> 4) & 1, lm = (lane & 15) >> 2, lq = lane & 3;
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-        for (int d = 0; d < DT; ++d) {
-          const bf16* p0 = vb + (16 * ks + 4 * hh + lm) * VP + 32 * d + 16 * gsub + 4 * lq;
-          const bf16x4 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p0));
-          const bf16x4 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p0 + 8 * VP));
-          acc[d] = mfma32(bf16x8{x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]}, pb[ks], acc[d]);
-        }
+    // keys of the block beyond every query of the wave, or before every query's document: skip;
+    // keys after some query or before some query's document: mask (both conditions wave-uniform)
+    if (wave_live && k0 <= wq1 && k0 + kAttnBN > wds0) {
+      block((k0 + kAttnBN - 1 > wq0) || (k0 < wds1), Ks[buf], Vs[buf], k0);
     }
     if (more) stage(buf ^ 1, kr, vr);
     __syncthreads();
@@ -400,9 +436,14 @@ extern "C" int gdn_attn_fwd(const void* q, const void* k, const void* v, int64_t
   if (T == 0) return GDN_OK;
   AttnParams p{static_cast<const bf16*>(q), static_cast<const bf16*>(k), static_cast<const bf16*>(v),
                static_cast<const bf16*>(gate), static_cast<bf16*>(o), cu_seqlens,
-               (flags & GDN_FLAG_CU_INT32) ? 1 : 0, T, HQ, HKV, N, v_row_stride, gate_row_stride,
+               (flags & GDN_FLAG_CU_INT32) ? 1 : 0, B, T, HQ, HKV, N, v_row_stride, gate_row_stride,
                scale * 1.4426950408889634f};
-  const dim3 grid((unsigned)((T + kAttnBM - 1) / kAttnBM), (unsigned)HQ, (unsigned)B);
+  const int64_t wgs = ((T + kAttnBM - 1) / kAttnBM) * HQ * B;
+  if (wgs > 0x7fffffffLL) {
+    gdn_internal_set_error("gdn_attn_fwd: grid too large");
+    return GDN_ERR_UNSUPPORTED;
+  }
+  const dim3 grid((unsigned)wgs);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (D == 128) hipLaunchKernelGGL(gated_attn_flash_fwd_kernel<128>, grid, dim3(kAttnNT), 0, s, p);
   else hipLaunchKernelGGL(gated_attn_flash_fwd_kernel<64>, grid, dim3(kAttnNT), 0, s, p);
