@@ -8,8 +8,10 @@ the reference's call expressions (``gdn.py:145-189``) with ``chunk_gated_delta_r
 patch of the FLA path (``gdn.py:31-78``) has no counterpart: the chunk kernel's grid depends only on
 the number of sequences, so nothing is read back from the device.
 
-Forward only (the ops raise on inputs that require grad); activations in bf16 (e.g. under
-``torch.autocast("cuda", dtype=torch.bfloat16)``, as the reference trains).
+The layer trains: the conv, the chunked rule and the gated norm are autograd functions over the
+HIP backward kernels. Activations are bf16 (e.g. under ``torch.autocast("cuda",
+dtype=torch.bfloat16)``, as the reference trains). The constructor reads only the ``ModelConfig``
+fields ``GDNLayerConfig`` holds, so the reference's ``ModelConfig`` can be passed as is.
 """
 from __future__ import annotations
 
