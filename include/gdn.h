@@ -228,6 +228,22 @@ GDN_API int gdn_rms_norm_gated_bwd(const void* x, const void* gate, const float*
 GDN_API size_t gdn_rms_norm_gated_bwd_workspace_size(int64_t rows, int64_t D);
 
 /*
+ * The GDN layer's q/k/v prologue in one pass (inference): x [B, T, >= 2*Cqk + Cv] with row stride
+ * x_row_stride elements holds the q | k | v projection outputs (e.g. column slices of one fused
+ * projection GEMM); weight [2*Cqk + Cv, 4] fp32 (the q, k, v conv weights stacked), bias or NULL.
+ * Depthwise causal conv of width 4 + activation, rounded to x_dtype; with GDN_FLAG_QK_L2NORM every
+ * head of head_dim channels of q and k is then L2-normalised (x / max(||x||, 1e-12), fp32, rounded).
+ * Writes contiguous q, k [B, T, Cqk] and v [B, T, Cv]. Document resets with cu_seqlens (B == 1).
+ * bf16 or fp16; head_dim 64 or 128. Replaces the three causal_conv1d calls of
+ * sore/model/gdn.py:199-207 (FLA causal_conv1d; torch path causal_conv1d_varlen + F.silu,
+ * gdn.py:208-209) and the q/k normalisation of gdn.py:177 (use_qk_l2norm_in_kernel, gdn.py:168):
+ * the same fp32 formulas as the separate conv followed by the normalisation (within two ulps).
+ */
+GDN_API int gdn_qkv_conv_fwd(const void* x, int64_t x_row_stride, const float* weight, const float* bias, void* q,
+                     void* k, void* v, const void* cu_seqlens, int64_t B, int64_t T, int64_t Cqk, int64_t Cv,
+                     int64_t head_dim, int64_t N, int x_dtype, int activation, unsigned flags, void* stream);
+
+/*
  * Gated attention prologue: per (token, head) row of q_in [B, T, HQ*D] and k_in [B, T, HKV*D]
  * (row strides q_row_stride / k_row_stride elements, e.g. column slices of one fused projection
  * output), RMSNorm over D with weights q_weight / k_weight [D] (w_dtype fp32 or bf16), then the

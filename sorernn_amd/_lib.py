@@ -49,6 +49,7 @@ SIGNATURES = {
     "gdn_l2norm_bwd": [_P, _P, _P, _I64, _I64, _INT, _F, _P],
     "gdn_rms_norm_gated_bwd": [_P] * 9 + [_I64, _I64, _INT, _F, _INT, _P, _SZ, _P],
     "gdn_rms_norm_gated_bwd_workspace_size": [_I64, _I64],
+    "gdn_qkv_conv_fwd": [_P, _I64, _P, _P, _P, _P, _P, _P] + [_I64] * 6 + [_INT, _INT, _U, _P],
     "gdn_attn_qk_norm_rope_fwd": [_P, _I64, _P, _I64, _P, _P, _INT, _P, _P, _P] + [_I64] * 6 + [_INT, _F, _F, _U, _P],
     "gdn_attn_fwd": [_P, _P, _P, _I64, _P, _I64, _P, _P] + [_I64] * 6 + [_F, _U, _P],
 }

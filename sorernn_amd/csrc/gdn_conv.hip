@@ -198,6 +198,129 @@ __global__ __launch_bounds__(256) void gated_delta_conv1d_v8_kernel(ConvParams p
   }
 }
 
+// The GDN layer's whole q/k/v prologue in one pass (inference): the packed projection output
+// x [B, T, >= 2*Cqk + Cv] (row stride x_stride, e.g. the q|k|v columns of one fused GEMM output)
+// -> depthwise causal conv (width 4) + SiLU, rounded to the activation dtype as the separate conv
+// stores it, then, with l2, each q and k head of D channels L2-normalised (F.normalize, eps 1e-12,
+// fp32 math, rounded again) -> contiguous q, k [B, T, Cqk] and v [B, T, Cv]. The normalised q/k
+// follow the same formulas as the separate conv followed by the chunk kernels' in-kernel norm.
+// Thread = 8 channels as in gated_delta_conv1d_v8_kernel; a head of D channels is D/8 consecutive
+// lanes, so its sum of squares is a DPP group sum. No conv caches (the layer's forward uses none).
+struct QkvConvParams {
+  const void* x;
+  int64_t x_stride;
+  const float* w;  // [2*Cqk + Cv][4]
+  const float* bias;
+  void *q, *k, *v;
+  const void* cu;
+  int cu_i32;
+  int64_t T, Cqk, Cv, N;
+  int act, l2;
+};
+
+template <typename E, int D>
+__global__ __launch_bounds__(256) void gated_delta_qkv_conv1d_kernel(QkvConvParams p) {
+  constexpr int W = 4;
+  typedef E V8 __attribute__((ext_vector_type(8)));
+  const int64_t ctot = 2 * p.Cqk + p.Cv;
+  const int64_t c0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+  // threads past the channel count still run (clamped to the last chunk) so that every lane of a
+  // head's group takes part in the group sum; only their stores are dropped
+  const bool ch_ok = c0 < ctot;
+  const int64_t cc = ch_ok ? c0 : ctot - 8;
+  const int64_t bb = blockIdx.z;
+  const int64_t t0 = (int64_t)blockIdx.y * kConvV8Tokens;
+  if (t0 >= p.T) return;
+  const int64_t t1 = t0 + kConvV8Tokens < p.T ? t0 + kConvV8Tokens : p.T;
+  const E* __restrict__ xs = static_cast<const E*>(p.x) + bb * p.T * p.x_stride + cc;
+  // output and its channel offset: q | k | v
+  E* dst;
+  int64_t dc, dstride;
+  if (cc < p.Cqk) {
+    dst = static_cast<E*>(p.q); dc = cc; dstride = p.Cqk;
+  } else if (cc < 2 * p.Cqk) {
+    dst = static_cast<E*>(p.k); dc = cc - p.Cqk; dstride = p.Cqk;
+  } else {
+    dst = static_cast<E*>(p.v); dc = cc - 2 * p.Cqk; dstride = p.Cv;
+  }
+  E* __restrict__ ys = dst + bb * p.T * dstride + dc;
+  const bool norm = p.l2 && cc < 2 * p.Cqk;  // uniform across a head's lanes (heads never straddle q|k|v)
+  float w[8][W], bias[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+#pragma unroll
+    for (int i = 0; i < W; ++i) w[e][i] = p.w[(cc + e) * W + i];
+    bias[e] = p.bias ? p.bias[cc + e] : 0.f;
+  }
+  int64_t d = 0, ds = 0, de = p.T;
+  if (p.cu) {
+    int64_t lo = 0, hi = p.N - 1;  // largest d with cu[d] <= t0
+    while (lo < hi) {
+      const int64_t mid = (lo + hi + 1) / 2;
+      if (load_index(p.cu, p.cu_i32, mid) <= t0) lo = mid;
+      else hi = mid - 1;
+    }
+    d = lo;
+    ds = load_index(p.cu, p.cu_i32, d);
+    de = load_index(p.cu, p.cu_i32, d + 1);
+  }
+  float win[W - 1][8];
+#pragma unroll
+  for (int i = 0; i < W - 1; ++i) {
+    const int64_t pos = t0 - (W - 1) + i;
+    if (pos >= ds) {
+      const V8 xv = *reinterpret_cast<const V8*>(xs + pos * p.x_stride);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) win[i][e] = (float)xv[e];
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) win[i][e] = 0.f;
+    }
+  }
+  for (int64_t tg = t0; tg < t1; tg += 8) {
+    V8 xv[8];
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {  // rows past t1 re-read the last valid row (never used)
+      const int64_t tt = tg + g < t1 ? tg + g : t1 - 1;
+      xv[g] = *reinterpret_cast<const V8*>(xs + tt * p.x_stride);
+    }
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      const int64_t t = tg + g;
+      if (t >= t1) break;  // uniform: t1 is the same for the whole block
+      while (t >= de) {  // next document: the window restarts from zeros
+        ++d;
+        ds = de;
+        de = load_index(p.cu, p.cu_i32, d + 1);
+#pragma unroll
+        for (int i = 0; i < W - 1; ++i)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) win[i][e] = 0.f;
+      }
+      float y[8], ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float xt = (float)xv[g][e];
+        float acc = bias[e] + w[e][W - 1] * xt;
+#pragma unroll
+        for (int i = 0; i < W - 1; ++i) acc += w[e][i] * win[i][e];
+        if (p.act == GDN_ACT_SILU) acc = silu_f32(acc);
+        y[e] = (float)(E)acc;  // the separate conv's stored value
+        ss += y[e] * y[e];
+#pragma unroll
+        for (int i = 0; i + 1 < W - 1; ++i) win[i][e] = win[i + 1][e];
+        win[W - 2][e] = xt;
+      }
+      ss = group_sum<D / 8>(ss);
+      const float inv = norm ? 1.f / fmaxf(sqrtf(ss), 1e-12f) : 1.f;
+      V8 yv;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) yv[e] = (E)(norm ? y[e] * inv : y[e]);
+      if (ch_ok) *reinterpret_cast<V8*>(ys + t * dstride) = yv;
+    }
+  }
+}
+
 // Backward (the reference trains through it: FLA causal_conv1d's backward, or autograd through
 // sore/model/conv.py:6-23 + F.silu). With z_t = bias + sum_j w[W-1-j] x_{t-j} and dz_t = dy_t act'(z_t):
 //   dx_s = sum_j w[W-1-j] dz_{s+j}   (s + j in s's document),
@@ -456,4 +579,58 @@ extern "C" int gdn_causal_conv1d_bwd(const void* x, const float* weight, const f
   hipLaunchKernelGGL(gated_delta_conv1d_param_grad_kernel, dim3((unsigned)((ne + 255) / 256)), dim3(256), 0, s,
                      static_cast<const float*>(workspace), B * tb, C, (int)W, dweight, dbias);
   return gdn_internal_check_launch("gated_delta_conv1d_param_grad_kernel");
+}
+
+extern "C" int gdn_qkv_conv_fwd(const void* x, int64_t x_row_stride, const float* weight, const float* bias, void* q,
+                                void* k, void* v, const void* cu_seqlens, int64_t B, int64_t T, int64_t Cqk,
+                                int64_t Cv, int64_t head_dim, int64_t N, int x_dtype, int activation,
+                                unsigned flags, void* stream) {
+  if (!x || !weight || !q || !k || !v) {
+    gdn_internal_set_error("gdn_qkv_conv_fwd: null tensor pointer");
+    return GDN_ERR_INVALID;
+  }
+  if (B <= 0 || T < 0 || Cqk <= 0 || Cv <= 0 || N <= 0 || (cu_seqlens ? B != 1 : N != B)) {
+    gdn_internal_set_error("gdn_qkv_conv_fwd: bad sizes B=%lld T=%lld Cqk=%lld Cv=%lld N=%lld (cu_seqlens needs B == 1)",
+                           (long long)B, (long long)T, (long long)Cqk, (long long)Cv, (long long)N);
+    return GDN_ERR_INVALID;
+  }
+  if ((head_dim != 64 && head_dim != 128) || Cqk % head_dim || Cv % head_dim) {
+    gdn_internal_set_error("gdn_qkv_conv_fwd: head_dim %lld unsupported (64 or 128, dividing Cqk and Cv)",
+                           (long long)head_dim);
+    return GDN_ERR_UNSUPPORTED;
+  }
+  if (x_dtype != GDN_DTYPE_BF16 && x_dtype != GDN_DTYPE_F16) {
+    gdn_internal_set_error("gdn_qkv_conv_fwd: activation dtype %d unsupported (bf16 or fp16)", x_dtype);
+    return GDN_ERR_UNSUPPORTED;
+  }
+  if (activation != GDN_ACT_NONE && activation != GDN_ACT_SILU) {
+    gdn_internal_set_error("gdn_qkv_conv_fwd: unknown activation %d", activation);
+    return GDN_ERR_INVALID;
+  }
+  const uintptr_t al = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(q) |
+                       reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v);
+  if (x_row_stride < 2 * Cqk + Cv || x_row_stride % 8 || (al & 15)) {
+    gdn_internal_set_error("gdn_qkv_conv_fwd: x row stride %lld too small or buffers not 16-byte aligned",
+                           (long long)x_row_stride);
+    return GDN_ERR_INVALID;
+  }
+  if (T == 0) return GDN_OK;
+  const int64_t tb = (T + kConvV8Tokens - 1) / kConvV8Tokens;
+  if (tb > 65535 || B > 65535) {
+    gdn_internal_set_error("gdn_qkv_conv_fwd: T=%lld B=%lld exceed the grid limits", (long long)T, (long long)B);
+    return GDN_ERR_UNSUPPORTED;
+  }
+  QkvConvParams p{x, x_row_stride, weight, bias, q, k, v, cu_seqlens, (flags & GDN_FLAG_CU_INT32) ? 1 : 0, T, Cqk, Cv,
+                  N, activation, (flags & GDN_FLAG_QK_L2NORM) ? 1 : 0};
+  const int64_t threads = (2 * Cqk + Cv) / 8;
+  const dim3 grid((unsigned)((threads + 255) / 256), (unsigned)tb, (unsigned)B), block(256);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (x_dtype == GDN_DTYPE_BF16) {
+    if (head_dim == 128) hipLaunchKernelGGL((gated_delta_qkv_conv1d_kernel<bf16, 128>), grid, block, 0, s, p);
+    else hipLaunchKernelGGL((gated_delta_qkv_conv1d_kernel<bf16, 64>), grid, block, 0, s, p);
+  } else {
+    if (head_dim == 128) hipLaunchKernelGGL((gated_delta_qkv_conv1d_kernel<f16, 128>), grid, block, 0, s, p);
+    else hipLaunchKernelGGL((gated_delta_qkv_conv1d_kernel<f16, 64>), grid, block, 0, s, p);
+  }
+  return gdn_internal_check_launch("gated_delta_qkv_conv1d_kernel");
 }

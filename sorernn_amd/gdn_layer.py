@@ -9,7 +9,10 @@ patch of the FLA path (``gdn.py:31-78``) has no counterpart: the chunk kernel's 
 the number of sequences, so nothing is read back from the device.
 
 The layer trains: the conv, the chunked rule and the gated norm are autograd functions over the
-HIP backward kernels. Activations are bf16 (e.g. under ``torch.autocast("cuda",
+HIP backward kernels. With autograd off (inference), ``forward`` takes a fused route to the same
+values: one GEMM for the q | k | v projections and one for a | b (weight concatenations cached
+until a weight changes), then one ``qkv_causal_conv1d`` launch for the three convs + SiLU and the
+q/k L2 norm, so the chunked rule runs without its in-kernel normalisation. Activations are bf16 (e.g. under ``torch.autocast("cuda",
 dtype=torch.bfloat16)``, as the reference trains). The constructor reads only the ``ModelConfig``
 fields ``GDNLayerConfig`` holds, so the reference's ``ModelConfig`` can be passed as is.
 """
@@ -22,7 +25,7 @@ import torch
 import torch.nn.functional as F
 from torch import Tensor, nn
 
-from sorernn_amd.ops import causal_conv1d, chunk_gated_delta_rule, rms_norm_gated
+from sorernn_amd.ops import causal_conv1d, chunk_gated_delta_rule, qkv_causal_conv1d, rms_norm_gated
 
 _DT_MIN, _DT_MAX = 1e-3, 1e-1
 
@@ -90,7 +93,53 @@ class GatedDeltaNet(nn.Module):
         self.o_norm = _NormWeight(self.head_dim, cfg.norm_eps)
         self.o_proj = nn.Linear(v_dim, d, bias=False)
 
+    def _fused_weights(self, dtype: torch.dtype):
+        key = tuple((w.data_ptr(), w._version) for w in (self.q_proj.weight, self.k_proj.weight, self.v_proj.weight,
+                                                          self.a_proj.weight, self.b_proj.weight, self.conv_q,
+                                                          self.conv_k, self.conv_v)) + (dtype,)
+        if key != getattr(self, "_fused_key", None):
+            self._w_qkv = torch.cat([w.detach().to(dtype) for w in (self.q_proj.weight, self.k_proj.weight,
+                                                                     self.v_proj.weight)], 0)
+            self._w_ab = torch.cat([self.a_proj.weight.detach().to(dtype), self.b_proj.weight.detach().to(dtype)], 0)
+            self._w_conv = torch.cat([self.conv_q.detach(), self.conv_k.detach(), self.conv_v.detach()], 0).float()
+            self._fused_key = key
+        return self._w_qkv, self._w_ab, self._w_conv
+
+    def _forward_fused(self, x: Tensor, cu_seqlens: Tensor | None, cu_seqlens_cpu: Tensor | None) -> Tensor:
+        b, t, _ = x.shape
+        hk, hv, dh = self.qk_heads, self.v_heads, self.head_dim
+        dt = torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda") else self.q_proj.weight.dtype
+        w_qkv, w_ab, w_conv = self._fused_weights(dt)
+        proj = F.linear(x, w_qkv)  # [B, T, q | k | v]
+        q, k, v = qkv_causal_conv1d(proj, w_conv, hk * dh, hv * dh, dh, activation="silu", l2norm=True,
+                                    cu_seqlens=cu_seqlens, cu_seqlens_cpu=cu_seqlens_cpu)
+        ab = F.linear(x, w_ab)  # [B, T, a | b]
+        a, bl = ab[..., :hv], ab[..., hv:]
+        if self.kernel_gate:
+            gate_kwargs = dict(use_gate_in_kernel=True, A_log=self.A_log, dt_bias=self.dt_bias,
+                               use_beta_sigmoid_in_kernel=True)
+            g, beta = a, bl
+        else:
+            gate_kwargs = {}
+            g = -self.A_log.float().exp() * F.softplus(a.float() + self.dt_bias.float())
+            beta = bl.sigmoid()
+        o, _ = chunk_gated_delta_rule(
+            q.view(b, t, hk, dh), k.view(b, t, hk, dh), v.view(b, t, hv, dh), g, beta, scale=dh**-0.5,
+            cu_seqlens=cu_seqlens, cu_seqlens_cpu=cu_seqlens_cpu, **gate_kwargs,
+        )
+        gate = self.g_proj(x).view(b, t, hv, dh)
+        o = rms_norm_gated(o, gate, self.o_norm.weight, None, activation="swish", eps=self.o_norm.eps)
+        return self.o_proj(o.flatten(-2))
+
     def forward(self, x: Tensor, cu_seqlens: Tensor | None = None, cu_seqlens_cpu: Tensor | None = None) -> Tensor:
+        if not torch.is_grad_enabled() and self.head_dim in (64, 128):
+            dt = torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda") else self.q_proj.weight.dtype
+            if dt in (torch.bfloat16, torch.float16):
+                return self._forward_fused(x, cu_seqlens, cu_seqlens_cpu)
+        return self._forward_reference(x, cu_seqlens, cu_seqlens_cpu)
+
+    def _forward_reference(self, x: Tensor, cu_seqlens: Tensor | None = None,
+                           cu_seqlens_cpu: Tensor | None = None) -> Tensor:
         b, t, _ = x.shape
 
         def conv(h: Tensor, weight: Tensor) -> Tensor:

@@ -10,6 +10,7 @@ its imports:
 - ``rms_norm_gated``                    <- ``fla.modules.fused_norm_gate.rms_norm_gated`` (gdn.py:182-186)
 - ``l2norm``                            <- ``F.normalize(x, dim=-1)`` / FLA ``l2norm`` (gdn.py:177)
 - ``gated_delta_decode_step``           (no reference counterpart: the fused decode step)
+- ``qkv_causal_conv1d``                 <- the three ``causal_conv1d`` calls + q/k ``l2norm`` of gdn.py:177,199-209, in one pass
 
 Outputs are allocated here from torch's caching allocator; the C ABI never allocates.
 ``chunk_gated_delta_rule`` (bf16 q/k/v), ``causal_conv1d``, ``l2norm`` and ``rms_norm_gated`` are
@@ -36,6 +37,7 @@ __all__ = [
     "fused_recurrent_gated_delta_rule",
     "gated_delta_decode_step",
     "l2norm",
+    "qkv_causal_conv1d",
     "rms_norm_gated",
 ]
 
@@ -368,6 +370,46 @@ def causal_conv1d(
     cu = cu_seqlens.contiguous() if cu_seqlens is not None else None
     y, fin = _library.conv_fwd(x, weight, bias, initial_state, cu, act, flags, n, bool(output_final_state))
     return y, (fin if output_final_state else None)
+
+
+def qkv_causal_conv1d(x: Tensor, weight: Tensor, qk_dim: int, v_dim: int, head_dim: int, activation: str | None = "silu",
+                      l2norm: bool = True, cu_seqlens: Tensor | None = None, cu_seqlens_cpu: Tensor | None = None):
+    """The GDN layer's q/k/v prologue in one launch (inference): conv + SiLU (+ per-head L2 norm of q, k).
+
+    ``x [B, T, >= 2*qk_dim + v_dim]`` holds the q | k | v projection outputs (its rows may be wider,
+    e.g. one fused projection GEMM's output); ``weight [2*qk_dim + v_dim, W=4]`` stacks the three
+    conv weights. Returns contiguous ``q, k [B, T, qk_dim]`` and ``v [B, T, v_dim]``, equal to three
+    ``causal_conv1d(..., activation)`` calls followed by ``l2norm`` of every q/k head
+    (``sore/model/gdn.py:177,199-209``). Forward only.
+    """
+    name = "qkv_causal_conv1d"
+    _no_grad_check(name, x, weight)
+    _check_cuda(name, x, weight, cu_seqlens)
+    if x.dim() != 3 or x.stride(2) != 1 or x.shape[2] < 2 * qk_dim + v_dim:
+        raise ValueError(f"{name}: x must be [B, T, >= {2 * qk_dim + v_dim}] with a contiguous last axis")
+    b, t = x.shape[:2]
+    if t > 1 and b > 1 and x.stride(0) != t * x.stride(1):
+        raise ValueError(f"{name}: x rows must be evenly strided")
+    if tuple(weight.shape) != (2 * qk_dim + v_dim, 4):
+        raise ValueError(f"{name}: weight must be [{2 * qk_dim + v_dim}, 4], got {tuple(weight.shape)}")
+    if activation in ("silu", "swish"):
+        act = _lib.ACT_SILU
+    elif activation is None:
+        act = _lib.ACT_NONE
+    else:
+        raise NotImplementedError(f"{name}: activation {activation!r} is not supported")
+    n, flags = _cu_info(name, cu_seqlens, cu_seqlens_cpu, b, t)
+    if l2norm:
+        flags |= _lib.FLAG_QK_L2NORM
+    stride = x.stride(1) if t > 1 else (x.stride(0) if b > 1 else x.shape[2])
+    w = weight.detach().float().contiguous()
+    q = torch.empty(b, t, qk_dim, device=x.device, dtype=x.dtype)
+    k = torch.empty_like(q)
+    v = torch.empty(b, t, v_dim, device=x.device, dtype=x.dtype)
+    cu = cu_seqlens.contiguous() if cu_seqlens is not None else None
+    _lib.call("gdn_qkv_conv_fwd", x.data_ptr(), stride, w.data_ptr(), None, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+              _lib.ptr(cu), b, t, qk_dim, v_dim, head_dim, n, _lib.dtype_code(x.dtype), act, flags, _lib.stream_of(x))
+    return q, k, v
 
 
 def l2norm(x: Tensor, eps: float = 1e-12) -> Tensor:

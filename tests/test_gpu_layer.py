@@ -108,3 +108,20 @@ def test_layer_state_dict_names_match_reference():
     expected = {"q_proj.weight", "k_proj.weight", "v_proj.weight", "g_proj.weight", "a_proj.weight", "b_proj.weight",
                 "conv_q", "conv_k", "conv_v", "A_log", "dt_bias", "o_norm.weight", "o_proj.weight"}
     assert names == expected
+
+
+@pytest.mark.parametrize("kernel_gate", [True, False], ids=["kernel_gate", "torch_gate"])
+@pytest.mark.parametrize("cu", [None, [0, 1, 3, 4, 70, 200, 512]], ids=["rows", "short_docs"])
+def test_inference_route_matches_reference_route(kernel_gate, cu):
+    """With autograd off the layer fuses its projections and its q/k/v prologue; the output equals
+    the reference-expression route up to the GEMMs' accumulation order."""
+    layer = _layer(kernel_gate).to(DEV)
+    b = 2 if cu is None else 1
+    x = torch.randn(b, 512, 256, generator=torch.Generator().manual_seed(3)).to(DEV)
+    cu_t = None if cu is None else torch.tensor(cu)
+    cu_dev = None if cu_t is None else cu_t.to(DEV)
+    with torch.no_grad(), torch.autocast("cuda", dtype=BF16):
+        fused = layer(x, cu_seqlens=cu_dev, cu_seqlens_cpu=cu_t).float()
+        ref = layer._forward_reference(x, cu_seqlens=cu_dev, cu_seqlens_cpu=cu_t).float()
+    rel = ((fused - ref).norm() / ref.norm()).item()
+    assert rel <= 1e-2, f"relative L2 {rel:.3e}"

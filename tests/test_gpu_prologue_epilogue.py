@@ -11,6 +11,7 @@ from oracle import (
     rms_norm_gated as rms_norm_gated_ref,
 )
 from sorernn_amd import causal_conv1d, l2norm, rms_norm_gated
+from sorernn_amd.ops import qkv_causal_conv1d
 from tests.parity import assert_output_close
 
 pytestmark = pytest.mark.gpu
@@ -104,3 +105,33 @@ def test_rms_norm_gated_matches_oracle(dtype, d):
     w = torch.randn(d, generator=gen)
     y = rms_norm_gated(x.to(DEV), gate.to(DEV), w.to(DEV), None, activation="swish", eps=1e-6).cpu()
     assert_output_close(y, rms_norm_gated_ref(x, gate, w, 1e-6), tol=2e-2 if dtype == torch.bfloat16 else 1e-5)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("cu", [None, [0, 1, 3, 40, 41, 200]], ids=["rows", "varlen"])
+def test_qkv_conv_equals_three_convs_and_l2norm(dtype, head_dim, cu):
+    """The fused prologue (one launch over q | k | v read from a wider projection row) equals three
+    causal_conv1d calls followed by l2norm of every q/k head: the same fp32 formulas (the two kernels
+    may contract a multiply-add differently), so within two ulps and almost always equal."""
+    gen = torch.Generator().manual_seed(5)
+    b = 2 if cu is None else 1
+    t, cqk, cv = 200, 2 * head_dim, 4 * head_dim
+    proj = torch.randn(b, t, 2 * cqk + cv + 64, generator=gen).to(dtype).to(DEV)  # 64 extra columns per row
+    w = (torch.randn(2 * cqk + cv, 4, generator=gen) * 0.5).to(DEV)
+    cu_t = None if cu is None else torch.tensor(cu)
+    kw = dict(cu_seqlens=None if cu_t is None else cu_t.to(DEV), cu_seqlens_cpu=cu_t)
+    q, k, v = qkv_causal_conv1d(proj, w, cqk, cv, head_dim, **kw)
+    parts = (proj[..., :cqk], proj[..., cqk:2 * cqk], proj[..., 2 * cqk:2 * cqk + cv])
+    wq, wk, wv = w[:cqk], w[cqk:2 * cqk], w[2 * cqk:]
+    rq = causal_conv1d(parts[0].contiguous(), wq, activation="silu", **kw)[0]
+    rk = causal_conv1d(parts[1].contiguous(), wk, activation="silu", **kw)[0]
+    rv = causal_conv1d(parts[2].contiguous(), wv, activation="silu", **kw)[0]
+    rq = l2norm(rq.view(b, t, -1, head_dim)).view(b, t, cqk)
+    rk = l2norm(rk.view(b, t, -1, head_dim)).view(b, t, cqk)
+    # one ulp of x is at most |x| 2^-7 (bf16) or |x| 2^-10 (fp16); q/k are rounded twice (conv, norm)
+    ulp = 2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -10
+    for out, ref, nm in ((q, rq, "q"), (k, rk, "k"), (v, rv, "v")):
+        o, r = out.float(), ref.float()
+        assert ((o - r).abs() <= 2 * ulp * r.abs().clamp_min(2.0 ** -14)).all(), f"{nm}: more than two ulps apart"
+        assert (out != ref).float().mean().item() <= 1e-2, f"{nm}: {(out != ref).float().mean().item():.2%} differ"
