@@ -70,6 +70,12 @@ __device__ __forceinline__ int64_t load_index(const void* p, int is_i32, int64_t
 __device__ __forceinline__ float softplus_f32(float x) { return x > 20.f ? x : log1pf(expf(x)); }
 __device__ __forceinline__ float sigmoid_f32(float x) { return 1.f / (1.f + expf(-x)); }
 __device__ __forceinline__ float silu_f32(float x) { return x / (1.f + expf(-x)); }
+// SiLU for kernels whose outputs are rounded to a 16-bit type: v_exp_f32 and v_rcp_f32 (about 2 ulp
+// of fp32, far below the bf16/fp16 rounding) instead of the accurate expf and an IEEE divide.
+// x -> -inf gives -0 (exp overflows to inf, rcp(inf) = 0); x -> +inf gives x.
+__device__ __forceinline__ float silu_fast(float x) {
+  return x * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-x * 1.4426950408889634f));
+}
 
 // ---------------------------------------------------------------- wave reductions
 __device__ __forceinline__ float wave_xor_sum(float x, int from_stride) {

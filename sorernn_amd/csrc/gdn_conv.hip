@@ -172,7 +172,7 @@ __global__ __launch_bounds__(256) void gated_delta_conv1d_v8_kernel(ConvParams p
         float acc = bias[e] + w[e][W - 1] * xt[e];
 #pragma unroll
         for (int i = 0; i < W - 1; ++i) acc += w[e][i] * win[i][e];
-        if (p.act == GDN_ACT_SILU) acc = silu_f32(acc);
+        if (p.act == GDN_ACT_SILU) acc = silu_fast(acc);
         yv[e] = (E)acc;
         dropped[e] = W > 1 ? win[0][e] : xt[e];
 #pragma unroll
@@ -304,7 +304,7 @@ __global__ __launch_bounds__(256) void gated_delta_qkv_conv1d_kernel(QkvConvPara
         float acc = bias[e] + w[e][W - 1] * xt;
 #pragma unroll
         for (int i = 0; i < W - 1; ++i) acc += w[e][i] * win[i][e];
-        if (p.act == GDN_ACT_SILU) acc = silu_f32(acc);
+        if (p.act == GDN_ACT_SILU) acc = silu_fast(acc);
         y[e] = (float)(E)acc;  // the separate conv's stored value
         ss += y[e] * y[e];
 #pragma unroll

@@ -98,7 +98,7 @@ __global__ __launch_bounds__(256) void gated_delta_norm_v8_kernel(NormParams p) 
         out = out * wv[e] + bv[e];
         if (p.gate) {
           const float g = (float)gv[e];
-          out *= (p.act == GDN_ACT_SILU) ? silu_f32(g) : g;
+          out *= (p.act == GDN_ACT_SILU) ? silu_fast(g) : g;
         }
       }
       yv[e] = (E)out;
