@@ -138,7 +138,11 @@ def block_pair(torch, steps: int) -> dict:
                        "in-kernel gate) and gated attention layer (16 q / 4 kv heads, d=128, RoPE theta=1e6 on "
                        "25% of dims, sigmoid output gate), forward"}
     with torch.no_grad():
-        for name, fn in (("gdn_layer", lambda: gdn(x)), ("attn_layer", lambda: attn(x))):
+        # gdn_layer: the inference route (fused projections and prologue); gdn_layer_reference_route:
+        # the reference's call expressions (three convs, chunked rule with in-kernel q/k L2 norm),
+        # the route the layer takes under autograd
+        for name, fn in (("gdn_layer", lambda: gdn(x)), ("gdn_layer_reference_route", lambda: gdn._forward_reference(x)),
+                         ("attn_layer", lambda: attn(x))):
             for _ in range(2):
                 fn()
             ms, _ = time_launches(torch, fn, steps)
@@ -271,7 +275,7 @@ def run_only(torch, args) -> int:
 
     if args.only == "block_pair":
         bp = block_pair(torch, args.steps)
-        print(f"ran block_pair: gdn {bp['gdn_layer_ms']} ms, attn {bp['attn_layer_ms']} ms, "
+        print(f"ran block_pair: gdn {bp['gdn_layer_ms']} ms (reference route {bp['gdn_layer_reference_route_ms']} ms), attn {bp['attn_layer_ms']} ms, "
               f"attention kernel {bp['attn_kernel_ms']} ms", flush=True)
         return 0
     if args.only == "train":

@@ -192,13 +192,16 @@ __device__ __forceinline__ void chunk_gates_from_raw(ChunkGates& gs, uint32_t gr
 }
 
 // F.normalize over a q/k row held by KCH consecutive lanes (8 bf16 each), rounded back to bf16.
+// 1 / max(||x||, 1e-12) as v_rsq_f32 of max(||x||^2, 1e-24): about 1 ulp of fp32 from the IEEE
+// sqrt and divide, far below the bf16 rounding that follows, and a few instructions instead of the
+// IEEE sequences (this runs on the helper waves once per 16-byte chunk of every q/k row).
 template <int KCH>
 __device__ __forceinline__ bf16x8 l2norm_row_chunk(bf16x8 x) {
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) ss += (float)x[i] * (float)x[i];
   ss = group_sum<KCH>(ss);
-  const float inv = 1.f / fmaxf(sqrtf(ss), 1e-12f);
+  const float inv = __builtin_amdgcn_rsqf(fmaxf(ss, 1e-24f));
 #pragma unroll
   for (int i = 0; i < 8; ++i) x[i] = static_cast<bf16>((float)x[i] * inv);
   return x;
