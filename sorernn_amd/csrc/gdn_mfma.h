@@ -175,8 +175,16 @@ __device__ __forceinline__ void chunk_gates_from_raw(ChunkGates& gs, uint32_t gr
                                                      int lane) {
   float gval = raw32_to_f32(graw, dg), bval = raw32_to_f32(braw, db);
   if (lane < valid_rows) {
-    if (flags & GDN_FLAG_GATE_IN_KERNEL) gval = -__expf(A_log) * softplus_f32(gval + dt_bias);
-    if (flags & GDN_FLAG_BETA_SIGMOID) bval = sigmoid_f32(bval);
+    // softplus and sigmoid from v_exp_f32 / v_log_f32 / v_rcp_f32 (this runs once per chunk on a
+    // wave that shares its SIMD with a state wave). softplus(x) = ln(1 + e^x) for x <= 20 loses
+    // only ~e^x absolutely where 1 + e^x rounds to 1, i.e. |error in g| <= exp(A_log) * 1e-7.
+    constexpr float kLog2e = 1.4426950408889634f, kLn2 = 0.6931471805599453f;
+    if (flags & GDN_FLAG_GATE_IN_KERNEL) {
+      const float x = gval + dt_bias;
+      const float sp = x > 20.f ? x : __builtin_amdgcn_logf(1.f + __builtin_amdgcn_exp2f(x * kLog2e)) * kLn2;
+      gval = -__builtin_amdgcn_exp2f(A_log * kLog2e) * sp;
+    }
+    if (flags & GDN_FLAG_BETA_SIGMOID) bval = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-bval * kLog2e));
   } else {
     gval = 0.f;
     bval = 0.f;
