@@ -49,8 +49,9 @@ __device__ __forceinline__ int64_t doc_start_of(const void* cu, int cu_i32, int6
 
 // ------------------------------------------------------------------------------------------------
 // q/k RMSNorm + partial rotary embedding (GPT-NeoX rotate_half on the first `rot` dims).
-// One workgroup per token: its rot/2 cos/sin pairs are computed once into LDS, then every q and k
-// head row of the token is normalised and rotated, D/8 lanes per row (one 16-byte chunk each).
+// One workgroup per 4 tokens: their rot/2 cos/sin pairs are computed once into LDS, then every q and
+// k head row of the tokens is normalised and rotated, D/8 lanes per row (one 16-byte chunk each),
+// the loads of 4 passes over the rows issued before their math.
 // The reference's rounding points are kept: RMSNorm in fp32 rounded to the activation dtype
 // (layers.py:15-17), cos/sin computed in fp32 and rounded to the activation dtype (rope.py:29-34),
 // then x*cos and rotate_half(x)*sin each rounded before their sum is rounded (rope.py:36-40, bf16
@@ -68,63 +69,95 @@ struct RopeParams {
   float theta, eps;
 };
 
+constexpr int kRopeTokens = 4;  // tokens per workgroup
+
 template <int D>
 __global__ __launch_bounds__(256) void gated_attn_qk_norm_rope_elementwise_kernel(RopeParams p) {
   constexpr int LPR = D / 8;        // lanes per row
   constexpr int RPP = 256 / LPR;    // rows per pass of the workgroup
-  __shared__ float cs[2][D / 2];    // bf16-rounded cos / sin of each frequency
-  const int64_t bt = blockIdx.x;    // flat token (batch row * T + t)
+  constexpr int NP = 4;             // passes whose loads are issued together
+  __shared__ float cs[kRopeTokens][2][D / 2];  // bf16-rounded cos / sin of each frequency, per token
+  const int64_t bt0 = (int64_t)blockIdx.x * kRopeTokens;  // first flat token (batch row * T + t)
+  const int64_t ntok = p.B * p.T;
   const int half = p.rot >> 1;
-  if ((int)threadIdx.x < half) {
+  const int li = threadIdx.x % LPR, d0 = 8 * li, lane = threadIdx.x % kWave;
+  const int64_t hs = p.HQ + p.HKV, rows = kRopeTokens * hs;  // rows of the workgroup: token-major
+  const bool lo = d0 < half, in_rot = d0 < p.rot;
+  const int src_lane = in_rot ? (lo ? lane + (half >> 3) : lane - (half >> 3)) : lane;
+  // the loads of a group of NP passes over the rows (rows past the end re-read a valid row)
+  auto load_rows = [&](int64_t r0, bf16x8 (&xv)[NP]) {
+#pragma unroll
+    for (int u = 0; u < NP; ++u) {
+      int64_t r = r0 + u * RPP;
+      r = r < rows ? r : rows - 1;
+      int64_t bt = bt0 + r / hs;
+      bt = bt < ntok ? bt : ntok - 1;
+      const int64_t hh = r % hs;
+      const bf16* src = hh < p.HQ ? p.q_in + bt * p.q_stride + hh * D : p.k_in + bt * p.k_stride + (hh - p.HQ) * D;
+      xv[u] = *reinterpret_cast<const bf16x8*>(src + d0);
+    }
+  };
+  bf16x8 xv[NP];
+  int64_t r0 = threadIdx.x / LPR;
+  load_rows(r0, xv);  // in flight while the cos/sin table is computed
+  float wq[8], wk[8];  // this lane's 8 RMSNorm weights of q and of k
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    wq[e] = load_as_f32(p.qw, p.w_dtype, d0 + e);
+    wk[e] = load_as_f32(p.kw, p.w_dtype, d0 + e);
+  }
+  if ((int)threadIdx.x < kRopeTokens * half) {
+    const int tk = threadIdx.x / half, f = threadIdx.x % half;
+    const int64_t bt = bt0 + tk < ntok ? bt0 + tk : ntok - 1;
     int64_t pos = bt % p.T;
     if (p.cu) pos = bt - doc_start_of(p.cu, p.cu_i32, p.N, bt);
-    const int f = threadIdx.x;
     const float inv = 1.f / powf(p.theta, (float)(2 * f) / (float)p.rot);
     float sv, cv;
     sincosf((float)pos * inv, &sv, &cv);
-    cs[0][f] = (float)(bf16)cv;
-    cs[1][f] = (float)(bf16)sv;
+    cs[tk][0][f] = (float)(bf16)cv;
+    cs[tk][1][f] = (float)(bf16)sv;
   }
   __syncthreads();
-  const int li = threadIdx.x % LPR, d0 = 8 * li;
-  const int64_t rows = p.HQ + p.HKV;
-  for (int64_t r = threadIdx.x / LPR; r < rows; r += RPP) {  // uniform inside a row's lane group
-    const bool is_q = r < p.HQ;
-    const int64_t head = is_q ? r : r - p.HQ;
-    const bf16* src = is_q ? p.q_in + bt * p.q_stride + head * D : p.k_in + bt * p.k_stride + head * D;
-    bf16* dst = is_q ? p.q_out + (bt * p.HQ + head) * D : p.k_out + (bt * p.HKV + head) * D;
-    const void* w = is_q ? p.qw : p.kw;
-    const bf16x8 xv = *reinterpret_cast<const bf16x8*>(src + d0);
-    float x[8], ss = 0.f;
+  for (; r0 < rows; r0 += NP * RPP) {  // uniform inside a row's lane group
+    if (r0 != threadIdx.x / LPR) load_rows(r0, xv);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      x[e] = (float)xv[e];
-      ss += x[e] * x[e];
-    }
-    ss = group_sum<LPR>(ss);
-    const float rr = 1.f / sqrtf(ss / (float)D + p.eps);
-    float y[8];
+    for (int u = 0; u < NP; ++u) {
+      const int64_t r = r0 + u * RPP;
+      if (r >= rows) break;  // uniform inside the row's lane group
+      const int tk = (int)(r / hs);
+      const int64_t bt = bt0 + tk, hh = r % hs;
+      const bool is_q = hh < p.HQ;
+      float x[8], ss = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) y[e] = (float)(bf16)(x[e] * rr * load_as_f32(w, p.w_dtype, d0 + e));
-    // rotate_half partner: element d < half pairs with d + half, i.e. lane li with li +- half/8
-    const bool lo = d0 < half, in_rot = d0 < p.rot;
-    const int lane = threadIdx.x % kWave;
-    const int src_lane = in_rot ? (lo ? lane + (half >> 3) : lane - (half >> 3)) : lane;
-    float py[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) py[e] = __shfl(y[e], src_lane, kWave);
-    bf16x8 ov;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float o = y[e];
-      if (in_rot) {
-        const int f = (lo ? d0 : d0 - half) + e;
-        const float rv = lo ? -py[e] : py[e];  // rotate_half(x) = cat(-x[half:rot], x[:half])
-        o = (float)(bf16)((float)(bf16)(y[e] * cs[0][f]) + (float)(bf16)(rv * cs[1][f]));
+      for (int e = 0; e < 8; ++e) {
+        x[e] = (float)xv[u][e];
+        ss += x[e] * x[e];
       }
-      ov[e] = (bf16)o;
+      ss = group_sum<LPR>(ss);
+      const float rr = __builtin_amdgcn_rsqf(ss / (float)D + p.eps);  // torch.rsqrt in the reference
+      float y[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) y[e] = (float)(bf16)(x[e] * rr * (is_q ? wq[e] : wk[e]));
+      // rotate_half partner: element d < half pairs with d + half, i.e. lane li with li +- half/8
+      float py[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) py[e] = __shfl(y[e], src_lane, kWave);
+      bf16x8 ov;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float o = y[e];
+        if (in_rot) {
+          const int f = (lo ? d0 : d0 - half) + e;
+          const float rv = lo ? -py[e] : py[e];  // rotate_half(x) = cat(-x[half:rot], x[:half])
+          o = (float)(bf16)((float)(bf16)(y[e] * cs[tk][0][f]) + (float)(bf16)(rv * cs[tk][1][f]));
+        }
+        ov[e] = (bf16)o;
+      }
+      if (bt < ntok) {
+        bf16* dst = is_q ? p.q_out + (bt * p.HQ + hh) * D : p.k_out + (bt * p.HKV + (hh - p.HQ)) * D;
+        *reinterpret_cast<bf16x8*>(dst + d0) = ov;
+      }
     }
-    *reinterpret_cast<bf16x8*>(dst + d0) = ov;
   }
 }
 
@@ -400,8 +433,9 @@ extern "C" int gdn_attn_qk_norm_rope_fwd(const void* q_in, int64_t q_row_stride,
                q_weight, k_weight, w_dtype, static_cast<bf16*>(q_out), static_cast<bf16*>(k_out), cu_seqlens,
                (flags & GDN_FLAG_CU_INT32) ? 1 : 0, B, T, HQ, HKV, N, rot_dim, theta, eps};
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (D == 128) hipLaunchKernelGGL(gated_attn_qk_norm_rope_elementwise_kernel<128>, dim3((unsigned)(B * T)), dim3(256), 0, s, p);
-  else hipLaunchKernelGGL(gated_attn_qk_norm_rope_elementwise_kernel<64>, dim3((unsigned)(B * T)), dim3(256), 0, s, p);
+  const dim3 grid((unsigned)((B * T + kRopeTokens - 1) / kRopeTokens));
+  if (D == 128) hipLaunchKernelGGL(gated_attn_qk_norm_rope_elementwise_kernel<128>, grid, dim3(256), 0, s, p);
+  else hipLaunchKernelGGL(gated_attn_qk_norm_rope_elementwise_kernel<64>, grid, dim3(256), 0, s, p);
   return gdn_internal_check_launch("gated_attn_qk_norm_rope_elementwise_kernel");
 }
 

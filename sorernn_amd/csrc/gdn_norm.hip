@@ -61,49 +61,60 @@ __global__ __launch_bounds__(256) void gated_delta_norm_kernel(NormParams p) {
 // Vector path of the same two norms for 16-bit rows of D = 64 or 128: LPR = D / 8 lanes per row,
 // each lane one 16-byte chunk of x (and of the gate), so a wave covers 64 / LPR rows with
 // 16-byte loads and stores; the sum of squares is reduced inside the row's lane group by DPP.
-// Same math as gated_delta_norm_kernel (fp32, one rounding).
+// Each wave takes kNormV8Groups row groups per pass and issues all their loads before the first
+// use (memory-level parallelism for an HBM-bound pass). fp32 math, one rounding; the RMS factor is
+// v_rsq_f32 (the reference computes it with torch.rsqrt).
+constexpr int kNormV8Groups = 4;
+
 template <typename E, int LPR>
 __global__ __launch_bounds__(256) void gated_delta_norm_v8_kernel(NormParams p) {
   typedef E V8 __attribute__((ext_vector_type(8)));
-  constexpr int RPW = kWave / LPR;
+  constexpr int RPW = kWave / LPR, U = kNormV8Groups;
   const int lane = threadIdx.x % kWave, sub = lane / LPR, li = lane % LPR;
   const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
   const int64_t nwaves = ((int64_t)gridDim.x * blockDim.x) / kWave;
+  const bool gated = p.mode == 1 && p.gate;
   float wv[8], bv[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     wv[e] = (p.mode == 1 && p.w) ? p.w[li * 8 + e] : 1.f;
     bv[e] = (p.mode == 1 && p.bias) ? p.bias[li * 8 + e] : 0.f;
   }
-  for (int64_t r0 = wave * RPW; r0 < p.rows; r0 += nwaves * RPW) {
-    const int64_t r = r0 + sub;
-    const bool ok = r < p.rows;
-    const int64_t base = (ok ? r : p.rows - 1) * p.D + li * 8;  // every lane loads: the reduction needs all
-    const V8 xv = *reinterpret_cast<const V8*>(static_cast<const E*>(p.x) + base);
-    V8 gv{};
-    if (p.mode == 1 && p.gate) gv = *reinterpret_cast<const V8*>(static_cast<const E*>(p.gate) + base);
-    float xf[8], ss = 0.f;
+  for (int64_t r0 = wave * RPW * U; r0 < p.rows; r0 += nwaves * RPW * U) {
+    V8 xv[U], gv[U];
+    int64_t base[U];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      xf[e] = (float)xv[e];
-      ss += xf[e] * xf[e];
+    for (int u = 0; u < U; ++u) {  // every lane loads (clamped rows): the reductions need all lanes
+      const int64_t r = r0 + u * RPW + sub;
+      base[u] = (r < p.rows ? r : p.rows - 1) * p.D + li * 8;
+      xv[u] = *reinterpret_cast<const V8*>(static_cast<const E*>(p.x) + base[u]);
+      if (gated) gv[u] = *reinterpret_cast<const V8*>(static_cast<const E*>(p.gate) + base[u]);
     }
-    ss = group_sum<LPR>(ss);
-    const float scale = p.mode == 0 ? 1.f / fmaxf(sqrtf(ss), p.eps) : 1.f / sqrtf(ss / (float)p.D + p.eps);
-    V8 yv;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float out = xf[e] * scale;
-      if (p.mode == 1) {
-        out = out * wv[e] + bv[e];
-        if (p.gate) {
-          const float g = (float)gv[e];
-          out *= (p.act == GDN_ACT_SILU) ? silu_fast(g) : g;
-        }
+    for (int u = 0; u < U; ++u) {
+      float xf[8], ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        xf[e] = (float)xv[u][e];
+        ss += xf[e] * xf[e];
       }
-      yv[e] = (E)out;
+      ss = group_sum<LPR>(ss);
+      const float scale = p.mode == 0 ? 1.f / fmaxf(sqrtf(ss), p.eps) : __builtin_amdgcn_rsqf(ss / (float)p.D + p.eps);
+      V8 yv;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float out = xf[e] * scale;
+        if (p.mode == 1) {
+          out = out * wv[e] + bv[e];
+          if (gated) {
+            const float g = (float)gv[u][e];
+            out *= (p.act == GDN_ACT_SILU) ? silu_fast(g) : g;
+          }
+        }
+        yv[e] = (E)out;
+      }
+      if (r0 + u * RPW + sub < p.rows) *reinterpret_cast<V8*>(static_cast<E*>(p.y) + base[u]) = yv;
     }
-    if (ok) *reinterpret_cast<V8*>(static_cast<E*>(p.y) + base) = yv;
   }
 }
 
@@ -226,7 +237,7 @@ static int launch_norm(const NormParams& p, void* stream, const char* what) {
   const bool aligned = ((reinterpret_cast<uintptr_t>(p.x) | reinterpret_cast<uintptr_t>(p.y) |
                          reinterpret_cast<uintptr_t>(p.gate)) & 15) == 0;
   if (aligned && (p.D == 64 || p.D == 128) && (p.dt == GDN_DTYPE_BF16 || p.dt == GDN_DTYPE_F16)) {
-    const int64_t rpb = 4 * (kWave / (p.D / 8));  // rows per 256-thread block
+    const int64_t rpb = 4 * (kWave / (p.D / 8)) * kNormV8Groups;  // rows per 256-thread block and pass
     int64_t vb = (p.rows + rpb - 1) / rpb;
     if (vb > 65536) vb = 65536;
     const dim3 g((unsigned)vb), b(256);
