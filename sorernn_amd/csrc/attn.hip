@@ -6,8 +6,9 @@
 // cu_seqlens (attention.py:124-135), then o * sigmoid(gate) (attention.py:122).
 //
 // gated_attn_flash_fwd_kernel: one workgroup of 4 waves per (128-query tile, q head, batch row);
-// wave w owns queries 32w..32w+31 of the tile. Per 64-key block (K and V staged through LDS, double
-// buffered, the next block's global loads in flight during the current block's math):
+// wave w owns queries 32w..32w+31 of the tile. Per 64-key block (K and V loaded from HBM straight
+// into LDS by buffer_load ... lds, double buffered, the next block's loads in flight during the
+// current block's math; rows unpadded with an XOR swizzle of their 16-byte chunks):
 //   S^T = K Q^T   v_mfma_f32_32x32x16_bf16, A = K rows from LDS, B = the wave's Q rows held in
 //                 registers for the whole loop. The transposed product puts one query in each
 //                 lane's accumulator column (lane (h, i): query i, keys 8j + 4h + r of a 32-key
@@ -18,8 +19,10 @@
 //                 over the block's keys runs in the order {16s + 4h + r, 16s + 8 + 4h + r}, which is
 //                 the accumulator's own key order, so P never passes through LDS.
 // The softmax runs on raw scores: p = 2^(s c - m c), c = scale log2(e), one FMA and one v_exp_f32 per
-// score; the running max starts at -inf and a row whose keys are all masked so far uses 0 as its max
-// (no inf - inf); O^T is rescaled only in blocks where some row's max moved.
+// score. The reference max m of a row starts at -inf (a row whose keys are all masked so far uses 0,
+// no inf - inf) and moves only when a block's max exceeds it by more than 8 / c, so O^T and the row
+// sum are rescaled in the first blocks and rarely after; the row sum adds the bf16-rounded p that the
+// PV product uses.
 // Tiles are dispatched longest first over all heads (the last query tiles have the most keys under
 // the causal mask), the q heads of one kv head on one XCD; with cu_seqlens a tile may straddle
 // documents and every query masks keys before its own document's start.
@@ -178,13 +181,18 @@ constexpr int kAttnNT = 256;
 
 template <int D>
 __global__ __launch_bounds__(kAttnNT, 2) void gated_attn_flash_fwd_kernel(AttnParams p) {
-  constexpr int KP = D + 8;   // K row pitch: 16 consecutive rows of one 16-byte column hit distinct banks
-  constexpr int VP = D + 32;  // V row pitch: the 4 rows of a transposed read sit 64 bytes apart in the banks
   constexpr int DS = D / 16;  // k-steps of S^T over the head dim
   constexpr int DT = D / 32;  // 32-row d tiles of O^T
-  constexpr int LPT = kAttnBN * D / 8 / kAttnNT;  // 16-byte loads per thread per K (or V) block
-  __shared__ __align__(16) bf16 Ks[2][kAttnBN * KP];
-  __shared__ __align__(16) bf16 Vs[2][kAttnBN * VP];
+  constexpr int LPT = kAttnBN * D / 8 / kAttnNT;  // 1 KB LDS-DMA loads per wave per K (or V) block
+  constexpr int RPL = 512 / D;                   // K/V rows per 1 KB load
+  __shared__ __align__(16) bf16 Ks0[kAttnBN * D];
+  __shared__ __align__(16) bf16 Ks1[kAttnBN * D];
+  __shared__ __align__(16) bf16 Vs0[kAttnBN * D];
+  __shared__ __align__(16) bf16 Vs1[kAttnBN * D];
+  // K/V rows sit unpadded in LDS (the DMA writes 1 KB contiguously per wave instruction); the 16-byte
+  // chunk c of row r is stored at chunk c ^ swz(r), which keeps the K row-fragment reads and the V
+  // transposed reads free of bank conflicts
+  auto swz = [](int r) { return D == 128 ? (((r & 3) << 2) | ((r >> 2) & 3)) : (((r & 3) << 1) | ((r >> 2) & 1)); };
 
   // w is read back as a scalar, so everything derived from it (the wave's query range, its masks
   // and skips) is wave-uniform and its branches are scalar
@@ -242,40 +250,59 @@ __global__ __launch_bounds__(kAttnNT, 2) void gated_attn_flash_fwd_kernel(AttnPa
     }
   }
 
-  // cooperative K/V block loads: thread t handles 16-byte chunks t + 256u (row (t + 256u) / (D/8)).
-  // The per-lane byte offsets inside a block are loop constants; each block gets buffer resources
-  // based at its first key and sized to the keys left in the sequence, so keys past the end read as
-  // zeros and no offset is recomputed per block.
+  // K/V blocks go from HBM straight into LDS (buffer_load ... lds): load u of wave w fills LDS bytes
+  // [(w + 4u) KB, +1 KB) of the block, lane l the 16 bytes at l * 16, i.e. row (w + 4u) RPL + l / (D/8),
+  // chunk slot l % (D/8), which receives the source chunk slot ^ swz(row). The swizzle of a lane's
+  // row does not depend on w or u, so the per-lane source offset is a loop constant plus a scalar step.
+  // Each block gets buffer resources based at its first key and sized to the keys left in the
+  // sequence; keys past the end are masked for every query.
   const bf16* const kbase = p.k + (b * p.T * p.HKV + hkv) * D;
   const bf16* const vbase = p.v + b * p.T * p.v_stride + (int64_t)hkv * D;
-  // thread t's chunks u sit (2048 / D) rows apart: one per-lane offset plus a scalar step
-  constexpr int RSTEP = kAttnNT / (D / 8);
-  const uint32_t koff = (uint32_t)(((t / (D / 8)) * rowk + (t % (D / 8)) * 8) * 2);
-  const uint32_t voff = (uint32_t)(((t / (D / 8)) * p.v_stride + (t % (D / 8)) * 8) * 2);
-  const uint32_t kstep = (uint32_t)(RSTEP * rowk * 2), vstep = (uint32_t)(RSTEP * p.v_stride * 2);
-  auto fetch = [&](int64_t jb, bf16x8 (&kr)[LPT], bf16x8 (&vr)[LPT]) {
+  const int drow = w * RPL + lane / (D / 8), dslot = lane % (D / 8), dch = dslot ^ swz(drow);
+  const uint32_t koff = (uint32_t)((drow * rowk + dch * 8) * 2), voff = (uint32_t)((drow * p.v_stride + dch * 8) * 2);
+  const uint32_t kstep = (uint32_t)(4 * RPL * rowk * 2), vstep = (uint32_t)(4 * RPL * p.v_stride * 2);
+  auto fetch = [&](int64_t jb, bf16* kd, bf16* vd) {
     const int64_t key0 = jb * kAttnBN, left = p.T - key0 > 0 ? p.T - key0 : 0;
     const auto rk = make_rsrc(kbase + key0 * rowk, (uint32_t)(left * rowk * 2));
     const auto rv = make_rsrc(vbase + key0 * p.v_stride, (uint32_t)(left * p.v_stride * 2));
 #pragma unroll
     for (int u = 0; u < LPT; ++u) {
-      kr[u] = buf_load16(rk, koff + u * kstep);
-      vr[u] = buf_load16(rv, voff + u * vstep);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)(kd + (w + 4 * u) * 512), 16,
+                                               koff + u * kstep, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)(vd + (w + 4 * u) * 512), 16,
+                                               voff + u * vstep, 0, 0, 0);
     }
   };
-  auto stage = [&](int buf, const bf16x8 (&kr)[LPT], const bf16x8 (&vr)[LPT]) {
+  // the wave's own LDS-DMA loads have landed (vmcnt(0)); the barrier after it publishes them
+  auto dma_wait = [] { __builtin_amdgcn_s_waitcnt(0x0F70); };
+  // K row-fragment and V transposed-read offsets (elements) inside a block buffer: K row 32kt + li,
+  // chunk 2st + hh; V rows 16ks + 4hh + lm (+ 8), chunk 4d + 2gsub + lq / 2, half lq % 2
+  const int gsub = (lane >> 4) & 1, lm = (lane & 15) >> 2, lq = lane & 3;
+  int kq_off[DS], v_off[DT][2];
 #pragma unroll
-    for (int u = 0; u < LPT; ++u) {
-      const int c = t + kAttnNT * u, r = c / (D / 8), col = (c % (D / 8)) * 8;
-      *reinterpret_cast<bf16x8*>(&Ks[buf][r * KP + col]) = kr[u];
-      *reinterpret_cast<bf16x8*>(&Vs[buf][r * VP + col]) = vr[u];
+  for (int st = 0; st < DS; ++st) kq_off[st] = li * D + (((2 * st + hh) ^ swz(li)) << 3);
+#pragma unroll
+  for (int d = 0; d < DT; ++d)
+#pragma unroll
+    for (int h8 = 0; h8 < 2; ++h8) {
+      const int row = 4 * hh + lm + 8 * h8;
+      v_off[d][h8] = row * D + (((4 * d + 2 * gsub + (lq >> 1)) ^ swz(row)) << 3) + 4 * (lq & 1);
     }
-  };
+  if (p.T % kAttnBN) {  // a partial last block: rows past the end read as zeros from a cleared buffer
+    for (int e = t; e < kAttnBN * D / 8; e += kAttnNT) {
+      reinterpret_cast<bf16x8*>(Ks0)[e] = bf16x8{};
+      reinterpret_cast<bf16x8*>(Ks1)[e] = bf16x8{};
+      reinterpret_cast<bf16x8*>(Vs0)[e] = bf16x8{};
+      reinterpret_cast<bf16x8*>(Vs1)[e] = bf16x8{};
+    }
+    __syncthreads();
+  }
 
   f32x16 acc[DT];
 #pragma unroll
   for (int d = 0; d < DT; ++d) acc[d] = f32x16{};
   float m_run = -INFINITY, l_run = 0.f;
+  const float lazy_thr = 8.f / p.scale_log2;
 
   // One 64-key block of the wave's 32 queries. `masked` (wave-uniform, a scalar branch) applies the
   // causal / document mask; blocks strictly below every query of the wave and inside every query's
@@ -287,7 +314,7 @@ __global__ __launch_bounds__(kAttnNT, 2) void gated_attn_flash_fwd_kernel(AttnPa
       s[kt] = f32x16{};
 #pragma unroll
       for (int st = 0; st < DS; ++st)
-        s[kt] = mfma32(ld8(kb + (32 * kt + li) * KP + 16 * st + 8 * hh), qf[st], s[kt]);
+        s[kt] = mfma32(ld8(kb + 32 * kt * D + kq_off[st]), qf[st], s[kt]);
     }
     if (masked) {  // 32-bit key offsets inside the block against this lane's limits
       const int hi_lim = (int)(qi - k0), lo_lim = (int)(ds_q - k0);
@@ -300,75 +327,74 @@ __global__ __launch_bounds__(kAttnNT, 2) void gated_attn_flash_fwd_kernel(AttnPa
         }
     }
     // online softmax on the raw scores (scale > 0 commutes with the max): p = 2^(s c - m c) with
-    // c = scale log2(e), one FMA and one v_exp_f32 per score
+    // c = scale log2(e), one FMA and one v_exp_f32 per score. The reference max m of a row moves only
+    // when a block max exceeds it by more than 8 / c (p <= 2^8 meanwhile), so O^T is rescaled in the
+    // first blocks and then rarely; a row whose keys are all masked so far keeps m = -inf and uses 0.
     float mx = -INFINITY;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[kt][e]);
     mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-    const float m_new = fmaxf(m_run, mx);
-    const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float c = p.scale_log2, nmc = -m_use * c;
-    const float alpha = __builtin_amdgcn_exp2f((m_run - m_use) * c);  // 0 while no key was seen
-    m_run = m_new;
-    float rs = 0.f;
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const float pv = __builtin_amdgcn_exp2f(fmaf(s[kt][e], c, nmc));
-        s[kt][e] = pv;
-        rs += pv;
-      }
-    l_run = l_run * alpha + rs;
-    // the running max of most rows stops moving after the first blocks: rescale O^T only when
-    // some lane's max moved (alpha != 1)
-    if (!__all(alpha == 1.f)) {
+    const float c = p.scale_log2;
+    const bool grow = mx > m_run + lazy_thr;
+    if (!__all(!grow)) {
+      const float alpha = grow ? __builtin_amdgcn_exp2f((m_run - mx) * c) : 1.f;  // 0 while no key was seen
+      m_run = grow ? mx : m_run;
+      l_run *= alpha;
 #pragma unroll
       for (int d = 0; d < DT; ++d) acc[d] *= alpha;
     }
-    // P^T as B operands: k-step ks covers keys 16ks + {4hh + r, 8 + 4hh + r}
+    const float nmc = m_run == -INFINITY ? 0.f : -m_run * c;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) s[kt][e] = __builtin_amdgcn_exp2f(fmaf(s[kt][e], c, nmc));
+    // P^T as B operands: k-step ks covers keys 16ks + {4hh + r, 8 + 4hh + r}; the row sum adds the
+    // bf16-rounded p (the values the PV product uses), two per v_dot2_f32_bf16
     bf16x8 pb[4];
+    float rs = 0.f;
+    const bf16x2 ones = {(bf16)1.f, (bf16)1.f};
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       const int kt = ks >> 1, j0 = 2 * (ks & 1);
       pb[ks] = bf16x8{(bf16)s[kt][4 * j0], (bf16)s[kt][4 * j0 + 1], (bf16)s[kt][4 * j0 + 2], (bf16)s[kt][4 * j0 + 3],
                       (bf16)s[kt][4 * j0 + 4], (bf16)s[kt][4 * j0 + 5], (bf16)s[kt][4 * j0 + 6], (bf16)s[kt][4 * j0 + 7]};
+#pragma unroll
+      for (int h2 = 0; h2 < 4; ++h2) rs = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{pb[ks][2 * h2], pb[ks][2 * h2 + 1]}, ones, rs, false);
     }
+    l_run += rs;
     // V^T A operands: lane 4m + q of 16-lane group G reads row 16ks + 4hh + m (then + 8) at
     // columns 32d + 16(G & 1) + 4q, and receives V[16ks + 4hh + m'][32d + li], m' = 0..3
-    const int gsub = (lane >> 4) & 1, lm = (lane & 15) >> 2, lq = lane & 3;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
       for (int d = 0; d < DT; ++d) {
-        const bf16* p0 = vb + (16 * ks + 4 * hh + lm) * VP + 32 * d + 16 * gsub + 4 * lq;
-        const bf16x4 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p0));
-        const bf16x4 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p0 + 8 * VP));
+        const bf16x4 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(vb + 16 * ks * D + v_off[d][0]));
+        const bf16x4 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(vb + 16 * ks * D + v_off[d][1]));
         acc[d] = mfma32(bf16x8{x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]}, pb[ks], acc[d]);
       }
   };
 
-  {
-    bf16x8 kr[LPT], vr[LPT];
-    fetch(jb0, kr, vr);
-    stage(0, kr, vr);
-  }
-  __syncthreads();
-  for (int64_t jb = jb0; jb < jb1; ++jb) {
-    const int buf = (int)((jb - jb0) & 1);
-    bf16x8 kr[LPT], vr[LPT];
-    const bool more = jb + 1 < jb1;
-    if (more) fetch(jb + 1, kr, vr);
+  // one key block on the buffers (kc, vc) while the next block is loaded into (kn, vn); the two
+  // buffer pairs alternate through a loop unrolled by two, so every LDS access names its array
+  auto step = [&](int64_t jb, const bf16* kc, const bf16* vc, bf16* kn, bf16* vn) {
+    if (jb + 1 < jb1) fetch(jb + 1, kn, vn);
     const int64_t k0 = jb * kAttnBN;
     // keys of the block beyond every query of the wave, or before every query's document: skip;
     // keys after some query or before some query's document: mask (both conditions wave-uniform)
     if (wave_live && k0 <= wq1 && k0 + kAttnBN > wds0) {
-      block((k0 + kAttnBN - 1 > wq0) || (k0 < wds1), Ks[buf], Vs[buf], k0);
+      block((k0 + kAttnBN - 1 > wq0) || (k0 < wds1), kc, vc, k0);
     }
-    if (more) stage(buf ^ 1, kr, vr);
+    dma_wait();
     __syncthreads();
+  };
+  fetch(jb0, Ks0, Vs0);
+  dma_wait();
+  __syncthreads();
+  for (int64_t jb = jb0; jb < jb1; jb += 2) {
+    step(jb, Ks0, Vs0, Ks1, Vs1);
+    if (jb + 1 < jb1) step(jb + 1, Ks1, Vs1, Ks0, Vs0);
   }
 
   // epilogue: O = O^T / l * sigmoid(gate); lane (hh, li) holds query qi, d = 32d + 8j + 4hh + r
@@ -456,6 +482,10 @@ extern "C" int gdn_attn_fwd(const void* q, const void* k, const void* v, int64_t
   if (D != 64 && D != 128) {
     gdn_internal_set_error("gdn_attn_fwd: head dim %lld unsupported (64 or 128)", (long long)D);
     return GDN_ERR_UNSUPPORTED;
+  }
+  if (!(scale > 0.f) || scale > 3.0e38f) {
+    gdn_internal_set_error("gdn_attn_fwd: scale %g unsupported (a positive finite softmax scale)", (double)scale);
+    return GDN_ERR_INVALID;
   }
   if (v_row_stride < HKV * D || gate_row_stride < HQ * D || v_row_stride % 8 || gate_row_stride % 4) {
     gdn_internal_set_error("gdn_attn_fwd: v/gate row strides %lld/%lld too small or misaligned",

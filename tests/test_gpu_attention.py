@@ -93,6 +93,30 @@ def test_attention_sharp_scores():
 
 
 @pytest.mark.gpu
+def test_attention_late_dominant_keys():
+    """Keys whose scores exceed every earlier key's by far more than the lazy-rescale margin arrive
+    in a late block (keys 300-309 scaled x40): the rows that see them must move their reference max
+    and rescale the sums accumulated over the earlier blocks; rows before them must not change."""
+    from sorernn_amd.attention import gated_attention
+
+    q, k, v, gate = _attn_inputs(1, 400, 4, 2, 128, seed=8)
+    k = k.clone()
+    k[:, 300:310] = (k[:, 300:310].float() * 40.0).to(torch.bfloat16)
+    o = gated_attention(q.to(DEV), k.to(DEV), v.to(DEV), gate.to(DEV))
+    assert_output_close(o.cpu(), _attn_ref(q, k, v, gate))
+
+
+@pytest.mark.gpu
+def test_attention_rejects_non_positive_scale():
+    from sorernn_amd.attention import gated_attention
+
+    q, k, v, gate = _attn_inputs(1, 64, 2, 1, 64, seed=9)
+    for bad in (0.0, -0.125, float("inf")):
+        with pytest.raises(ValueError, match="scale"):
+            gated_attention(q.to(DEV), k.to(DEV), v.to(DEV), gate.to(DEV), scale=bad)
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("cu_dtype", [torch.int64, torch.int32])
 @pytest.mark.parametrize("bounds", [[0, 5, 70, 200, 333], [0, 1, 2, 3, 129, 130, 333], [0, 333]])
 def test_attention_varlen_matches_oracle(bounds, cu_dtype):
