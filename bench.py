@@ -24,6 +24,11 @@ The same line carries
   4 d T (T + 1) / 2 per head and batch row);
 - ``cpu_baseline``: the CPU oracle (``oracle/``, torch fp32 recurrence) on the GPU box's host
   cores over the full config-1 input, plus 100 decode steps of config 2.
+
+Each GPU workload runs in its own child process (``bench.py --part NAME`` prints its raw
+measurements as JSON), so every workload is measured in a fresh HIP context and allocator, as it would
+run alone; this process never initialises the GPU and runs the CPU baseline itself. A failing
+workload ends the bench with its status. ``--only NAME`` runs one workload for profiler runs.
 """
 from __future__ import annotations
 
@@ -31,6 +36,7 @@ import argparse
 import json
 import os
 import platform
+import subprocess
 import sys
 import time
 
@@ -51,6 +57,18 @@ def chunk_flops(lengths, heads: int, d: int) -> int:
         total += full * (10 * C * C * d + 6 * C * d * d)
         if rem:
             total += 10 * rem * rem * d + 6 * rem * d * d
+    return total * heads
+
+
+def chunk_flops_causal(lengths, heads: int, d: int) -> int:
+    """The same with the intra-chunk C x C products counted over their causal half only:
+    (5 c^2 d + 6 c d^2) x heads per chunk (36.51 GFLOP at config 1)."""
+    total = 0
+    for L in lengths:
+        full, rem = divmod(L, C)
+        total += full * (5 * C * C * d + 6 * C * d * d)
+        if rem:
+            total += 5 * rem * rem * d + 6 * rem * d * d
     return total * heads
 
 
@@ -188,6 +206,22 @@ def time_launches(torch, fn, steps: int) -> tuple[float, float]:
     return e0.elapsed_time(e1) / steps, per_launch
 
 
+def launch_percentiles(torch, fn, steps: int) -> dict:
+    """p10 / median / p90 of per-launch HIP-event times (ms), one event pair per launch."""
+    stream = torch.cuda.current_stream()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    torch.cuda.synchronize()
+    for i in range(steps):
+        starts[i].record(stream)
+        fn(i)
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    ts = sorted(s.elapsed_time(e) for s, e in zip(starts, ends))
+    q = lambda f: ts[min(len(ts) - 1, int(round(f * (len(ts) - 1))))]
+    return {"p10_ms": round(q(0.1), 4), "median_ms": round(q(0.5), 4), "p90_ms": round(q(0.9), 4)}
+
+
 def capture_graph(torch, fn):
     """Capture fn (kernel launches on the current stream) into a CUDA/HIP graph after a side-stream warmup."""
     side = torch.cuda.Stream()
@@ -300,45 +334,15 @@ def run_only(torch, args) -> int:
     return 0
 
 
-def main() -> int:
-    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--decode-steps", type=int, default=1000)
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--calibrate-copy", action="store_true",
-                    help="only run a plain 256 MiB device copy (the reference kernel for PMC byte counters)")
-    ap.add_argument("--only", choices=["prefill", "decode", "varlen", "train", "block_pair"], default=None,
-                    help="run one workload only (for profiler runs); prints no JSON line")
-    args = ap.parse_args()
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print(f"bench.py: this build runs one GPU only (the GDN op needs no collective: every (sequence, head) "
-              f"chain is independent); got --gpus {args.gpus}. Run with --gpus 1.", file=sys.stderr)
-        return 2
+PARTS = ("prefill", "decode", "varlen", "train", "block_pair")
 
-    import torch
 
-    if not torch.cuda.is_available():
-        print("bench.py: no GPU visible", file=sys.stderr)
-        return 1
-    from sorernn_amd import chunk_gated_delta_rule, gated_delta_decode_step
-    from sorernn_amd.synthetic import config_inputs, decode_inputs
+def part_prefill(torch, args) -> dict:
+    """Config 1: the chunked prefill op (two kernels on one stream), events around every launch."""
+    from sorernn_amd import chunk_gated_delta_rule
+    from sorernn_amd.synthetic import config_inputs
 
-    dev = "cuda"
-    if args.calibrate_copy:
-        # 256 MiB read + 256 MiB written per launch: divides FETCH_SIZE / WRITE_SIZE into a scale factor
-        src = torch.empty(64 * 1024 * 1024, device=dev, dtype=torch.float32).fill_(1.0)
-        dst = torch.empty_like(src)
-        for _ in range(args.steps):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        print(json.dumps({"copy_bytes_each_way": src.numel() * 4, "launches": args.steps}))
-        return 0
-    if args.only:
-        return run_only(torch, args)
-    # ------------------------------------------------------------------ config 1: prefill
-    inp = config_inputs(1).to(dev)
+    inp = config_inputs(1).to("cuda")
     B, T, H, K = inp.q.shape
 
     def step():
@@ -351,16 +355,30 @@ def main() -> int:
     t0 = time.perf_counter()
     ms_step, ms_launch = time_launches(torch, step, args.steps)
     wall = (time.perf_counter() - t0) / args.steps * 1e3
-    flops = chunk_flops([T] * B, H, K)
-    achieved = flops / (ms_launch * 1e-3) / 1e12
-    tok_s = B * T / (ms_step * 1e-3)
-    min_bytes = 4 * inp.q.numel() * 2 + 2 * inp.g.numel() * 4 + 2 * inp.h0.numel() * 4
-    tparts = [load_traffic(k) for k in PREFILL_KERNELS]
-    traffic = sum(tparts) if all(x is not None for x in tparts) else None
+    pct = launch_percentiles(torch, lambda i: step(), args.steps)
+    # the same launches alternating over two input sets (separate tensors, 2 x 281 MB > the 256 MB
+    # Infinity Cache), so no launch finds its inputs left in the cache by the previous one
+    alt = [(inp.q, inp.k, inp.v, inp.g, inp.beta, inp.h0),
+           tuple(x.clone() for x in (inp.q, inp.k, inp.v, inp.g, inp.beta, inp.h0))]
 
-    # ------------------------------------------------------------------ config 2: decode
-    # The step is captured once into a HIP graph and replayed back to back (a serving loop launches
-    # the same fixed-shape step every token); the eager, host-launched rate is reported beside it.
+    def step_alt(i):
+        q_, k_, v_, g_, b_, h_ = alt[i % 2]
+        return chunk_gated_delta_rule(q_, k_, v_, g_, b_, scale=inp.scale, initial_state=h_, output_final_state=True)
+
+    pct_rot = launch_percentiles(torch, step_alt, args.steps)
+    return {"B": B, "T": T, "H": H, "K": K, "ms_step": ms_step, "ms_launch": ms_launch, "wall_ms": wall,
+            "pct": pct, "pct_rot": pct_rot,
+            "min_bytes": 4 * inp.q.numel() * 2 + 2 * inp.g.numel() * 4 + 2 * inp.h0.numel() * 4}
+
+
+def part_decode(torch, args) -> dict:
+    """Config 2: the fused decode step. The step is captured once into a HIP graph and replayed back
+    to back (a serving loop launches the same fixed-shape step every token); the eager,
+    host-launched rate is reported beside it, and a run rotating over 5 state copies forces DRAM."""
+    from sorernn_amd import gated_delta_decode_step
+    from sorernn_amd.synthetic import decode_inputs
+
+    dev = "cuda"
     di = decode_inputs()
     x, cs, cw, g, b, st = (t.to(dev) for t in (di.x_qkv, di.conv_state, di.conv_weight, di.g, di.beta, di.state))
     out = torch.empty(di.x_qkv.shape[0], 1, di.HV, di.D, device=dev, dtype=di.x_qkv.dtype)
@@ -390,13 +408,19 @@ def main() -> int:
 
     rgraph = capture_graph(torch, dstep_rot)
     rot_ms = time_replays(torch, rgraph, max(1, args.decode_steps // per_graph)) / per_graph
-    dbytes = decode_bytes()
-    del states, convs, rgraph, graph
+    torch.cuda.synchronize()
+    return {"us_step": dec_ms * 1e3, "rot_us_step": rot_ms * 1e3, "eager_us_step": eager_ms * 1e3,
+            "per_graph": per_graph}
 
-    # ------------------------------------------------------------------ config 3: varlen
+
+def part_varlen(torch, args) -> dict:
+    """Config 3: 8 packed documents, 32768 tokens, per-document initial and final states."""
+    from sorernn_amd import chunk_gated_delta_rule
+    from sorernn_amd.synthetic import config_inputs
+
     v3 = config_inputs(3)
     cu_cpu = v3.cu_seqlens
-    v3 = v3.to(dev)
+    v3 = v3.to("cuda")
 
     def vstep():
         return chunk_gated_delta_rule(v3.q, v3.k, v3.v, v3.g, v3.beta, scale=v3.scale, initial_state=v3.h0,
@@ -404,27 +428,54 @@ def main() -> int:
 
     for _ in range(3):
         vstep()
-    v_ms, v_launch = time_launches(torch, vstep, max(5, args.steps // 5))
-    lens = (cu_cpu[1:] - cu_cpu[:-1]).tolist()
+    n = max(5, args.steps // 5)
+    v_ms, v_launch = time_launches(torch, vstep, n)
+    v_pct = launch_percentiles(torch, lambda i: vstep(), n)
+    return {"ms_step": v_ms, "ms_launch": v_launch, "pct": v_pct, "lens": (cu_cpu[1:] - cu_cpu[:-1]).tolist()}
+
+
+def part_train(torch, args) -> dict:
+    """Config 1 under autograd: the training forward and the backward, timed separately."""
+    from sorernn_amd.synthetic import config_inputs
+
+    inp = config_inputs(1).to("cuda")
+    tf, tb = train_step_times(torch, inp, max(5, args.steps // 5))
+    return {"fwd_ms": tf, "bwd_ms": tb}
+
+
+def part_block_pair(torch, args) -> dict:
+    return block_pair(torch, max(5, args.steps // 5))
+
+
+PART_FNS = {"prefill": part_prefill, "decode": part_decode, "varlen": part_varlen, "train": part_train,
+            "block_pair": part_block_pair}
+
+
+def assemble(parts: dict, args, cpu: dict | None) -> dict:
+    """The one JSON line from the workloads' raw measurements (no GPU work here)."""
+    pf, dc, vl, tr = parts["prefill"], parts["decode"], parts["varlen"], parts["train"]
+    B, T, H, K = pf["B"], pf["T"], pf["H"], pf["K"]
+    ms_step, ms_launch = pf["ms_step"], pf["ms_launch"]
+    flops = chunk_flops([T] * B, H, K)
+    flops_c = chunk_flops_causal([T] * B, H, K)
+    achieved = flops / (ms_launch * 1e-3) / 1e12
+    tparts = [load_traffic(k) for k in PREFILL_KERNELS]
+    traffic = sum(tparts) if all(x is not None for x in tparts) else None
+    dbytes = decode_bytes()
+    dec_s, rot_s = dc["us_step"] * 1e-6, dc["rot_us_step"] * 1e-6
+    lens = vl["lens"]
     v_flops = chunk_flops(lens, 16, 128)
-    del v3
-
-    # ------------------------------------------------------------------ config 1 under autograd
-    tr_f, tr_b = train_step_times(torch, inp, max(5, args.steps // 5))
     b_flops = chunk_bwd_flops([T] * B, H, K)
-
-    # ------------------------------------------------------------------ config 4: block pair
-    bp = block_pair(torch, max(5, args.steps // 5))
-
+    tr_f, tr_b = tr["fwd_ms"], tr["bwd_ms"]
     result = {
         "metric": "GDN prefill tokens/s & decode-step µs (H=16,d=128); % of MI355X roofline",
-        "value": round(tok_s, 1),
+        "value": round(B * T / (ms_step * 1e-3), 1),
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_step, 4),
-        "wall_ms_per_step": round(wall, 4),
+        "wall_ms_per_step": round(pf["wall_ms"], 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -442,32 +493,41 @@ def main() -> int:
             "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
             "traffic": traffic,
             "flops_per_launch": flops,
-            "min_hbm_bytes_per_launch": min_bytes,
-            "hbm_frac_at_min_bytes": round(min_bytes / (ms_launch * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "min_hbm_bytes_per_launch": pf["min_bytes"],
+            "hbm_frac_at_min_bytes": round(pf["min_bytes"] / (ms_launch * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "ms_per_launch": round(ms_launch, 4),
+            "launch_percentiles": pf["pct"],
+            "launch_percentiles_two_input_sets": pf["pct_rot"],
+            # secondary FLOP conventions: causal tiles only (5C^2d + 6Cd^2 per chunk-head), and the
+            # reference's flops.py count of 4*K*V per token-head
+            "flops_causal_halved": flops_c,
+            "frac_causal_halved": round(flops_c / (ms_launch * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+            "flops_reference_flops_py": 4 * K * K * B * T * H,
         },
         "decode": {
             "workload": "config2: B=64, H=HV=16, D=128, conv cache [64,6144,4] bf16, fp32 state in place",
             "kernel": "gated_delta_decode_w4_kernel",
-            "us_per_step": round(dec_ms * 1e3, 3),
-            "timing": f"{args.decode_steps} back-to-back fused steps: replays of a HIP graph holding {per_graph} steps",
+            "us_per_step": round(dc["us_step"], 3),
+            "timing": f"{args.decode_steps} back-to-back fused steps: replays of a HIP graph holding "
+                      f"{dc['per_graph']} steps",
             "bytes_per_step": dbytes,
-            "achieved_GBs": round(dbytes / (dec_ms * 1e-3) / 1e9, 1),
-            "frac_hbm_peak": round(dbytes / (dec_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "rotating_5_states_us_per_step": round(rot_ms * 1e3, 3),
+            "achieved_GBs": round(dbytes / dec_s / 1e9, 1),
+            "frac_hbm_peak": round(dbytes / dec_s / 1e9 / HBM_PEAK_GBS, 4),
+            "rotating_5_states_us_per_step": round(dc["rot_us_step"], 3),
             "rotating_note": "5 state/conv copies (335 MB > 256 MB Infinity Cache) visited in turn: DRAM-served state",
-            "rotating_achieved_GBs": round(dbytes / (rot_ms * 1e-3) / 1e9, 1),
-            "rotating_frac_hbm_peak": round(dbytes / (rot_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "eager_us_per_step": round(eager_ms * 1e3, 3),
+            "rotating_achieved_GBs": round(dbytes / rot_s / 1e9, 1),
+            "rotating_frac_hbm_peak": round(dbytes / rot_s / 1e9 / HBM_PEAK_GBS, 4),
+            "eager_us_per_step": round(dc["eager_us_step"], 3),
             "steps": args.decode_steps,
         },
         "varlen": {
             "workload": "config3: 8 packed docs, 32768 tokens, H=16, d=128, per-doc h0 and final states",
             "doc_lengths": lens,
-            "tokens_per_s": round(32768 / (v_ms * 1e-3), 1),
-            "ms_per_launch": round(v_launch, 4),
-            "tflops": round(v_flops / (v_launch * 1e-3) / 1e12, 2),
-            "frac_mfma_peak": round(v_flops / (v_launch * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+            "tokens_per_s": round(32768 / (vl["ms_step"] * 1e-3), 1),
+            "ms_per_launch": round(vl["ms_launch"], 4),
+            "launch_percentiles": vl["pct"],
+            "tflops": round(v_flops / (vl["ms_launch"] * 1e-3) / 1e12, 2),
+            "frac_mfma_peak": round(v_flops / (vl["ms_launch"] * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
         },
         "train": {
             "workload": "config1 under autograd: training forward (saves bf16 per-chunk states) + backward "
@@ -481,11 +541,81 @@ def main() -> int:
             "kernels": "gated_delta_chunk_kernel<SAVE>; gated_delta_chunk_bwd_prep_kernel, "
                        "gated_delta_chunk_bwd_state_kernel, gated_delta_chunk_bwd_grad_kernel",
         },
-        "block_pair": bp,
+        "block_pair": parts["block_pair"],
+        "isolation": "each workload ran in its own child process (a fresh HIP context and allocator)",
     }
-    if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(torch)
-    print(json.dumps(result), flush=True)
+    if cpu is not None:
+        result["cpu_baseline"] = cpu
+    return result
+
+
+def run_part(part: str, args) -> dict:
+    """Run one workload in a child process and return the JSON object it prints last. Its stderr
+    (progress) passes through; a failing child ends the bench with the child's status."""
+    cmd = [sys.executable, "-u", os.path.abspath(__file__), "--part", part, "--steps", str(args.steps),
+           "--warmup", str(args.warmup), "--decode-steps", str(args.decode_steps)]
+    res = subprocess.run(cmd, stdout=subprocess.PIPE, text=True)
+    if res.returncode != 0:
+        print(f"bench.py: workload {part} failed (status {res.returncode}); output:\n{res.stdout}", file=sys.stderr)
+        raise SystemExit(res.returncode if res.returncode > 0 else 1)
+    lines = [ln for ln in res.stdout.splitlines() if ln.strip()]
+    if not lines:
+        print(f"bench.py: workload {part} printed nothing", file=sys.stderr)
+        raise SystemExit(1)
+    return json.loads(lines[-1])
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--decode-steps", type=int, default=1000)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain 256 MiB device copy (the reference kernel for PMC byte counters)")
+    ap.add_argument("--only", choices=["prefill", "decode", "varlen", "train", "block_pair"], default=None,
+                    help="run one workload only (for profiler runs); prints no JSON line")
+    ap.add_argument("--part", choices=PARTS, default=None,
+                    help="(internal) run one workload and print its raw measurements as JSON")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(f"bench.py: this build runs one GPU only (the GDN op needs no collective: every (sequence, head) "
+              f"chain is independent); got --gpus {args.gpus}. Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    if args.part or args.only or args.calibrate_copy:
+        if not torch.cuda.is_available():
+            print("bench.py: no GPU visible", file=sys.stderr)
+            return 1
+        if args.calibrate_copy:
+            # 256 MiB read + 256 MiB written per launch: divides FETCH_SIZE / WRITE_SIZE into a scale factor
+            src = torch.empty(64 * 1024 * 1024, device="cuda", dtype=torch.float32).fill_(1.0)
+            dst = torch.empty_like(src)
+            for _ in range(args.steps):
+                dst.copy_(src)
+            torch.cuda.synchronize()
+            print(json.dumps({"copy_bytes_each_way": src.numel() * 4, "launches": args.steps}))
+            return 0
+        if args.only:
+            return run_only(torch, args)
+        out = PART_FNS[args.part](torch, args)
+        torch.cuda.synchronize()
+        print(f"bench.py: {args.part} done", file=sys.stderr, flush=True)
+        print(json.dumps(out), flush=True)
+        return 0
+    # The full run: every workload in its own child process (this process never touches the GPU;
+    # counting devices does not initialise it), then the CPU baseline here.
+    if torch.cuda.device_count() < 1:
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 1
+    parts = {}
+    for part in PARTS:
+        parts[part] = run_part(part, args)
+    cpu = None if args.no_cpu_baseline else cpu_baseline(torch)
+    print(json.dumps(assemble(parts, args, cpu)), flush=True)
     return 0
 
 
