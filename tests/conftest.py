@@ -26,3 +26,16 @@ def pytest_collection_modifyitems(config, items):
     for item in items:
         if "gpu" in item.keywords:
             item.add_marker(skip)
+
+
+@pytest.fixture(scope="session", autouse=True)
+def _blas_workspace_first():
+    """torch sets up its BLAS-Lt handle and workspace at the first GEMM of the process. One bf16
+    linear (the layers' GEMM path) before any test allocates and frees device memory gives a full
+    run the same GEMM setup as a run of a single test file."""
+    if torch.cuda.is_available():
+        x = torch.zeros(2, 64, 256, device="cuda", dtype=torch.bfloat16)
+        w = torch.zeros(512, 256, device="cuda", dtype=torch.bfloat16)
+        torch.nn.functional.linear(x, w)
+        torch.cuda.synchronize()
+    yield
