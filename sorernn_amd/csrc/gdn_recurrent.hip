@@ -130,6 +130,24 @@ __device__ __forceinline__ void store_state(const StateRegs<KD, VD>& sr, float* 
   for (int i = 0; i < L::RPT; ++i) *reinterpret_cast<float4*>(base + (int64_t)(rg + L::RG * i) * VD + 4 * cg) = s[i];
 }
 
+// A VB-column block of a [KD][stride] state (columns col0 .. col0 + VB - 1), in the layout above.
+template <int KD, int VB>
+__device__ __forceinline__ void load_state_cols(StateRegs<KD, VB>& sr, const float* base, int stride, int col0) {
+  using L = RecLayout<KD, VB>;
+  const int t = threadIdx.x, cg = t % L::CG, rg = t / L::CG;
+#pragma unroll
+  for (int i = 0; i < L::RPT; ++i)
+    sr.r[i] = *reinterpret_cast<const float4*>(base + (int64_t)(rg + L::RG * i) * stride + col0 + 4 * cg);
+}
+template <int KD, int VB>
+__device__ __forceinline__ void store_state_cols(const StateRegs<KD, VB>& sr, float* base, int stride, int col0) {
+  using L = RecLayout<KD, VB>;
+  const int t = threadIdx.x, cg = t % L::CG, rg = t / L::CG;
+#pragma unroll
+  for (int i = 0; i < L::RPT; ++i)
+    *reinterpret_cast<float4*>(base + (int64_t)(rg + L::RG * i) * stride + col0 + 4 * cg) = sr.r[i];
+}
+
 // grid (HV, N): one workgroup per (value head, sequence), tokens in order.
 template <int KD, int VD>
 __global__ __launch_bounds__(256) void gated_delta_recurrent_kernel(RecParams p) {
@@ -263,13 +281,16 @@ struct alignas(W * sizeof(T) >= 16 ? 16 : W * sizeof(T)) ConvWindow {
 };
 
 // Fast decode step for width-4 conv caches whose dtype equals the activation dtype T. Every
-// global load of the step is issued before the first dependent use: the first value head's state
-// (64 KB per workgroup at D = 128), the conv caches, inputs and weights of the q/k channels and of
-// that head's v channels, and the gates; the conv math then overlaps the state's arrival.
+// global load of the step is issued before the first dependent use: the first column block of the
+// value head's state, the conv caches, inputs and weights of the q/k channels and of that head's v
+// channels, and the gates; the conv math then overlaps the state's arrival. The state streams in
+// NB column blocks (the columns of the recurrence are independent: column j needs only S[:, j]):
+// block b + 1's loads are in flight while block b is reduced, updated and written back, so the
+// reads and writes of the step overlap in HBM instead of running as two phases.
 template <int D, class T>
 __global__ __launch_bounds__(256) void gated_delta_decode_w4_kernel(DecodeParams p) {
-  constexpr int W = 4;
-  using L = RecLayout<D, D>;
+  constexpr int W = 4, NB = D / 32, VB = D / NB;  // 32-column blocks: 128-byte row segments
+  using L = RecLayout<D, VB>;
   using Win = ConvWindow<W, T>;
   __shared__ float qk[2 * D];
   __shared__ float vs[2][D];
@@ -279,6 +300,7 @@ __global__ __launch_bounds__(256) void gated_delta_decode_w4_kernel(DecodeParams
   const int rep = (int)(p.HV / p.H);
   const int64_t C = (2 * p.H + p.HV) * D;
   const int t = threadIdx.x;
+  int rb = 0;  // red buffer of the next reduction (consecutive reductions alternate)
   const T* __restrict__ xg = static_cast<const T*>(p.x);
   Win* __restrict__ cs = static_cast<Win*>(p.conv_state);
   const float4* __restrict__ wg = reinterpret_cast<const float4*>(p.conv_w);
@@ -292,8 +314,8 @@ __global__ __launch_bounds__(256) void gated_delta_decode_w4_kernel(DecodeParams
     const int hv = h * rep + r;
     const int par = r & 1;
     const int64_t sbase = (b * p.HV + hv) * (int64_t)D * D;
-    StateRegs<D, D> s;
-    load_state<D, D>(s, p.state + sbase);
+    StateRegs<D, VB> s[2];
+    load_state_cols<D, VB>(s[0], p.state + sbase, D, 0);
     const int64_t ch_v = 2 * p.H * D + (int64_t)hv * D + t;
     Win wq{}, wv{};
     T xq{}, xv{};
@@ -333,14 +355,19 @@ __global__ __launch_bounds__(256) void gated_delta_decode_w4_kernel(DecodeParams
     if (p.flags & GDN_FLAG_BETA_SIGMOID) bv = sigmoid_f32(bv);
     const float a = expf(gv);
     __syncthreads();
-    float o4[4];
-    rec_token<D, D>(s, qk, qk + D, vs[par], a, bv, l2, p.scale, red[par], o4);
-    if (t < L::CG) {
-      T* og = static_cast<T*>(p.o) + (b * p.HV + hv) * D + 4 * t;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) og[c] = f32_to_elem<T>(o4[c]);
+    for (int blk = 0; blk < NB; ++blk) {
+      if (blk + 1 < NB) load_state_cols<D, VB>(s[(blk + 1) & 1], p.state + sbase, D, (blk + 1) * VB);
+      float o4[4];
+      rec_token<D, VB>(s[blk & 1], qk, qk + D, vs[par] + blk * VB, a, bv, l2, p.scale, red[rb], o4);
+      rb ^= 1;
+      if (t < L::CG) {
+        T* og = static_cast<T*>(p.o) + (b * p.HV + hv) * D + blk * VB + 4 * t;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) og[c] = f32_to_elem<T>(o4[c]);
+      }
+      store_state_cols<D, VB>(s[blk & 1], p.state + sbase, D, blk * VB);
     }
-    store_state<D, D>(s, p.state + sbase);
   }
 }
 
