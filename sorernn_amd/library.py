@@ -50,8 +50,7 @@ def bwd_workspace_bytes(b, t, hv, kd, vd, n, varlen: bool):
             + _align256(chunks * hv * 2 * 4))
 
 
-@torch.library.custom_op("sorernn::chunk_gated_delta_rule_fwd", mutates_args=())
-def chunk_fwd(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor, initial_state: Optional[Tensor],
+def chunk_fwd_impl(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor, initial_state: Optional[Tensor],
               A_log: Optional[Tensor], dt_bias: Optional[Tensor], cu_seqlens: Optional[Tensor], scale: float,
               flags: int, num_seqs: int, output_final_state: bool,
               save_states: bool) -> tuple[Tensor, Tensor, Tensor, Tensor]:
@@ -82,6 +81,11 @@ def chunk_fwd(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor, initial_
     elif fin is not None:
         fin.copy_(h0 if h0 is not None else torch.zeros_like(fin))
     return o, final, states, ws
+
+
+# The registered op; ``chunk_fwd_impl`` is its implementation, which the eager inference path of
+# ``ops.py`` calls directly (no dispatcher round trip when nothing traces, records or differentiates).
+chunk_fwd = torch.library.custom_op("sorernn::chunk_gated_delta_rule_fwd", mutates_args=())(chunk_fwd_impl)
 
 
 @chunk_fwd.register_fake

@@ -129,6 +129,13 @@ def _delta_rule_args(name, q, k, v, g, beta, scale, initial_state, cu_seqlens, c
     return b, t, h, kd, hv, vd, n, flags, float(scale), A_log, dt_bias
 
 
+def _plain_eager(x: Tensor) -> bool:
+    """True for an ordinary tensor outside torch.compile, FX tracing and any active dispatch mode."""
+    return (type(x) is torch.Tensor and not torch.compiler.is_compiling()
+            and not torch.fx._symbolic_trace._is_fx_tracing_flag
+            and torch.utils._python_dispatch._get_current_dispatch_mode() is None)
+
+
 def _gdn_call(entry, name, q, k, v, g, beta, scale, initial_state, output_final_state, cu_seqlens, cu_seqlens_cpu,
               use_qk_l2norm_in_kernel, use_beta_sigmoid_in_kernel, use_gate_in_kernel, A_log, dt_bias,
               inplace_final_state=False):
@@ -150,11 +157,14 @@ def _gdn_call(entry, name, q, k, v, g, beta, scale, initial_state, output_final_
         )
     if entry == "gdn_chunk_fwd":
         # the torch.library op (sorernn::chunk_gated_delta_rule_fwd): traceable by torch.compile, with
-        # the backward registered on it; with grad it also keeps the per-chunk states for the backward
-        o, final, _, _ = _library.chunk_fwd(q, k, v, g, beta, initial_state,
-                                            a_log_in if use_gate_in_kernel else None,
-                                            dt_bias_in if use_gate_in_kernel else None, cu_seqlens, scale, flags, n,
-                                            bool(output_final_state), needs_grad)
+        # the backward registered on it; with grad it also keeps the per-chunk states for the backward.
+        # Plain eager inference (no grad, no compile or fake tensors, no dispatch mode recording ops)
+        # calls the op's implementation directly: the dispatcher round trip costs more host time
+        # than the two kernel launches.
+        op = _library.chunk_fwd if (needs_grad or not _plain_eager(q)) else _library.chunk_fwd_impl
+        o, final, _, _ = op(q, k, v, g, beta, initial_state, a_log_in if use_gate_in_kernel else None,
+                            dt_bias_in if use_gate_in_kernel else None, cu_seqlens, scale, flags, n,
+                            bool(output_final_state), needs_grad)
         return o, (final if output_final_state else None)
     q, k, v, g, beta = (x.contiguous() for x in (q, k, v, g, beta))
     h0 = None
