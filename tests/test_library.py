@@ -63,3 +63,25 @@ def test_backward_formulas_are_registered():
         out = library.chunk_bwd(q, k, v, g, beta, do, None, states, ws, None, None, None, 0.125, 0, 1, True)
         assert [tuple(x.shape) for x in out] == [(1, 130, 2, 64), (1, 130, 2, 64), (1, 130, 4, 64), (1, 130, 4),
                                                  (1, 130, 4), (1, 4, 64, 64), (0,), (0,)]
+
+
+def test_eager_fast_path_yields_to_tracing_and_dispatch_modes():
+    """Plain eager inference calls the op implementation directly; anything that records, traces or
+    fakes tensors must see the registered torch.library op instead."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    from torch.utils._python_dispatch import TorchDispatchMode
+
+    from sorernn_amd.ops import _plain_eager
+
+    x = torch.zeros(2)
+    assert _plain_eager(x)
+
+    class Record(TorchDispatchMode):
+        def __torch_dispatch__(self, func, types, args=(), kwargs=None):
+            return func(*args, **(kwargs or {}))
+
+    with Record():
+        assert not _plain_eager(x)
+    with FakeTensorMode() as mode:
+        assert not _plain_eager(mode.from_tensor(x))
+    assert not torch.compile(lambda t: torch.tensor(_plain_eager(t)), fullgraph=True, backend="eager")(x)
