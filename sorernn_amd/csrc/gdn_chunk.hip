@@ -204,23 +204,31 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
 #pragma unroll
     for (int u = 0; u < 2; ++u) *reinterpret_cast<bf16x8*>(v0 + 32 * u * kVP) = pv[u];
   };
-  // The gate bits of a chunk are loaded as both a 32-bit and a 16-bit word (each range-checked) and
-  // the dtype picks one at the use: a load whose width depends on the dtype would be two
-  // instructions on two paths, and the loop-carried register they share would then be copied at
-  // the loop's join under a wait for every load and store in flight.
+  // The gate bits of a chunk are loaded by one 32-bit and one 16-bit load per tensor, both issued
+  // whatever the dtype (a load whose width depends on the dtype would be two instructions on two
+  // paths, and the loop-carried register they share would then be copied at the loop's join under
+  // a wait for every load and store in flight). Each width has its own buffer resource: the one
+  // matching the dtype spans exactly this head's elements of the chunk, from its first token to
+  // the last byte of its last token, and the other spans zero bytes, so that load returns 0 and
+  // touches no memory. (A 32-bit load at a 16-bit element would read 2 bytes beyond it, past the
+  // end of the tensor for the last head of the last token.)
   struct GateBits {
     uint32_t g32, g16, b32, b16;
   };
   auto fetch_gates = [&](int c, GateBits& r) {  // wave 4, lane = token
     const int64_t c0 = bos + (int64_t)c * kC;
-    const uint32_t gb = (uint32_t)(p.HV * dtype_bytes(p.dg)), bb = (uint32_t)(p.HV * dtype_bytes(p.db));
+    const uint32_t eg = (uint32_t)dtype_bytes(p.dg), eb = (uint32_t)dtype_bytes(p.db);
+    const uint32_t gb = (uint32_t)p.HV * eg, bb = (uint32_t)p.HV * eb;
     const uint32_t len = (uint32_t)chunk_len(c);
-    const auto rg = make_rsrc(static_cast<const char*>(p.g) + (c0 * p.HV + hv) * dtype_bytes(p.dg), len * gb);
-    const auto rb = make_rsrc(static_cast<const char*>(p.beta) + (c0 * p.HV + hv) * dtype_bytes(p.db), len * bb);
-    r.g32 = __builtin_amdgcn_raw_buffer_load_b32(rg, (int)(lane * gb), 0, 0);
-    r.g16 = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rg, (int)(lane * gb), 0, 0);
-    r.b32 = __builtin_amdgcn_raw_buffer_load_b32(rb, (int)(lane * bb), 0, 0);
-    r.b16 = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rb, (int)(lane * bb), 0, 0);
+    const uint32_t gext = len ? (len - 1) * gb + eg : 0u, bext = len ? (len - 1) * bb + eb : 0u;
+    const char* gsrc = static_cast<const char*>(p.g) + (c0 * p.HV + hv) * eg;
+    const char* bsrc = static_cast<const char*>(p.beta) + (c0 * p.HV + hv) * eb;
+    const auto rg32 = make_rsrc(gsrc, eg == 4 ? gext : 0u), rg16 = make_rsrc(gsrc, eg == 4 ? 0u : gext);
+    const auto rb32 = make_rsrc(bsrc, eb == 4 ? bext : 0u), rb16 = make_rsrc(bsrc, eb == 4 ? 0u : bext);
+    r.g32 = __builtin_amdgcn_raw_buffer_load_b32(rg32, (int)(lane * gb), 0, 0);
+    r.g16 = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rg16, (int)(lane * gb), 0, 0);
+    r.b32 = __builtin_amdgcn_raw_buffer_load_b32(rb32, (int)(lane * bb), 0, 0);
+    r.b16 = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rb16, (int)(lane * bb), 0, 0);
   };
   auto stage_gates = [&](int c, const GateBits& r) {
     // (A_log through opaque_int: its exp is recomputed here, not held in a register)

@@ -92,6 +92,32 @@ def test_chunk_kernel_options_match_oracle():
     assert_state_close(st.cpu(), st_ref)
 
 
+def test_chunk_in_kernel_gate_bf16_config1_size():
+    """Regression for the state kernel's gate loads: raw bf16 a/b (the layer's gdn_kernel_gate route)
+    at config-1 size. Each bf16 gate tensor is exactly 512 KiB; the last head of the last token is
+    its final element, which the loads once read 2 bytes past. Checked against the oracle on a slice
+    that holds that element (batch row 3, value heads 0 and 15, all 4096 tokens)."""
+    print("config1 in-kernel gate, bf16 a/b", flush=True)
+    inp = config_inputs(1)
+    gen = torch.Generator().manual_seed(77)
+    a = torch.randn(4, 4096, 16, generator=gen).to(torch.bfloat16)
+    b = torch.randn(4, 4096, 16, generator=gen).to(torch.bfloat16)
+    assert a.numel() * a.element_size() == 512 * 1024
+    A_log = torch.empty(16).uniform_(1, 16, generator=gen).log()
+    dt_bias = torch.randn(16, generator=gen) * 0.3
+    d = inp.to(DEV)
+    o, st = chunk_gated_delta_rule(d.q, d.k, d.v, a.to(DEV), b.to(DEV), scale=inp.scale, initial_state=d.h0,
+                                   output_final_state=True, use_gate_in_kernel=True, A_log=A_log.to(DEV),
+                                   dt_bias=dt_bias.to(DEV), use_beta_sigmoid_in_kernel=True)
+    torch.cuda.synchronize()
+    g_ref = -A_log.exp() * F.softplus(a.float() + dt_bias)
+    sl = lambda x: x[3:4, :, [0, 15]]  # noqa: E731
+    o_ref, st_ref = recurrent_gated_delta_rule(sl(inp.q), sl(inp.k), sl(inp.v), sl(g_ref), sl(b.float().sigmoid()),
+                                               inp.scale, inp.h0[3:4, [0, 15]], True)
+    assert_output_close(o[3:4, :, [0, 15]].cpu(), o_ref)
+    assert_state_close(st[3:4, [0, 15]].cpu(), st_ref)
+
+
 def test_chunk_matches_recurrent_kernel_config1_full_size():
     inp = config_inputs(1)
     print("config1 full size", flush=True)
