@@ -100,6 +100,24 @@ GDN_API int gdn_chunk_fwd_train(const void* q, const void* k, const void* v, con
                         const float* A_log, const float* dt_bias, void* chunk_states, void* workspace,
                         size_t workspace_bytes, void* stream);
 
+/*
+ * gdn_chunk_fwd without a workspace argument; it allocates nothing. No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). The workspace is a fixed array in the library's device
+ * memory of gdn_chunk_fwd_noalloc_max_workspace() bytes (64 MiB + 64 KiB: up to 524,288 token-heads,
+ * e.g. BASELINE config 1 or 3), held on every device the library runs on until the process ends.
+ * Sizes needing more return GDN_ERR_INVALID. The stream's device must be the current device. Calls
+ * on one device share the array: calls that overlap on one device race.
+ */
+GDN_API int gdn_chunk_fwd_noalloc(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                          const float* initial_state, void* o, float* final_state, const void* cu_seqlens,
+                          int64_t B, int64_t T, int64_t H, int64_t HV, int64_t K, int64_t V, int64_t N,
+                          int qkv_dtype, int g_dtype, int beta_dtype, float scale, unsigned flags,
+                          const float* A_log, const float* dt_bias, void* stream);
+
+/* Bytes of the array gdn_chunk_fwd_noalloc uses as its workspace. */
+GDN_API size_t gdn_chunk_fwd_noalloc_max_workspace(void);
+
 /* Bytes of chunk_states for gdn_chunk_fwd_train / gdn_chunk_bwd (0 for invalid sizes). */
 GDN_API size_t gdn_chunk_states_size(int64_t B, int64_t T, int64_t HV, int64_t K, int64_t V, int64_t N, int varlen);
 

@@ -36,6 +36,8 @@ SIGNATURES = {
     "gdn_chunk_fwd": [_P] * 9 + [_I64] * 7 + [_INT] * 3 + [_F, _U, _P, _P, _P, _SZ, _P],
     "gdn_chunk_workspace_size": [_I64] * 4 + [_INT],
     "gdn_chunk_fwd_train": [_P] * 9 + [_I64] * 7 + [_INT] * 3 + [_F, _U, _P, _P, _P, _P, _SZ, _P],
+    "gdn_chunk_fwd_noalloc": [_P] * 9 + [_I64] * 7 + [_INT] * 3 + [_F, _U, _P, _P, _P],
+    "gdn_chunk_fwd_noalloc_max_workspace": [],
     "gdn_chunk_states_size": [_I64] * 6 + [_INT],
     "gdn_chunk_bwd": [_P] * 10 + [_I64] * 7 + [_INT] * 3 + [_F, _U] + [_P] * 11 + [_SZ, _P],
     "gdn_chunk_bwd_workspace_size": [_I64] * 6 + [_INT],
@@ -58,6 +60,7 @@ RESTYPES = {
     "gdn_last_error": ctypes.c_char_p,
     "gdn_chunk_workspace_size": ctypes.c_size_t,
     "gdn_chunk_states_size": ctypes.c_size_t,
+    "gdn_chunk_fwd_noalloc_max_workspace": ctypes.c_size_t,
     "gdn_chunk_bwd_workspace_size": ctypes.c_size_t,
     "gdn_causal_conv1d_bwd_workspace_size": ctypes.c_size_t,
     "gdn_rms_norm_gated_bwd_workspace_size": ctypes.c_size_t,

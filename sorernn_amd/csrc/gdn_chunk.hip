@@ -40,6 +40,7 @@
 //
 // LDS: K (3 slots), Q (2 slots), T - I, P, V and O (2 slots each), gate terms (3 slots).
 
+#include <mutex>
 #include <type_traits>
 
 #include "gdn_chunk.h"
@@ -696,4 +697,87 @@ extern "C" int gdn_chunk_fwd_train(const void* q, const void* k, const void* v, 
   return chunk_fwd_impl(q, k, v, g, beta, initial_state, o, final_state, cu_seqlens, B, T, H, HV, K, V, N, qkv_dtype,
                         g_dtype, beta_dtype, scale, flags, A_log, dt_bias, chunk_states, workspace, workspace_bytes,
                         stream);
+}
+
+// ------------------------------------------------------------------ allocation-free variant
+// gdn_chunk_fwd_noalloc runs the same two kernels as gdn_chunk_fwd, with the workspace (the T - I
+// rows and the varlen index arrays) in `scratch`, a fixed array in the library's device memory
+// instead of a caller buffer. Each device holds its own copy, at its own address, from the load of
+// the library until the process ends. In host code `scratch` names a host-side stand-in, not device
+// memory: its device address is looked up once per device (hipGetSymbolAddress, with that device
+// current) and only that address is passed to kernels.
+// Nothing in the workspace has to start at zero: the prep kernel writes every T - I row the state
+// kernel reads, and the index kernel writes both index arrays. Calls that overlap on one device
+// share the array and race.
+namespace {
+
+constexpr size_t kScratchBytes = (size_t(64) << 20) + (size_t(64) << 10);  // 64 MiB + 64 KiB
+__device__ __align__(256) char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of `scratch` on the device that runs `stream` (which must be current).
+int scratch_for_stream(void* stream, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    gdn_internal_set_error("gdn_chunk_fwd_noalloc: hipGetDevice failed: %s", hipGetErrorString(e));
+    return GDN_ERR_HIP;
+  }
+  if (stream) {
+    int sdev = -1;
+    e = hipStreamGetDevice(static_cast<hipStream_t>(stream), &sdev);
+    if (e != hipSuccess) {
+      gdn_internal_set_error("gdn_chunk_fwd_noalloc: hipStreamGetDevice failed: %s", hipGetErrorString(e));
+      return GDN_ERR_HIP;
+    }
+    if (sdev != dev) {
+      gdn_internal_set_error("gdn_chunk_fwd_noalloc: the stream belongs to device %d but device %d is current", sdev,
+                             dev);
+      return GDN_ERR_INVALID;
+    }
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    gdn_internal_set_error("gdn_chunk_fwd_noalloc: device %d out of range", dev);
+    return GDN_ERR_UNSUPPORTED;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      gdn_internal_set_error("gdn_chunk_fwd_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                             hipGetErrorString(e));
+      return GDN_ERR_HIP;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return GDN_OK;
+}
+
+}  // namespace
+
+extern "C" size_t gdn_chunk_fwd_noalloc_max_workspace(void) { return kScratchBytes; }
+
+extern "C" int gdn_chunk_fwd_noalloc(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                                     const float* initial_state, void* o, float* final_state, const void* cu_seqlens,
+                                     int64_t B, int64_t T, int64_t H, int64_t HV, int64_t K, int64_t V, int64_t N,
+                                     int qkv_dtype, int g_dtype, int beta_dtype, float scale, unsigned flags,
+                                     const float* A_log, const float* dt_bias, void* stream) {
+  const size_t need = gdn_chunk_workspace_size(B, T, HV, N, cu_seqlens != nullptr);
+  if (need > kScratchBytes) {
+    gdn_internal_set_error(
+        "gdn_chunk_fwd_noalloc: these sizes need %zu bytes of workspace, more than the %zu bytes of the built-in "
+        "scratch array (128 bytes per token and value head); use gdn_chunk_fwd with a caller workspace",
+        need, kScratchBytes);
+    return GDN_ERR_INVALID;
+  }
+  void* ws = nullptr;
+  const int rc = scratch_for_stream(stream, &ws);
+  if (rc != GDN_OK) return rc;
+  return chunk_fwd_impl(q, k, v, g, beta, initial_state, o, final_state, cu_seqlens, B, T, H, HV, K, V, N, qkv_dtype,
+                        g_dtype, beta_dtype, scale, flags, A_log, dt_bias, nullptr, ws, kScratchBytes, stream);
 }

@@ -1,0 +1,62 @@
+"""``gdn_chunk_fwd_noalloc`` (the allocation-free prefill entry point) against ``gdn_chunk_fwd``.
+
+Both run the same two kernels; only the workspace differs (the library's built-in scratch array vs a
+caller buffer), so outputs and final states must agree bit for bit. Two calls in a row, the second
+with a smaller input (the array keeps the first call's contents), then a varlen call, all through the
+C ABI. Oversized inputs are rejected on the host before any launch.
+"""
+import pytest
+import torch
+
+from sorernn_amd import _lib
+from sorernn_amd.synthetic import gdn_inputs
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _run(entry, inp, flags=0):
+    d = inp.to(DEV)
+    b, t, h, kd = d.q.shape
+    hv, vd = d.v.shape[2], d.v.shape[3]
+    n = b if d.cu_seqlens is None else d.cu_seqlens.numel() - 1
+    o = torch.empty_like(d.v)
+    final = torch.empty(n, hv, kd, vd, device=DEV, dtype=torch.float32)
+    args = [_lib.ptr(d.q), _lib.ptr(d.k), _lib.ptr(d.v), _lib.ptr(d.g), _lib.ptr(d.beta), _lib.ptr(d.h0),
+            _lib.ptr(o), _lib.ptr(final), _lib.ptr(d.cu_seqlens), b, t, h, hv, kd, vd, n,
+            _lib.DTYPE_BF16, _lib.DTYPE_F32, _lib.DTYPE_F32, inp.scale, flags, None, None]
+    if entry == "gdn_chunk_fwd":
+        nbytes = int(_lib.load().gdn_chunk_workspace_size(b, t, hv, n, int(d.cu_seqlens is not None)))
+        ws = torch.full((max(nbytes, 1),), 0x7F, dtype=torch.uint8, device=DEV)
+        args += [_lib.ptr(ws), nbytes]
+    _lib.call(entry, *args, _lib.stream_of(o))
+    torch.cuda.synchronize()
+    return o.cpu(), final.cpu()
+
+
+def _same(inp):
+    o1, s1 = _run("gdn_chunk_fwd", inp)
+    o2, s2 = _run("gdn_chunk_fwd_noalloc", inp)
+    assert torch.equal(o1, o2), "outputs differ"
+    assert torch.equal(s1, s2), "final states differ"
+
+
+def test_noalloc_matches_workspace_entry_twice_then_smaller():
+    print("noalloc: config-1 shape, then a smaller call", flush=True)
+    _same(gdn_inputs(4, 4096, 16, 128, dtype=torch.bfloat16, seed=1001, h0=True))
+    _same(gdn_inputs(2, 300, 4, 64, V=128, HV=8, dtype=torch.bfloat16, seed=5, h0=True))
+
+
+def test_noalloc_matches_workspace_entry_varlen():
+    print("noalloc: varlen", flush=True)
+    cu = torch.tensor([0, 1, 70, 200, 777, 1024])
+    _same(gdn_inputs(1, 1024, 2, 128, HV=4, dtype=torch.bfloat16, seed=9, h0=True, cu_seqlens=cu))
+
+
+def test_noalloc_rejects_sizes_beyond_its_array():
+    cap = int(_lib.load().gdn_chunk_fwd_noalloc_max_workspace())
+    tokens = cap // (16 * 128) + 64  # more token-heads than the array holds at HV = 16
+    p = 1 << 20  # never dereferenced: the size check fails before anything is launched
+    with pytest.raises(ValueError, match="scratch array"):
+        _lib.call("gdn_chunk_fwd_noalloc", p, p, p, p, p, None, p, None, None, 1, tokens, 16, 16, 128, 128, 1,
+                  _lib.DTYPE_BF16, _lib.DTYPE_F32, _lib.DTYPE_F32, 0.088, 0, None, None, None)
