@@ -20,7 +20,10 @@
 //   conversion) and the scaled P of the next chunk. Waves 4 and 5, which share SIMDs 0 and 1 with
 //   the state waves, copy the T - I rows and the V slice, scan the gates (wave 4) and store O of
 //   the previous chunk.
-// One barrier per chunk separates the two sides.
+// One barrier per chunk separates the two sides. Each role runs its own chunk loop (the barrier counts
+// match), so a role's loop-carried registers (the helpers' loads in flight for the next step, the
+// state waves' accumulators) do not share one register allocation; the state loop is unrolled by six
+// so that every LDS slot index is a compile-time constant.
 //
 // Fragment layouts (16x16x32 MFMA, lane (g, i), element r = 0..3 of an accumulator):
 //   S tile a = 2s + h (s = 32-deep key step): row 4g + r is key 32s + 8g + 4h + r, so the pair
@@ -333,6 +336,12 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
                                             (int)(off + (32 * (a >> 1) + 4 * (a & 1)) * 2), 0, 0);
   };
   // K row fragments of Y = K S for chunk c, key steps s < KSH (row tile b), read ahead
+  auto load_kf_slot = [&](const f16* kb) {
+#pragma unroll
+    for (int s = 0; s < KSH; ++s)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) KF[4 * s + b] = __builtin_bit_cast(f32x4, ld8h(kb + (16 * b + li) * KP + kq_col(s, li, g4)));
+  };
   auto load_kf = [&](int c) {
     const f16* kb = Kc[c % 3];
 #pragma unroll
@@ -353,6 +362,10 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
     reinterpret_cast<f16x8*>(Pb[0])[e] = f16x8{};
     reinterpret_cast<f16x8*>(Pb[1])[e] = f16x8{};
   }
+  // Each role runs its own prologue and chunk loop; every loop runs nc steps with one barrier each,
+  // so the barriers line up. Separate loops keep each role's loop-carried registers out of the
+  // others' register allocation: the helpers hold the global loads of the next step's tiles across
+  // the barrier, a full step of latency hiding.
   if (w < 2) {
 #pragma unroll
     for (int a = 0; a < KT; ++a) {
@@ -364,30 +377,8 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
     if constexpr (SAVE) {
       if (nc > 0) save_state(0);
     }
-  } else if (qk_wave) {  // K/Q of chunks 0 and 1
-    bf16x8 pk[QKPT], pq[QKPT];
-    for (int c = 0; c < 2; ++c) {
-      fetch_rows(pk, kg, c, thq);
-      fetch_rows(pq, qg, c, thq);
-      stage_rows(pk, Kc[c], thq);
-      stage_rows(pq, Qc[c], thq);
-    }
-  } else {  // T/V of chunk 0, gates of chunks 0 and 1
-    bf16x8 pt[4], pv[2];
-    fetch_tv(pt, pv, 0, thv);
-    stage_tv(pt, pv, 0, thv);
-    if (w == 4) {
-      for (int c = 0; c < 2; ++c) {
-        GateBits gb0;
-        fetch_gates(c, gb0);
-        stage_gates(c, gb0);
-      }
-      fetch_gates(2, ngate);
-    }
-  }
-  __syncthreads();
-  if (nc > 0) {
-    if (w < 2) {
+    __syncthreads();
+    if (nc > 0) {
       f16x8 qf[KS][4];
 #pragma unroll
       for (int s2 = 0; s2 < KS; ++s2)
@@ -401,24 +392,19 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
       for (int s2 = 0; s2 < KS; ++s2)
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb) Zt[tb] = mmah(sb(s2), qf[s2][tb], Zt[tb]);
-    } else {
-      run_p_side(0, lane);
     }
-  }
-  __syncthreads();
-
-  // ------------------------------------------------------------------ chunk loop
-  // Slots in use during step i: state waves read K_i, T_i, V_i, P_i, gates_i and Q_{i+1}, write
-  // O_i; helpers read K_{i+1}, Q_{i+1}, gates_{i+1} (P_{i+1}) and O_{i-1}, write K_{i+2}, Q_{i+2},
-  // T_{i+1}, V_{i+1}, P_{i+1}, gates_{i+2}. No slot is written and read in the same step.
-  for (int i = 0; i < nc; ++i) {
-    if (w < 2) {
-      const f16* kb = Kc[i % 3];
-      const f16* tp = Tb[i & 1];
-      const bf16* vp = Vc[i & 1];
-      const f16* pp = Pb[i & 1];
-      bf16* op = Ob[i & 1];
-      const ChunkGates& G = gv[i % 3];
+    __syncthreads();
+    // Slots in use during step i: state waves read K_i, T_i, V_i, P_i, gates_i and Q_{i+1}, write
+    // O_i; helpers read K_{i+1}, Q_{i+1}, gates_{i+1} (P_{i+1}) and O_{i-1}, write K_{i+2}, Q_{i+2},
+    // T_{i+1}, V_{i+1}, P_{i+1}, gates_{i+2}. No slot is written and read in the same step.
+    auto step = [&](auto ph_c, int i) {
+      constexpr int PH = decltype(ph_c)::value;
+      const f16* kb = Kc[PH % 3];
+      const f16* tp = Tb[PH & 1];
+      const bf16* vp = Vc[PH & 1];
+      const f16* pp = Pb[PH & 1];
+      bf16* op = Ob[PH & 1];
+      const ChunkGates& G = gv[PH % 3];
 
       // The chain S -> Y -> X -> Delta -> Delta~ -> S' runs through phases 1-5; the rest is placed
       // where it overlaps the chain's MFMAs: the e^{gam_c} scaling of S under Y, and O of this chunk
@@ -524,7 +510,7 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
       // ---- 5: Q reads of the next chunk; S in fp16
       f16x8 qf[KS][4];
       {
-        const f16* qb = Qc[(i + 1) & 1];
+        const f16* qb = Qc[(PH + 1) & 1];
 #pragma unroll
         for (int s2 = 0; s2 < KS; ++s2)
 #pragma unroll
@@ -534,8 +520,8 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
       phase();
       // ---- 6: K reads for the next Y and its e^{gam_c}; O^T = scale e^gam Z^T + Delta^T (scale P)^T
       //      -> Ob[token][column]; Z^T = S^T Q^T of the next chunk
-      load_kf(i + 1);
-      ec_next = __expf(gv[(i + 1) % 3].gam[kC - 1]);
+      load_kf_slot(Kc[(PH + 1) % 3]);
+      ec_next = __expf(gv[(PH + 1) % 3].gam[kC - 1]);
       phase();
 #pragma unroll
       for (int tb = 0; tb < 4; ++tb) {
@@ -555,36 +541,76 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
         // from the helpers' load burst at its start
         if (i + 1 < nc) save_state(i + 1);
       }
-    } else if (qk_wave) {  // K/Q of chunk i+2 (loads first, P of chunk i+1 while they land)
+      __syncthreads();
+    };
+    // unrolled by 6 so that every slot index (mod 2 and mod 3) is a constant
+    for (int i = 0; i < nc; i += 6) {
+      step(std::integral_constant<int, 0>{}, i);
+      if (i + 1 < nc) step(std::integral_constant<int, 1>{}, i + 1);
+      if (i + 2 < nc) step(std::integral_constant<int, 2>{}, i + 2);
+      if (i + 3 < nc) step(std::integral_constant<int, 3>{}, i + 3);
+      if (i + 4 < nc) step(std::integral_constant<int, 4>{}, i + 4);
+      if (i + 5 < nc) step(std::integral_constant<int, 5>{}, i + 5);
+    }
+    if (p.ht) {
+#pragma unroll
+      for (int a = 0; a < KT; ++a) {
+        const int kd0 = 32 * (a >> 1) + 8 * g4 + 4 * (a & 1);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) p.ht[sbase + (int64_t)(kd0 + r) * VD + li] = S[a][r];
+      }
+    }
+  } else if (qk_wave) {
+    // K/Q of chunks 0 and 1 staged, chunk 2 in flight
+    bf16x8 pk[QKPT], pq[QKPT];
+    for (int c = 0; c < 2; ++c) {
+      fetch_rows(pk, kg, c, thq);
+      fetch_rows(pq, qg, c, thq);
+      stage_rows(pk, Kc[c], thq);
+      stage_rows(pq, Qc[c], thq);
+    }
+    fetch_rows(pk, kg, 2, thq);
+    fetch_rows(pq, qg, 2, thq);
+    __syncthreads();
+    if (nc > 0) run_p_side(0, lane);
+    __syncthreads();
+    for (int i = 0; i < nc; ++i) {  // P of chunk i+1, K/Q of chunk i+2 (loaded a step ago) into LDS, loads of chunk i+3
       const int tq = thq_of(opaque_int(lane));
-      bf16x8 pk[QKPT], pq[QKPT];
-      fetch_rows(pk, kg, i + 2, tq);
-      fetch_rows(pq, qg, i + 2, tq);
       if (i + 1 < nc) run_p_side(i + 1, opaque_int(lane));
       stage_rows(pk, Kc[(i + 2) % 3], tq);
       stage_rows(pq, Qc[i & 1], tq);
-    } else {  // T/V of chunk i+1, gates of chunk i+2, O of chunk i-1 out
+      fetch_rows(pk, kg, i + 3, tq);
+      fetch_rows(pq, qg, i + 3, tq);
+      __syncthreads();
+    }
+  } else {
+    // T/V of chunk 0 staged and chunk 1 in flight; gates of chunks 0 and 1 staged, chunk 2 in flight
+    bf16x8 pt[4], pv[2];
+    fetch_tv(pt, pv, 0, thv);
+    stage_tv(pt, pv, 0, thv);
+    fetch_tv(pt, pv, 1, thv);
+    if (w == 4) {
+      for (int c = 0; c < 2; ++c) {
+        GateBits gb0;
+        fetch_gates(c, gb0);
+        stage_gates(c, gb0);
+      }
+      fetch_gates(2, ngate);
+    }
+    __syncthreads();
+    __syncthreads();
+    for (int i = 0; i < nc; ++i) {  // gates of chunk i+2, O of chunk i-1 out, T/V of chunk i+1 into LDS, loads of chunk i+2
       const int tq = thv_of(opaque_int(lane));
-      bf16x8 pt[4], pv[2];
-      fetch_tv(pt, pv, i + 1, tq);
       if (w == 4) {  // gates of chunk i+2 (loaded a step ago), then the loads for chunk i+3
         stage_gates(i + 2, ngate);
         fetch_gates(i + 3, ngate);
       }
       if (i > 0) store_o(i - 1, tq);
       stage_tv(pt, pv, (i + 1) & 1, tq);
+      fetch_tv(pt, pv, i + 2, tq);
+      __syncthreads();
     }
-    __syncthreads();
-  }
-  if (w >= 4 && !qk_wave && nc > 0) store_o(nc - 1, thv);
-
-  if (p.ht && w < 2) {
-#pragma unroll
-    for (int a = 0; a < KT; ++a) {
-      const int kd0 = 32 * (a >> 1) + 8 * g4 + 4 * (a & 1);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) p.ht[sbase + (int64_t)(kd0 + r) * VD + li] = S[a][r];
-    }
+    if (nc > 0) store_o(nc - 1, thv);
   }
 }
 

@@ -203,9 +203,9 @@ def state_kernel(s: Shape, eg: int, eb: int, save: bool) -> int:
     kch = K // 8
     qkpt = C * kch // 256
     done = 0
-    # q/k rows of chunks c < nc + 2 (fetch_rows: thread tq of the q/k waves, 16-byte piece tq % KCH of
-    # rows tq / KCH + (256 / KCH) u)
-    c0, ln, cg, nn = chunk_rows(s, extra=2)
+    # q/k rows of chunks c < nc + 3 (fetch_rows, one step ahead of the staging: thread tq of the q/k
+    # waves, 16-byte piece tq % KCH of rows tq / KCH + (256 / KCH) u)
+    c0, ln, cg, nn = chunk_rows(s, extra=3)
     h = np.arange(H)
     qk_row = H * K * 2
     tq = np.arange(256)
@@ -213,8 +213,9 @@ def state_kernel(s: Shape, eg: int, eb: int, save: bool) -> int:
     base = (_col(c0) * H + _mid(h)) * K * 2
     for name in ("q", "k"):
         done += check(f"fwd {name} rows", s.tokens * H * K * 2, base, _col(ln) * qk_row, _last(off.ravel()), 16)
-    # T - I rows and the V slice of chunks c < nc + 1 (fetch_tv: threads tq < 128 of waves 4, 5)
-    c0, ln, cg, nn = chunk_rows(s, extra=1)
+    # T - I rows and the V slice of chunks c < nc + 2 (fetch_tv, one step ahead of the staging:
+    # threads tq < 128 of waves 4, 5)
+    c0, ln, cg, nn = chunk_rows(s, extra=2)
     t_row, v_row = HV * C * 2, HV * V * 2
     tq = np.arange(128)
     off_t = ((tq >> 3) * t_row + (tq & 7) * 16)[:, None] + (np.arange(4) * 16 * t_row)[None, :]
