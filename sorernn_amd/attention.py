@@ -188,11 +188,13 @@ class GatedAttention(nn.Module):
             raise ValueError(f"cu_seqlens requires B == 1 (packed [1, N] layout); got B={b}")
         _no_grad_check("GatedAttention", x, *self.parameters())
         hq, hkv, dh = self.heads, self.kv_heads, self.head_dim
-        # under autocast the projections run in the autocast dtype, as nn.Linear's would
+        # under autocast the projections run in the autocast dtype with the input cast to it, as
+        # nn.Linear's would (the reference feeds its fp32 residual stream into the mixers under
+        # autocast); without autocast the input is cast to the weights' dtype
         dt = torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda") else self.q_proj.weight.dtype
-        if x.dtype != dt:
-            raise ValueError(f"GatedAttention: activations ({x.dtype}) and projections ({dt}) must share a dtype")
-        proj = F.linear(x, self._fused_weight(dt))  # [B, T, q | gate | k | v]
+        if dt not in (torch.bfloat16, torch.float16):
+            raise NotImplementedError(f"GatedAttention: the gfx950 kernels take bf16/fp16 activations, got {dt}")
+        proj = F.linear(x.to(dt), self._fused_weight(dt))  # [B, T, q | gate | k | v]
         nq, nkv = hq * dh, hkv * dh
         q_in, gate = proj[..., :nq], proj[..., nq:2 * nq]
         k_in, v = proj[..., 2 * nq:2 * nq + nkv], proj[..., 2 * nq + nkv:]

@@ -501,7 +501,8 @@ __global__ __launch_bounds__(256, 2) void gated_delta_chunk_bwd_grad_kernel(Chun
   __shared__ __align__(16) bf16 Kb[kC * KPB], Qb[kC * KPB];
   __shared__ __align__(16) bf16 big[kBig];
   __shared__ __align__(16) ChunkGates gs;
-  __shared__ float tb_[kC], tg_[kC], red_[2];
+  // per-token row/column sums, one row per wave, added in wave order (deterministic, no atomics)
+  __shared__ float tb_[4][kC], tg_[4][kC], red_[4][2];
   bf16* const SbT = big;             // S^T of the pass: [32 value columns][KD keys]
   bf16* const dSbT = big + kSB;      // dS'^T of the pass
   bf16* const dOb = big + 2 * kSB;   // [64 tokens][32 value columns]
@@ -561,10 +562,13 @@ __global__ __launch_bounds__(256, 2) void gated_delta_chunk_bwd_grad_kernel(Chun
     uint32_t graw = 0, braw = 0;
     if (w == 0) fetch_gates_bwd(graw, braw, p, c0, hv, len, lane);
     if (t < kC) {
-      tb_[t] = 0.f;
-      tg_[t] = 0.f;
+#pragma unroll
+      for (int x = 0; x < 4; ++x) {
+        tb_[x][t] = 0.f;
+        tg_[x][t] = 0.f;
+      }
     }
-    if (t < 2) red_[t] = 0.f;
+    if (t < 8) red_[t >> 1][t & 1] = 0.f;
     if (w == 0) put_gates_bwd(gs, graw, braw, p, hv, len, lane);
 
     f32x4 dA[4], dP[4];
@@ -723,7 +727,7 @@ __global__ __launch_bounds__(256, 2) void gated_delta_chunk_bwd_grad_kernel(Chun
 
     // e^{gam_c} <S, dS'> and sum_t r_t (K dS')_t . Delta_t go to the chunk's last position
     sdot = wave_xor_sum(sdot, 1);
-    if (lane == 0) atomicAdd(&red_[0], sdot);
+    if (lane == 0) red_[w][0] = sdot;
     __syncthreads();  // the passes are done with the LDS tiles: dG and dQK go over them
     // c x c elementwise: G = K K^T, QK = Q K^T; dA, dG, dQK; their row and column sums
 #pragma unroll
@@ -758,7 +762,7 @@ __global__ __launch_bounds__(256, 2) void gated_delta_chunk_bwd_grad_kernel(Chun
       put_acc(cc2, kCPb, tok0, 16 * jt, ln, dQK);
       colp += __shfl_xor(colp, 16, kWave);
       colp += __shfl_xor(colp, 32, kWave);
-      if ((ln >> 4) == 0 && jt <= w) atomicAdd(&tg_[jj], -colp);
+      if ((ln >> 4) == 0 && jt <= w) tg_[w][jj] -= colp;
       __builtin_amdgcn_sched_barrier(0);  // one c x c tile at a time
     }
     float rsum = 0.f;
@@ -767,13 +771,13 @@ __global__ __launch_bounds__(256, 2) void gated_delta_chunk_bwd_grad_kernel(Chun
       const float b = group_sum<16>(pb[r]), gg = group_sum<16>(pg[r]), rr2 = group_sum<16>(pr[r]);
       if (li == 0) {
         const int tok = tok0 + 4 * g4 + r;
-        atomicAdd(&tb_[tok], b);
-        atomicAdd(&tg_[tok], gg - rr2);
+        tb_[w][tok] += b;
+        tg_[w][tok] += gg - rr2;
         rsum += rr2;
       }
     }
     rsum = wave_xor_sum(rsum, 1);
-    if (lane == 0) atomicAdd(&red_[1], rsum);
+    if (lane == 0) red_[w][1] = rsum;
     __syncthreads();
     // dQ += dQK K;  dK += dQK^T Q + dG K + dG^T K
 #pragma unroll
@@ -792,12 +796,16 @@ __global__ __launch_bounds__(256, 2) void gated_delta_chunk_bwd_grad_kernel(Chun
     // dg = reverse in-chunk cumsum of dgam; dbeta; the gate and sigmoid backwards
     if (w == 0) {
       const float ac = gs.egam[kC - 1];
-      float dgam = tg_[lane];
-      if (lane == kC - 1) dgam += ac * red_[0] + red_[1];
+      float dgam = ((tg_[0][lane] + tg_[1][lane]) + tg_[2][lane]) + tg_[3][lane];
+      if (lane == kC - 1) {
+        const float r0 = ((red_[0][0] + red_[1][0]) + red_[2][0]) + red_[3][0];
+        const float r1 = ((red_[0][1] + red_[1][1]) + red_[2][1]) + red_[3][1];
+        dgam += ac * r0 + r1;
+      }
       const float incl = wave_inclusive_sum(dgam);
       const float tot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(incl), kWave - 1));
       float dgv = tot - incl + dgam;
-      float dbv = tb_[lane];
+      float dbv = ((tb_[0][lane] + tb_[1][lane]) + tb_[2][lane]) + tb_[3][lane];
       const int64_t gi = (c0 + lane) * p.HV + hv;
       float pa = 0.f, pd = 0.f;
       if (lane < len) {

@@ -192,3 +192,20 @@ def test_gated_attention_layer_raises_on_grad():
     x = _randn(1, 16, 256, seed=1).to(DEV)
     with pytest.raises(NotImplementedError):
         layer(x)
+
+
+@pytest.mark.gpu
+def test_gated_attention_layer_fp32_stream_under_autocast():
+    """The reference runs its mixers on the fp32 residual stream under autocast(bf16)
+    (sore/train/trainer.py:175-176): fp32 parameters and fp32 x go in, the projections run in bf16 on
+    the input cast to bf16, as nn.Linear's would. Checked against the oracle's bf16 composition."""
+    layer = _layer(512, 8, 2, 128, 0.25, 1e6, seed=7)  # fp32 parameters
+    g = torch.Generator().manual_seed(41)
+    x = torch.randn(2, 160, 512, generator=g)  # fp32 activations
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        out = layer.to(DEV)(x.to(DEV)).float().cpu()
+    w = {n: p.detach().cpu() for n, p in layer.state_dict().items()}
+    ref = gated_attention_layer(x.to(torch.bfloat16), w, 8, 2, 128, layer.rotary.rot_dim, 1e6)
+    rel = ((out.double() - ref.double()).norm() / ref.double().norm()).item()
+    assert rel <= 2e-2, f"layer output relative L2 {rel:.3e}"
+    assert_output_close(out.to(torch.bfloat16), ref.float())

@@ -45,10 +45,17 @@ def _run(layer, x, cu=None):
         return layer(x.to(DEV), cu_seqlens=cu_dev, cu_seqlens_cpu=cu).float().cpu()
 
 
+# the reference's options matrix (tests/model/test_gdn.py:104-162): GVA 1 and 2, documents of 1-3
+# tokens and one document over the whole window, plus plain batch rows
+_CU_CASES = {"rows": None, "short_docs": [0, 1, 3, 4, 70, 200, 512], "one_doc": [0, 512]}
+
+
 @pytest.mark.parametrize("kernel_gate", [True, False], ids=["kernel_gate", "torch_gate"])
-@pytest.mark.parametrize("cu", [None, [0, 1, 3, 4, 70, 200, 512]], ids=["rows", "short_docs"])
-def test_layer_matches_oracle(kernel_gate, cu):
-    layer = _layer(kernel_gate)
+@pytest.mark.parametrize("cu_case", sorted(_CU_CASES))
+@pytest.mark.parametrize("rep", [1, 2], ids=["no_gva", "gva2x"])
+def test_layer_matches_oracle(kernel_gate, cu_case, rep):
+    cu = _CU_CASES[cu_case]
+    layer = _layer(kernel_gate, rep=rep)
     b = 2 if cu is None else 1
     x = torch.randn(b, 512, 256, generator=torch.Generator().manual_seed(2))
     cu_t = None if cu is None else torch.tensor(cu)
@@ -125,3 +132,47 @@ def test_inference_route_matches_reference_route(kernel_gate, cu):
         ref = layer._forward_reference(x, cu_seqlens=cu_dev, cu_seqlens_cpu=cu_t).float()
     rel = ((fused - ref).norm() / ref.norm()).item()
     assert rel <= 1e-2, f"relative L2 {rel:.3e}"
+
+
+def test_layer_extreme_inputs_stay_finite():
+    """x100 inputs (reference tests/model/test_gdn.py:60-71) through the bf16 layer: output and input
+    gradient finite, with packed documents."""
+    torch.manual_seed(0)
+    cfg = GDNLayerConfig(d_model=128, gdn_qk_heads=2, gdn_v_heads=4, gdn_head_dim=64, gdn_kernel_gate=True)
+    layer = GatedDeltaNet(cfg).to(DEV)
+    x = (torch.randn(1, 64, 128, generator=torch.Generator().manual_seed(6)) * 100).to(DEV).requires_grad_(True)
+    cu = torch.tensor([0, 30, 64])
+    with torch.autocast("cuda", dtype=BF16):
+        out = layer(x, cu_seqlens=cu.to(DEV), cu_seqlens_cpu=cu)
+    assert torch.isfinite(out).all()
+    out.float().square().mean().backward()
+    torch.cuda.synchronize()
+    assert torch.isfinite(x.grad).all()
+
+
+def test_layer_cu_seqlens_cpu_is_exact():
+    """cu_seqlens_cpu only saves reading cu_seqlens back on the host: the same values reach the same
+    kernels, so output and gradients are bitwise equal with and without it (reference
+    tests/model/test_lm.py:339-361); two runs without it are first shown bitwise equal."""
+    cu = torch.tensor([0, 1, 3, 4, 70, 200, 300])
+    gen = torch.Generator().manual_seed(8)
+    x = torch.randn(1, 300, 128, generator=gen)
+    cot = torch.randn(1, 300, 128, generator=gen)
+
+    def run(with_cpu):
+        torch.manual_seed(0)
+        cfg = GDNLayerConfig(d_model=128, gdn_qk_heads=2, gdn_v_heads=4, gdn_head_dim=64, gdn_kernel_gate=True)
+        layer = GatedDeltaNet(cfg).to(DEV)
+        xd = x.to(DEV).requires_grad_(True)
+        with torch.autocast("cuda", dtype=BF16):
+            out = layer(xd, cu_seqlens=cu.to(DEV), cu_seqlens_cpu=cu if with_cpu else None)
+        (out.float() * cot.to(DEV)).sum().backward()
+        torch.cuda.synchronize()
+        return out.detach(), xd.grad, {n: p.grad for n, p in layer.named_parameters()}
+
+    a, b, c = run(False), run(False), run(True)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1]) and all(torch.equal(a[2][n], b[2][n]) for n in a[2]), \
+        "two identical runs differ: the bitwise comparison below would prove nothing"
+    assert torch.equal(c[0], a[0]) and torch.equal(c[1], a[1])
+    for n in a[2]:
+        assert torch.equal(c[2][n], a[2][n]), n

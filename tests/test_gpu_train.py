@@ -123,15 +123,23 @@ def _oracle_layer_loss(layer, x, cotangent, cu):
     return xr.grad, {n: v.grad for n, v in p.items()}
 
 
-@pytest.mark.parametrize("cu", [None, [0, 1, 3, 4, 70, 200, 256]], ids=["rows", "short_docs"])
-def test_layer_backward_matches_oracle(cu):
+# the reference's options matrix for gradients (tests/model/test_gdn.py:104-162): GVA 1 and 2 x
+# {documents of 1-3 tokens, one document over the window} x {in-kernel gate, torch gate}, plus rows
+_CU_CASES = {"rows": None, "short_docs": [0, 1, 3, 4, 70, 200, 512], "one_doc": [0, 512]}
+
+
+@pytest.mark.parametrize("kernel_gate", [True, False], ids=["kernel_gate", "torch_gate"])
+@pytest.mark.parametrize("cu_case", sorted(_CU_CASES))
+@pytest.mark.parametrize("rep", [1, 2], ids=["no_gva", "gva2x"])
+def test_layer_backward_matches_oracle(rep, cu_case, kernel_gate):
+    cu = _CU_CASES[cu_case]
     torch.manual_seed(0)
-    cfg = GDNLayerConfig(d_model=128, gdn_qk_heads=2, gdn_v_heads=4, gdn_head_dim=64, gdn_kernel_gate=True)
+    cfg = GDNLayerConfig(d_model=128, gdn_qk_heads=2, gdn_v_heads=2 * rep, gdn_head_dim=64, gdn_kernel_gate=kernel_gate)
     layer = GatedDeltaNet(cfg)
     gen = torch.Generator().manual_seed(2)
     b = 2 if cu is None else 1
-    x = torch.randn(b, 256, 128, generator=gen)
-    cot = torch.randn(b, 256, 128, generator=gen)
+    x = torch.randn(b, 512, 128, generator=gen)
+    cot = torch.randn(b, 512, 128, generator=gen)
     cu_t = None if cu is None else torch.tensor(cu)
     gx_ref, gp_ref = _oracle_layer_loss(layer, x, cot, cu_t)
     layer = layer.to(DEV)

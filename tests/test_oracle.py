@@ -349,6 +349,25 @@ def test_rms_norm_formula():
     assert rms_norm(x.bfloat16(), torch.ones(16)).dtype == torch.bfloat16
 
 
+def test_rms_norm_weight_known_values():
+    """A row with a hand-computable RMS and a non-trivial weight: x = [3, 4, 0, 0] has mean(x^2) = 6.25,
+    so with eps = 0 the normalised row is x / 2.5 = [1.2, 1.6, 0, 0], scaled elementwise by the weight;
+    scaling x by any c > 0 leaves the output unchanged (eps = 0); a weight applied before the RMS (a
+    planted mistake) would change mean(x^2) and is caught."""
+    x = torch.tensor([[3.0, 4.0, 0.0, 0.0]], dtype=torch.float64)
+    w = torch.tensor([2.0, -0.5, 7.0, 1.0], dtype=torch.float64)
+    expected = torch.tensor([[2.4, -0.8, 0.0, 0.0]], dtype=torch.float64)
+    torch.testing.assert_close(rms_norm(x, w, 0.0), expected, atol=1e-15, rtol=0)
+    torch.testing.assert_close(rms_norm(37.5 * x, w, 0.0), expected, atol=1e-14, rtol=0)
+    wrong = (x * w) * torch.rsqrt((x * w).pow(2).mean(-1, keepdim=True))
+    assert (wrong - expected).abs().max() > 0.1
+    # the gated form on the same row: silu(0) = 0; silu(40) = 40 sigmoid(40) = 40 to 1e-17 relative
+    gate = torch.tensor([[0.0, 40.0, 1.0, 40.0]], dtype=torch.float64)
+    got = rms_norm_gated(x, gate, w, 0.0)
+    torch.testing.assert_close(got[0, 0], torch.tensor(0.0, dtype=torch.float64))
+    torch.testing.assert_close(got[0, 1], torch.tensor(-0.8 * 40, dtype=torch.float64), atol=0, rtol=1e-14)
+
+
 def test_rms_norm_gated_equals_norm_times_silu():
     gen = torch.Generator().manual_seed(4)
     x = torch.randn(4, 3, 32, generator=gen, dtype=torch.float64)
