@@ -16,6 +16,9 @@ The same line carries
   update, state updated in place) with HBM bytes/step = 141,664,256, plus a run rotating over
   5 state copies (335 MB > the 256 MB Infinity Cache) that forces DRAM traffic;
 - ``varlen``: config 3 (8 packed documents, 32768 tokens);
+- ``varlen_docs``: the reference model's call (zero initial state, no final state) on its real
+  document-length distribution: 8 windows of 4096 tokens filled from the reference's corpus sample
+  (``tests/golden/doc_lengths_pt.json``, drawn as the reference's bench ``--doc-lengths`` does);
 - ``train``: config 1 under autograd -- the training forward (which also saves the bf16 state
   entering every chunk) and the backward (dq, dk, dv, dg, dbeta, dh0), timed separately with HIP
   events; backward algorithmic FLOPs = (22 C^2 d + 14 C d^2) per (chunk, head);
@@ -33,6 +36,7 @@ workload ends the bench with its status. ``--only NAME`` runs one workload for p
 from __future__ import annotations
 
 import argparse
+import itertools
 import json
 import os
 import platform
@@ -329,7 +333,13 @@ def run_only(torch, args) -> int:
         tf, tb = train_step_times(torch, config_inputs(1).to("cuda"), args.steps)
         print(f"ran train: {args.steps} steps, forward {tf:.3f} ms, backward {tb:.3f} ms", flush=True)
         return 0
-    if args.only in ("prefill", "varlen"):
+    if args.only == "varlen_docs":
+        _, cu_cpu, inp = varlen_docs_inputs(torch)
+        d = inp.to("cuda")
+        for _ in range(args.warmup + args.steps):
+            chunk_gated_delta_rule(d.q, d.k, d.v, d.g, d.beta, scale=inp.scale, cu_seqlens=d.cu_seqlens,
+                                   cu_seqlens_cpu=cu_cpu)
+    elif args.only in ("prefill", "varlen"):
         idx = 1 if args.only == "prefill" else 3
         inp = config_inputs(idx)
         cu_cpu = inp.cu_seqlens
@@ -347,7 +357,25 @@ def run_only(torch, args) -> int:
     return 0
 
 
-PARTS = ("prefill", "decode", "varlen", "train", "block_pair")
+PARTS = ("prefill", "decode", "varlen", "varlen_docs", "train", "block_pair")
+DOC_LENGTHS = os.path.join(ROOT, "tests", "golden", "doc_lengths_pt.json")
+
+
+def doc_length_windows() -> list[list[int]]:
+    """Document lengths of the real-distribution leg: 8 windows of 4,096 tokens filled with lengths
+    drawn from the reference's Portuguese-corpus sample (data/sample_pt/doc_lengths.json, sampled by
+    tests/golden/make_doc_lengths.py as the reference's bench --doc-lengths does)."""
+    with open(DOC_LENGTHS) as f:
+        return json.load(f)["windows"]
+
+
+def varlen_docs_inputs(torch):
+    """Lengths, host cu_seqlens and seeded inputs of the real-distribution leg (one packed batch row)."""
+    from sorernn_amd.synthetic import gdn_inputs
+
+    lens = [n for w in doc_length_windows() for n in w]
+    cu = torch.tensor([0] + list(itertools.accumulate(lens)), dtype=torch.long)
+    return lens, cu, gdn_inputs(1, int(cu[-1]), 16, 128, dtype=torch.bfloat16, seed=1005, h0=False, cu_seqlens=cu)
 
 
 def part_prefill(torch, args) -> dict:
@@ -450,6 +478,28 @@ def part_varlen(torch, args) -> dict:
     return {"ms_step": v_ms, "ms_launch": v_launch, "pct": v_pct, "lens": (cu_cpu[1:] - cu_cpu[:-1]).tolist()}
 
 
+def part_varlen_docs(torch, args) -> dict:
+    """The reference model's call on its real document-length distribution: 8 windows of 4,096 tokens
+    packed into one batch row (53 documents, lengths from the committed fixture), H=16, d=128, bf16
+    q/k/v, fp32 g/beta as in config 1, zero initial state and no final state (sore/model/gdn.py:166-169
+    discards it)."""
+    from sorernn_amd import chunk_gated_delta_rule
+
+    lens, cu, inp = varlen_docs_inputs(torch)
+    d = inp.to("cuda")
+
+    def step():
+        return chunk_gated_delta_rule(d.q, d.k, d.v, d.g, d.beta, scale=inp.scale, cu_seqlens=d.cu_seqlens,
+                                      cu_seqlens_cpu=cu)
+
+    for _ in range(3):
+        step()
+    n = max(5, args.steps // 5)
+    ms, launch = time_launches(torch, step, n)
+    pct = launch_percentiles(torch, lambda i: step(), n)
+    return {"ms_step": ms, "ms_launch": launch, "pct": pct, "lens": lens}
+
+
 def part_train(torch, args) -> dict:
     """Config 1 under autograd: the training forward and the backward, timed separately."""
     from sorernn_amd.synthetic import config_inputs
@@ -463,8 +513,25 @@ def part_block_pair(torch, args) -> dict:
     return block_pair(torch, max(5, args.steps // 5))
 
 
-PART_FNS = {"prefill": part_prefill, "decode": part_decode, "varlen": part_varlen, "train": part_train,
-            "block_pair": part_block_pair}
+PART_FNS = {"prefill": part_prefill, "decode": part_decode, "varlen": part_varlen, "varlen_docs": part_varlen_docs,
+            "train": part_train, "block_pair": part_block_pair}
+
+
+def varlen_docs_entry(vd: dict) -> dict:
+    lens = vd["lens"]
+    fl = chunk_flops(lens, 16, 128)
+    srt = sorted(lens)
+    return {
+        "workload": f"reference document-length distribution: 8 windows of 4096 tokens, {len(lens)} packed docs "
+                    f"(median {srt[len(srt) // 2]}, max {srt[-1]}; tests/golden/doc_lengths_pt.json), H=16, d=128, "
+                    "zero h0, no final state",
+        "tokens_per_s": round(sum(lens) / (vd["ms_step"] * 1e-3), 1),
+        "ms_per_launch": round(vd["ms_launch"], 4),
+        "launch_percentiles": vd["pct"],
+        "tflops": round(fl / (vd["ms_launch"] * 1e-3) / 1e12, 2),
+        "frac_mfma_peak": round(fl / (vd["ms_launch"] * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+        "longest_doc_chunks": -(-srt[-1] // C),
+    }
 
 
 def assemble(parts: dict, args, cpu: dict | None) -> dict:
@@ -545,6 +612,7 @@ def assemble(parts: dict, args, cpu: dict | None) -> dict:
             "tflops": round(v_flops / (vl["ms_launch"] * 1e-3) / 1e12, 2),
             "frac_mfma_peak": round(v_flops / (vl["ms_launch"] * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
         },
+        "varlen_docs": varlen_docs_entry(parts["varlen_docs"]),
         "train": {
             "workload": "config1 under autograd: training forward (saves bf16 per-chunk states) + backward "
                         "(dq, dk, dv, dg, dbeta, dh0) of chunk_gated_delta_rule",
@@ -590,7 +658,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 256 MiB device copy (the reference kernel for PMC byte counters)")
-    ap.add_argument("--only", choices=["prefill", "decode", "varlen", "train", "block_pair"], default=None,
+    ap.add_argument("--only", choices=list(PARTS), default=None,
                     help="run one workload only (for profiler runs); prints no JSON line")
     ap.add_argument("--part", choices=PARTS, default=None,
                     help="(internal) run one workload and print its raw measurements as JSON")

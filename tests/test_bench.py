@@ -26,6 +26,7 @@ def _fake_parts():
                     "pct": pct, "pct_rot": pct, "min_bytes": 278921216},
         "decode": {"us_step": 25.0, "rot_us_step": 32.0, "eager_us_step": 40.0, "per_graph": 50},
         "varlen": {"ms_step": 0.4, "ms_launch": 0.39, "pct": pct, "lens": [4096] * 8},
+        "varlen_docs": {"ms_step": 0.5, "ms_launch": 0.49, "pct": pct, "lens": [100, 4000, 28668]},
         "train": {"fwd_ms": 0.28, "bwd_ms": 0.6},
         "block_pair": {"gdn_layer_ms": 1.0, "attn_layer_ms": 1.0},
     }
@@ -46,6 +47,19 @@ def test_assembled_line_keeps_the_driver_contract():
     assert rf["frac"] == pytest.approx(rf["achieved"] / bench.BF16_PEAK_TFLOPS, rel=1e-3)
     assert rf["flops_causal_halved"] == 36_507_222_016 and rf["flops_reference_flops_py"] == 17_179_869_184
     assert line["decode"]["frac_hbm_peak"] == pytest.approx(bench.decode_bytes() / 25e-6 / 8e12, rel=1e-3)
+    vd = line["varlen_docs"]
+    assert vd["tokens_per_s"] == pytest.approx(32768 / 0.5e-3, rel=1e-6) and vd["longest_doc_chunks"] == 448
+
+
+def test_doc_length_fixture_fills_every_window():
+    """The committed lengths of the real-distribution leg: 8 windows of exactly 4,096 tokens, every
+    document at least one token, drawn from a pool with the reference sample's statistics."""
+    windows = bench.doc_length_windows()
+    assert len(windows) == 8 and all(sum(w) == 4096 for w in windows)
+    assert all(n >= 1 for w in windows for n in w)
+    with open(bench.DOC_LENGTHS) as f:
+        rec = json.load(f)
+    assert rec["source_stats"]["n"] == 100_000 and rec["source_stats"]["median"] == 454.0
 
 
 def test_more_than_one_gpu_is_refused():
