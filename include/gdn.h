@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define GDN_ABI_VERSION 4
+#define GDN_ABI_VERSION 5
 
 #if defined(__GNUC__) || defined(__clang__)
 #define GDN_API __attribute__((visibility("default")))
@@ -117,6 +117,19 @@ GDN_API int gdn_chunk_fwd_noalloc(const void* q, const void* k, const void* v, c
 
 /* Bytes of the array gdn_chunk_fwd_noalloc uses as its workspace. */
 GDN_API size_t gdn_chunk_fwd_noalloc_max_workspace(void);
+
+/*
+ * Range flag of the chunked forward on `device`. After this call every gdn_chunk_fwd,
+ * gdn_chunk_fwd_train and gdn_chunk_fwd_noalloc launch on that device sets *flag to 1 (never back
+ * to 0) when it stores an o or final_state element that is inf or NaN. The forward's MFMA operands
+ * for S, X, Delta, T - I and scale * P are fp16 (largest finite value 65504); an operand past that
+ * range becomes inf and reaches o (and final_state), so a set flag means such an overflow or
+ * non-finite inputs. flag: pinned host memory (written with system scope, so the host can poll it
+ * without a device synchronisation) or memory of `device`; NULL turns the check off (the default).
+ * The caller clears the word. No counterpart in the reference: FLA's bf16 operands keep fp32's
+ * exponent range, so its chunk kernel has no such limit to report.
+ */
+GDN_API int gdn_set_range_flag(int device, unsigned* flag);
 
 /* Bytes of chunk_states for gdn_chunk_fwd_train / gdn_chunk_bwd (0 for invalid sizes). */
 GDN_API size_t gdn_chunk_states_size(int64_t B, int64_t T, int64_t HV, int64_t K, int64_t V, int64_t N, int varlen);

@@ -12,5 +12,6 @@ from sorernn_amd.ops import (  # noqa: F401
     l2norm,
     rms_norm_gated,
 )
+from sorernn_amd.range_guard import check_chunk_range, range_guard, set_range_guard  # noqa: F401
 
 __version__ = "0.1.0"

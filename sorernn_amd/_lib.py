@@ -14,13 +14,14 @@ import torch  # noqa: F401  (load torch's HIP runtime first)
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libgdn.so")
 
 GDN_OK = 0
+GDN_ERR_INVALID, GDN_ERR_UNSUPPORTED, GDN_ERR_HIP = 1, 2, 3
 DTYPE_F32, DTYPE_BF16, DTYPE_F16 = 0, 1, 2
 FLAG_QK_L2NORM = 0x1
 FLAG_BETA_SIGMOID = 0x2
 FLAG_GATE_IN_KERNEL = 0x4
 FLAG_CU_INT32 = 0x8
 ACT_NONE, ACT_SILU = 0, 1
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -38,6 +39,7 @@ SIGNATURES = {
     "gdn_chunk_fwd_train": [_P] * 9 + [_I64] * 7 + [_INT] * 3 + [_F, _U, _P, _P, _P, _P, _SZ, _P],
     "gdn_chunk_fwd_noalloc": [_P] * 9 + [_I64] * 7 + [_INT] * 3 + [_F, _U, _P, _P, _P],
     "gdn_chunk_fwd_noalloc_max_workspace": [],
+    "gdn_set_range_flag": [_INT, _P],
     "gdn_chunk_states_size": [_I64] * 6 + [_INT],
     "gdn_chunk_bwd": [_P] * 10 + [_I64] * 7 + [_INT] * 3 + [_F, _U] + [_P] * 11 + [_SZ, _P],
     "gdn_chunk_bwd_workspace_size": [_I64] * 6 + [_INT],

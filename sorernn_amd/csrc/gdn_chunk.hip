@@ -43,6 +43,7 @@
 //
 // LDS: K (3 slots), Q (2 slots), T - I, P, V and O (2 slots each), gate terms (3 slots).
 
+#include <atomic>
 #include <mutex>
 #include <type_traits>
 
@@ -66,7 +67,23 @@ struct ChunkParams {
   const float *A_log, *dt_bias;
   bf16* hs;                  // SAVE only: the state entering each chunk, bf16 [chunks][HV][V][K] (transposed)
   const int* chunk_first;    // SAVE with cu: chunks before each sequence
+  unsigned* range_flag;      // set to 1 when a stored output is inf or NaN (null: no check)
 };
+
+// Running maximum, per 16-bit half, of the magnitude bits of the bf16 values in x: a half at or
+// above 0x7f80 (all-ones exponent) has seen an inf or a NaN.
+__device__ __forceinline__ u16x2 bf16_mag_max(u16x2 m, const bf16x8& x) {
+  const u32x4 w = __builtin_bit_cast(u32x4, x);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2, w[i] & 0x7fff7fffu));
+  return m;
+}
+
+// Records a non-finite output: a system-scope vector store, so that a host word registered with
+// gdn_set_range_flag sees it without a device-wide synchronisation.
+__device__ __forceinline__ void flag_nonfinite(unsigned* flag, bool bad) {
+  if (bad) __hip_atomic_store(flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
 
 constexpr int kVB = 32;       // value columns per workgroup (two state waves of 16)
 constexpr int kNT = 512;      // threads per workgroup (8 waves)
@@ -240,14 +257,17 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
     const uint32_t graw = p.dg == GDN_DTYPE_F32 ? r.g32 : r.g16, braw = p.db == GDN_DTYPE_F32 ? r.b32 : r.b16;
     chunk_gates_from_raw(gv[c % 3], graw, braw, p.dg, p.db, chunk_len(c), p.flags, al, dt_b, lane);
   };
-  auto store_o = [&](int c, int tq) {  // waves 4-5: O of chunk c from Ob to HBM, rows tq / 4 + 32u
+  // waves 4-5: O of chunk c from Ob to HBM, rows tq / 4 + 32u; om keeps the stored values' magnitude maximum
+  auto store_o = [&](int c, int tq, u16x2& om) {
     const int64_t c0 = bos + (int64_t)c * kC;
     const auto ro = make_rsrc(og + (c0 * p.HV + hv) * VD + vb * kVB, (uint32_t)chunk_len(c) * v_row);
     const int row = tq >> 2, c8 = tq & 3;
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
-      buf_store16(*reinterpret_cast<const bf16x8*>(&Ob[c & 1][(row + 32 * u) * kVP + c8 * 8]), ro,
-                  (uint32_t)(row + 32 * u) * v_row + c8 * 16);
+    for (int u = 0; u < 2; ++u) {
+      const bf16x8 x = *reinterpret_cast<const bf16x8*>(&Ob[c & 1][(row + 32 * u) * kVP + c8 * 8]);
+      om = bf16_mag_max(om, x);
+      buf_store16(x, ro, (uint32_t)(row + 32 * u) * v_row + c8 * 16);
+    }
   };
 
   // scale * P^T of chunk c for key-row tiles JA..JA+JN-1 and query-row tiles TA..TA+TN-1 (tiles
@@ -553,12 +573,17 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
       if (i + 5 < nc) step(std::integral_constant<int, 5>{}, i + 5);
     }
     if (p.ht) {
+      uint32_t smax = 0;  // magnitude bits: at or above 0x7f800000 for inf and NaN
 #pragma unroll
       for (int a = 0; a < KT; ++a) {
         const int kd0 = 32 * (a >> 1) + 8 * g4 + 4 * (a & 1);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) p.ht[sbase + (int64_t)(kd0 + r) * VD + li] = S[a][r];
+        for (int r = 0; r < 4; ++r) {
+          p.ht[sbase + (int64_t)(kd0 + r) * VD + li] = S[a][r];
+          smax = max(smax, __float_as_uint(S[a][r]) & 0x7fffffffu);
+        }
       }
+      if (p.range_flag) flag_nonfinite(p.range_flag, smax >= 0x7f800000u);
     }
   } else if (qk_wave) {
     // K/Q of chunks 0 and 1 staged, chunk 2 in flight
@@ -586,6 +611,7 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
   } else {
     // T/V of chunk 0 staged and chunk 1 in flight; gates of chunks 0 and 1 staged, chunk 2 in flight
     bf16x8 pt[4], pv[2];
+    u16x2 om = {0, 0};
     fetch_tv(pt, pv, 0, thv);
     stage_tv(pt, pv, 0, thv);
     fetch_tv(pt, pv, 1, thv);
@@ -605,12 +631,13 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
         stage_gates(i + 2, ngate);
         fetch_gates(i + 3, ngate);
       }
-      if (i > 0) store_o(i - 1, tq);
+      if (i > 0) store_o(i - 1, tq, om);
       stage_tv(pt, pv, (i + 1) & 1, tq);
       fetch_tv(pt, pv, i + 2, tq);
       __syncthreads();
     }
-    if (nc > 0) store_o(nc - 1, thv);
+    if (nc > 0) store_o(nc - 1, thv, om);
+    if (p.range_flag) flag_nonfinite(p.range_flag, om[0] >= 0x7f80 || om[1] >= 0x7f80);
   }
 }
 
@@ -626,6 +653,20 @@ extern "C" size_t gdn_chunk_workspace_size(int64_t B, int64_t T, int64_t HV, int
 }
 
 namespace {
+
+constexpr int kMaxDevices = 64;
+
+// Non-finite output flags, one device-accessible word per device (null: no check); written under
+// g_flag_mu, read without it by every launch.
+std::mutex g_flag_mu;
+std::atomic<unsigned*> g_range_flag[kMaxDevices] = {};
+
+// The device that runs `stream` (the current device for the null stream), or -1.
+int stream_device(hipStream_t stream) {
+  int dev = -1;
+  if (stream ? hipStreamGetDevice(stream, &dev) != hipSuccess : hipGetDevice(&dev) != hipSuccess) return -1;
+  return dev;
+}
 
 int chunk_fwd_impl(const void* q, const void* k, const void* v, const void* g, const void* beta,
                    const float* initial_state, void* o, float* final_state, const void* cu_seqlens, int64_t B,
@@ -681,8 +722,12 @@ int chunk_fwd_impl(const void* q, const void* k, const void* v, const void* g, c
                      A_log, dt_bias};
   const int rc = launch_chunk_prep(pp, B, K, s);
   if (rc != GDN_OK) return rc;
+  const int dev = stream_device(s);
+  unsigned* const range_flag = dev >= 0 && dev < kMaxDevices ? g_range_flag[dev].load(std::memory_order_acquire)
+                                                             : nullptr;
   ChunkParams p{q, k, v, g, beta, initial_state, o, final_state, tw, cu_seqlens, order, cu_i32, T, H, HV, N,
-                g_dtype, beta_dtype, scale, flags, A_log, dt_bias, static_cast<bf16*>(chunk_states), chunk_first};
+                g_dtype, beta_dtype, scale, flags, A_log, dt_bias, static_cast<bf16*>(chunk_states), chunk_first,
+                range_flag};
   dim3 grid((unsigned)blocks), block(kNT);
   if (chunk_states) {
     if (K == 128 && V == 128) hipLaunchKernelGGL((gated_delta_chunk_kernel<128, 128, true>), grid, block, 0, s, p);
@@ -699,6 +744,28 @@ int chunk_fwd_impl(const void* q, const void* k, const void* v, const void* g, c
 }
 
 }  // namespace
+
+extern "C" int gdn_set_range_flag(int device, unsigned* flag) {
+  if (device < 0 || device >= kMaxDevices) {
+    gdn_internal_set_error("gdn_set_range_flag: device %d out of range", device);
+    return GDN_ERR_INVALID;
+  }
+  unsigned* dptr = nullptr;
+  if (flag) {
+    hipPointerAttribute_t a{};
+    const hipError_t e = hipPointerGetAttributes(&a, flag);
+    if (e != hipSuccess || !a.devicePointer ||
+        (a.type != hipMemoryTypeHost && !(a.type == hipMemoryTypeDevice && a.device == device))) {
+      (void)hipGetLastError();  // a failed query must not surface as the next launch's error
+      gdn_internal_set_error("gdn_set_range_flag: the flag must be pinned host memory or memory of device %d", device);
+      return GDN_ERR_INVALID;
+    }
+    dptr = static_cast<unsigned*>(a.devicePointer);
+  }
+  std::lock_guard<std::mutex> lock(g_flag_mu);
+  g_range_flag[device].store(dptr, std::memory_order_release);
+  return GDN_OK;
+}
 
 extern "C" int gdn_chunk_fwd(const void* q, const void* k, const void* v, const void* g, const void* beta,
                              const float* initial_state, void* o, float* final_state, const void* cu_seqlens,
@@ -740,7 +807,6 @@ namespace {
 constexpr size_t kScratchBytes = (size_t(64) << 20) + (size_t(64) << 10);  // 64 MiB + 64 KiB
 __device__ __align__(256) char scratch[kScratchBytes];
 
-constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices] = {};
 

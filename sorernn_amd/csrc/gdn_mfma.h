@@ -103,6 +103,7 @@ __device__ __forceinline__ f16x8 bf16_to_f16x8(bf16x8 x) {
 constexpr int kRsrcWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit dword format, no swizzle
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kRsrcWord3);

@@ -25,11 +25,14 @@ recurrent/decode operators are forward-only: a call that would need their backwa
 """
 from __future__ import annotations
 
+import warnings
+
 import torch
 from torch import Tensor
 
 from sorernn_amd import _lib
 from sorernn_amd import library as _library
+from sorernn_amd import range_guard as _range
 
 __all__ = [
     "causal_conv1d",
@@ -136,6 +139,18 @@ def _plain_eager(x: Tensor) -> bool:
             and torch.utils._python_dispatch._get_current_dispatch_mode() is None)
 
 
+_recurrent_noted: set = set()
+
+
+def _note_recurrent_route(name: str, dtype: torch.dtype) -> None:
+    """Warn once per dtype that non-bf16 q/k/v take the token-by-token kernel (no MFMA)."""
+    if dtype not in _recurrent_noted:
+        _recurrent_noted.add(dtype)
+        warnings.warn(f"{name}: {dtype} q/k/v run on the token-by-token fp32 recurrent kernel, not the chunked "
+                      "MFMA prefill (bf16 q/k/v only); cast q/k/v to bfloat16 for the chunked path "
+                      "(reported once per dtype)", RuntimeWarning, stacklevel=4)
+
+
 def _gdn_call(entry, name, q, k, v, g, beta, scale, initial_state, output_final_state, cu_seqlens, cu_seqlens_cpu,
               use_qk_l2norm_in_kernel, use_beta_sigmoid_in_kernel, use_gate_in_kernel, A_log, dt_bias,
               inplace_final_state=False):
@@ -147,6 +162,7 @@ def _gdn_call(entry, name, q, k, v, g, beta, scale, initial_state, output_final_
     if entry == "gdn_chunk_fwd" and q.dtype != torch.bfloat16:
         # The chunk kernels stage bf16 MFMA operands. fp32/fp16 q/k/v keep their precision on the
         # recurrent kernel, which computes the same recurrence token by token in fp32.
+        _note_recurrent_route(name, q.dtype)
         entry = "gdn_recurrent_fwd"
     grad_inputs = [q, k, v, g, beta, initial_state] + ([a_log_in, dt_bias_in] if use_gate_in_kernel else [])
     needs_grad = torch.is_grad_enabled() and any(x is not None and x.requires_grad for x in grad_inputs)
@@ -161,10 +177,23 @@ def _gdn_call(entry, name, q, k, v, g, beta, scale, initial_state, output_final_
         # Plain eager inference (no grad, no compile or fake tensors, no dispatch mode recording ops)
         # calls the op's implementation directly: the dispatcher round trip costs more host time
         # than the two kernel launches.
-        op = _library.chunk_fwd if (needs_grad or not _plain_eager(q)) else _library.chunk_fwd_impl
+        eager = _plain_eager(q)
+        op = _library.chunk_fwd if (needs_grad or not eager) else _library.chunk_fwd_impl
+        # the fp16 operand range guard (sorernn_amd/range_guard.py) reads its flag in eager calls only
+        word = _range.before_call(q.device) if eager else None
         o, final, _, _ = op(q, k, v, g, beta, initial_state, a_log_in if use_gate_in_kernel else None,
                             dt_bias_in if use_gate_in_kernel else None, cu_seqlens, scale, flags, n,
                             bool(output_final_state), needs_grad)
+        if _range.call_overflowed(word, q.device):
+            if _range.range_guard() == "raise" or needs_grad:
+                raise FloatingPointError(
+                    f"{name}: the chunked forward stored inf or NaN outputs (an fp16 operand of the chunk "
+                    "kernel past 65504, or non-finite inputs)"
+                    + ("; no fallback with grad: the backward needs the chunk forward" if needs_grad else ""))
+            _range.note_fallback(name)
+            return _gdn_call("gdn_recurrent_fwd", name, q, k, v, g, beta, scale, initial_state, output_final_state,
+                             cu_seqlens, cu_seqlens_cpu, use_qk_l2norm_in_kernel, use_beta_sigmoid_in_kernel,
+                             use_gate_in_kernel, a_log_in, dt_bias_in)
         return o, (final if output_final_state else None)
     q, k, v, g, beta = (x.contiguous() for x in (q, k, v, g, beta))
     h0 = None
@@ -226,6 +255,15 @@ def chunk_gated_delta_rule(
     With ``cu_seqlens`` (``[N+1]``, needs ``B == 1``) the state and the chunking restart at every
     document. ``cu_seqlens_cpu`` only serves to validate the bounds without a device sync; the
     kernel's grid depends on ``N`` alone.
+
+    Range: the chunk kernel's matrix-core operands for the state, X, Delta, T - I and scale * P are
+    fp16 (largest finite value 65504; FLA's bf16 operands reach fp32's range). L2-normalised q/k
+    with activation-scale v stay far inside it (|scale * P| <= scale, states of order |v|); an
+    operand past it turns o and the final state non-finite. The kernel flags every inf or NaN it
+    stores, and ``sorernn_amd.set_range_guard`` selects the response: a warning at the next call
+    (default, no synchronisation), ``FloatingPointError``, or a recomputation of the call by the
+    fp32 recurrent kernel. ``sorernn_amd.check_chunk_range()`` reports the flag on demand.
+    fp32/fp16 q/k/v run on the recurrent kernel (a warning says so once per dtype).
     """
     if allow_neg_eigval or state_v_first or cp_context is not None:
         raise NotImplementedError("chunk_gated_delta_rule: allow_neg_eigval, state_v_first and cp_context are not supported")

@@ -1,0 +1,127 @@
+"""Range guard of the chunked forward's fp16 matrix-core operands.
+
+The chunk forward (``gdn_chunk.hip``) feeds the state S, X, Delta, T - I and scale * P to the
+matrix cores as fp16, whose largest finite value is 65504; FLA's kernels use bf16 operands, which
+keep fp32's exponent range. An operand past the fp16 range becomes inf, and every product that
+reads it carries the inf (or a NaN) into ``o`` and the final state. The kernels check what they
+store and set a flag word (``gdn_set_range_flag`` in ``include/gdn.h``) when an ``o`` or
+final-state element is inf or NaN. This module keeps one pinned host word per device, registered
+with the library on the first chunk call on that device, and decides what a set flag does:
+
+- ``"warn"`` (the default): no synchronisation. A flag that earlier calls set is cleared and
+  reported with a ``RuntimeWarning`` by the next ``chunk_gated_delta_rule`` call on that device,
+  or by ``check_chunk_range()``.
+- ``"raise"``: every call waits for its stream and raises ``FloatingPointError`` if it set the flag.
+- ``"fallback"``: every call waits for its stream; a call that set the flag is computed again by
+  the fp32 recurrent kernel (the same recurrence token by token, no fp16 operands), with a
+  warning the first time. A call that needs a backward cannot fall back (the backward reads the
+  chunk forward's saved states) and raises instead.
+- ``"off"``: no flag, no check.
+
+Non-finite inputs set the flag as well; FLA returns non-finite outputs for them too, and the
+fallback recomputation then returns them unchanged. ``SORERNN_RANGE_GUARD`` sets the initial mode.
+"""
+from __future__ import annotations
+
+import os
+import warnings
+
+import numpy as np
+import torch
+
+from sorernn_amd import _lib
+
+MODES = ("warn", "raise", "fallback", "off")
+
+_mode = os.environ.get("SORERNN_RANGE_GUARD", "warn")
+if _mode not in MODES:
+    raise ValueError(f"SORERNN_RANGE_GUARD={_mode!r}: expected one of {MODES}")
+_words: dict[int, tuple[torch.Tensor, np.ndarray]] = {}
+_fallback_noted = False
+
+_EARLIER = ("chunk_gated_delta_rule: an earlier chunked forward on cuda:{dev} stored inf or NaN outputs (an fp16 "
+            "operand of the chunk kernel past 65504, or non-finite inputs). Set sorernn_amd.set_range_guard("
+            "'fallback') to recompute such calls with the fp32 recurrent kernel, or 'raise' to stop at the call.")
+
+
+def set_range_guard(mode: str) -> None:
+    """Select what a non-finite chunk output does: ``"warn"``, ``"raise"``, ``"fallback"`` or ``"off"``."""
+    global _mode
+    if mode not in MODES:
+        raise ValueError(f"set_range_guard: mode must be one of {MODES}, got {mode!r}")
+    _mode = mode
+    if mode == "off":
+        for dev in list(_words):
+            _lib.call("gdn_set_range_flag", dev, None)
+            del _words[dev]
+
+
+def range_guard() -> str:
+    """The current mode."""
+    return _mode
+
+
+def _device_index(device: torch.device | int | None) -> int:
+    if device is None:
+        return torch.cuda.current_device()
+    if isinstance(device, int):
+        return device
+    return device.index if device.index is not None else torch.cuda.current_device()
+
+
+def _word(dev: int) -> np.ndarray:
+    w = _words.get(dev)
+    if w is None:
+        t = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+        _lib.call("gdn_set_range_flag", dev, t.data_ptr())
+        w = _words[dev] = (t, t.numpy())
+    return w[1]
+
+
+def before_call(device: torch.device) -> np.ndarray | None:
+    """Before a chunk launch (eager calls): the device's flag word, after reporting and clearing a
+    flag left by earlier calls. None when the guard is off."""
+    if _mode == "off":
+        return None
+    dev = _device_index(device)
+    word = _word(dev)
+    if word[0]:
+        word[0] = 0
+        warnings.warn(_EARLIER.format(dev=dev), RuntimeWarning, stacklevel=4)
+    return word
+
+
+def call_overflowed(word: np.ndarray | None, device: torch.device) -> bool:
+    """After a chunk launch in the "raise" and "fallback" modes: wait for the call's stream and
+    return True (clearing the word) when the call set the flag. False in the other modes."""
+    if word is None or _mode not in ("raise", "fallback"):
+        return False
+    torch.cuda.current_stream(device).synchronize()
+    if not word[0]:
+        return False
+    word[0] = 0
+    return True
+
+
+def note_fallback(name: str) -> None:
+    global _fallback_noted
+    if not _fallback_noted:
+        _fallback_noted = True
+        warnings.warn(f"{name}: a chunked forward overflowed its fp16 operands (or saw non-finite inputs); "
+                      "recomputed with the fp32 recurrent kernel (reported once per process)",
+                      RuntimeWarning, stacklevel=4)
+
+
+def check_chunk_range(device: torch.device | int | None = None, clear: bool = True) -> bool:
+    """Wait for the device and return whether a chunked forward on it stored an inf or NaN since the
+    flag was last cleared. The flag is cleared unless ``clear=False``. Always False when the guard is
+    off or no chunk call has run on the device."""
+    dev = _device_index(device)
+    w = _words.get(dev)
+    if w is None:
+        return False
+    torch.cuda.synchronize(dev)
+    hit = bool(w[1][0])
+    if hit and clear:
+        w[1][0] = 0
+    return hit

@@ -37,6 +37,14 @@ def test_library_exports_every_declared_symbol_with_matching_arity():
     assert lib.gdn_abi_version() == _lib.ABI_VERSION
 
 
+def test_set_range_flag_checks_the_device_first():
+    """gdn_set_range_flag validates the device index before any HIP call (no GPU needed)."""
+    lib = _lib.load()
+    assert lib.gdn_set_range_flag(-1, None) == _lib.GDN_ERR_INVALID
+    assert b"out of range" in lib.gdn_last_error()
+    assert lib.gdn_set_range_flag(64, None) == _lib.GDN_ERR_INVALID
+
+
 def test_no_cpu_path():
     q = torch.randn(1, 4, 1, 64)
     with pytest.raises(ValueError, match="GPU"):

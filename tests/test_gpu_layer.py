@@ -136,7 +136,11 @@ def test_inference_route_matches_reference_route(kernel_gate, cu):
 
 def test_layer_extreme_inputs_stay_finite():
     """x100 inputs (reference tests/model/test_gdn.py:60-71) through the bf16 layer: output and input
-    gradient finite, with packed documents."""
+    gradient finite, with packed documents, and the chunk kernel's fp16 operands inside their range
+    (the range guard's flag stays clear)."""
+    import sorernn_amd
+
+    sorernn_amd.check_chunk_range()
     torch.manual_seed(0)
     cfg = GDNLayerConfig(d_model=128, gdn_qk_heads=2, gdn_v_heads=4, gdn_head_dim=64, gdn_kernel_gate=True)
     layer = GatedDeltaNet(cfg).to(DEV)
@@ -148,6 +152,7 @@ def test_layer_extreme_inputs_stay_finite():
     out.float().square().mean().backward()
     torch.cuda.synchronize()
     assert torch.isfinite(x.grad).all()
+    assert not sorernn_amd.check_chunk_range(), "x100 layer inputs overflowed the chunk kernel's fp16 operands"
 
 
 def test_layer_cu_seqlens_cpu_is_exact():
