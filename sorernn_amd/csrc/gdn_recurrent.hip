@@ -12,6 +12,7 @@
 // No MFMA: per token the work is two matrix-vector products and a rank-1 update, bandwidth-bound.
 
 #include "gdn_common.h"
+#include "gdn_mfma.h"
 
 namespace gdn {
 
@@ -128,24 +129,6 @@ __device__ __forceinline__ void store_state(const StateRegs<KD, VD>& sr, float* 
   const int t = threadIdx.x, cg = t % L::CG, rg = t / L::CG;
 #pragma unroll
   for (int i = 0; i < L::RPT; ++i) *reinterpret_cast<float4*>(base + (int64_t)(rg + L::RG * i) * VD + 4 * cg) = s[i];
-}
-
-// A VB-column block of a [KD][stride] state (columns col0 .. col0 + VB - 1), in the layout above.
-template <int KD, int VB>
-__device__ __forceinline__ void load_state_cols(StateRegs<KD, VB>& sr, const float* base, int stride, int col0) {
-  using L = RecLayout<KD, VB>;
-  const int t = threadIdx.x, cg = t % L::CG, rg = t / L::CG;
-#pragma unroll
-  for (int i = 0; i < L::RPT; ++i)
-    sr.r[i] = *reinterpret_cast<const float4*>(base + (int64_t)(rg + L::RG * i) * stride + col0 + 4 * cg);
-}
-template <int KD, int VB>
-__device__ __forceinline__ void store_state_cols(const StateRegs<KD, VB>& sr, float* base, int stride, int col0) {
-  using L = RecLayout<KD, VB>;
-  const int t = threadIdx.x, cg = t % L::CG, rg = t / L::CG;
-#pragma unroll
-  for (int i = 0; i < L::RPT; ++i)
-    *reinterpret_cast<float4*>(base + (int64_t)(rg + L::RG * i) * stride + col0 + 4 * cg) = sr.r[i];
 }
 
 // grid (HV, N): one workgroup per (value head, sequence), tokens in order.
@@ -280,33 +263,41 @@ struct alignas(W * sizeof(T) >= 16 ? 16 : W * sizeof(T)) ConvWindow {
   T v[W];
 };
 
-// Fast decode step for width-4 conv caches whose dtype equals the activation dtype T. Every
-// global load of the step is issued before the first dependent use: the first column block of the
-// value head's state, the conv caches, inputs and weights of the q/k channels and of that head's v
-// channels, and the gates; the conv math then overlaps the state's arrival. The state streams in
-// NB column blocks (the columns of the recurrence are independent: column j needs only S[:, j]):
-// block b + 1's loads are in flight while block b is reduced, updated and written back, so the
-// reads and writes of the step overlap in HBM instead of running as two phases.
+// Sum over the 8 row groups of a column group (lanes l ^ 8, l ^ 16, l ^ 32) in three VALU steps:
+// DPP row_ror:8 inside each 16-lane row, then the 16- and 32-lane swaps of gfx950
+__device__ __forceinline__ float rg_sum(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xf, 0xf, false));
+  auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+  auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
+}
+
+// Fast decode step for width-4 conv caches whose dtype equals the activation dtype T: one
+// workgroup per (sequence, q/k head), looping over that head's value heads. Wave w owns the 32-column
+// block w of the state (columns of the recurrence are independent: column j needs only S[:, j]), 16
+// rows x 4 columns per lane, so the reductions over the state's rows (S^T k, S^T q) stay inside the
+// wave and no reduction crosses waves: one barrier per value head publishes the conv outputs q, k, v
+// in LDS. The four waves read their blocks at once, i.e. the whole 64 KB state, with non-temporal
+// loads and write it back with non-temporal stores: the state is touched once per step, and with
+// the state served from DRAM (B = 64, H = 16, D = 128) the step took 25.0 us this way against
+// 29.0 us for cached accesses in column blocks.
 template <int D, class T>
 __global__ __launch_bounds__(256) void gated_delta_decode_w4_kernel(DecodeParams p) {
-  constexpr int W = 4, NB = D / 32, VB = D / NB;  // 32-column blocks: 128-byte row segments
-  using L = RecLayout<D, VB>;
+  constexpr int W = 4, VB = 32, NWB = D / VB;                // column blocks, one per wave (waves 0..NWB-1)
+  constexpr int CG = VB / 4, RG = kWave / CG, RPT = D / RG;  // lane (rg, cg): rows rg + RG i, columns 4cg..+3
   using Win = ConvWindow<W, T>;
   __shared__ float qk[2 * D];
   __shared__ float vs[2][D];
-  __shared__ float red[2][L::NW * L::CG * 12];
   const int h = blockIdx.x;
   const int64_t b = blockIdx.y;
   const int rep = (int)(p.HV / p.H);
   const int64_t C = (2 * p.H + p.HV) * D;
-  const int t = threadIdx.x;
-  int rb = 0;  // red buffer of the next reduction (consecutive reductions alternate)
+  const int t = threadIdx.x, lane = t & (kWave - 1), w = t / kWave, cg = lane % CG, rg = lane / CG;
   const T* __restrict__ xg = static_cast<const T*>(p.x);
   Win* __restrict__ cs = static_cast<Win*>(p.conv_state);
   const float4* __restrict__ wg = reinterpret_cast<const float4*>(p.conv_w);
   const bool l2 = p.flags & GDN_FLAG_QK_L2NORM;
-
-  // channel handled by this thread: q/k channel e = t (t < 2D) and v channel e = t (t < D)
   const bool has_qk = t < 2 * D, has_v = t < D;
   const int64_t ch_qk = (t < D) ? (int64_t)h * D + t : p.H * D + (int64_t)h * D + (t - D);
 
@@ -314,8 +305,6 @@ __global__ __launch_bounds__(256) void gated_delta_decode_w4_kernel(DecodeParams
     const int hv = h * rep + r;
     const int par = r & 1;
     const int64_t sbase = (b * p.HV + hv) * (int64_t)D * D;
-    StateRegs<D, VB> s[2];
-    load_state_cols<D, VB>(s[0], p.state + sbase, D, 0);
     const int64_t ch_v = 2 * p.H * D + (int64_t)hv * D + t;
     Win wq{}, wv{};
     T xq{}, xv{};
@@ -333,7 +322,18 @@ __global__ __launch_bounds__(256) void gated_delta_decode_w4_kernel(DecodeParams
     }
     const uint32_t graw = load_raw32(p.g, p.dg, b * p.HV + hv);
     const uint32_t braw = load_raw32(p.beta, p.db, b * p.HV + hv);
-    // conv: window = (cache[1..3], x); y = sum_i w[i] window[i]; the new cache is the window
+    float4 s[RPT];
+    // the state through a buffer resource: one lane offset plus a scalar offset per row step, so
+    // the 16 row addresses take no registers; loads non-temporal (the state is touched once a step)
+    const auto rs = make_rsrc(p.state + sbase, (uint32_t)(D * D * 4));
+    const int voff = ((rg * D) + w * VB + 4 * cg) * 4;
+    if (w < NWB) {
+#pragma unroll
+      for (int i = 0; i < RPT; ++i) {
+        const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, i * RG * D * 4, 2);
+        s[i] = __builtin_bit_cast(float4, x);
+      }
+    }
     if (do_qk) {
       const float y = kq.x * elem_to_f32(wq.v[1]) + kq.y * elem_to_f32(wq.v[2]) + kq.z * elem_to_f32(wq.v[3]) +
                       kq.w * elem_to_f32(xq);
@@ -355,18 +355,45 @@ __global__ __launch_bounds__(256) void gated_delta_decode_w4_kernel(DecodeParams
     if (p.flags & GDN_FLAG_BETA_SIGMOID) bv = sigmoid_f32(bv);
     const float a = expf(gv);
     __syncthreads();
+    if (w < NWB) {
+      const float* q_l = qk;
+      const float* k_l = qk + D;
+      float pr[11];
 #pragma unroll
-    for (int blk = 0; blk < NB; ++blk) {
-      if (blk + 1 < NB) load_state_cols<D, VB>(s[(blk + 1) & 1], p.state + sbase, D, (blk + 1) * VB);
-      float o4[4];
-      rec_token<D, VB>(s[blk & 1], qk, qk + D, vs[par] + blk * VB, a, bv, l2, p.scale, red[rb], o4);
-      rb ^= 1;
-      if (t < L::CG) {
-        T* og = static_cast<T*>(p.o) + (b * p.HV + hv) * D + blk * VB + 4 * t;
+      for (int j2 = 0; j2 < 11; ++j2) pr[j2] = 0.f;
+#pragma unroll
+      for (int i = 0; i < RPT; ++i) {
+        const int row = rg + RG * i;
+        const float kr = k_l[row], qr = q_l[row];
+        pr[0] += s[i].x * kr; pr[1] += s[i].y * kr; pr[2] += s[i].z * kr; pr[3] += s[i].w * kr;
+        pr[4] += s[i].x * qr; pr[5] += s[i].y * qr; pr[6] += s[i].z * qr; pr[7] += s[i].w * qr;
+        pr[8] += kr * qr; pr[9] += kr * kr; pr[10] += qr * qr;
+      }
+#pragma unroll
+      for (int j2 = 0; j2 < 11; ++j2) pr[j2] = rg_sum(pr[j2]);
+      const float ik = l2 ? 1.f / fmaxf(sqrtf(pr[9]), 1e-12f) : 1.f;
+      const float iq = l2 ? 1.f / fmaxf(sqrtf(pr[10]), 1e-12f) : 1.f;
+      const float* v_l = vs[par] + w * VB + 4 * cg;
+      float d[4], o4[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        d[c] = bv * (v_l[c] - a * pr[c] * ik);
+        o4[c] = p.scale * (a * pr[4 + c] * iq + d[c] * pr[8] * ik * iq);
+      }
+      if (rg == 0) {
+        T* og = static_cast<T*>(p.o) + (b * p.HV + hv) * D + w * VB + 4 * cg;
 #pragma unroll
         for (int c = 0; c < 4; ++c) og[c] = f32_to_elem<T>(o4[c]);
       }
-      store_state_cols<D, VB>(s[blk & 1], p.state + sbase, D, blk * VB);
+      // the row step goes into the lane offset, not the scalar offset: for a wide buffer store whose
+      // scalar offset is a register the compiler inserts no wait states before the store's data
+      // registers are rewritten, and the last lanes of a row then stored the rewritten values
+#pragma unroll
+      for (int i = 0; i < RPT; ++i) {
+        const float kr = k_l[rg + RG * i] * ik;
+        const float4 n{a * s[i].x + kr * d[0], a * s[i].y + kr * d[1], a * s[i].z + kr * d[2], a * s[i].w + kr * d[3]};
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, n), rs, voff + i * RG * D * 4, 0, 2);
+      }
     }
   }
 }

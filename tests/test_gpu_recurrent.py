@@ -96,6 +96,54 @@ def test_decode_step_matches_oracle(shape):
     assert_state_close(state.cpu(), st_ref)
 
 
+DECODE_OPTIONS = [
+    # (activation dtype, gate/beta dtype, use_qk_l2norm, gate in kernel + beta sigmoid, D)
+    (torch.float16, torch.float32, True, False, 128),
+    (torch.float32, torch.float32, True, False, 128),
+    (torch.bfloat16, torch.bfloat16, True, False, 128),
+    (torch.bfloat16, torch.float32, False, False, 128),
+    (torch.bfloat16, torch.float32, True, True, 128),
+    (torch.bfloat16, torch.bfloat16, True, True, 64),
+]
+
+
+@pytest.mark.parametrize("dt,gdt,l2,kgate,d", DECODE_OPTIONS,
+                         ids=["f16", "f32", "bf16_gates", "no_l2norm", "kernel_gate", "kernel_gate_bf16_d64"])
+def test_decode_step_options_match_oracle(dt, gdt, l2, kgate, d):
+    """The fused decode step over its input dtypes, 16-bit gates (the last element of g and beta is
+    read at the tensors' final 2 bytes), the L2 norm on and off, and the in-kernel gate
+    g = -exp(A_log) softplus(a + dt_bias) with beta = sigmoid(b) (oracle gate_and_beta), with GVA."""
+    from oracle import gate_and_beta
+
+    b, h, hv = 5, 2, 4
+    print(f"decode options dt={dt} gates={gdt} l2={l2} kernel_gate={kgate} D={d}", flush=True)
+    di = decode_inputs(B=b, H=h, HV=hv, D=d, dtype=dt, seed=1100 + d)
+    gen = torch.Generator().manual_seed(7)
+    if kgate:
+        a_raw = torch.randn(b, hv, generator=gen).to(gdt)
+        b_raw = torch.randn(b, hv, generator=gen).to(gdt)
+        A_log = torch.rand(hv, generator=gen) * 2 - 1
+        dt_bias = torch.randn(hv, generator=gen) * 0.5
+        g_ref, beta_ref = gate_and_beta(a_raw[:, None], b_raw[:, None], A_log, dt_bias)
+        g_ref, beta_ref = g_ref[:, 0], beta_ref[:, 0]
+        g_in, beta_in = a_raw, b_raw
+    else:
+        g_in, beta_in = di.g.to(gdt), di.beta.to(gdt)
+        g_ref, beta_ref = g_in.float(), beta_in.float()
+    dev = lambda x: x.to(DEV)  # noqa: E731
+    conv, state = dev(di.conv_state), dev(di.state)
+    kw = dict(use_qk_l2norm_in_kernel=l2)
+    if kgate:
+        kw.update(use_gate_in_kernel=True, use_beta_sigmoid_in_kernel=True, A_log=dev(A_log), dt_bias=dev(dt_bias))
+    o = gated_delta_decode_step(dev(di.x_qkv), conv, dev(di.conv_weight), dev(g_in), dev(beta_in), state, h, hv, d, **kw)
+    torch.cuda.synchronize()
+    o_ref, conv_ref, st_ref = decode_step_ref(di.x_qkv, di.conv_state, di.conv_weight, g_ref, beta_ref, di.state,
+                                              h, hv, d, use_qk_l2norm=l2)
+    assert torch.equal(conv.cpu(), conv_ref), "conv cache must be shifted exactly"
+    assert_output_close(o.cpu(), o_ref.to(dt))
+    assert_state_close(state.cpu(), st_ref)
+
+
 def test_decode_three_steps_in_a_row():
     di = decode_inputs(B=8, H=2, HV=2, D=128, seed=99)
     dev = lambda x: x.to(DEV)  # noqa: E731
