@@ -87,7 +87,6 @@ __device__ __forceinline__ void flag_nonfinite(unsigned* flag, bool bad) {
 
 constexpr int kVB = 32;       // value columns per workgroup (two state waves of 16)
 constexpr int kNT = 512;      // threads per workgroup (8 waves)
-constexpr int kVP = kVB + 8;  // bf16 pitch of the V and O slices (80 B rows)
 
 // SAVE (training forward): the state waves also store the state entering every chunk, rounded to
 // bf16 and transposed ([V][K]: a lane's four consecutive keys are one 8-byte store), the input of
@@ -96,9 +95,9 @@ template <int KD, int VD, bool SAVE>
 __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p) {
   constexpr int NVB = VD / kVB;
   // q/k tiles in LDS: at KD = 128 rows are unpadded (256 B) and the 16-byte chunk c of row r sits
-  // at chunk c ^ kq_sw(r), which keeps both the row-fragment reads (16 rows, one chunk) and the
-  // transposed K^T reads (4 rows x 4 chunks per 16 lanes) free of bank conflicts; at KD = 64 rows
-  // are padded by 16 bytes instead.
+  // at chunk c ^ kq_sw(r) = c ^ ((r & 7) << 1). Measured with SQ_LDS_BANK_CONFLICT on gfx950, the
+  // row-fragment reads (16 rows, one chunk) and the staging writes are then conflict-free and the
+  // transposed K^T reads take 2 extra cycles per instruction; at KD = 64 rows are padded by 16 bytes.
   constexpr bool SWZ = KD == 128;
   constexpr int KP = SWZ ? KD : KD + 8;       // element pitch of the q/k tiles
   constexpr int KS = KD / 32;                 // MFMA k-steps over the key dim
@@ -108,10 +107,10 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
 
   __shared__ __align__(16) f16 Kc[3][kC * KP];   // K of chunk c in slot c % 3 (fp16)
   __shared__ __align__(16) f16 Qc[2][kC * KP];   // Q of chunk c in slot c % 2 (fp16)
-  __shared__ __align__(16) f16 Tb[2][kC * kCP];  // T - I of chunk c in slot c % 2 (tok_col columns)
-  __shared__ __align__(16) f16 Pb[2][kC * kCP];  // scale * P of chunk c in slot c % 2 (tok_col columns)
-  __shared__ __align__(16) bf16 Vc[2][kC * kVP];  // V slice of chunk c in slot c % 2
-  __shared__ __align__(16) bf16 Ob[2][kC * kVP];  // O of chunk c, stored to HBM during chunk c + 1
+  __shared__ __align__(16) f16 Tb[2][kC * kC];    // T - I of chunk c in slot c % 2 (tok_col columns, tp_off)
+  __shared__ __align__(16) f16 Pb[2][kC * kC];    // scale * P of chunk c in slot c % 2 (tok_col columns, tp_off)
+  __shared__ __align__(16) bf16 Vc[2][kC * kVB];  // V slice of chunk c in slot c % 2 (vo_off)
+  __shared__ __align__(16) bf16 Ob[2][kC * kVB];  // O of chunk c, stored to HBM during chunk c + 1 (vo_off)
   __shared__ __align__(16) ChunkGates gv[3];      // gate terms of chunk c in slot c % 3
 
   // w is read back as a scalar: the compiler then treats the role branches as wave-uniform
@@ -121,8 +120,13 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
   // key step s (lane row li, lane group g: keys 32s + 8g..+7), and the transposed K^T fragment of
   // state tile a = 2s + h against token rows 32u + 4g + m and 32u + 16 + 4g + m (ld8_tr_pair's
   // layout: lane 4m + q reads keys 32s + 8q + 4h..+3, i.e. chunk 4s + q, half h).
-  auto kq_sw = [](int r) { return SWZ ? (((r & 3) << 2) | ((r >> 2) & 3)) : 0; };
+  auto kq_sw = [](int r) { return SWZ ? ((r & 7) << 1) : 0; };
   auto kq_col = [&](int s, int l_i, int l_g) { return (((4 * s + l_g) ^ kq_sw(l_i)) << 3); };
+  // T - I and P tiles: 64 rows of 64 fp16 (128 B, unpadded), the 16-byte chunk c of row r at chunk
+  // c ^ (r & 7). V and O slices: 64 rows of 32 bf16 (64 B), chunk c of row r at c ^ ((r >> 2) & 3).
+  // Element offsets of (row r, column col); an access never spans two chunks.
+  auto tp_off = [](int r, int col) { return r * kC + ((((col >> 3) ^ (r & 7)) << 3) | (col & 7)); };
+  auto vo_off = [](int r, int col) { return r * kVB + ((((col >> 3) ^ ((r >> 2) & 3)) << 3) | (col & 7)); };
   auto kt_pair = [&](const f16* tile, int u, int a) {
     const int m = li >> 2, q = li & 3;
     const int row = 32 * u + 4 * g4 + m;  // row & 3 = m, (row >> 2) & 3 = g4: the swizzle of both rows
@@ -218,12 +222,13 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
     for (int u = 0; u < 2; ++u) pv[u] = buf_load16(rv, bv + (uint32_t)(32 * u) * v_row);
   };
   auto stage_tv = [&](const bf16x8 (&pt)[4], const bf16x8 (&pv)[2], int slot, int tq) {
-    f16* const t0 = Tb[slot] + (tq >> 3) * kCP + (tq & 7) * 8;
+    // rows tq / 8 + 16u (T) and tq / 4 + 32u (V) share their row's swizzle
+    f16* const t0 = Tb[slot] + tp_off(tq >> 3, (tq & 7) * 8);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) *reinterpret_cast<bf16x8*>(t0 + 16 * u * kCP) = pt[u];  // fp16 bits, copied
-    bf16* const v0 = Vc[slot] + (tq >> 2) * kVP + (tq & 3) * 8;
+    for (int u = 0; u < 4; ++u) *reinterpret_cast<bf16x8*>(t0 + 16 * u * kC) = pt[u];  // fp16 bits, copied
+    bf16* const v0 = Vc[slot] + vo_off(tq >> 2, (tq & 3) * 8);
 #pragma unroll
-    for (int u = 0; u < 2; ++u) *reinterpret_cast<bf16x8*>(v0 + 32 * u * kVP) = pv[u];
+    for (int u = 0; u < 2; ++u) *reinterpret_cast<bf16x8*>(v0 + 32 * u * kVB) = pv[u];
   };
   // The gate bits of a chunk are loaded by one 32-bit and one 16-bit load per tensor, both issued
   // whatever the dtype (a load whose width depends on the dtype would be two instructions on two
@@ -264,7 +269,7 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
     const int row = tq >> 2, c8 = tq & 3;
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      const bf16x8 x = *reinterpret_cast<const bf16x8*>(&Ob[c & 1][(row + 32 * u) * kVP + c8 * 8]);
+      const bf16x8 x = *reinterpret_cast<const bf16x8*>(&Ob[c & 1][vo_off(row + 32 * u, c8 * 8)]);
       om = bf16_mag_max(om, x);
       buf_store16(x, ro, (uint32_t)(row + 32 * u) * v_row + c8 * 16);
     }
@@ -312,7 +317,7 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
         float val[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) val[r] = (jt < tt_ || j0 + r <= tt) ? p.scale * __expf(gt - gjv[r]) * acc[a][b][r] : 0.f;
-        *reinterpret_cast<f16x4*>(pw + tt * kCP + tok_col(j0)) = to_f16x4(val[0], val[1], val[2], val[3]);
+        *reinterpret_cast<f16x4*>(pw + tp_off(tt, tok_col(j0))) = to_f16x4(val[0], val[1], val[2], val[3]);
       }
   };
   using I0 = std::integral_constant<int, 0>;
@@ -378,7 +383,7 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
 
   // ------------------------------------------------------------------ prologue
   // P is causally lower: its tiles above the diagonal stay zero for the whole run
-  for (int e = t; e < kC * kCP / 8; e += kNT) {
+  for (int e = t; e < kC * kC / 8; e += kNT) {
     reinterpret_cast<f16x8*>(Pb[0])[e] = f16x8{};
     reinterpret_cast<f16x8*>(Pb[1])[e] = f16x8{};
   }
@@ -442,7 +447,8 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
       float4 bt[4], bg[4];
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
-        vv[b] = ld4_tr(vp, kVP, 16 * b, 16 * sw, lane);
+        vv[b] = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(  // ld4_tr's lanes on the swizzled slice
+            (lds_bf16x4*)(vp + vo_off(16 * b + 4 * g4 + (li >> 2), 16 * sw + 4 * (li & 3))));
         bt[b] = ld4f(&G.bet[16 * b + 4 * g4]);
         bg[b] = ld4f(&G.begam[16 * b + 4 * g4]);
       }
@@ -461,12 +467,12 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
       phase();
       // ---- 2: reads of T - I; X = beta V - beta e^gam Y (kept in fp32 as the Delta accumulator's start)
       f16x8 tf[6];
-      tf[0] = ld8h(tp + li * kCP + 8 * g4);
-      tf[1] = ld8h(tp + (16 + li) * kCP + 8 * g4);
-      tf[2] = ld8h(tp + (32 + li) * kCP + 8 * g4);
-      tf[3] = ld8h(tp + (48 + li) * kCP + 8 * g4);
-      tf[4] = ld8h(tp + (32 + li) * kCP + 32 + 8 * g4);
-      tf[5] = ld8h(tp + (48 + li) * kCP + 32 + 8 * g4);
+      tf[0] = ld8h(tp + tp_off(0 + li, 0 + 8 * g4));
+      tf[1] = ld8h(tp + tp_off(16 + li, 0 + 8 * g4));
+      tf[2] = ld8h(tp + tp_off(32 + li, 0 + 8 * g4));
+      tf[3] = ld8h(tp + tp_off(48 + li, 0 + 8 * g4));
+      tf[4] = ld8h(tp + tp_off(32 + li, 32 + 8 * g4));
+      tf[5] = ld8h(tp + tp_off(48 + li, 32 + 8 * g4));
       phase();
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
@@ -516,9 +522,9 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
       f16x8 pf[6];
       float eg[4];
 #pragma unroll
-      for (int tb = 0; tb < 4; ++tb) pf[tb] = ld8h(pp + (16 * tb + li) * kCP + 8 * g4);
-      pf[4] = ld8h(pp + (32 + li) * kCP + 32 + 8 * g4);
-      pf[5] = ld8h(pp + (48 + li) * kCP + 32 + 8 * g4);
+      for (int tb = 0; tb < 4; ++tb) pf[tb] = ld8h(pp + tp_off(16 * tb + li, 8 * g4));
+      pf[4] = ld8h(pp + tp_off(32 + li, 32 + 8 * g4));
+      pf[5] = ld8h(pp + tp_off(48 + li, 32 + 8 * g4));
 #pragma unroll
       for (int tb = 0; tb < 4; ++tb) eg[tb] = p.scale * G.egam[16 * tb + li];
       phase();
@@ -548,7 +554,7 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
         f32x4 o = Zt[tb] * eg[tb];
         o = mmah(db0, pf[tb], o);
         if (tb >= 2) o = mmah(db1, pf[tb + 2], o);
-        *reinterpret_cast<bf16x4*>(op + (16 * tb + li) * kVP + 16 * sw + 4 * g4) = to_bf16x4(o[0], o[1], o[2], o[3]);
+        *reinterpret_cast<bf16x4*>(op + vo_off(16 * tb + li, 16 * sw + 4 * g4)) = to_bf16x4(o[0], o[1], o[2], o[3]);
       }
 #pragma unroll
       for (int tb = 0; tb < 4; ++tb) Zt[tb] = f32x4{};
