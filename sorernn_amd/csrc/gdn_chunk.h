@@ -30,6 +30,7 @@ struct ChunkPrepParams {
   int dg, db;
   unsigned flags;
   const float *A_log, *dt_bias;
+  int64_t items;           // set by launch_chunk_prep: chunks per value head (an upper bound with cu)
 };
 
 inline int64_t align256(int64_t b) { return (b + 255) / 256 * 256; }

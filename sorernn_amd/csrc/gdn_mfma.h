@@ -18,7 +18,6 @@ constexpr int kAoP = 52;     // fp32 pitch of the off-diagonal A rows 16..63 x c
 constexpr int kTfP = 36;     // fp32 pitch of the two 32x32 diagonal T blocks
 
 typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
-typedef short i16x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ bf16x8 ld8(const bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
 
@@ -37,9 +36,6 @@ __device__ __forceinline__ f32x4 mmah(f16x8 a, f16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 __device__ __forceinline__ f16x8 ld8h(const f16* p) { return *reinterpret_cast<const f16x8*>(p); }
-__device__ __forceinline__ f32x4 mma16(bf16x4 a, bf16x4 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, a), __builtin_bit_cast(i16x4, b), c, 0, 0, 0);
-}
 
 // Transposed reads of a row-major bf16 LDS tile M (pitch in elements) with ds_read_b64_tr_b16.
 // The instruction works inside groups of 16 lanes: each lane supplies 4 consecutive elements
@@ -139,27 +135,11 @@ __device__ __forceinline__ f16x4 to_f16x4(float a, float b, float c, float d) {
   return f16x4{static_cast<f16>(a), static_cast<f16>(b), static_cast<f16>(c), static_cast<f16>(d)};
 }
 
-// fp32 x4 -> bf16 hi and lo parts (x ~= hi + lo to about 2^-16 relative)
-__device__ __forceinline__ void split4(float a, float b, float c, float d, bf16x4& hi, bf16x4& lo) {
-  hi = to_bf16x4(a, b, c, d);
-  lo = to_bf16x4(a - (float)hi[0], b - (float)hi[1], c - (float)hi[2], d - (float)hi[3]);
-}
-// Two fp32 accumulator fragments as the hi and lo bf16 operands of 8 (see pack8)
-__device__ __forceinline__ void split8(f32x4 a, f32x4 b, bf16x8& hi, bf16x8& lo) {
-  hi = pack8(a, b);
-  const f32x4 ra = {a[0] - (float)hi[0], a[1] - (float)hi[1], a[2] - (float)hi[2], a[3] - (float)hi[3]};
-  const f32x4 rb = {b[0] - (float)hi[4], b[1] - (float)hi[5], b[2] - (float)hi[6], b[3] - (float)hi[7]};
-  lo = pack8(ra, rb);
-}
-
-// Three-term bf16 product step for a 16x16x16 fp32 tile: acc += A(4 k) * B(4 k).
-__device__ __forceinline__ f32x4 mma16x3(const float (&a)[4], const float (&b)[4], f32x4 acc) {
-  bf16x4 ah, al, bh, bl;
-  split4(a[0], a[1], a[2], a[3], ah, al);
-  split4(b[0], b[1], b[2], b[3], bh, bl);
-  acc = mma16(ah, bh, acc);
-  acc = mma16(ah, bl, acc);
-  acc = mma16(al, bh, acc);
+// fp32 product step for a 16x16x16 tile, acc += A B, with lane (i, g) holding A[i][4g..4g+3] and
+// B[4g..4g+3][i]: four v_mfma_f32_16x16x4_f32, the m-th contracting the indices 4g + m.
+__device__ __forceinline__ f32x4 mma16f(const float (&a)[4], const float (&b)[4], f32x4 acc) {
+#pragma unroll
+  for (int m = 0; m < 4; ++m) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[m], b[m], acc, 0, 0, 0);
   return acc;
 }
 
