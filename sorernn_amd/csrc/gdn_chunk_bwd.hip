@@ -215,13 +215,17 @@ __device__ __forceinline__ void stage_gates_bwd(ChunkGates& gs, const ChunkBwdPa
 // product it computes.
 template <int KD, int VD>
 __global__ __launch_bounds__(256) void gated_delta_chunk_bwd_prep_kernel(ChunkBwdParams p) {
-  constexpr int KPB = row_pitch<KD>(), VPB = row_pitch<VD>(), KS = KD / 32, VT = VD / 16;
-  // F reuses K's space: K is dead once P is computed. 72 KB at K = V = 128, two workgroups per CU.
-  constexpr int kKF = kC * (KPB > VPB ? KPB : VPB);
-  __shared__ __align__(16) bf16 KFb[kKF], Qb[kC * KPB], dOb[kC * VPB];
-  __shared__ __align__(16) bf16 Pb[kC * kCPb], Tm[kC * kCPb];
+  // Pitches (bf16 elements): 272-byte q/k/dO/F rows and 136-byte P/T rows at K = V = 128. F reuses
+  // K's space and dO Q's: both are dead once P is computed. 53,504 bytes at K = V = 128: three
+  // workgroups per CU.
+  constexpr int KPB = KD + 8, VPB = VD + 8, TPB = kC + 4, KS = KD / 32, VT = VD / 16;
+  constexpr int kTile = kC * (KPB > VPB ? KPB : VPB);
+  __shared__ __align__(16) bf16 KFb[kTile], QOb[kTile];
+  __shared__ __align__(16) bf16 Pb[kC * TPB], Tm[kC * TPB];
   bf16* const Kb = KFb;
   bf16* const Fb = KFb;
+  bf16* const Qb = QOb;
+  bf16* const dOb = QOb;
   __shared__ __align__(16) ChunkGates gs;
   ChunkLoc L;
   if (!locate_chunk(p, blockIdx.x, L)) return;
@@ -243,7 +247,6 @@ __global__ __launch_bounds__(256) void gated_delta_chunk_bwd_prep_kernel(ChunkBw
   if (w == 0) fetch_gates_bwd(graw, braw, p, c0, hv, len, lane);
   put_qk(xk, Kb, KPB, l2, t);
   put_qk(xq, Qb, KPB, l2, t);
-  put_slice(xo, dOb, VPB, t);
   {  // T - I: fp16 rows with tok_col columns -> bf16 natural columns (LDS and the workspace)
 #pragma unroll
     for (int u8 = 0; u8 < Slice<kC, 256>::N; ++u8) {
@@ -252,8 +255,8 @@ __global__ __launch_bounds__(256) void gated_delta_chunk_bwd_prep_kernel(ChunkBw
       const f16x8 x = __builtin_bit_cast(f16x8, xt.x[u8]);
       const bf16x4 lo = to_bf16x4((float)x[0], (float)x[1], (float)x[2], (float)x[3]);
       const bf16x4 hi = to_bf16x4((float)x[4], (float)x[5], (float)x[6], (float)x[7]);
-      *reinterpret_cast<bf16x4*>(Tm + row * kCPb + 32 * u + 4 * gq) = lo;
-      *reinterpret_cast<bf16x4*>(Tm + row * kCPb + 32 * u + 16 + 4 * gq) = hi;
+      *reinterpret_cast<bf16x4*>(Tm + row * TPB + 32 * u + 4 * gq) = lo;
+      *reinterpret_cast<bf16x4*>(Tm + row * TPB + 32 * u + 16 + 4 * gq) = hi;
       if (row < len) {
         bf16* tn = p.tn + ((c0 + row) * p.HV + hv) * kC;
         *reinterpret_cast<bf16x4*>(tn + 32 * u + 4 * gq) = lo;
@@ -269,7 +272,7 @@ __global__ __launch_bounds__(256) void gated_delta_chunk_bwd_prep_kernel(ChunkBw
       const int e = u8 * 256 + t, row = e >> 3, j0 = (e & 7) * 8;
       bf16x8 x;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) x[j] = Tm[(j0 + j) * kCPb + row];
+      for (int j = 0; j < 8; ++j) x[j] = Tm[(j0 + j) * TPB + row];
       if (row < len) *reinterpret_cast<bf16x8*>(p.tnt + ((c0 + row) * p.HV + hv) * kC + j0) = x;
     }
   }
@@ -288,8 +291,10 @@ __global__ __launch_bounds__(256) void gated_delta_chunk_bwd_prep_kernel(ChunkBw
       const int tt = 16 * w + 4 * g4 + r;
       acc[r] = j <= tt ? p.scale * __expf(gs.gam[tt] - gs.gam[j]) * acc[r] : 0.f;
     }
-    put_acc(Pb, kCPb, 16 * w, 16 * jt, lane, acc);
+    put_acc(Pb, TPB, 16 * w, 16 * jt, lane, acc);
   }
+  __syncthreads();
+  put_slice(xo, dOb, VPB, t);  // Q is dead
   __syncthreads();
   // F = (scale P)^T dO, rows (key tokens j) 16w..16w+15 (into K's space: K is dead now)
   f32x4 F[VT];
@@ -298,7 +303,7 @@ __global__ __launch_bounds__(256) void gated_delta_chunk_bwd_prep_kernel(ChunkBw
     F[ct] = f32x4{};
 #pragma unroll
     for (int s = 0; s < 2; ++s)
-      if (s == 1 || w <= 1) F[ct] = mma(frag_col(Pb, kCPb, 32 * s, 16 * w, lane), frag_col(dOb, VPB, 32 * s, 16 * ct, lane), F[ct]);
+      if (s == 1 || w <= 1) F[ct] = mma(frag_col(Pb, TPB, 32 * s, 16 * w, lane), frag_col(dOb, VPB, 32 * s, 16 * ct, lane), F[ct]);
   }
 #pragma unroll
   for (int ct = 0; ct < VT; ++ct) put_acc(Fb, VPB, 16 * w, 16 * ct, lane, F[ct]);
@@ -308,7 +313,7 @@ __global__ __launch_bounds__(256) void gated_delta_chunk_bwd_prep_kernel(ChunkBw
   for (int ct = 0; ct < VT; ++ct) {
 #pragma unroll
     for (int u = 0; u < 2; ++u)
-      if (u == 1 || w <= 1) F[ct] = mma(frag_col(Tm, kCPb, 32 * u, 16 * w, lane), frag_col(Fb, VPB, 32 * u, 16 * ct, lane), F[ct]);
+      if (u == 1 || w <= 1) F[ct] = mma(frag_col(Tm, TPB, 32 * u, 16 * w, lane), frag_col(Fb, VPB, 32 * u, 16 * ct, lane), F[ct]);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int tt = 16 * w + 4 * g4 + r;
