@@ -363,67 +363,95 @@ __global__ __launch_bounds__(256, 1) void gated_delta_chunk_bwd_state_kernel(Chu
   const int nc = (int)((eos - bos + kC - 1) / kC);
   const bool l2 = p.flags & GDN_FLAG_QK_L2NORM;
 
-  auto load_chunk = [&](int c, int slot, int tl) {  // tl = 0..127 (waves 2, 3): all loads, then the LDS writes
-    const int64_t c0 = bos + (int64_t)c * kC;
-    const int len = (int)((eos - c0) < kC ? (eos - c0) : kC);
+  // Loader waves (2, 3; tl = 0..127): a chunk's tiles are fetched into registers a step before they
+  // are written to LDS, so each step hides a step of load latency.
+  struct ChunkRegs {
     QKRows<KD, 128> xk, xq;
     Slice<kC, 128> xt;
     Slice<32, 128> xo;
     Slice<64, 128> xg;  // the G1 slice: 32 fp32 = 128 bytes per row, handled as 64 16-bit columns
-    fetch_qk(xk, static_cast<const bf16*>(p.k) + (c0 * p.H + h) * KD, p.H, len, tl);
-    fetch_qk(xq, static_cast<const bf16*>(p.q) + (c0 * p.H + h) * KD, p.H, len, tl);
-    fetch_slice(xt, p.tn + (c0 * p.HV + hv) * kC, (uint32_t)(p.HV * kC * 2), len, tl);
-    fetch_slice(xo, static_cast<const bf16*>(p.dout) + (c0 * p.HV + hv) * VD + vb * 32, (uint32_t)(p.HV * VD * 2), len, tl);
-    fetch_slice(xg, p.g1 + (c0 * p.HV + hv) * VD + vb * 32, (uint32_t)(p.HV * VD * 4), len, tl);
-    uint32_t graw = 0, braw = 0;
-    if (w == 2) fetch_gates_bwd(graw, braw, p, c0, hv, len, lane);
-    put_qk(xk, Kb[slot], KPB, l2, tl);
-    put_qk(xq, Qb[slot], KPB, l2, tl);
-    put_slice(xt, Tm[slot], kCPb, tl);
-    put_slice(xo, dOs[slot], OP, tl);
-    put_slice(xg, G1s[slot], GP, tl);
-    if (w == 2) put_gates_bwd(gv[slot], graw, braw, p, hv, len, lane);
+    uint32_t graw, braw;
+    int len;
+  };
+  auto fetch_chunk = [&](ChunkRegs& r, int c, int tl) {
+    const int64_t c0 = bos + (int64_t)c * kC;
+    r.len = (int)((eos - c0) < kC ? (eos - c0) : kC);
+    fetch_qk(r.xk, static_cast<const bf16*>(p.k) + (c0 * p.H + h) * KD, p.H, r.len, tl);
+    fetch_qk(r.xq, static_cast<const bf16*>(p.q) + (c0 * p.H + h) * KD, p.H, r.len, tl);
+    fetch_slice(r.xt, p.tn + (c0 * p.HV + hv) * kC, (uint32_t)(p.HV * kC * 2), r.len, tl);
+    fetch_slice(r.xo, static_cast<const bf16*>(p.dout) + (c0 * p.HV + hv) * VD + vb * 32, (uint32_t)(p.HV * VD * 2),
+                r.len, tl);
+    fetch_slice(r.xg, p.g1 + (c0 * p.HV + hv) * VD + vb * 32, (uint32_t)(p.HV * VD * 4), r.len, tl);
+    r.graw = r.braw = 0;
+    if (w == 2) fetch_gates_bwd(r.graw, r.braw, p, c0, hv, r.len, lane);
+  };
+  auto put_chunk = [&](const ChunkRegs& r, int slot, int tl) {
+    put_qk(r.xk, Kb[slot], KPB, l2, tl);
+    put_qk(r.xq, Qb[slot], KPB, l2, tl);
+    put_slice(r.xt, Tm[slot], kCPb, tl);
+    put_slice(r.xo, dOs[slot], OP, tl);
+    put_slice(r.xg, G1s[slot], GP, tl);
+    if (w == 2) put_gates_bwd(gv[slot], r.graw, r.braw, p, hv, r.len, lane);
   };
 
-  const int sw = w & 1, col = vb * 32 + 16 * sw + li;  // state waves: value column of this lane
-  f32x4 dS[KT];
+  // Each role runs its own loop of nc steps with one barrier each (the counts match), so the
+  // loaders' registers in flight are not live through the state waves' code.
   if (w < 2) {
+    const int sw = w & 1, col = vb * 32 + 16 * sw + li;  // value column of this lane
+    f32x4 dS[KT];
 #pragma unroll
     for (int a = 0; a < KT; ++a)
 #pragma unroll
       for (int r = 0; r < 4; ++r)
         dS[a][r] = p.dht ? p.dht[((n * p.HV + hv) * KD + 16 * a + 4 * g4 + r) * VD + col] : 0.f;
-  } else if (nc > 0) {
-    load_chunk(nc - 1, 0, t - 128);
-  }
-  __syncthreads();
-
-  for (int i = 0; i < nc; ++i) {
-    const int c = nc - 1 - i, slot = i & 1;
-    if (w < 2) {
-      // dS' of chunk c (the gradient of the state leaving it), bf16, transposed: keys 16a + 4g..+3 of column col
-      bf16* dp = p.dhs + (((cgb + c) * p.HV + hv) * VD + col) * (int64_t)KD + 4 * g4;
-#pragma unroll
-      for (int a = 0; a < KT; ++a)
-        *reinterpret_cast<bf16x4*>(dp + 16 * a) = to_bf16x4(dS[a][0], dS[a][1], dS[a][2], dS[a][3]);
+    __syncthreads();
+    for (int i = 0; i < nc; ++i) {
+      const int c = nc - 1 - i, slot = i & 1;
       const bf16* kb = Kb[slot];
       const bf16* qb = Qb[slot];
       const bf16* tm = Tm[slot];
       const ChunkGates& G = gv[slot];
-      // W1 = K dS': contraction slots (g, j) hold keys 32s + 4g + j and 32s + 16 + 4g + j
-      f32x4 W[4];
-#pragma unroll
-      for (int b = 0; b < 4; ++b) W[b] = f32x4{};
+      // W1 = K dS': contraction slots (g, j) hold keys 32s + 4g + j and 32s + 16 + 4g + j. Every
+      // K fragment is read before the first MFMA.
+      bf16x8 sb[KS], kf[KS][4];
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        const bf16x8 sb = pack8(dS[2 * s], dS[2 * s + 1]);
+        sb[s] = pack8(dS[2 * s], dS[2 * s + 1]);
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
           const bf16* kr = kb + (16 * b + li) * KPB + 32 * s + 4 * g4;
           const bf16x4 k0 = ld4b(kr), k1 = ld4b(kr + 16);
-          W[b] = mma(bf16x8{k0[0], k0[1], k0[2], k0[3], k1[0], k1[1], k1[2], k1[3]}, sb, W[b]);
+          kf[s][b] = bf16x8{k0[0], k0[1], k0[2], k0[3], k1[0], k1[1], k1[2], k1[3]};
         }
       }
+      __builtin_amdgcn_sched_barrier(0);
+      f32x4 W[4];
+#pragma unroll
+      for (int b = 0; b < 4; ++b) W[b] = f32x4{};
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) W[b] = mma(kf[s][b], sb[s], W[b]);
+      // dS' of chunk c (the gradient of the state leaving it) from the bf16 operand just built,
+      // transposed: keys 32s + 4g..+3 (tile 2s) and 32s + 16 + 4g..+3 (tile 2s + 1) of column col
+      {
+        bf16* dp = p.dhs + (((cgb + c) * p.HV + hv) * VD + col) * (int64_t)KD + 4 * g4;
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          *reinterpret_cast<bf16x4*>(dp + 32 * s) = bf16x4{sb[s][0], sb[s][1], sb[s][2], sb[s][3]};
+          *reinterpret_cast<bf16x4*>(dp + 32 * s + 16) = bf16x4{sb[s][4], sb[s][5], sb[s][6], sb[s][7]};
+        }
+      }
+      // (T - I)^T fragments for dX
+      bf16x8 tf[4][2];
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+          if (u == 1 || b <= 1) {
+            const bf16x4 t0 = ld4_tr(tm, kCPb, 32 * u, 16 * b, lane), t1 = ld4_tr(tm, kCPb, 32 * u + 16, 16 * b, lane);
+            tf[b][u] = bf16x8{t0[0], t0[1], t0[2], t0[3], t1[0], t1[1], t1[2], t1[3]};
+          }
       // dX = G1 + Z + (T - I)^T Z, Z = r o W1 (token pairs 32u + 4g + r, 32u + 16 + 4g + r)
       f32x4 X[4];
 #pragma unroll
@@ -439,10 +467,7 @@ __global__ __launch_bounds__(256, 1) void gated_delta_chunk_bwd_state_kernel(Chu
       for (int b = 0; b < 4; ++b)
 #pragma unroll
         for (int u = 0; u < 2; ++u)
-          if (u == 1 || b <= 1) {
-            const bf16x4 t0 = ld4_tr(tm, kCPb, 32 * u, 16 * b, lane), t1 = ld4_tr(tm, kCPb, 32 * u + 16, 16 * b, lane);
-            X[b] = mma(bf16x8{t0[0], t0[1], t0[2], t0[3], t1[0], t1[1], t1[2], t1[3]}, zb[u], X[b]);
-          }
+          if (u == 1 || b <= 1) X[b] = mma(tf[b][u], zb[u], X[b]);
       // dY = -beta a dX; scale a dO
 #pragma unroll
       for (int b = 0; b < 4; ++b)
@@ -459,29 +484,59 @@ __global__ __launch_bounds__(256, 1) void gated_delta_chunk_bwd_state_kernel(Chu
           qa[u][4 + m] = static_cast<bf16>(p.scale * G.egam[32 * u + 16 + 4 * g4 + m] * (float)d1[m]);
         }
       }
-      // dS = e^{gam_c} dS' + K^T dY + Q^T (scale a dO)
+      // dS = e^{gam_c} dS' + K^T dY + Q^T (scale a dO), in two halves of the key tiles, each half's
+      // K^T and Q^T fragments read before its MFMAs
       const float ac = G.egam[kC - 1];
 #pragma unroll
-      for (int a = 0; a < KT; ++a) {
-        dS[a] *= ac;
+      for (int hh = 0; hh < 2; ++hh) {
+        bf16x8 ktf[KT / 2][2], qtf[KT / 2][2];
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const bf16x4 k0 = ld4_tr(kb, KPB, 32 * u, 16 * a, lane), k1 = ld4_tr(kb, KPB, 32 * u + 16, 16 * a, lane);
-          dS[a] = mma(bf16x8{k0[0], k0[1], k0[2], k0[3], k1[0], k1[1], k1[2], k1[3]}, yb[u], dS[a]);
-          const bf16x4 q0 = ld4_tr(qb, KPB, 32 * u, 16 * a, lane), q1 = ld4_tr(qb, KPB, 32 * u + 16, 16 * a, lane);
-          dS[a] = mma(bf16x8{q0[0], q0[1], q0[2], q0[3], q1[0], q1[1], q1[2], q1[3]}, qa[u], dS[a]);
+        for (int aa = 0; aa < KT / 2; ++aa)
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const int a = hh * (KT / 2) + aa;
+            const bf16x4 k0 = ld4_tr(kb, KPB, 32 * u, 16 * a, lane), k1 = ld4_tr(kb, KPB, 32 * u + 16, 16 * a, lane);
+            ktf[aa][u] = bf16x8{k0[0], k0[1], k0[2], k0[3], k1[0], k1[1], k1[2], k1[3]};
+            const bf16x4 q0 = ld4_tr(qb, KPB, 32 * u, 16 * a, lane), q1 = ld4_tr(qb, KPB, 32 * u + 16, 16 * a, lane);
+            qtf[aa][u] = bf16x8{q0[0], q0[1], q0[2], q0[3], q1[0], q1[1], q1[2], q1[3]};
+          }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int aa = 0; aa < KT / 2; ++aa) {
+          const int a = hh * (KT / 2) + aa;
+          dS[a] *= ac;
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            dS[a] = mma(ktf[aa][u], yb[u], dS[a]);
+            dS[a] = mma(qtf[aa][u], qa[u], dS[a]);
+          }
         }
       }
-    } else if (i + 1 < nc) {
-      load_chunk(c - 1, slot ^ 1, t - 128);
+      __syncthreads();
+    }
+    if (p.dh0) {
+#pragma unroll
+      for (int a = 0; a < KT; ++a)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) p.dh0[((n * p.HV + hv) * KD + 16 * a + 4 * g4 + r) * VD + col] = dS[a][r];
+    }
+  } else {
+    const int tl = t - 128;
+    ChunkRegs nx;  // the next chunk's tiles, in flight across a step
+    if (nc > 0) {
+      fetch_chunk(nx, nc - 1, tl);
+      put_chunk(nx, 0, tl);
+      if (nc > 1) fetch_chunk(nx, nc - 2, tl);
     }
     __syncthreads();
-  }
-  if (w < 2 && p.dh0) {
-#pragma unroll
-    for (int a = 0; a < KT; ++a)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) p.dh0[((n * p.HV + hv) * KD + 16 * a + 4 * g4 + r) * VD + col] = dS[a][r];
+    for (int i = 0; i < nc; ++i) {
+      const int c = nc - 1 - i, slot = i & 1;
+      if (i + 1 < nc) {
+        put_chunk(nx, slot ^ 1, tl);                  // chunk c - 1, fetched a step ago
+        if (i + 2 < nc) fetch_chunk(nx, c - 2, tl);  // chunk c - 2
+      }
+      __syncthreads();
+    }
   }
 }
 
