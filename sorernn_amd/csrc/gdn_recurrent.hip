@@ -306,6 +306,19 @@ __global__ __launch_bounds__(256) void gated_delta_decode_w4_kernel(DecodeParams
     const int par = r & 1;
     const int64_t sbase = (b * p.HV + hv) * (int64_t)D * D;
     const int64_t ch_v = 2 * p.H * D + (int64_t)hv * D + t;
+    // The state first, so that the step's 64 KB per head is in flight before the conv window and
+    // gate loads: through a buffer resource (one lane offset plus a scalar offset per row step, so
+    // the 16 row addresses take no registers), non-temporal (the state is touched once a step).
+    float4 s[RPT];
+    const auto rs = make_rsrc(p.state + sbase, (uint32_t)(D * D * 4));
+    const int voff = ((rg * D) + w * VB + 4 * cg) * 4;
+    if (w < NWB) {
+#pragma unroll
+      for (int i = 0; i < RPT; ++i) {
+        const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, i * RG * D * 4, 2);
+        s[i] = __builtin_bit_cast(float4, x);
+      }
+    }
     Win wq{}, wv{};
     T xq{}, xv{};
     float4 kq{}, kv{};
@@ -322,18 +335,6 @@ __global__ __launch_bounds__(256) void gated_delta_decode_w4_kernel(DecodeParams
     }
     const uint32_t graw = load_raw32(p.g, p.dg, b * p.HV + hv);
     const uint32_t braw = load_raw32(p.beta, p.db, b * p.HV + hv);
-    float4 s[RPT];
-    // the state through a buffer resource: one lane offset plus a scalar offset per row step, so
-    // the 16 row addresses take no registers; loads non-temporal (the state is touched once a step)
-    const auto rs = make_rsrc(p.state + sbase, (uint32_t)(D * D * 4));
-    const int voff = ((rg * D) + w * VB + 4 * cg) * 4;
-    if (w < NWB) {
-#pragma unroll
-      for (int i = 0; i < RPT; ++i) {
-        const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, i * RG * D * 4, 2);
-        s[i] = __builtin_bit_cast(float4, x);
-      }
-    }
     if (do_qk) {
       const float y = kq.x * elem_to_f32(wq.v[1]) + kq.y * elem_to_f32(wq.v[2]) + kq.z * elem_to_f32(wq.v[3]) +
                       kq.w * elem_to_f32(xq);
