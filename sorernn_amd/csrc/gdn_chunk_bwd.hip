@@ -177,18 +177,6 @@ __device__ __forceinline__ void put_slice(const Slice<W, NT>& r, E* dst, int pit
     *reinterpret_cast<u32x4*>(dst + row * pitch + ch * EPC) = r.x[u];
   }
 }
-template <int KD, int NT>
-__device__ __forceinline__ void stage_qk_rows(bf16* dst, int pitch, const bf16* src, int64_t H, int len, bool l2, int tid) {
-  QKRows<KD, NT> r;
-  fetch_qk(r, src, H, len, tid);
-  put_qk(r, dst, pitch, l2, tid);
-}
-template <int W, int NT>
-__device__ __forceinline__ void stage_slice(bf16* dst, int pitch, const bf16* src, uint32_t rb, int len, int tid) {
-  Slice<W, NT> r;
-  fetch_slice(r, src, rb, len, tid);
-  put_slice(r, dst, pitch, tid);
-}
 // Gate terms of a chunk (one wave, lane = token), as the forward computes them: raw loads, then the put.
 __device__ __forceinline__ void fetch_gates_bwd(uint32_t& graw, uint32_t& braw, const ChunkBwdParams& p, int64_t c0,
                                                 int64_t hv, int len, int lane) {
@@ -202,12 +190,6 @@ __device__ __forceinline__ void put_gates_bwd(ChunkGates& gs, uint32_t graw, uin
                                               int64_t hv, int len, int lane) {
   chunk_gates_from_raw(gs, graw, braw, p.dg, p.db, len, p.flags, p.A_log ? p.A_log[hv] : 0.f,
                        p.dt_bias ? p.dt_bias[hv] : 0.f, lane);
-}
-__device__ __forceinline__ void stage_gates_bwd(ChunkGates& gs, const ChunkBwdParams& p, int64_t c0, int64_t hv, int len,
-                                                int lane) {
-  uint32_t graw, braw;
-  fetch_gates_bwd(graw, braw, p, c0, hv, len, lane);
-  put_gates_bwd(gs, graw, braw, p, hv, len, lane);
 }
 
 // ================================================================== 1. prep: T - I (natural) and G1
@@ -583,8 +565,13 @@ __global__ __launch_bounds__(256, 2) void gated_delta_chunk_bwd_grad_kernel(Chun
   const int64_t c0 = L.c0, cg = blockIdx.x;
   const uint32_t vrow = (uint32_t)(p.HV * VD * 2), trow = (uint32_t)(p.HV * kC * 2), grow = (uint32_t)(p.HV * VD * 4);
 
-  stage_qk_rows<KD, 256>(Kb, KPB, static_cast<const bf16*>(p.k) + (c0 * p.H + h) * KD, p.H, len, l2, t);
-  stage_qk_rows<KD, 256>(Qb, KPB, static_cast<const bf16*>(p.q) + (c0 * p.H + h) * KD, p.H, len, l2, t);
+  {  // K and Q rows: both tiles' loads in flight before the first LDS write
+    QKRows<KD, 256> xk, xq;
+    fetch_qk(xk, static_cast<const bf16*>(p.k) + (c0 * p.H + h) * KD, p.H, len, t);
+    fetch_qk(xq, static_cast<const bf16*>(p.q) + (c0 * p.H + h) * KD, p.H, len, t);
+    put_qk(xk, Kb, KPB, l2, t);
+    put_qk(xq, Qb, KPB, l2, t);
+  }
 
   f32x4 dqa[KT], dka[KT];
 #pragma unroll
