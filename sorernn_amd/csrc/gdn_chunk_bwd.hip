@@ -526,11 +526,10 @@ __global__ __launch_bounds__(256, 1) void gated_delta_chunk_bwd_state_kernel(Chu
 // One workgroup of 4 waves per (chunk, q/k head), looping over the value heads of the head (GVA:
 // dq and dk are summed in registers) and, per value head, over 32-column passes of V. Wave w owns
 // the tokens 16w..16w+15 of every product: the pass's two 16-column tiles, the c x c tiles (w, jt)
-// with jt <= w, and all key tiles of dq and dk, so per-token sums stay inside a wave. 77 KB of LDS
-// and at most 256 VGPRs: two workgroups share a CU, so one's loads and barriers overlap the
-// other's MFMAs. The row
-// scalings of the state terms (scale e^gam of dQ_S, -beta e^gam of dY, r of Delta) are applied to
-// the A fragments per lane (a lane's A row is one token).
+// with jt <= w, and all key tiles of dq and dk, so per-token sums stay inside a wave. 80,160 bytes
+// of LDS and at most 256 VGPRs: two workgroups share a CU, so one's loads and barriers overlap the
+// other's MFMAs. The row scalings of the state terms (scale e^gam of dQ_S, -beta e^gam of dY, r of
+// Delta) are applied to the A fragments per lane (a lane's A row is one token).
 template <int KD, int VD>
 __global__ __launch_bounds__(256, 2) void gated_delta_chunk_bwd_grad_kernel(ChunkBwdParams p) {
   constexpr int KPB = KD + 8, KS = KD / 32, KT = KD / 16, NP = VD / 32;
