@@ -163,6 +163,32 @@ def test_chunk_varlen_config3_matches_recurrent_kernel():
     assert_state_close(st, st_r)
 
 
+@pytest.mark.parametrize("varlen", [False, True], ids=["batched", "varlen"])
+def test_tsolve_chunk_walk_covers_every_chunk(varlen):
+    """The T-solve kernel's workgroups each solve several chunks of one value head in turn (stride =
+    the grid's width). At 64 value heads and 102 chunks per head, a 256-CU device gets 15 workgroups
+    per head, some walking 7 chunks and some 6, with a partial last chunk per sequence; with cu_seqlens
+    the walk runs over an upper bound on the chunk count. Every output row and final state must match
+    the GPU recurrent kernel (the exact fp32 token-by-token path)."""
+    if varlen:
+        gen = torch.Generator().manual_seed(7)
+        lengths = (torch.randint(1, 400, (37,), generator=gen)).tolist()
+        cu = torch.tensor([0] + torch.tensor(lengths).cumsum(0).tolist(), dtype=torch.int64)
+        inp = gdn_inputs(1, int(cu[-1]), 16, 64, HV=64, dtype=torch.bfloat16, seed=8, h0=True, n_states=37,
+                         cu_seqlens=cu)
+    else:
+        inp = gdn_inputs(2, 3211, 16, 64, HV=64, dtype=torch.bfloat16, seed=8, h0=True)
+    print("T-solve walk", "varlen" if varlen else "batched", tuple(inp.q.shape), flush=True)
+    o, st = _chunk(inp)
+    d = inp.to(DEV)
+    o_r, st_r = fused_recurrent_gated_delta_rule(d.q, d.k, d.v, d.g, d.beta, scale=inp.scale, initial_state=d.h0,
+                                                 output_final_state=True, cu_seqlens=d.cu_seqlens,
+                                                 cu_seqlens_cpu=inp.cu_seqlens)
+    torch.cuda.synchronize()
+    assert_output_close(o, o_r.float())
+    assert_state_close(st, st_r)
+
+
 def test_varlen_generator_sums_exactly():
     cu = varlen_cu_seqlens(8, 32768, 512, 8192, 1003)
     assert cu[0] == 0 and cu[-1] == 32768 and (cu[1:] > cu[:-1]).all()
