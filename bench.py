@@ -4,6 +4,10 @@
 ``python bench.py [--gpus 1] [--steps K] [--warmup W]`` prints ONE JSON line. A step is one
 ``chunk_gated_delta_rule`` call over BASELINE config 1 (B=4, T=4096, H=16, d_k=d_v=128, bf16 q/k/v,
 fp32 g/beta/h0, final state out), inputs already resident in HBM; ``value`` is prefill tokens/s.
+Every workload first runs its own step untimed for 100 ms (``settle``: from idle the GPU's clocks
+need ~35 ms of this load to reach their sustained rate), then W warmup steps, then the K timed steps;
+``cold_ms_per_step`` / ``cold_value`` report the prefill's first K steps after W warmup steps
+without that phase.
 
 The same line carries
 - ``roofline``: the chunked prefill op -- its two kernels, gated_delta_chunk_prep_kernel (the
@@ -106,7 +110,7 @@ def train_step_times(torch, inp, steps: int):
 
     for _ in range(2):
         bwd(*fwd())
-    torch.cuda.synchronize()
+    settle(torch, lambda: bwd(*fwd()))
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
     tf = tb = 0.0
     for _ in range(steps):
@@ -168,6 +172,7 @@ def block_pair(torch, steps: int) -> dict:
                          ("attn_layer", lambda: attn(x))):
             for _ in range(2):
                 fn()
+            settle(torch, fn)
             ms, _ = time_launches(torch, fn, steps)
             out[f"{name}_ms"] = round(ms, 4)
         # the attention kernel alone on the layer's own q, k, v, gate
@@ -178,6 +183,7 @@ def block_pair(torch, steps: int) -> dict:
         v, gate = proj[..., 2 * nq + nkv:], proj[..., nq:2 * nq]
         fa = lambda: gated_attention(q, k, v, gate)  # noqa: E731
         fa()
+        settle(torch, fa)
         _, fa_ms = time_launches(torch, fa, steps)
         fl = attn_flops(B, T, H, Dh)
     pair_ms = out["gdn_layer_ms"] + out["attn_layer_ms"]
@@ -222,6 +228,31 @@ def time_back_to_back(torch, fn, steps: int) -> float:
     e1.record(stream)
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / steps
+
+
+SETTLE_MS = 100.0  # default untimed run of a workload's own step before its warmup steps
+_settle_ms = SETTLE_MS  # this process's value (--settle-ms)
+
+
+def settle(torch, fn, ms: float | None = None) -> dict:
+    """Runs `fn` untimed, back to back, for at least `ms` milliseconds (default: --settle-ms; a
+    device sync every 8 calls).
+
+    From idle this GPU's clocks take about 35 ms of this kind of load to settle: the first 50
+    prefill steps of a fresh process run at ~157 us, the steady state at ~131 us. The same time
+    spent on bf16 GEMMs or device copies does not settle them, and a 200 ms pause undoes it. The
+    timed steps then measure the sustained rate a training or serving loop runs at; the prefill
+    part also reports its first K steps without this phase."""
+    ms = _settle_ms if ms is None else ms
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    calls = 0
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(8):
+            fn()
+        calls += 8
+        torch.cuda.synchronize()
+    return {"calls": calls, "ms": round((time.perf_counter() - t0) * 1e3, 1)}
 
 
 def launch_percentiles(torch, fn, steps: int) -> dict:
@@ -337,7 +368,8 @@ def run_only(torch, args) -> int:
     if args.only == "varlen_docs":
         _, cu_cpu, inp = varlen_docs_inputs(torch)
         d = inp.to("cuda")
-        for _ in range(args.warmup + args.steps):
+
+        def step(i):
             chunk_gated_delta_rule(d.q, d.k, d.v, d.g, d.beta, scale=inp.scale, cu_seqlens=d.cu_seqlens,
                                    cu_seqlens_cpu=cu_cpu)
     elif args.only in ("prefill", "varlen"):
@@ -345,7 +377,8 @@ def run_only(torch, args) -> int:
         inp = config_inputs(idx)
         cu_cpu = inp.cu_seqlens
         d = inp.to("cuda")
-        for _ in range(args.warmup + args.steps):
+
+        def step(i):
             chunk_gated_delta_rule(d.q, d.k, d.v, d.g, d.beta, scale=d.scale, initial_state=d.h0,
                                    output_final_state=True, cu_seqlens=d.cu_seqlens, cu_seqlens_cpu=cu_cpu)
     else:
@@ -356,10 +389,16 @@ def run_only(torch, args) -> int:
         nrot = 5 if args.only == "decode_rot" else 1
         states = [st] + [st.clone() for _ in range(nrot - 1)]
         convs = [cs] + [cs.clone() for _ in range(nrot - 1)]
-        for i in range(args.warmup + args.steps):
+
+        def step(i):
             gated_delta_decode_step(x, convs[i % nrot], cw, g, b, states[i % nrot], di.H, di.HV, di.D)
+    # as in the bench: the workload's own step untimed for the settle time, then W + K launches (the
+    # last K of a trace are the ones the bench times)
+    st_ = settle(torch, lambda: step(0))
+    for i in range(args.warmup + args.steps):
+        step(i)
     torch.cuda.synchronize()
-    print(f"ran {args.only}: {args.warmup + args.steps} launches", flush=True)
+    print(f"ran {args.only}: {st_['calls']} settle launches, then {args.warmup + args.steps} launches", flush=True)
     return 0
 
 
@@ -399,6 +438,12 @@ def part_prefill(torch, args) -> dict:
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    # the first K steps of the process after W warmup steps (reported beside the headline)
+    cold_ms = time_back_to_back(torch, step, args.steps)
+    st = settle(torch, step)
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
     # the step rate from back-to-back calls with events only around the whole run; the per-launch
     # (op) times from a second run with an event pair around every call
     t0 = time.perf_counter()
@@ -417,7 +462,7 @@ def part_prefill(torch, args) -> dict:
 
     pct_rot = launch_percentiles(torch, step_alt, args.steps)
     return {"B": B, "T": T, "H": H, "K": K, "ms_step": ms_step, "ms_launch": ms_launch, "wall_ms": wall,
-            "pct": pct, "pct_rot": pct_rot,
+            "pct": pct, "pct_rot": pct_rot, "cold_ms_step": cold_ms, "settle": st,
             "min_bytes": 4 * inp.q.numel() * 2 + 2 * inp.g.numel() * 4 + 2 * inp.h0.numel() * 4}
 
 
@@ -438,6 +483,7 @@ def part_decode(torch, args) -> dict:
 
     for _ in range(10):
         dstep()
+    settle(torch, dstep)
     eager_ms, _ = time_launches(torch, dstep, min(args.decode_steps, 200))
     per_graph = 50  # steps per captured graph: one graph launch per 50 steps keeps the host off the critical path
 
@@ -478,6 +524,7 @@ def part_varlen(torch, args) -> dict:
 
     for _ in range(3):
         vstep()
+    settle(torch, vstep)
     n = max(5, args.steps // 5)
     v_ms, v_launch = time_launches(torch, vstep, n)
     v_pct = launch_percentiles(torch, lambda i: vstep(), n)
@@ -500,6 +547,7 @@ def part_varlen_docs(torch, args) -> dict:
 
     for _ in range(3):
         step()
+    settle(torch, step)
     n = max(5, args.steps // 5)
     ms, launch = time_launches(torch, step, n)
     pct = launch_percentiles(torch, lambda i: step(), n)
@@ -565,6 +613,13 @@ def assemble(parts: dict, args, cpu: dict | None) -> dict:
         "warmup": args.warmup,
         "ms_per_step": round(ms_step, 4),
         "wall_ms_per_step": round(pf["wall_ms"], 4),
+        "cold_ms_per_step": round(pf["cold_ms_step"], 4) if "cold_ms_step" in pf else None,
+        "cold_value": round(B * T / (pf["cold_ms_step"] * 1e-3), 1) if "cold_ms_step" in pf else None,
+        "settle": {"ms_per_workload": args.settle_ms, "prefill_calls": pf.get("settle", {}).get("calls"),
+                   "note": "every workload runs its own step untimed, back to back, for >= settle ms before "
+                           "its W warmup steps (from idle the GPU's clocks settle after ~35 ms of this load); "
+                           "cold_ms_per_step / cold_value are the process's first K prefill steps after W "
+                           "warmup steps, without the settle phase"},
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -645,7 +700,7 @@ def run_part(part: str, args) -> dict:
     """Run one workload in a child process and return the JSON object it prints last. Its stderr
     (progress) passes through; a failing child ends the bench with the child's status."""
     cmd = [sys.executable, "-u", os.path.abspath(__file__), "--part", part, "--steps", str(args.steps),
-           "--warmup", str(args.warmup), "--decode-steps", str(args.decode_steps)]
+           "--warmup", str(args.warmup), "--decode-steps", str(args.decode_steps), "--settle-ms", str(args.settle_ms)]
     res = subprocess.run(cmd, stdout=subprocess.PIPE, text=True)
     if res.returncode != 0:
         print(f"bench.py: workload {part} failed (status {res.returncode}); output:\n{res.stdout}", file=sys.stderr)
@@ -666,11 +721,15 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 256 MiB device copy (the reference kernel for PMC byte counters)")
+    ap.add_argument("--settle-ms", type=float, default=SETTLE_MS,
+                    help="untimed run of each workload's own step before its warmup steps (0: none)")
     ap.add_argument("--only", choices=list(PARTS) + ["decode_rot"], default=None,
                     help="run one workload only (for profiler runs); prints no JSON line")
     ap.add_argument("--part", choices=PARTS, default=None,
                     help="(internal) run one workload and print its raw measurements as JSON")
     args = ap.parse_args()
+    global _settle_ms
+    _settle_ms = args.settle_ms
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(f"bench.py: this build runs one GPU only (the GDN op needs no collective: every (sequence, head) "
               f"chain is independent); got --gpus {args.gpus}. Run with --gpus 1.", file=sys.stderr)

@@ -14,7 +14,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
 def _args(**kw):
-    base = dict(gpus=1, steps=50, warmup=5, decode_steps=1000, no_cpu_baseline=True)
+    base = dict(gpus=1, steps=50, warmup=5, decode_steps=1000, no_cpu_baseline=True, settle_ms=bench.SETTLE_MS)
     base.update(kw)
     return argparse.Namespace(**base)
 
@@ -23,7 +23,8 @@ def _fake_parts():
     pct = {"p10_ms": 0.16, "median_ms": 0.17, "p90_ms": 0.18}
     return {
         "prefill": {"B": 4, "T": 4096, "H": 16, "K": 128, "ms_step": 0.17, "ms_launch": 0.168, "wall_ms": 0.2,
-                    "pct": pct, "pct_rot": pct, "min_bytes": 278921216},
+                    "pct": pct, "pct_rot": pct, "min_bytes": 278921216, "cold_ms_step": 0.2,
+                    "settle": {"calls": 640, "ms": 100.2}},
         "decode": {"us_step": 25.0, "rot_us_step": 32.0, "eager_us_step": 40.0, "per_graph": 50},
         "varlen": {"ms_step": 0.4, "ms_launch": 0.39, "pct": pct, "lens": [4096] * 8},
         "varlen_docs": {"ms_step": 0.5, "ms_launch": 0.49, "pct": pct, "lens": [100, 4000, 28668]},
@@ -41,6 +42,9 @@ def test_assembled_line_keeps_the_driver_contract():
         assert key in line, key
     assert line["n_gpus"] == 1 and line["higher_is_better"] is True and line["vs_baseline"] is None
     assert line["value"] == pytest.approx(4 * 4096 / 0.17e-3, rel=1e-6)
+    # the first K steps without the settle phase are reported beside the headline
+    assert line["cold_ms_per_step"] == 0.2 and line["cold_value"] == pytest.approx(4 * 4096 / 0.2e-3, rel=1e-6)
+    assert line["settle"]["prefill_calls"] == 640 and line["settle"]["ms_per_workload"] == bench.SETTLE_MS
     rf = line["roofline"]
     assert set(("bound", "achieved", "peak", "unit", "frac", "traffic")) <= set(rf)
     assert rf["achieved"] == pytest.approx(47_244_640_256 / 0.168e-3 / 1e12, rel=1e-3)
