@@ -259,13 +259,16 @@ __global__ __launch_bounds__(256) void gated_delta_chunk_bwd_prep_kernel(ChunkBw
     }
   }
 
-  // scale P = scale (Q K^T) o E (j <= t), rows 16w..16w+15
+  // scale P = scale (Q K^T) o E (j <= t), rows 16w..16w+15 (this wave's Q fragments read once)
+  bf16x8 qw[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) qw[s] = frag_row(Qb, KPB, 16 * w, 32 * s, lane);
 #pragma unroll
   for (int jt = 0; jt < 4; ++jt) {
     f32x4 acc = f32x4{};
     if (jt <= w) {
 #pragma unroll
-      for (int s = 0; s < KS; ++s) acc = mma(frag_row(Qb, KPB, 16 * w, 32 * s, lane), frag_row(Kb, KPB, 16 * jt, 32 * s, lane), acc);
+      for (int s = 0; s < KS; ++s) acc = mma(qw[s], frag_row(Kb, KPB, 16 * jt, 32 * s, lane), acc);
     }
     const int j = 16 * jt + li;
 #pragma unroll
@@ -278,24 +281,30 @@ __global__ __launch_bounds__(256) void gated_delta_chunk_bwd_prep_kernel(ChunkBw
   __syncthreads();
   put_slice(xo, dOb, VPB, t);  // Q is dead
   __syncthreads();
-  // F = (scale P)^T dO, rows (key tokens j) 16w..16w+15 (into K's space: K is dead now)
+  // F = (scale P)^T dO, rows (key tokens j) 16w..16w+15 (into K's space: K is dead now); this
+  // wave's P^T fragments serve every value tile: read once
   f32x4 F[VT];
+  bf16x8 pw[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) pw[s] = frag_col(Pb, TPB, 32 * s, 16 * w, lane);
 #pragma unroll
   for (int ct = 0; ct < VT; ++ct) {
     F[ct] = f32x4{};
 #pragma unroll
     for (int s = 0; s < 2; ++s)
-      if (s == 1 || w <= 1) F[ct] = mma(frag_col(Pb, TPB, 32 * s, 16 * w, lane), frag_col(dOb, VPB, 32 * s, 16 * ct, lane), F[ct]);
+      if (s == 1 || w <= 1) F[ct] = mma(pw[s], frag_col(dOb, VPB, 32 * s, 16 * ct, lane), F[ct]);
   }
 #pragma unroll
   for (int ct = 0; ct < VT; ++ct) put_acc(Fb, VPB, 16 * w, 16 * ct, lane, F[ct]);
   __syncthreads();
-  // G1 = F + (T - I)^T F  ((T - I)_{t'j} vanishes unless t' > j)
+  // G1 = F + (T - I)^T F  ((T - I)_{t'j} vanishes unless t' > j); the (T - I)^T fragments read once
+#pragma unroll
+  for (int u = 0; u < 2; ++u) pw[u] = frag_col(Tm, TPB, 32 * u, 16 * w, lane);
 #pragma unroll
   for (int ct = 0; ct < VT; ++ct) {
 #pragma unroll
     for (int u = 0; u < 2; ++u)
-      if (u == 1 || w <= 1) F[ct] = mma(frag_col(Tm, TPB, 32 * u, 16 * w, lane), frag_col(Fb, VPB, 32 * u, 16 * ct, lane), F[ct]);
+      if (u == 1 || w <= 1) F[ct] = mma(pw[u], frag_col(Fb, VPB, 32 * u, 16 * ct, lane), F[ct]);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int tt = 16 * w + 4 * g4 + r;
@@ -564,6 +573,9 @@ __global__ __launch_bounds__(256, 2) void gated_delta_chunk_bwd_grad_kernel(Chun
   const int64_t c0 = L.c0, cg = blockIdx.x;
   const uint32_t vrow = (uint32_t)(p.HV * VD * 2), trow = (uint32_t)(p.HV * kC * 2), grow = (uint32_t)(p.HV * VD * 4);
 
+  // the first value head's gate loads go out first, in flight while K and Q are staged
+  uint32_t graw = 0, braw = 0;
+  if (w == 0) fetch_gates_bwd(graw, braw, p, c0, h * rep, len, lane);
   {  // K and Q rows: both tiles' loads in flight before the first LDS write
     QKRows<KD, 256> xk, xq;
     fetch_qk(xk, static_cast<const bf16*>(p.k) + (c0 * p.H + h) * KD, p.H, len, t);
@@ -605,8 +617,7 @@ __global__ __launch_bounds__(256, 2) void gated_delta_chunk_bwd_grad_kernel(Chun
 
   for (int64_t rr = 0; rr < rep; ++rr) {
     const int64_t hv = h * rep + rr;
-    uint32_t graw = 0, braw = 0;
-    if (w == 0) fetch_gates_bwd(graw, braw, p, c0, hv, len, lane);
+    if (w == 0 && rr > 0) fetch_gates_bwd(graw, braw, p, c0, hv, len, lane);
     if (t < kC) {
 #pragma unroll
       for (int x = 0; x < 4; ++x) {
@@ -775,7 +786,17 @@ __global__ __launch_bounds__(256, 2) void gated_delta_chunk_bwd_grad_kernel(Chun
     sdot = wave_xor_sum(sdot, 1);
     if (lane == 0) red_[w][0] = sdot;
     __syncthreads();  // the passes are done with the LDS tiles: dG and dQK go over them
-    // c x c elementwise: G = K K^T, QK = Q K^T; dA, dG, dQK; their row and column sums
+    // c x c elementwise: G = K K^T, QK = Q K^T; dA, dG, dQK; their row and column sums. The K and
+    // Q fragments of this wave's rows serve every tile: read once.
+    bf16x8 kown[KS], qown[KS];
+    {
+      const int ln = opaque_int(lane);
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        kown[s] = frag_row(Kb, KPB, tok0, 32 * s, ln);
+        qown[s] = frag_row(Qb, KPB, tok0, 32 * s, ln);
+      }
+    }
 #pragma unroll
     for (int jt = 0; jt < 4; ++jt) {
       const int ln = opaque_int(lane);
@@ -784,8 +805,8 @@ __global__ __launch_bounds__(256, 2) void gated_delta_chunk_bwd_grad_kernel(Chun
 #pragma unroll
         for (int s = 0; s < KS; ++s) {
           const bf16x8 bk = frag_row(Kb, KPB, 16 * jt, 32 * s, ln);
-          Gm = mma(frag_row(Kb, KPB, tok0, 32 * s, ln), bk, Gm);
-          QKm = mma(frag_row(Qb, KPB, tok0, 32 * s, ln), bk, QKm);
+          Gm = mma(kown[s], bk, Gm);
+          QKm = mma(qown[s], bk, QKm);
           __builtin_amdgcn_sched_barrier(0);
         }
       }
@@ -825,18 +846,29 @@ __global__ __launch_bounds__(256, 2) void gated_delta_chunk_bwd_grad_kernel(Chun
     rsum = wave_xor_sum(rsum, 1);
     if (lane == 0) red_[w][1] = rsum;
     __syncthreads();
-    // dQ += dQK K;  dK += dQK^T Q + dG K + dG^T K
-#pragma unroll
-    for (int kt = 0; kt < KT; ++kt) {
+    // dQ += dQK K;  dK += dQK^T Q + dG K + dG^T K. The dQK and dG fragments of this wave's rows
+    // (and of its columns, transposed) are the same for every key tile: read once.
+    {
       const int ln = opaque_int(lane);
+      bf16x8 qr[2], qc[2], gr[2], gc[2];
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
-        const bf16x8 bk = frag_col(Kb, KPB, 32 * u, 16 * kt, ln);
-        dqa[kt] = mma(frag_row(cc2, kCPb, tok0, 32 * u, ln), bk, dqa[kt]);
-        dka[kt] = mma(frag_col(cc2, kCPb, 32 * u, tok0, ln), frag_col(Qb, KPB, 32 * u, 16 * kt, ln), dka[kt]);
-        dka[kt] = mma(frag_row(cc1, kCPb, tok0, 32 * u, ln), bk, dka[kt]);
-        dka[kt] = mma(frag_col(cc1, kCPb, 32 * u, tok0, ln), bk, dka[kt]);
-        __builtin_amdgcn_sched_barrier(0);
+        qr[u] = frag_row(cc2, kCPb, tok0, 32 * u, ln);
+        qc[u] = frag_col(cc2, kCPb, 32 * u, tok0, ln);
+        gr[u] = frag_row(cc1, kCPb, tok0, 32 * u, ln);
+        gc[u] = frag_col(cc1, kCPb, 32 * u, tok0, ln);
+      }
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const bf16x8 bk = frag_col(Kb, KPB, 32 * u, 16 * kt, ln);
+          dqa[kt] = mma(qr[u], bk, dqa[kt]);
+          dka[kt] = mma(qc[u], frag_col(Qb, KPB, 32 * u, 16 * kt, ln), dka[kt]);
+          dka[kt] = mma(gr[u], bk, dka[kt]);
+          dka[kt] = mma(gc[u], bk, dka[kt]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
       }
     }
     // dg = reverse in-chunk cumsum of dgam; dbeta; the gate and sigmoid backwards
