@@ -263,6 +263,9 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
     chunk_gates_from_raw(gv[c % 3], graw, braw, p.dg, p.db, chunk_len(c), p.flags, al, dt_b, lane);
   };
   // waves 4-5: O of chunk c from Ob to HBM, rows tq / 4 + 32u; om keeps the stored values' magnitude maximum
+  // O rows go out as non-temporal stores in the inference kernel: streamed past the caches, they
+  // leave L2 to the q/k/T/V tiles that the slices of a chain share (config-1 call 130.3 -> 125.2 us,
+  // same-box A/B). The training kernel keeps cached stores (non-temporal ones measured slower there).
   auto store_o = [&](int c, int tq, u16x2& om) {
     const int64_t c0 = bos + (int64_t)c * kC;
     const auto ro = make_rsrc(og + (c0 * p.HV + hv) * VD + vb * kVB, (uint32_t)chunk_len(c) * v_row);
@@ -271,7 +274,8 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
     for (int u = 0; u < 2; ++u) {
       const bf16x8 x = *reinterpret_cast<const bf16x8*>(&Ob[c & 1][vo_off(row + 32 * u, c8 * 8)]);
       om = bf16_mag_max(om, x);
-      buf_store16(x, ro, (uint32_t)(row + 32 * u) * v_row + c8 * 16);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), ro,
+                                             (int)((uint32_t)(row + 32 * u) * v_row + c8 * 16), 0, SAVE ? 0 : 2);
     }
   };
 
