@@ -295,19 +295,30 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
     for (int a = 0; a < JN; ++a)
 #pragma unroll
       for (int b = 0; b < TN; ++b) acc[a][b] = f32x4{};
+    // every fragment and gate read of the job first, then the MFMAs: one LDS round trip instead of
+    // one per key step
+    f16x8 fk[KS][JN], fq[KS][TN];
+    float gtv[TN];
+    float4 gjv4[JN];
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
-      f16x8 fk[JN], fq[TN];
 #pragma unroll
-      for (int a = 0; a < JN; ++a) fk[a] = ld8h(kb + (16 * (JA + a) + li) * KP + kq_col(s, li, g4));
+      for (int a = 0; a < JN; ++a) fk[s][a] = ld8h(kb + (16 * (JA + a) + li) * KP + kq_col(s, li, g4));
 #pragma unroll
-      for (int b = 0; b < TN; ++b) fq[b] = ld8h(qb + (16 * (TA + b) + li) * KP + kq_col(s, li, g4));
+      for (int b = 0; b < TN; ++b) fq[s][b] = ld8h(qb + (16 * (TA + b) + li) * KP + kq_col(s, li, g4));
+    }
+#pragma unroll
+    for (int b = 0; b < TN; ++b) gtv[b] = gs.gam[16 * (TA + b) + li];
+#pragma unroll
+    for (int a = 0; a < JN; ++a) gjv4[a] = ld4f(&gs.gam[16 * (JA + a) + 4 * g4]);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
 #pragma unroll
       for (int a = 0; a < JN; ++a)
 #pragma unroll
         for (int b = 0; b < TN; ++b)
-          if (JA + a <= TA + b) acc[a][b] = mmah(fk[a], fq[b], acc[a][b]);
-    }
+          if (JA + a <= TA + b) acc[a][b] = mmah(fk[s][a], fq[s][b], acc[a][b]);
 #pragma unroll
     for (int a = 0; a < JN; ++a)
 #pragma unroll
@@ -315,8 +326,8 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
         const int jt = JA + a, tt_ = TA + b;
         if (jt > tt_) continue;
         const int tt = 16 * tt_ + li, j0 = 16 * jt + 4 * g4;
-        const float gt = gs.gam[tt];
-        const float4 gj = ld4f(&gs.gam[j0]);
+        const float gt = gtv[b];
+        const float4 gj = gjv4[a];
         const float gjv[4] = {gj.x, gj.y, gj.z, gj.w};
         float val[4];
 #pragma unroll
