@@ -772,12 +772,21 @@ __global__ __launch_bounds__(256, 2) void gated_delta_chunk_bwd_grad_kernel(Chun
           sd[x] = static_cast<bf16>(fd * (float)ad[x]);
         }
 #pragma unroll
-        for (int kt = 0; kt < KT; ++kt) {
-          const bf16x8 bs = frag_col(SbT, KPB, 0, 16 * kt, ln);
-          dqa[kt] = mma(so, bs, dqa[kt]);
-          dka[kt] = mma(sy, bs, dka[kt]);
-          dka[kt] = mma(sd, frag_col(dSbT, KPB, 0, 16 * kt, ln), dka[kt]);
-          if (kt & 1) __builtin_amdgcn_sched_barrier(0);
+        for (int k4 = 0; k4 < KT; k4 += 4) {  // four key tiles' fragments read before their MFMAs
+          bf16x8 bs[4], bd[4];
+#pragma unroll
+          for (int x = 0; x < 4; ++x) {
+            bs[x] = frag_col(SbT, KPB, 0, 16 * (k4 + x), ln);
+            bd[x] = frag_col(dSbT, KPB, 0, 16 * (k4 + x), ln);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int x = 0; x < 4; ++x) {
+            dqa[k4 + x] = mma(so, bs[x], dqa[k4 + x]);
+            dka[k4 + x] = mma(sy, bs[x], dka[k4 + x]);
+            dka[k4 + x] = mma(sd, bd[x], dka[k4 + x]);
+          }
+          __builtin_amdgcn_sched_barrier(0);
         }
       }
     }
@@ -802,13 +811,16 @@ __global__ __launch_bounds__(256, 2) void gated_delta_chunk_bwd_grad_kernel(Chun
       const int ln = opaque_int(lane);
       f32x4 Gm = f32x4{}, QKm = f32x4{};
       if (jt <= w) {
+        bf16x8 bk[KS];  // the tile's K fragments read before its MFMAs
+#pragma unroll
+        for (int s = 0; s < KS; ++s) bk[s] = frag_row(Kb, KPB, 16 * jt, 32 * s, ln);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int s = 0; s < KS; ++s) {
-          const bf16x8 bk = frag_row(Kb, KPB, 16 * jt, 32 * s, ln);
-          Gm = mma(kown[s], bk, Gm);
-          QKm = mma(qown[s], bk, QKm);
-          __builtin_amdgcn_sched_barrier(0);
+          Gm = mma(kown[s], bk[s], Gm);
+          QKm = mma(qown[s], bk[s], QKm);
         }
+        __builtin_amdgcn_sched_barrier(0);
       }
       const int jj = 16 * jt + (ln & 15);
       f32x4 dG, dQK;
@@ -858,17 +870,29 @@ __global__ __launch_bounds__(256, 2) void gated_delta_chunk_bwd_grad_kernel(Chun
         gr[u] = frag_row(cc1, kCPb, tok0, 32 * u, ln);
         gc[u] = frag_col(cc1, kCPb, 32 * u, tok0, ln);
       }
+      // two key tiles at a time: their K and Q fragments read before their MFMAs
 #pragma unroll
-      for (int kt = 0; kt < KT; ++kt) {
+      for (int k2 = 0; k2 < KT; k2 += 2) {
+        bf16x8 bk[2][2], bq[2][2];
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const bf16x8 bk = frag_col(Kb, KPB, 32 * u, 16 * kt, ln);
-          dqa[kt] = mma(qr[u], bk, dqa[kt]);
-          dka[kt] = mma(qc[u], frag_col(Qb, KPB, 32 * u, 16 * kt, ln), dka[kt]);
-          dka[kt] = mma(gr[u], bk, dka[kt]);
-          dka[kt] = mma(gc[u], bk, dka[kt]);
-          __builtin_amdgcn_sched_barrier(0);
-        }
+        for (int x = 0; x < 2; ++x)
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            bk[x][u] = frag_col(Kb, KPB, 32 * u, 16 * (k2 + x), ln);
+            bq[x][u] = frag_col(Qb, KPB, 32 * u, 16 * (k2 + x), ln);
+          }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int x = 0; x < 2; ++x)
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const int kt = k2 + x;
+            dqa[kt] = mma(qr[u], bk[x][u], dqa[kt]);
+            dka[kt] = mma(qc[u], bq[x][u], dka[kt]);
+            dka[kt] = mma(gr[u], bk[x][u], dka[kt]);
+            dka[kt] = mma(gc[u], bk[x][u], dka[kt]);
+          }
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
     // dg = reverse in-chunk cumsum of dgam; dbeta; the gate and sigmoid backwards
