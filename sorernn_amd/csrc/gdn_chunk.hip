@@ -352,9 +352,9 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
   // ------------------------------------------------------------------ state-side registers
   const int sw = w & 1;  // state wave 0 or 1: value columns 16 sw .. 16 sw + 15 of the slice
   // Loop-carried: S tiles; Z^T = S^T Q^T of the current chunk, tile tb (value column 4g + r, token
-  // 16tb + i); (S_2s, S_2s+1) in fp16 (SB); the K row fragments of the next Y = K S for its first
-  // KSH key steps (KF, read ahead across the barrier).
-  f32x4 S[KT], Zt[4], SB[KS], KF[4 * KSH];
+  // 16tb + i); (S_2s, S_2s+1) in fp16 (SB); Y = K S of the chunk the next step processes (YN,
+  // computed at the end of a step: its K was staged a step earlier, so it needs no barrier).
+  f32x4 S[KT], Zt[4], SB[KS], YN[4];
   float ec_next = 1.f;  // e^{gam_c} of the chunk the next step processes
   auto sb = [&](int s) { return __builtin_bit_cast(f16x8, SB[s]); };
   const int64_t sbase = (n * p.HV + hv) * (int64_t)KD * VD + vb * kVB + 16 * sw;
@@ -374,20 +374,6 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
     for (int a = 0; a < KT; ++a)
       __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, to_bf16x4(S[a][0], S[a][1], S[a][2], S[a][3])), rs,
                                             (int)(off + (32 * (a >> 1) + 4 * (a & 1)) * 2), 0, 0);
-  };
-  // K row fragments of Y = K S for chunk c, key steps s < KSH (row tile b), read ahead
-  auto load_kf_slot = [&](const f16* kb) {
-#pragma unroll
-    for (int s = 0; s < KSH; ++s)
-#pragma unroll
-      for (int b = 0; b < 4; ++b) KF[4 * s + b] = __builtin_bit_cast(f32x4, ld8h(kb + (16 * b + li) * KP + kq_col(s, li, g4)));
-  };
-  auto load_kf = [&](int c) {
-    const f16* kb = Kc[c % 3];
-#pragma unroll
-    for (int s = 0; s < KSH; ++s)
-#pragma unroll
-      for (int b = 0; b < 4; ++b) KF[4 * s + b] = __builtin_bit_cast(f32x4, ld8h(kb + (16 * b + li) * KP + kq_col(s, li, g4)));
   };
   // Each phase of the state step issues the LDS reads of the next phase before its own MFMAs, and
   // the scheduler may not move instructions across the phase boundaries: LDS reads complete in
@@ -424,8 +410,18 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
       for (int s2 = 0; s2 < KS; ++s2)
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb) qf[s2][tb] = ld8h(Qc[0] + (16 * tb + li) * KP + kq_col(s2, li, g4));
-      load_kf(0);
       ec_next = __expf(gv[0].gam[kC - 1]);
+      // Y = K S of chunk 0 (the steps compute the next chunk's Y at their end)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) YN[b] = f32x4{};
+#pragma unroll
+      for (int s2 = 0; s2 < KS; ++s2) {
+        f16x8 kf0[4];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) kf0[b] = ld8h(Kc[0] + (16 * b + li) * KP + kq_col(s2, li, g4));
+#pragma unroll
+        for (int b = 0; b < 4; ++b) YN[b] = mmah(kf0[b], sb(s2), YN[b]);
+      }
 #pragma unroll
       for (int tb = 0; tb < 4; ++tb) Zt[tb] = f32x4{};
 #pragma unroll
@@ -446,18 +442,15 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
       bf16* op = Ob[PH & 1];
       const ChunkGates& G = gv[PH % 3];
 
-      // The chain S -> Y -> X -> Delta -> Delta~ -> S' runs through phases 1-5; the rest is placed
-      // where it overlaps the chain's MFMAs: the e^{gam_c} scaling of S under Y, and O of this chunk
-      // with Z^T of the next under phase 6. Phases 5 and 6 run unconditionally: after the last chunk
-      // they read slots holding stale tiles and compute values nobody uses, which keeps the step
-      // free of branches (a branch around loads costs the register allocator dearly here).
-      // ---- 1: reads for Y's second half and for X (V, beta, beta e^gam); Y = K S from the
-      //      fragments read ahead in the previous step; S *= e^{gam_c} (Y used S in fp16)
-      f16x8 kf2[KS - KSH][4];
-#pragma unroll
-      for (int s2 = KSH; s2 < KS; ++s2)
-#pragma unroll
-        for (int b = 0; b < 4; ++b) kf2[s2 - KSH][b] = ld8h(kb + (16 * b + li) * KP + kq_col(s2, li, g4));
+      // The chain S -> Y -> X -> Delta -> Delta~ -> S' runs through phases 6 (Y of the next chunk,
+      // from S' in fp16) and 1-5; the rest is placed where it overlaps the chain: the e^{gam_c}
+      // scaling of S under the phase-1 reads, and O of this chunk with Z^T of the next in phase 6,
+      // between the two halves of the next Y. Phases 5 and 6 run unconditionally: after the last
+      // chunk they read slots holding stale tiles and compute values nobody uses, which keeps the
+      // step free of branches (a branch around loads costs the register allocator dearly here).
+      // Computing the next Y before the barrier instead of after it took ~2.5 us off a config-1
+      // call (same-box A/B, bitwise-equal outputs).
+      // ---- 1: reads for X (V, beta, beta e^gam); S *= e^{gam_c} (Y used S in fp16)
       bf16x4 vv[4];
       float4 bt[4], bg[4];
 #pragma unroll
@@ -471,12 +464,7 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
       phase();
       f32x4 D[4];
 #pragma unroll
-      for (int b = 0; b < 4; ++b) D[b] = f32x4{};
-#pragma unroll
-      for (int s2 = 0; s2 < KS; ++s2)
-#pragma unroll
-        for (int b = 0; b < 4; ++b)
-          D[b] = mmah(s2 < KSH ? __builtin_bit_cast(f16x8, KF[4 * s2 + b]) : kf2[s2 - KSH][b], sb(s2), D[b]);
+      for (int b = 0; b < 4; ++b) D[b] = YN[b];  // Y = K S of this chunk, computed at the previous step's end
 #pragma unroll
       for (int a = 0; a < KT; ++a) S[a] *= ec;
       phase();
@@ -548,7 +536,13 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
 #pragma unroll
         for (int u = 0; u < 2; ++u) S[a] = mmah(ktf[a][u], dt[u], S[a]);
       phase();
-      // ---- 5: Q reads of the next chunk; S in fp16
+      // ---- 5: Q reads and the first half of the K reads of the next chunk; S in fp16
+      const f16* kn = Kc[(PH + 1) % 3];
+      f16x8 kfa[KSH][4];
+#pragma unroll
+      for (int s2 = 0; s2 < KSH; ++s2)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) kfa[s2][b] = ld8h(kn + (16 * b + li) * KP + kq_col(s2, li, g4));
       f16x8 qf[KS][4];
       {
         const f16* qb = Qc[(PH + 1) & 1];
@@ -559,11 +553,18 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
       }
       make_sb();
       phase();
-      // ---- 6: K reads for the next Y and its e^{gam_c}; O^T = scale e^gam Z^T + Delta^T (scale P)^T
-      //      -> Ob[token][column]; Z^T = S^T Q^T of the next chunk
-      load_kf_slot(Kc[(PH + 1) % 3]);
+      // ---- 6: the next chunk's Y (first half), its e^{gam_c}; O^T = scale e^gam Z^T + Delta^T (scale P)^T
+      //      -> Ob[token][column]; K reads of Y's second half; Z^T = S^T Q^T of the next chunk; Y's
+      //      second half
       ec_next = __expf(gv[(PH + 1) % 3].gam[kC - 1]);
       phase();
+      // the next chunk's Y = K S from S' in fp16 (its K was staged a step ago): first half
+#pragma unroll
+      for (int b = 0; b < 4; ++b) YN[b] = f32x4{};
+#pragma unroll
+      for (int s2 = 0; s2 < KSH; ++s2)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) YN[b] = mmah(kfa[s2][b], sb(s2), YN[b]);
 #pragma unroll
       for (int tb = 0; tb < 4; ++tb) {
         f32x4 o = Zt[tb] * eg[tb];
@@ -571,12 +572,21 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
         if (tb >= 2) o = mmah(db1, pf[tb + 2], o);
         *reinterpret_cast<bf16x4*>(op + vo_off(16 * tb + li, 16 * sw + 4 * g4)) = to_bf16x4(o[0], o[1], o[2], o[3]);
       }
+      f16x8 kfb[KS - KSH][4];
+#pragma unroll
+      for (int s2 = KSH; s2 < KS; ++s2)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) kfb[s2 - KSH][b] = ld8h(kn + (16 * b + li) * KP + kq_col(s2, li, g4));
 #pragma unroll
       for (int tb = 0; tb < 4; ++tb) Zt[tb] = f32x4{};
 #pragma unroll
       for (int s2 = 0; s2 < KS; ++s2)
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb) Zt[tb] = mmah(sb(s2), qf[s2][tb], Zt[tb]);
+#pragma unroll
+      for (int s2 = KSH; s2 < KS; ++s2)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) YN[b] = mmah(kfb[s2 - KSH][b], sb(s2), YN[b]);
       if constexpr (SAVE) {
         // S' (updated in phase 4) is the state entering chunk i + 1; stored at the step's end, away
         // from the helpers' load burst at its start
