@@ -21,8 +21,9 @@
 // Four launches on the caller's stream, after a forward that saved the state entering every chunk
 // (gdn_chunk_fwd_train):
 //   1. gated_delta_chunk_bwd_prep_kernel, per (chunk, value head): T - I in natural column order
-//      (bf16, for launches 2 and 3) and G1 = T^T (scale P^T dO) (fp32), the state-independent part
-//      of dX.
+//      (bf16, for launches 2 and 3) and G1 = T^T (scale P^T dO), the state-independent part of dX
+//      (bf16, chunk-blocked [chunk][value head][value column][64 tokens], so that a lane's four
+//      adjacent tokens of one column are one 8-byte access in every kernel that touches it).
 //   2. gated_delta_chunk_bwd_state_kernel, per (sequence, value head, 32 value columns): the reverse
 //      recurrence dS <- e^{gam_c} dS + K^T (-beta a dX) + Q^T (scale a dO) with
 //      dX = G1 + T^T (r o K dS), over the chunks from last to first; it stores dS' of every chunk
@@ -46,7 +47,7 @@ struct ChunkBwdParams {
   const f16* tw;      // the forward's T - I rows (fp16, tok_col columns)
   bf16* tn;           // T - I rows, natural columns, bf16 [tokens][HV][64]      (workspace)
   bf16* tnt;          // (T - I)^T rows, bf16 [tokens][HV][64]                   (workspace)
-  float* g1;          // G1 = T^T (scale P^T dO), fp32 [tokens][HV][V]           (workspace)
+  bf16* g1;           // G1 = T^T (scale P^T dO), bf16 [chunks][HV][V][64 tokens] (workspace)
   bf16* dhs;          // gradient of the state leaving each chunk, bf16 [chunks][HV][V][K]   (workspace)
   float* gate_part;   // per-chunk partial sums of dA_log and ddt_bias [chunks][HV][2] (workspace)
   const void* cu;
@@ -305,11 +306,12 @@ __global__ __launch_bounds__(256) void gated_delta_chunk_bwd_prep_kernel(ChunkBw
 #pragma unroll
     for (int u = 0; u < 2; ++u)
       if (u == 1 || w <= 1) F[ct] = mma(pw[u], frag_col(Fb, VPB, 32 * u, 16 * ct, lane), F[ct]);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int tt = 16 * w + 4 * g4 + r;
-      if (tt < len) p.g1[((c0 + tt) * p.HV + hv) * VD + 16 * ct + li] = F[ct][r];
-    }
+    // the lane's 4 tokens of one value column are adjacent in the chunk-blocked G1: one 8-byte
+    // store; every token slot of the chunk is written (zero past len)
+    const int tt = 16 * w + 4 * g4;
+    const bf16x4 gv = to_bf16x4(tt < len ? F[ct][0] : 0.f, tt + 1 < len ? F[ct][1] : 0.f,
+                                tt + 2 < len ? F[ct][2] : 0.f, tt + 3 < len ? F[ct][3] : 0.f);
+    *reinterpret_cast<bf16x4*>(p.g1 + (((int64_t)blockIdx.x * p.HV + hv) * VD + 16 * ct + li) * kC + tt) = gv;
   }
 }
 
@@ -320,9 +322,9 @@ __global__ __launch_bounds__(256) void gated_delta_chunk_bwd_prep_kernel(ChunkBw
 template <int KD, int VD>
 __global__ __launch_bounds__(256, 1) void gated_delta_chunk_bwd_state_kernel(ChunkBwdParams p) {
   constexpr int KPB = row_pitch<KD>(), KS = KD / 32, KT = KD / 16, NVB = VD / 32;
-  constexpr int GP = 36, OP = 40;  // fp32 pitch of the G1 slice, bf16 pitch of the dO slice
+  constexpr int OP = 40;  // bf16 pitch of the dO slice
   __shared__ __align__(16) bf16 Kb[2][kC * KPB], Qb[2][kC * KPB], Tm[2][kC * kCPb], dOs[2][kC * OP];
-  __shared__ __align__(16) float G1s[2][kC * GP];
+  __shared__ __align__(16) bf16 G1s[2][32 * kCPb];  // G1 slice: [32 value columns][64 tokens]
   __shared__ __align__(16) ChunkGates gv[2];
 
   const int t = threadIdx.x, lane = t & 63, w = __builtin_amdgcn_readfirstlane(t >> 6), g4 = lane >> 4, li = lane & 15;
@@ -360,7 +362,7 @@ __global__ __launch_bounds__(256, 1) void gated_delta_chunk_bwd_state_kernel(Chu
     QKRows<KD, 128> xk, xq;
     Slice<kC, 128> xt;
     Slice<32, 128> xo;
-    Slice<64, 128> xg;  // the G1 slice: 32 fp32 = 128 bytes per row, handled as 64 16-bit columns
+    u32x4 xg[2];  // the G1 slice: 32 columns x 64 tokens, 4 KB contiguous in the chunk-blocked G1
     uint32_t graw, braw;
     int len;
   };
@@ -372,7 +374,9 @@ __global__ __launch_bounds__(256, 1) void gated_delta_chunk_bwd_state_kernel(Chu
     fetch_slice(r.xt, p.tn + (c0 * p.HV + hv) * kC, (uint32_t)(p.HV * kC * 2), r.len, tl);
     fetch_slice(r.xo, static_cast<const bf16*>(p.dout) + (c0 * p.HV + hv) * VD + vb * 32, (uint32_t)(p.HV * VD * 2),
                 r.len, tl);
-    fetch_slice(r.xg, p.g1 + (c0 * p.HV + hv) * VD + vb * 32, (uint32_t)(p.HV * VD * 4), r.len, tl);
+    const bf16* g1src = p.g1 + (((cgb + c) * p.HV + hv) * VD + vb * 32) * kC;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) r.xg[u] = *reinterpret_cast<const u32x4*>(g1src + (u * 128 + tl) * 8);
     r.graw = r.braw = 0;
     if (w == 2) fetch_gates_bwd(r.graw, r.braw, p, c0, hv, r.len, lane);
   };
@@ -381,7 +385,11 @@ __global__ __launch_bounds__(256, 1) void gated_delta_chunk_bwd_state_kernel(Chu
     put_qk(r.xq, Qb[slot], KPB, l2, tl);
     put_slice(r.xt, Tm[slot], kCPb, tl);
     put_slice(r.xo, dOs[slot], OP, tl);
-    put_slice(r.xg, G1s[slot], GP, tl);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int e = u * 128 + tl;  // column e / 8, tokens 8 (e % 8) .. + 7
+      *reinterpret_cast<u32x4*>(G1s[slot] + (e >> 3) * kCPb + (e & 7) * 8) = r.xg[u];
+    }
     if (w == 2) put_gates_bwd(gv[slot], r.graw, r.braw, p, hv, r.len, lane);
   };
 
@@ -446,13 +454,15 @@ __global__ __launch_bounds__(256, 1) void gated_delta_chunk_bwd_state_kernel(Chu
       // dX = G1 + Z + (T - I)^T Z, Z = r o W1 (token pairs 32u + 4g + r, 32u + 16 + 4g + r)
       f32x4 X[4];
 #pragma unroll
-      for (int b = 0; b < 4; ++b)
+      for (int b = 0; b < 4; ++b) {
+        const bf16x4 g1v = ld4b(G1s[slot] + (16 * sw + li) * kCPb + 16 * b + 4 * g4);  // tokens 16b + 4g..+3
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int tok = 16 * b + 4 * g4 + r;
           W[b][r] *= G.dlast[tok];
-          X[b][r] = G1s[slot][tok * GP + 16 * sw + li] + W[b][r];
+          X[b][r] = (float)g1v[r] + W[b][r];
         }
+      }
       const bf16x8 zb[2] = {pack8(W[0], W[1]), pack8(W[2], W[3])};
 #pragma unroll
       for (int b = 0; b < 4; ++b)
@@ -571,7 +581,7 @@ __global__ __launch_bounds__(256, 2) void gated_delta_chunk_bwd_grad_kernel(Chun
   const bool l2 = p.flags & GDN_FLAG_QK_L2NORM;
   const int len = L.len;
   const int64_t c0 = L.c0, cg = blockIdx.x;
-  const uint32_t vrow = (uint32_t)(p.HV * VD * 2), trow = (uint32_t)(p.HV * kC * 2), grow = (uint32_t)(p.HV * VD * 4);
+  const uint32_t vrow = (uint32_t)(p.HV * VD * 2), trow = (uint32_t)(p.HV * kC * 2);
 
   // the first value head's gate loads go out first, in flight while K and Q are staged
   uint32_t graw = 0, braw = 0;
@@ -606,13 +616,15 @@ __global__ __launch_bounds__(256, 2) void gated_delta_chunk_bwd_grad_kernel(Chun
     const auto rv = make_rsrc(static_cast<const bf16*>(p.v) + (c0 * p.HV + hv) * VD + 32 * ps_i, (uint32_t)len * vrow);
     po = __builtin_amdgcn_raw_buffer_load_b128(ro, (int)((uint32_t)row * vrow + ch * 16), 0, 0);
     pv = __builtin_amdgcn_raw_buffer_load_b128(rv, (int)((uint32_t)row * vrow + ch * 16), 0, 0);
-    const auto rg = make_rsrc(p.g1 + (c0 * p.HV + hv) * VD + 32 * ps_i, (uint32_t)len * grow);
+    // chunk-blocked G1: the lane's tokens tok0 + 4g..+3 of a column are one 8-byte load (zeros
+    // past len, as the prep kernel writes them)
+    const bf16* g1src = p.g1 + ((cg * p.HV + hv) * VD + 32 * ps_i + li) * kC + tok0 + 4 * g4;
 #pragma unroll
-    for (int ct = 0; ct < 2; ++ct)
+    for (int ct = 0; ct < 2; ++ct) {
+      const bf16x4 x = *reinterpret_cast<const bf16x4*>(g1src + 16 * ct * kC);
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        g1[4 * ct + r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-            rg, (int)((uint32_t)(tok0 + 4 * g4 + r) * grow + (16 * ct + li) * 4), 0, 0));
+      for (int r = 0; r < 4; ++r) g1[4 * ct + r] = (float)x[r];
+    }
   };
 
   for (int64_t rr = 0; rr < rep; ++rr) {
@@ -1036,7 +1048,7 @@ extern "C" size_t gdn_chunk_bwd_workspace_size(int64_t B, int64_t T, int64_t HV,
                                                int varlen) {
   if (B <= 0 || T < 0 || HV <= 0 || K <= 0 || V <= 0 || N <= 0) return 0;
   const int64_t tok = B * T, ch = chunk_bound(B, T, N, varlen != 0);
-  return (size_t)(2 * align256(tok * HV * kC * 2) + align256(tok * HV * V * 4) + align256(ch * HV * K * V * 2) +
+  return (size_t)(2 * align256(tok * HV * kC * 2) + align256(ch * HV * V * kC * 2) + align256(ch * HV * K * V * 2) +
                   align256(ch * HV * 2 * 4));
 }
 
@@ -1087,9 +1099,10 @@ extern "C" int gdn_chunk_bwd(const void* q, const void* k, const void* v, const 
   const int64_t tnb = align256(tok * HV * kC * 2);
   p.tn = reinterpret_cast<bf16*>(ws);
   p.tnt = reinterpret_cast<bf16*>(ws + tnb);
-  p.g1 = reinterpret_cast<float*>(ws + 2 * tnb);
-  p.dhs = reinterpret_cast<bf16*>(ws + 2 * tnb + align256(tok * HV * V * 4));
-  p.gate_part = reinterpret_cast<float*>(ws + 2 * tnb + align256(tok * HV * V * 4) + align256(chunks * HV * K * V * 2));
+  const int64_t g1b = align256(chunks * HV * V * kC * 2);
+  p.g1 = reinterpret_cast<bf16*>(ws + 2 * tnb);
+  p.dhs = reinterpret_cast<bf16*>(ws + 2 * tnb + g1b);
+  p.gate_part = reinterpret_cast<float*>(ws + 2 * tnb + g1b + align256(chunks * HV * K * V * 2));
   p.cu = cu_seqlens;
   p.chunk_first = varlen ? reinterpret_cast<const int*>(fws + chunk_t_bytes(tok, HV)) : nullptr;
   p.cu_i32 = (flags & GDN_FLAG_CU_INT32) ? 1 : 0;
