@@ -74,9 +74,11 @@ __global__ __launch_bounds__(kPrepNT, 4) void gated_delta_chunk_prep_kernel(Chun
       eos = load_index(p.cu, p.cu_i32, n + 1);
     } else {
       if (item >= p.items) return false;
-      const int64_t ncs = (p.T + kC - 1) / kC;
-      n = item / ncs;
-      c = item % ncs;
+      // 32-bit division (items < 2^31, checked at launch): the 64-bit one expands to a few hundred
+      // instructions, paid for every chunk a workgroup walks
+      const uint32_t ncs = (uint32_t)((p.T + kC - 1) / kC), it = (uint32_t)item, q = it / ncs;
+      n = q;
+      c = it - q * ncs;
       bos = n * p.T;
       eos = bos + p.T;
     }
