@@ -20,8 +20,9 @@
 //
 // Four launches on the caller's stream, after a forward that saved the state entering every chunk
 // (gdn_chunk_fwd_train):
-//   1. gated_delta_chunk_bwd_prep_kernel, per (chunk, value head): T - I in natural column order
-//      (bf16, for launches 2 and 3) and G1 = T^T (scale P^T dO), the state-independent part of dX
+//   1. gated_delta_chunk_bwd_prep_kernel, per (chunk, value head): (T - I)^T rows (bf16, for
+//      launches 2 and 3, which read the forward's fp16 T - I rows where they need T - I itself)
+//      and G1 = T^T (scale P^T dO), the state-independent part of dX
 //      (bf16, chunk-blocked [chunk][value head][value column][64 tokens], so that a lane's four
 //      adjacent tokens of one column are one 8-byte access in every kernel that touches it).
 //   2. gated_delta_chunk_bwd_state_kernel, per (sequence, value head, 32 value columns): the reverse
@@ -45,7 +46,6 @@ struct ChunkBwdParams {
   const float* dht;   // gradient of the final state [N][HV][K][V], or null
   const bf16* hs;     // state entering each chunk, bf16 [chunks][HV][V][K] (forward output, transposed)
   const f16* tw;      // the forward's T - I rows (fp16, tok_col columns)
-  bf16* tn;           // T - I rows, natural columns, bf16 [tokens][HV][64]      (workspace)
   bf16* tnt;          // (T - I)^T rows, bf16 [tokens][HV][64]                   (workspace)
   bf16* g1;           // G1 = T^T (scale P^T dO), bf16 [chunks][HV][V][64 tokens] (workspace)
   bf16* dhs;          // gradient of the state leaving each chunk, bf16 [chunks][HV][V][K]   (workspace)
@@ -230,7 +230,7 @@ __global__ __launch_bounds__(256) void gated_delta_chunk_bwd_prep_kernel(ChunkBw
   if (w == 0) fetch_gates_bwd(graw, braw, p, c0, hv, len, lane);
   put_qk(xk, Kb, KPB, l2, t);
   put_qk(xq, Qb, KPB, l2, t);
-  {  // T - I: fp16 rows with tok_col columns -> bf16 natural columns (LDS and the workspace)
+  {  // T - I: fp16 rows with tok_col columns -> bf16 natural columns in LDS
 #pragma unroll
     for (int u8 = 0; u8 < Slice<kC, 256>::N; ++u8) {
       const int e = u8 * 256 + t, row = e >> 3, ch = e & 7, u = ch >> 2, gq = ch & 3;
@@ -240,16 +240,11 @@ __global__ __launch_bounds__(256) void gated_delta_chunk_bwd_prep_kernel(ChunkBw
       const bf16x4 hi = to_bf16x4((float)x[4], (float)x[5], (float)x[6], (float)x[7]);
       *reinterpret_cast<bf16x4*>(Tm + row * TPB + 32 * u + 4 * gq) = lo;
       *reinterpret_cast<bf16x4*>(Tm + row * TPB + 32 * u + 16 + 4 * gq) = hi;
-      if (row < len) {
-        bf16* tn = p.tn + ((c0 + row) * p.HV + hv) * kC;
-        *reinterpret_cast<bf16x4*>(tn + 32 * u + 4 * gq) = lo;
-        *reinterpret_cast<bf16x4*>(tn + 32 * u + 16 + 4 * gq) = hi;
-      }
     }
   }
   if (w == 0) put_gates_bwd(gs, graw, braw, p, hv, len, lane);
   __syncthreads();
-  {  // (T - I)^T rows for the gradient kernel: row t holds (T - I)[j][t], j = 0..63
+  {  // (T - I)^T rows for the next two kernels: row t holds (T - I)[j][t], j = 0..63
 #pragma unroll
     for (int u8 = 0; u8 < 2; ++u8) {
       const int e = u8 * 256 + t, row = e >> 3, j0 = (e & 7) * 8;
@@ -371,7 +366,7 @@ __global__ __launch_bounds__(256, 1) void gated_delta_chunk_bwd_state_kernel(Chu
     r.len = (int)((eos - c0) < kC ? (eos - c0) : kC);
     fetch_qk(r.xk, static_cast<const bf16*>(p.k) + (c0 * p.H + h) * KD, p.H, r.len, tl);
     fetch_qk(r.xq, static_cast<const bf16*>(p.q) + (c0 * p.H + h) * KD, p.H, r.len, tl);
-    fetch_slice(r.xt, p.tn + (c0 * p.HV + hv) * kC, (uint32_t)(p.HV * kC * 2), r.len, tl);
+    fetch_slice(r.xt, p.tnt + (c0 * p.HV + hv) * kC, (uint32_t)(p.HV * kC * 2), r.len, tl);
     fetch_slice(r.xo, static_cast<const bf16*>(p.dout) + (c0 * p.HV + hv) * VD + vb * 32, (uint32_t)(p.HV * VD * 2),
                 r.len, tl);
     const bf16* g1src = p.g1 + (((cgb + c) * p.HV + hv) * VD + vb * 32) * kC;
@@ -441,14 +436,16 @@ __global__ __launch_bounds__(256, 1) void gated_delta_chunk_bwd_state_kernel(Chu
           *reinterpret_cast<bf16x4*>(dp + 32 * s + 16) = bf16x4{sb[s][4], sb[s][5], sb[s][6], sb[s][7]};
         }
       }
-      // (T - I)^T fragments for dX
+      // (T - I)^T fragments for dX: row 16b + i of the staged (T - I)^T tile at the contraction
+      // slots' tokens 32u + 4g..+3 and 32u + 16 + 4g..+3
       bf16x8 tf[4][2];
 #pragma unroll
       for (int b = 0; b < 4; ++b)
 #pragma unroll
         for (int u = 0; u < 2; ++u)
           if (u == 1 || b <= 1) {
-            const bf16x4 t0 = ld4_tr(tm, kCPb, 32 * u, 16 * b, lane), t1 = ld4_tr(tm, kCPb, 32 * u + 16, 16 * b, lane);
+            const bf16* tr = tm + (16 * b + li) * kCPb + 32 * u + 4 * g4;
+            const bf16x4 t0 = ld4b(tr), t1 = ld4b(tr + 16);
             tf[b][u] = bf16x8{t0[0], t0[1], t0[2], t0[3], t1[0], t1[1], t1[2], t1[3]};
           }
       // dX = G1 + Z + (T - I)^T Z, Z = r o W1 (token pairs 32u + 4g + r, 32u + 16 + 4g + r)
@@ -650,16 +647,23 @@ __global__ __launch_bounds__(256, 2) void gated_delta_chunk_bwd_grad_kernel(Chun
     for (int pi = 0; pi < NP; ++pi) {
       fetch_pass(hv, pi, g1c);
       // T - I fragments of this wave's rows, (T - I) rows (Delta) and (T - I)^T rows (dX): loaded
-      // with each pass (L2 hits after the first) so they are not live through the c x K products
+      // with each pass (L2 hits after the first) so they are not live through the c x K products.
+      // The (T - I) rows are the forward's fp16 rows: their 16-byte piece 4u + g holds the tokens
+      // 32u + 4g..+3 and 32u + 16 + 4g..+3, the contraction slots that the Delta product's B
+      // fragments (ld4_tr pairs 16 rows apart) use; converted to bf16 as read.
       bf16x8 tfr[2], tft[2];
       {
         const int lq = opaque_int(lane);
-        const auto rn = make_rsrc(p.tn + (c0 * p.HV + hv) * kC, (uint32_t)len * trow);
+        const auto rw = make_rsrc(p.tw + (c0 * p.HV + hv) * kC, (uint32_t)len * trow);
         const auto rt = make_rsrc(p.tnt + (c0 * p.HV + hv) * kC, (uint32_t)len * trow);
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-          tfr[u] = buf_load16(rn, (uint32_t)(tok0 + (lq & 15)) * trow + (32 * u + 8 * (lq >> 4)) * 2);
-          tft[u] = buf_load16(rt, (uint32_t)(tok0 + (lq & 15)) * trow + (32 * u + 8 * (lq >> 4)) * 2);
+          const uint32_t off = (uint32_t)(tok0 + (lq & 15)) * trow + (4 * u + (lq >> 4)) * 16;
+          const f16x8 h = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(rw, (int)off, 0, 0));
+          const bf16x4 lo = to_bf16x4((float)h[0], (float)h[1], (float)h[2], (float)h[3]);
+          const bf16x4 hi = to_bf16x4((float)h[4], (float)h[5], (float)h[6], (float)h[7]);
+          tfr[u] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          tft[u] = buf_load16(rt, off);
         }
       }
       __syncthreads();  // the previous pass (or value head) is done with the LDS tiles
@@ -716,7 +720,10 @@ __global__ __launch_bounds__(256, 2) void gated_delta_chunk_bwd_grad_kernel(Chun
       for (int u = 0; u < 2; ++u)
         if (u == 0 || w >= 2) {
 #pragma unroll
-          for (int ct = 0; ct < 2; ++ct) Dl[ct] = mma(tfr[u], frag_col(Xb, XP, 32 * u, 16 * ct, ln), Dl[ct]);
+          for (int ct = 0; ct < 2; ++ct) {
+            const bf16x4 x0 = ld4_tr(Xb, XP, 32 * u, 16 * ct, ln), x1 = ld4_tr(Xb, XP, 32 * u + 16, 16 * ct, ln);
+            Dl[ct] = mma(tfr[u], bf16x8{x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]}, Dl[ct]);
+          }
         }
 #pragma unroll
       for (int ct = 0; ct < 2; ++ct) put_acc(Db, XP, tok0, 16 * ct, ln, Dl[ct]);
@@ -1048,7 +1055,7 @@ extern "C" size_t gdn_chunk_bwd_workspace_size(int64_t B, int64_t T, int64_t HV,
                                                int varlen) {
   if (B <= 0 || T < 0 || HV <= 0 || K <= 0 || V <= 0 || N <= 0) return 0;
   const int64_t tok = B * T, ch = chunk_bound(B, T, N, varlen != 0);
-  return (size_t)(2 * align256(tok * HV * kC * 2) + align256(ch * HV * V * kC * 2) + align256(ch * HV * K * V * 2) +
+  return (size_t)(align256(tok * HV * kC * 2) + align256(ch * HV * V * kC * 2) + align256(ch * HV * K * V * 2) +
                   align256(ch * HV * 2 * 4));
 }
 
@@ -1097,12 +1104,11 @@ extern "C" int gdn_chunk_bwd(const void* q, const void* k, const void* v, const 
   p.hs = static_cast<const bf16*>(chunk_states);
   p.tw = reinterpret_cast<const f16*>(fws);
   const int64_t tnb = align256(tok * HV * kC * 2);
-  p.tn = reinterpret_cast<bf16*>(ws);
-  p.tnt = reinterpret_cast<bf16*>(ws + tnb);
+  p.tnt = reinterpret_cast<bf16*>(ws);
   const int64_t g1b = align256(chunks * HV * V * kC * 2);
-  p.g1 = reinterpret_cast<bf16*>(ws + 2 * tnb);
-  p.dhs = reinterpret_cast<bf16*>(ws + 2 * tnb + g1b);
-  p.gate_part = reinterpret_cast<float*>(ws + 2 * tnb + g1b + align256(chunks * HV * K * V * 2));
+  p.g1 = reinterpret_cast<bf16*>(ws + tnb);
+  p.dhs = reinterpret_cast<bf16*>(ws + tnb + g1b);
+  p.gate_part = reinterpret_cast<float*>(ws + tnb + g1b + align256(chunks * HV * K * V * 2));
   p.cu = cu_seqlens;
   p.chunk_first = varlen ? reinterpret_cast<const int*>(fws + chunk_t_bytes(tok, HV)) : nullptr;
   p.cu_i32 = (flags & GDN_FLAG_CU_INT32) ? 1 : 0;

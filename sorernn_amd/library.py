@@ -46,7 +46,7 @@ def bwd_workspace_bytes(b, t, hv, kd, vd, n, varlen: bool):
     """``gdn_chunk_bwd_workspace_size``."""
     tok = b * t
     chunks = ((t + C - 1) // C + n) if varlen else b * ((t + C - 1) // C)
-    return (2 * _align256(tok * hv * C * 2) + _align256(chunks * hv * vd * C * 2) + _align256(chunks * hv * kd * vd * 2)
+    return (_align256(tok * hv * C * 2) + _align256(chunks * hv * vd * C * 2) + _align256(chunks * hv * kd * vd * 2)
             + _align256(chunks * hv * 2 * 4))
 
 

@@ -71,7 +71,7 @@ def test_chunk_workspace_size_matches_layout():
 
 def test_chunk_backward_buffer_sizes_match_layout():
     """gdn_chunk_states_size: one bf16 K x V state per chunk and value head (chunk count bounded by
-    ceil(T/64) + N with cu_seqlens). gdn_chunk_bwd_workspace_size: bf16 T - I rows and (T - I)^T rows [tokens][HV][64],
+    ceil(T/64) + N with cu_seqlens). gdn_chunk_bwd_workspace_size: bf16 (T - I)^T rows [tokens][HV][64],
     bf16 G1 [chunks][HV][V][64], bf16 dS' per chunk [chunks][HV][V][K] and two fp32 partial sums per
     chunk-head, each 256-byte aligned."""
     lib = _lib.load()
@@ -80,10 +80,10 @@ def test_chunk_backward_buffer_sizes_match_layout():
     assert lib.gdn_chunk_states_size(1, 100, 3, 64, 64, 5, 1) == (2 + 5) * 3 * 64 * 64 * 2
     tok, ch = 4 * 4096, 4 * 64
     assert lib.gdn_chunk_bwd_workspace_size(4, 4096, 16, 128, 128, 4, 0) == (
-        2 * a(tok * 16 * 128) + a(ch * 16 * 128 * 64 * 2) + a(ch * 16 * 128 * 128 * 2) + a(ch * 16 * 8))
+        a(tok * 16 * 128) + a(ch * 16 * 128 * 64 * 2) + a(ch * 16 * 128 * 128 * 2) + a(ch * 16 * 8))
     tok, ch = 100, 2 + 5  # varlen: the chunk bound ceil(T/64) + N sizes G1
     assert lib.gdn_chunk_bwd_workspace_size(1, 100, 3, 64, 64, 5, 1) == (
-        2 * a(tok * 3 * 128) + a(ch * 3 * 64 * 64 * 2) + a(ch * 3 * 64 * 64 * 2) + a(ch * 3 * 8))
+        a(tok * 3 * 128) + a(ch * 3 * 64 * 64 * 2) + a(ch * 3 * 64 * 64 * 2) + a(ch * 3 * 8))
     assert lib.gdn_chunk_bwd_workspace_size(0, 4096, 16, 128, 128, 4, 0) == 0
 
 

@@ -344,7 +344,7 @@ def bwd_kernels(s: Shape, eg: int, eb: int) -> int:
     done += check_plain("bwd prep G1 store", g1_bytes, g1i * 2, 8)
     # 2. reverse state kernel (per sequence, value head, 32 value columns; chunks from last to first)
     done += _qk_rows("bwd state k", s, c0, ln, 128) + _qk_rows("bwd state q", s, c0, ln, 128)
-    done += _slice("bwd state T-I", tn_bytes, (c0[:, None] * HV + hv[None, :]) * C * 2, ln, t_row, C, 128)
+    done += _slice("bwd state (T-I)^T", tn_bytes, (c0[:, None] * HV + hv[None, :]) * C * 2, ln, t_row, C, 128)
     for vb in range(V // 32):
         done += _slice(f"bwd state dO {vb}", tok_v, ((c0[:, None] * HV + hv[None, :]) * V + vb * 32) * 2, ln, v_row,
                        32, 128)
@@ -382,8 +382,9 @@ def bwd_kernels(s: Shape, eg: int, eb: int) -> int:
         done += check_plain("bwd grad G1 pass", g1_bytes,
                             ((cg[:, None, None] * HV + hv[None, :, None]) * V * C + g_off.ravel()[None, None, :]) * 2, 8)
         tf_off = ((tok0 + (lq & 15))[:, None] * t_row + (32 * np.arange(2)[None, :] + 8 * (lq >> 4)[:, None]) * 2).ravel()
-        for label in ("bwd grad T-I rows", "bwd grad (T-I)^T rows"):
-            done += check(label, tn_bytes, (_col(c0) * HV + _mid(hv)) * C * 2, _col(ln) * t_row, _last(tf_off), 16)
+        # the forward's fp16 T - I rows (piece 4u + g at the same byte offset) and the (T - I)^T rows
+        for label, nbytes in (("bwd grad T-I rows (forward's fp16)", tw_bytes), ("bwd grad (T-I)^T rows", tn_bytes)):
+            done += check(label, nbytes, (_col(c0) * HV + _mid(hv)) * C * 2, _col(ln) * t_row, _last(tf_off), 16)
     kch = K // 8
     rpp = 256 // kch
     raw_off = ((t // kch)[:, None] + (np.arange(C // rpp) * rpp)[None, :]) * (H * K * 2) + ((t % kch) * 16)[:, None]
