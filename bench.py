@@ -3,7 +3,9 @@
 
 ``python bench.py [--gpus 1] [--steps K] [--warmup W]`` prints ONE JSON line. A step is one
 ``chunk_gated_delta_rule`` call over BASELINE config 1 (B=4, T=4096, H=16, d_k=d_v=128, bf16 q/k/v,
-fp32 g/beta/h0, final state out), inputs already resident in HBM; ``value`` is prefill tokens/s.
+fp32 g/beta/h0, final state out), inputs already resident in HBM; ``value`` is prefill tokens/s, from
+launches alternating over two input sets (2 x 281 MB, more than the 256 MB Infinity Cache), so every
+launch reads its inputs from DRAM; the one-input-set (cache-resident) rate is reported beside it.
 Every workload first runs its own step untimed for 100 ms (``settle``: from idle the GPU's clocks
 need ~35 ms of this load to reach their sustained rate), then W warmup steps, then the K timed steps;
 ``cold_ms_per_step`` / ``cold_value`` report the prefill's first K steps after W warmup steps
@@ -31,7 +33,8 @@ The same line carries
   forward, each timed whole, plus the flash-attention kernel alone against bf16 peak (causal FLOPs
   4 d T (T + 1) / 2 per head and batch row);
 - ``cpu_baseline``: the CPU oracle (``oracle/``, torch fp32 recurrence) on the GPU box's host
-  cores over the full config-1 input, plus 100 decode steps of config 2.
+  cores over the full config-1 input, config 3's per-document loop over its full input, plus 100
+  decode steps of config 2.
 
 Each GPU workload runs in its own child process (``bench.py --part NAME`` prints its raw
 measurements as JSON), so every workload is measured in a fresh HIP context and allocator, as it would
@@ -149,7 +152,9 @@ def block_pair(torch, steps: int) -> dict:
 
     B, T, Dm, H, Dh, HKV = 2, 8192, 2048, 16, 128, 4
     torch.manual_seed(1004)
-    gdn = GatedDeltaNet(GDNLayerConfig(d_model=Dm, gdn_qk_heads=H, gdn_v_heads=H, gdn_head_dim=Dh, gdn_kernel_gate=True))
+    # the caller flags of the reference's training presets (sore/model/config.py:116,123)
+    gdn = GatedDeltaNet(GDNLayerConfig(d_model=Dm, gdn_qk_heads=H, gdn_v_heads=H, gdn_head_dim=Dh, gdn_kernel_gate=True,
+                                       gdn_fla_conv=True, fused_norm_gate=True))
     attn = GatedAttention(AttnLayerConfig(d_model=Dm, attn_heads=H, attn_kv_heads=HKV, attn_head_dim=Dh,
                                           rope_theta=1e6, rope_partial=0.25))
     with torch.no_grad():
@@ -199,8 +204,9 @@ def block_pair(torch, steps: int) -> dict:
     return out
 
 
-def time_launches(torch, fn, steps: int) -> tuple[float, float]:
-    """(mean ms per step from one event pair over all steps, mean ms per launch from per-launch event pairs)."""
+def time_launches(torch, fn, steps: int, indexed: bool = False) -> tuple[float, float]:
+    """(mean ms per step from one event pair over all steps, mean ms per launch from per-launch event pairs).
+    With `indexed`, call i is fn(i) (launches rotating over input sets)."""
     stream = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
@@ -209,7 +215,7 @@ def time_launches(torch, fn, steps: int) -> tuple[float, float]:
     e0.record(stream)
     for i in range(steps):
         starts[i].record(stream)
-        fn()
+        fn(i) if indexed else fn()
         ends[i].record(stream)
     e1.record(stream)
     torch.cuda.synchronize()
@@ -217,14 +223,15 @@ def time_launches(torch, fn, steps: int) -> tuple[float, float]:
     return e0.elapsed_time(e1) / steps, per_launch
 
 
-def time_back_to_back(torch, fn, steps: int) -> float:
-    """Mean ms per step from one event pair around `steps` back-to-back calls (no per-launch events)."""
+def time_back_to_back(torch, fn, steps: int, indexed: bool = False) -> float:
+    """Mean ms per step from one event pair around `steps` back-to-back calls (no per-launch events).
+    With `indexed`, call i is fn(i) (launches rotating over input sets)."""
     stream = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     e0.record(stream)
-    for _ in range(steps):
-        fn()
+    for i in range(steps):
+        fn(i) if indexed else fn()
     e1.record(stream)
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / steps
@@ -308,7 +315,8 @@ def load_traffic(name: str):
 
 
 def cpu_baseline(torch, decode_steps: int = 100, min_seconds: float = 12.0):
-    """The CPU oracle timed on this host: config-1 prefill (full input) and config-2 decode steps."""
+    """The CPU oracle timed on this host: config-1 prefill (full input), config-3's per-document loop
+    (full input) and config-2 decode steps."""
     from oracle import decode_step_ref, recurrent_gated_delta_rule
     from sorernn_amd.synthetic import config_inputs, decode_inputs
 
@@ -324,6 +332,21 @@ def cpu_baseline(torch, decode_steps: int = 100, min_seconds: float = 12.0):
     times.sort()
     med = times[len(times) // 2]
     tokens = inp.q.shape[0] * inp.q.shape[1]
+    # config 3: the oracle's per-document loop (one batch row, so every token step is a [1, 16, 128, 128]
+    # update: ~10x slower per token than config 1's batch of 4); a bounded sample -- whole documents in
+    # order until ~10 s have passed -- keeps the bench within minutes
+    v3 = config_inputs(3)
+    bounds = [int(x) for x in v3.cu_seqlens.tolist()]
+    v_docs, v_tokens, v_t = 0, 0, 0.0
+    for n, (a, e) in enumerate(zip(bounds[:-1], bounds[1:])):
+        cu1 = torch.tensor([0, e - a])
+        t0 = time.perf_counter()
+        recurrent_gated_delta_rule(v3.q[:, a:e], v3.k[:, a:e], v3.v[:, a:e], v3.g[:, a:e], v3.beta[:, a:e], v3.scale,
+                                   v3.h0[n:n + 1], True, cu_seqlens=cu1)
+        v_t += time.perf_counter() - t0
+        v_docs, v_tokens = v_docs + 1, v_tokens + (e - a)
+        if v_t >= 10.0:
+            break
     di = decode_inputs()
     conv, st = di.conv_state.clone(), di.state.clone()
     t0 = time.perf_counter()
@@ -343,8 +366,14 @@ def cpu_baseline(torch, decode_steps: int = 100, min_seconds: float = 12.0):
         "kind": "port",
         "sample": f"full config-1 input (B=4, T=4096, H=16, d=128; 16384 tokens) through the oracle's torch fp32 "
                   f"recurrence, median of {len(times)} passes ({times[0]:.2f}-{times[-1]:.2f} s each, "
-                  f"{sum(times):.1f} s total); decode: {decode_steps} config-2 steps incl. the conv cache",
+                  f"{sum(times):.1f} s total); decode: {decode_steps} config-2 steps incl. the conv cache; "
+                  f"config 3: the per-document loop (varlen_config3)",
         "decode_us_per_step": round(dec_us, 1),
+        "varlen_config3": {
+            "tokens_per_s": round(v_tokens / v_t, 1),
+            "sample": f"the first {v_docs} of config 3's 8 documents ({v_tokens} of {bounds[-1]} tokens, H=16, d=128, "
+                      f"per-document h0 and final state) through the oracle's per-document loop, {v_t:.1f} s",
+        },
         "cpu_model": cpu,
         "torch": torch.__version__,
         "host": platform.node(),
@@ -373,13 +402,16 @@ def run_only(torch, args) -> int:
             chunk_gated_delta_rule(d.q, d.k, d.v, d.g, d.beta, scale=inp.scale, cu_seqlens=d.cu_seqlens,
                                    cu_seqlens_cpu=cu_cpu)
     elif args.only in ("prefill", "varlen"):
+        # as in the bench: launches alternate over two input sets
         idx = 1 if args.only == "prefill" else 3
         inp = config_inputs(idx)
         cu_cpu = inp.cu_seqlens
         d = inp.to("cuda")
+        sets = rotating_sets(d)
 
         def step(i):
-            chunk_gated_delta_rule(d.q, d.k, d.v, d.g, d.beta, scale=d.scale, initial_state=d.h0,
+            q_, k_, v_, g_, b_, h_ = sets[i % len(sets)]
+            chunk_gated_delta_rule(q_, k_, v_, g_, b_, scale=d.scale, initial_state=h_,
                                    output_final_state=True, cu_seqlens=d.cu_seqlens, cu_seqlens_cpu=cu_cpu)
     else:
         di = decode_inputs()
@@ -394,7 +426,7 @@ def run_only(torch, args) -> int:
             gated_delta_decode_step(x, convs[i % nrot], cw, g, b, states[i % nrot], di.H, di.HV, di.D)
     # as in the bench: the workload's own step untimed for the settle time, then W + K launches (the
     # last K of a trace are the ones the bench times)
-    st_ = settle(torch, lambda: step(0))
+    st_ = settle(torch, lambda: [step(i) for i in range(2)])
     for i in range(args.warmup + args.steps):
         step(i)
     torch.cuda.synchronize()
@@ -423,46 +455,58 @@ def varlen_docs_inputs(torch):
     return lens, cu, gdn_inputs(1, int(cu[-1]), 16, 128, dtype=torch.bfloat16, seed=1005, h0=False, cu_seqlens=cu)
 
 
+def rotating_sets(inp, n: int = 2):
+    """`n` copies of a workload's device inputs (the first is `inp`'s own tensors), visited in turn so
+    that no launch finds its inputs left in the 256 MB Infinity Cache by the previous one: every
+    config-1 set (q, k, v, g, beta, h0 and the outputs it writes) is 281 MB."""
+    base = (inp.q, inp.k, inp.v, inp.g, inp.beta, inp.h0)
+    return [base] + [tuple(None if x is None else x.clone() for x in base) for _ in range(n - 1)]
+
+
 def part_prefill(torch, args) -> dict:
-    """Config 1: the chunked prefill op (two kernels on one stream), events around every launch."""
+    """Config 1: the chunked prefill op, events around every launch.
+
+    The headline (`ms_step`, `ms_launch`, the percentiles) comes from launches alternating over two
+    input sets (2 x 281 MB, more than the 256 MB Infinity Cache), so every launch reads its inputs
+    from DRAM, as the layers of a model do; the same figures with one input set, whose inputs the
+    previous launch leaves in the Infinity Cache, are reported beside them (`*_cache_resident`)."""
     from sorernn_amd import chunk_gated_delta_rule
     from sorernn_amd.synthetic import config_inputs
 
     inp = config_inputs(1).to("cuda")
     B, T, H, K = inp.q.shape
+    sets = rotating_sets(inp)
+
+    def step_rot(i):
+        q_, k_, v_, g_, b_, h_ = sets[i % len(sets)]
+        return chunk_gated_delta_rule(q_, k_, v_, g_, b_, scale=inp.scale, initial_state=h_, output_final_state=True)
 
     def step():
-        return chunk_gated_delta_rule(inp.q, inp.k, inp.v, inp.g, inp.beta, scale=inp.scale, initial_state=inp.h0,
-                                      output_final_state=True)
+        return step_rot(0)
 
-    for _ in range(args.warmup):
-        step()
+    for i in range(args.warmup):
+        step_rot(i)
     torch.cuda.synchronize()
     # the first K steps of the process after W warmup steps (reported beside the headline)
-    cold_ms = time_back_to_back(torch, step, args.steps)
-    st = settle(torch, step)
-    for _ in range(args.warmup):
-        step()
+    cold_ms = time_back_to_back(torch, step_rot, args.steps, indexed=True)
+    st = settle(torch, lambda: [step_rot(i) for i in range(len(sets))])
+    for i in range(args.warmup):
+        step_rot(i)
     torch.cuda.synchronize()
     # the step rate from back-to-back calls with events only around the whole run; the per-launch
     # (op) times from a second run with an event pair around every call
     t0 = time.perf_counter()
-    ms_step = time_back_to_back(torch, step, args.steps)
+    ms_step = time_back_to_back(torch, step_rot, args.steps, indexed=True)
     wall = (time.perf_counter() - t0) / args.steps * 1e3
-    _, ms_launch = time_launches(torch, step, args.steps)
-    pct = launch_percentiles(torch, lambda i: step(), args.steps)
-    # the same launches alternating over two input sets (separate tensors, 2 x 281 MB > the 256 MB
-    # Infinity Cache), so no launch finds its inputs left in the cache by the previous one
-    alt = [(inp.q, inp.k, inp.v, inp.g, inp.beta, inp.h0),
-           tuple(x.clone() for x in (inp.q, inp.k, inp.v, inp.g, inp.beta, inp.h0))]
-
-    def step_alt(i):
-        q_, k_, v_, g_, b_, h_ = alt[i % 2]
-        return chunk_gated_delta_rule(q_, k_, v_, g_, b_, scale=inp.scale, initial_state=h_, output_final_state=True)
-
-    pct_rot = launch_percentiles(torch, step_alt, args.steps)
+    _, ms_launch = time_launches(torch, step_rot, args.steps, indexed=True)
+    pct = launch_percentiles(torch, step_rot, args.steps)
+    # one input set, launch after launch: its inputs stay in the Infinity Cache
+    ms_step_c = time_back_to_back(torch, step, args.steps)
+    _, ms_launch_c = time_launches(torch, step, args.steps)
+    pct_c = launch_percentiles(torch, lambda i: step(), args.steps)
     return {"B": B, "T": T, "H": H, "K": K, "ms_step": ms_step, "ms_launch": ms_launch, "wall_ms": wall,
-            "pct": pct, "pct_rot": pct_rot, "cold_ms_step": cold_ms, "settle": st,
+            "pct": pct, "ms_step_cache_resident": ms_step_c, "ms_launch_cache_resident": ms_launch_c,
+            "pct_cache_resident": pct_c, "input_sets": len(sets), "cold_ms_step": cold_ms, "settle": st,
             "min_bytes": 4 * inp.q.numel() * 2 + 2 * inp.g.numel() * 4 + 2 * inp.h0.numel() * 4}
 
 
@@ -484,7 +528,17 @@ def part_decode(torch, args) -> dict:
     for _ in range(10):
         dstep()
     settle(torch, dstep)
-    eager_ms, _ = time_launches(torch, dstep, min(args.decode_steps, 200))
+    # eager: host-launched steps back to back, one event pair around the run (events around every
+    # step would add their own host time, which a serving loop does not pay); the host time per call
+    # is measured beside it with the device left to drain
+    n_eager = min(args.decode_steps, 200)
+    eager_ms = time_back_to_back(torch, dstep, n_eager)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(n_eager):
+        dstep()
+    host_us = (time.perf_counter() - t0) / n_eager * 1e6
+    torch.cuda.synchronize()
     per_graph = 50  # steps per captured graph: one graph launch per 50 steps keeps the host off the critical path
 
     def dsteps():
@@ -506,29 +560,34 @@ def part_decode(torch, args) -> dict:
     rot_ms = time_replays(torch, rgraph, max(1, args.decode_steps // per_graph)) / per_graph
     torch.cuda.synchronize()
     return {"us_step": dec_ms * 1e3, "rot_us_step": rot_ms * 1e3, "eager_us_step": eager_ms * 1e3,
-            "per_graph": per_graph}
+            "eager_host_us_per_call": host_us, "per_graph": per_graph}
 
 
 def part_varlen(torch, args) -> dict:
-    """Config 3: 8 packed documents, 32768 tokens, per-document initial and final states."""
+    """Config 3: 8 packed documents, 32768 tokens, per-document initial and final states; launches
+    alternate over two input sets (one set is 536 MB of q, k, v and o: more than the Infinity Cache
+    already, the second set makes that hold whatever the outputs' placement)."""
     from sorernn_amd import chunk_gated_delta_rule
     from sorernn_amd.synthetic import config_inputs
 
     v3 = config_inputs(3)
     cu_cpu = v3.cu_seqlens
     v3 = v3.to("cuda")
+    sets = rotating_sets(v3)
 
-    def vstep():
-        return chunk_gated_delta_rule(v3.q, v3.k, v3.v, v3.g, v3.beta, scale=v3.scale, initial_state=v3.h0,
+    def vstep(i):
+        q_, k_, v_, g_, b_, h_ = sets[i % len(sets)]
+        return chunk_gated_delta_rule(q_, k_, v_, g_, b_, scale=v3.scale, initial_state=h_,
                                       output_final_state=True, cu_seqlens=v3.cu_seqlens, cu_seqlens_cpu=cu_cpu)
 
-    for _ in range(3):
-        vstep()
-    settle(torch, vstep)
-    n = max(5, args.steps // 5)
-    v_ms, v_launch = time_launches(torch, vstep, n)
-    v_pct = launch_percentiles(torch, lambda i: vstep(), n)
-    return {"ms_step": v_ms, "ms_launch": v_launch, "pct": v_pct, "lens": (cu_cpu[1:] - cu_cpu[:-1]).tolist()}
+    for i in range(3):
+        vstep(i)
+    settle(torch, lambda: [vstep(i) for i in range(len(sets))])
+    n = max(6, args.steps // 5)
+    v_ms, v_launch = time_launches(torch, vstep, n, indexed=True)
+    v_pct = launch_percentiles(torch, vstep, n)
+    return {"ms_step": v_ms, "ms_launch": v_launch, "pct": v_pct, "lens": (cu_cpu[1:] - cu_cpu[:-1]).tolist(),
+            "input_sets": len(sets)}
 
 
 def part_varlen_docs(torch, args) -> dict:
@@ -615,6 +674,11 @@ def assemble(parts: dict, args, cpu: dict | None) -> dict:
         "wall_ms_per_step": round(pf["wall_ms"], 4),
         "cold_ms_per_step": round(pf["cold_ms_step"], 4) if "cold_ms_step" in pf else None,
         "cold_value": round(B * T / (pf["cold_ms_step"] * 1e-3), 1) if "cold_ms_step" in pf else None,
+        "cache_resident_ms_per_step": round(pf["ms_step_cache_resident"], 4),
+        "cache_resident_value": round(B * T / (pf["ms_step_cache_resident"] * 1e-3), 1),
+        "timing": "value / ms_per_step: back-to-back launches alternating over two input sets (2 x 281 MB > the "
+                  "256 MB Infinity Cache), one event pair around the run; cache_resident_*: the same with one "
+                  "input set",
         "settle": {"ms_per_workload": args.settle_ms, "prefill_calls": pf.get("settle", {}).get("calls"),
                    "note": "every workload runs its own step untimed, back to back, for >= settle ms before "
                            "its W warmup steps (from idle the GPU's clocks settle after ~35 ms of this load); "
@@ -641,7 +705,15 @@ def assemble(parts: dict, args, cpu: dict | None) -> dict:
             "hbm_frac_at_min_bytes": round(pf["min_bytes"] / (ms_launch * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "ms_per_launch": round(ms_launch, 4),
             "launch_percentiles": pf["pct"],
-            "launch_percentiles_two_input_sets": pf["pct_rot"],
+            "input_sets": pf["input_sets"],
+            "timing": "launches alternating over two input sets (2 x 281 MB > the 256 MB Infinity Cache): every "
+                      "launch reads its inputs from DRAM",
+            "cache_resident_ms_per_launch": round(pf["ms_launch_cache_resident"], 4),
+            "cache_resident_achieved": round(flops / (pf["ms_launch_cache_resident"] * 1e-3) / 1e12, 2),
+            "cache_resident_frac": round(flops / (pf["ms_launch_cache_resident"] * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+            "cache_resident_launch_percentiles": pf["pct_cache_resident"],
+            "cache_resident_note": "one input set, launch after launch: the previous launch leaves the inputs in "
+                                   "the Infinity Cache",
             # secondary FLOP conventions: causal tiles only (5C^2d + 6Cd^2 per chunk-head), and the
             # reference's flops.py count of 4*K*V per token-head
             "flops_causal_halved": flops_c,
@@ -664,6 +736,9 @@ def assemble(parts: dict, args, cpu: dict | None) -> dict:
                                    "the Infinity Cache",
             "cache_resident_frac_hbm_peak": round(dbytes / dec_s / 1e9 / HBM_PEAK_GBS, 4),
             "eager_us_per_step": round(dc["eager_us_step"], 3),
+            "eager_host_us_per_call": round(dc.get("eager_host_us_per_call", float("nan")), 2),
+            "eager_note": "host-launched steps back to back on one state (compare cache_resident_us_per_step); "
+                          "eager_host_us_per_call is the Python + launch time of one call",
             "steps": args.decode_steps,
         },
         "varlen": {
@@ -674,6 +749,7 @@ def assemble(parts: dict, args, cpu: dict | None) -> dict:
             "launch_percentiles": vl["pct"],
             "tflops": round(v_flops / (vl["ms_launch"] * 1e-3) / 1e12, 2),
             "frac_mfma_peak": round(v_flops / (vl["ms_launch"] * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+            "input_sets": vl.get("input_sets", 1),
         },
         "varlen_docs": varlen_docs_entry(parts["varlen_docs"]),
         "train": {

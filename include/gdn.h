@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define GDN_ABI_VERSION 5
+#define GDN_ABI_VERSION 6
 
 #if defined(__GNUC__) || defined(__clang__)
 #define GDN_API __attribute__((visibility("default")))
@@ -51,6 +51,7 @@ extern "C" {
 /* activation codes for the conv and the gated norm */
 #define GDN_ACT_NONE 0
 #define GDN_ACT_SILU 1
+#define GDN_ACT_SILU_ROUNDED 2 /* gdn_qkv_conv_fwd only: the conv output rounded to x_dtype, then SiLU */
 
 /* ABI version of the loaded library (GDN_ABI_VERSION at build time). */
 GDN_API int gdn_abi_version(void);
@@ -262,7 +263,9 @@ GDN_API size_t gdn_rms_norm_gated_bwd_workspace_size(int64_t rows, int64_t D);
  * The GDN layer's q/k/v prologue in one pass (inference): x [B, T, >= 2*Cqk + Cv] with row stride
  * x_row_stride elements holds the q | k | v projection outputs (e.g. column slices of one fused
  * projection GEMM); weight [2*Cqk + Cv, 4] fp32 (the q, k, v conv weights stacked), bias or NULL.
- * Depthwise causal conv of width 4 + activation, rounded to x_dtype; with GDN_FLAG_QK_L2NORM every
+ * Depthwise causal conv of width 4 + activation, rounded to x_dtype (GDN_ACT_SILU_ROUNDED rounds the
+ * conv output to x_dtype before the SiLU, as gdn.py:208-209's unfused route does with the weight
+ * passed already rounded to x_dtype); with GDN_FLAG_QK_L2NORM every
  * head of head_dim channels of q and k is then L2-normalised (x / max(||x||, 1e-12), fp32, rounded).
  * Writes contiguous q, k [B, T, Cqk] and v [B, T, Cv]. Document resets with cu_seqlens (B == 1).
  * bf16 or fp16; head_dim 64 or 128. Replaces the three causal_conv1d calls of

@@ -20,8 +20,8 @@ FLAG_QK_L2NORM = 0x1
 FLAG_BETA_SIGMOID = 0x2
 FLAG_GATE_IN_KERNEL = 0x4
 FLAG_CU_INT32 = 0x8
-ACT_NONE, ACT_SILU = 0, 1
-ABI_VERSION = 5
+ACT_NONE, ACT_SILU, ACT_SILU_ROUNDED = 0, 1, 2
+ABI_VERSION = 6
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -126,3 +126,10 @@ def ptr(t) -> int | None:
 
 def stream_of(t: torch.Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def raw_stream(device: torch.device) -> int:
+    """The current stream of ``device`` as a raw handle, without building a ``torch.cuda.Stream`` object
+    (the per-token decode path's host time)."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    return torch._C._cuda_getCurrentRawStream(idx)

@@ -305,6 +305,9 @@ __global__ __launch_bounds__(256) void gated_delta_qkv_conv1d_kernel(QkvConvPara
 #pragma unroll
         for (int i = 0; i < W - 1; ++i) acc += w[e][i] * win[i][e];
         if (p.act == GDN_ACT_SILU) acc = silu_fast(acc);
+        // the reference's unfused route (sore/model/gdn.py:208-209): the conv output is rounded to the
+        // activation dtype before F.silu
+        else if (p.act == GDN_ACT_SILU_ROUNDED) acc = silu_fast((float)(E)acc);
         y[e] = (float)(E)acc;  // the separate conv's stored value
         ss += y[e] * y[e];
 #pragma unroll
@@ -603,7 +606,7 @@ extern "C" int gdn_qkv_conv_fwd(const void* x, int64_t x_row_stride, const float
     gdn_internal_set_error("gdn_qkv_conv_fwd: activation dtype %d unsupported (bf16 or fp16)", x_dtype);
     return GDN_ERR_UNSUPPORTED;
   }
-  if (activation != GDN_ACT_NONE && activation != GDN_ACT_SILU) {
+  if (activation != GDN_ACT_NONE && activation != GDN_ACT_SILU && activation != GDN_ACT_SILU_ROUNDED) {
     gdn_internal_set_error("gdn_qkv_conv_fwd: unknown activation %d", activation);
     return GDN_ERR_INVALID;
   }

@@ -1,7 +1,13 @@
 """GatedDeltaNet layer on the gfx950 ops: the reference layer with only its kernel imports swapped.
 
-Counterpart of ``GatedDeltaNet`` in ``sore/model/gdn.py:81-209`` (its ``fla`` backend with
-``gdn_fla_conv`` and ``fused_norm_gate`` on). The parameters, their names, shapes and init are the
+Counterpart of ``GatedDeltaNet`` in ``sore/model/gdn.py:81-209`` (its ``fla`` backend). The
+reference's two caller flags keep their meaning and defaults (``sore/model/config.py:54-55``, both
+False): ``gdn_fla_conv`` selects FLA's conv (fp32 weight, conv and SiLU in one rounding) over
+``causal_conv1d_varlen(h, weight.to(h.dtype))`` followed by ``F.silu`` (the weight rounded to the
+activation dtype, the conv output rounded before the SiLU, ``gdn.py:208-209``); ``fused_norm_gate``
+selects ``rms_norm_gated`` (one rounding) over ``o_norm(o) * F.silu(gate)`` (the normalised ``o``
+rounded before the product, ``gdn.py:180-188``). The presets the reference trains with set both
+(``config.py:116,123``). The parameters, their names, shapes and init are the
 reference's (``gdn.py:97-132``), so a reference ``state_dict`` loads unchanged; the forward keeps
 the reference's call expressions (``gdn.py:145-189``) with ``chunk_gated_delta_rule``,
 ``causal_conv1d`` and ``rms_norm_gated`` taken from ``sorernn_amd`` instead of FLA. The chunk-index
@@ -32,7 +38,7 @@ _DT_MIN, _DT_MAX = 1e-3, 1e-1
 
 @dataclass
 class GDNLayerConfig:
-    """The ``ModelConfig`` fields the layer reads (``sore/model/config.py:11,20-23,43,53``)."""
+    """The ``ModelConfig`` fields the layer reads (``sore/model/config.py:11,20-23,43,53-55``)."""
 
     d_model: int
     gdn_qk_heads: int = 1
@@ -41,6 +47,8 @@ class GDNLayerConfig:
     conv_kernel: int = 4
     norm_eps: float = 1e-6
     gdn_kernel_gate: bool = False
+    gdn_fla_conv: bool = False
+    fused_norm_gate: bool = False
 
     def __post_init__(self) -> None:
         if self.gdn_v_heads % self.gdn_qk_heads:
@@ -68,6 +76,8 @@ class GatedDeltaNet(nn.Module):
     def __init__(self, cfg: GDNLayerConfig) -> None:
         super().__init__()
         self.kernel_gate = cfg.gdn_kernel_gate
+        self.fla_conv = cfg.gdn_fla_conv
+        self.fused_norm_gate = cfg.fused_norm_gate
         self.qk_heads = cfg.gdn_qk_heads
         self.v_heads = cfg.gdn_v_heads
         self.head_dim = cfg.gdn_head_dim
@@ -101,7 +111,9 @@ class GatedDeltaNet(nn.Module):
             self._w_qkv = torch.cat([w.detach().to(dtype) for w in (self.q_proj.weight, self.k_proj.weight,
                                                                      self.v_proj.weight)], 0)
             self._w_ab = torch.cat([self.a_proj.weight.detach().to(dtype), self.b_proj.weight.detach().to(dtype)], 0)
-            self._w_conv = torch.cat([self.conv_q.detach(), self.conv_k.detach(), self.conv_v.detach()], 0).float()
+            # the unfused conv rounds its weight to the activation dtype (sore/model/gdn.py:209)
+            wc = torch.cat([self.conv_q.detach(), self.conv_k.detach(), self.conv_v.detach()], 0)
+            self._w_conv = (wc if self.fla_conv else wc.to(dtype)).float()
             self._fused_key = key
         return self._w_qkv, self._w_ab, self._w_conv
 
@@ -112,7 +124,8 @@ class GatedDeltaNet(nn.Module):
         w_qkv, w_ab, w_conv = self._fused_weights(dt)
         proj = F.linear(x, w_qkv)  # [B, T, q | k | v]
         q, k, v = qkv_causal_conv1d(proj, w_conv, hk * dh, hv * dh, dh, activation="silu", l2norm=True,
-                                    cu_seqlens=cu_seqlens, cu_seqlens_cpu=cu_seqlens_cpu)
+                                    cu_seqlens=cu_seqlens, cu_seqlens_cpu=cu_seqlens_cpu,
+                                    round_before_activation=not self.fla_conv)
         ab = F.linear(x, w_ab)  # [B, T, a | b]
         a, bl = ab[..., :hv], ab[..., hv:]
         if self.kernel_gate:
@@ -128,8 +141,14 @@ class GatedDeltaNet(nn.Module):
             cu_seqlens=cu_seqlens, cu_seqlens_cpu=cu_seqlens_cpu, **gate_kwargs,
         )
         gate = self.g_proj(x).view(b, t, hv, dh)
-        o = rms_norm_gated(o, gate, self.o_norm.weight, None, activation="swish", eps=self.o_norm.eps)
-        return self.o_proj(o.flatten(-2))
+        return self.o_proj(self._norm_gate(o, gate).flatten(-2))
+
+    def _norm_gate(self, o: Tensor, gate: Tensor) -> Tensor:
+        if self.fused_norm_gate:
+            # RMSNorm(o) * silu(gate) in one kernel, fp32 math, one rounding (sore/model/gdn.py:182-186)
+            return rms_norm_gated(o, gate, self.o_norm.weight, None, activation="swish", eps=self.o_norm.eps)
+        # o_norm(o) rounded to o's dtype, then times silu(gate) (sore/model/gdn.py:188)
+        return rms_norm_gated(o, None, self.o_norm.weight, None, eps=self.o_norm.eps) * F.silu(gate)
 
     def forward(self, x: Tensor, cu_seqlens: Tensor | None = None, cu_seqlens_cpu: Tensor | None = None) -> Tensor:
         if not torch.is_grad_enabled() and self.head_dim in (64, 128):
@@ -143,7 +162,13 @@ class GatedDeltaNet(nn.Module):
         b, t, _ = x.shape
 
         def conv(h: Tensor, weight: Tensor) -> Tensor:
-            return causal_conv1d(h, weight, activation="silu", cu_seqlens=cu_seqlens, cu_seqlens_cpu=cu_seqlens_cpu)[0]
+            if self.fla_conv:
+                return causal_conv1d(h, weight, activation="silu", cu_seqlens=cu_seqlens,
+                                     cu_seqlens_cpu=cu_seqlens_cpu)[0]
+            # the weight rounded to the activation dtype, the conv output rounded before the SiLU
+            # (sore/model/gdn.py:208-209)
+            return F.silu(causal_conv1d(h, weight.to(h.dtype), activation=None, cu_seqlens=cu_seqlens,
+                                        cu_seqlens_cpu=cu_seqlens_cpu)[0])
 
         q = conv(self.q_proj(x), self.conv_q).view(b, t, self.qk_heads, self.head_dim)
         k = conv(self.k_proj(x), self.conv_k).view(b, t, self.qk_heads, self.head_dim)
@@ -161,8 +186,7 @@ class GatedDeltaNet(nn.Module):
             use_qk_l2norm_in_kernel=True, **gate_kwargs,
         )
         gate = self.g_proj(x).view(b, t, self.v_heads, self.head_dim)
-        o = rms_norm_gated(o, gate, self.o_norm.weight, None, activation="swish", eps=self.o_norm.eps)
-        return self.o_proj(o.flatten(-2))
+        return self.o_proj(self._norm_gate(o, gate).flatten(-2))
 
     def _gate_and_beta(self, x: Tensor) -> tuple[Tensor, Tensor]:
         # g (log-decay, <= 0) in fp32; beta may stay in the activation dtype (sore/model/gdn.py:191-194)

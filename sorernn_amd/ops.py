@@ -54,17 +54,18 @@ def _no_grad_check(name: str, *tensors) -> None:
 
 
 def _check_cuda(name: str, *tensors) -> torch.device:
-    dev = None
+    first, idx = None, -1
     for t in tensors:
         if t is None:
             continue
         if not t.is_cuda:
             raise ValueError(f"{name}: every tensor must be on the GPU (got {t.device})")
-        if dev is None:
-            dev = t.device
-        elif t.device != dev:
-            raise ValueError(f"{name}: tensors on different devices ({dev} vs {t.device})")
-    return dev
+        d = t.get_device()  # an int: cheaper than building a torch.device per tensor
+        if first is None:
+            first, idx = t, d
+        elif d != idx:
+            raise ValueError(f"{name}: tensors on different devices ({first.device} vs {t.device})")
+    return None if first is None else first.device
 
 
 def _cu_info(name: str, cu_seqlens: Tensor | None, cu_seqlens_cpu: Tensor | None, batch: int, t: int):
@@ -334,23 +335,28 @@ def gated_delta_decode_step(
     fp32. Returns ``o [B,1,HV,D]`` in ``x_qkv.dtype`` (written into ``out`` when given).
     """
     name = "gated_delta_decode_step"
-    _check_cuda(name, x_qkv, conv_state, conv_weight, g, beta, state, A_log, dt_bias, out)
+    # This runs once per generated token, so the host path avoids tensor-producing calls when they
+    # would be no-ops (reshape / contiguous / detach / float each build a new tensor object) and reads
+    # the stream as a raw handle: validation only, then one ctypes call.
+    dev = _check_cuda(name, x_qkv, conv_state, conv_weight, g, beta, state, A_log, dt_bias, out)
     _no_grad_check(name, x_qkv, conv_state, conv_weight, g, beta, state)
     b = x_qkv.shape[0]
-    x2 = x_qkv.reshape(b, -1)
+    x2 = x_qkv if x_qkv.dim() == 2 and x_qkv.is_contiguous() else x_qkv.reshape(b, -1).contiguous()
     c = x2.shape[1]
     h, hv, d = num_qk_heads, num_v_heads, head_dim
     if c != (2 * h + hv) * d:
         raise ValueError(f"{name}: x_qkv has {c} channels, expected {(2 * h + hv) * d}")
-    if conv_state.dim() != 3 or tuple(conv_state.shape[:2]) != (b, c) or not conv_state.is_contiguous():
+    cs = conv_state.shape
+    if len(cs) != 3 or cs[0] != b or cs[1] != c or not conv_state.is_contiguous():
         raise ValueError(f"{name}: conv_state must be a contiguous [B,C,W] = [{b},{c},W] tensor")
-    w = conv_state.shape[2]
-    if tuple(conv_weight.shape) != (c, w):
+    w = cs[2]
+    if conv_weight.shape != (c, w):
         raise ValueError(f"{name}: conv_weight must be [C,W] = {(c, w)}")
-    if tuple(state.shape) != (b, hv, d, d) or state.dtype != torch.float32 or not state.is_contiguous():
+    if state.shape != (b, hv, d, d) or state.dtype != torch.float32 or not state.is_contiguous():
         raise ValueError(f"{name}: state must be a contiguous fp32 [B,HV,D,D] = {(b, hv, d, d)} tensor")
-    g2, b2 = g.reshape(b, -1).contiguous(), beta.reshape(b, -1).contiguous()
-    if g2.shape[1] != hv or b2.shape[1] != hv:
+    g2 = g if g.dim() == 2 and g.is_contiguous() else g.reshape(b, -1).contiguous()
+    b2 = beta if beta.dim() == 2 and beta.is_contiguous() else beta.reshape(b, -1).contiguous()
+    if g2.shape != (b, hv) or b2.shape != (b, hv):
         raise ValueError(f"{name}: g and beta must be [B,HV] = {(b, hv)}")
     flags = 0
     if use_qk_l2norm_in_kernel:
@@ -361,22 +367,25 @@ def gated_delta_decode_step(
         if A_log is None or dt_bias is None:
             raise ValueError(f"{name}: use_gate_in_kernel needs A_log and dt_bias")
         flags |= _lib.FLAG_GATE_IN_KERNEL
-        A_log = A_log.detach().float().contiguous()
-        dt_bias = dt_bias.detach().float().contiguous()
+        A_log, dt_bias = _f32(A_log), _f32(dt_bias)
     else:
         A_log = dt_bias = None
-    wgt = conv_weight.detach().float().contiguous()
-    x2 = x2.contiguous()
+    wgt = _f32(conv_weight)
     if out is None:
-        out = torch.empty(b, 1, hv, d, device=x_qkv.device, dtype=x_qkv.dtype)
-    elif tuple(out.shape) != (b, 1, hv, d) or out.dtype != x_qkv.dtype or not out.is_contiguous():
+        out = torch.empty(b, 1, hv, d, device=dev, dtype=x_qkv.dtype)
+    elif out.shape != (b, 1, hv, d) or out.dtype != x_qkv.dtype or not out.is_contiguous():
         raise ValueError(f"{name}: out must be a contiguous [B,1,HV,D] tensor of x_qkv's dtype")
-    _lib.call("gdn_decode_step", _lib.ptr(x2), _lib.ptr(conv_state), _lib.ptr(wgt), _lib.ptr(g2), _lib.ptr(b2),
-              _lib.ptr(state), _lib.ptr(out), b, h, hv, d, w, _lib.dtype_code(x2.dtype),
-              _lib.dtype_code(conv_state.dtype), _lib.dtype_code(g2.dtype), _lib.dtype_code(b2.dtype),
-              float(d**-0.5 if scale is None else scale), flags, _lib.ptr(A_log), _lib.ptr(dt_bias),
-              _lib.stream_of(x2))
+    dc = _lib.dtype_code
+    _lib.call("gdn_decode_step", x2.data_ptr(), conv_state.data_ptr(), wgt.data_ptr(), g2.data_ptr(), b2.data_ptr(),
+              state.data_ptr(), out.data_ptr(), b, h, hv, d, w, dc(x2.dtype), dc(conv_state.dtype), dc(g2.dtype),
+              dc(b2.dtype), float(d**-0.5 if scale is None else scale), flags, _lib.ptr(A_log), _lib.ptr(dt_bias),
+              _lib.raw_stream(dev))
     return out
+
+
+def _f32(t: Tensor) -> Tensor:
+    """``t`` as a contiguous fp32 tensor for a kernel that only reads it (no new tensor when it already is one)."""
+    return t if t.dtype == torch.float32 and t.is_contiguous() else t.detach().float().contiguous()
 
 
 def causal_conv1d(
@@ -421,14 +430,17 @@ def causal_conv1d(
 
 
 def qkv_causal_conv1d(x: Tensor, weight: Tensor, qk_dim: int, v_dim: int, head_dim: int, activation: str | None = "silu",
-                      l2norm: bool = True, cu_seqlens: Tensor | None = None, cu_seqlens_cpu: Tensor | None = None):
+                      l2norm: bool = True, cu_seqlens: Tensor | None = None, cu_seqlens_cpu: Tensor | None = None,
+                      round_before_activation: bool = False):
     """The GDN layer's q/k/v prologue in one launch (inference): conv + SiLU (+ per-head L2 norm of q, k).
 
     ``x [B, T, >= 2*qk_dim + v_dim]`` holds the q | k | v projection outputs (its rows may be wider,
     e.g. one fused projection GEMM's output); ``weight [2*qk_dim + v_dim, W=4]`` stacks the three
     conv weights. Returns contiguous ``q, k [B, T, qk_dim]`` and ``v [B, T, v_dim]``, equal to three
     ``causal_conv1d(..., activation)`` calls followed by ``l2norm`` of every q/k head
-    (``sore/model/gdn.py:177,199-209``). Forward only.
+    (``sore/model/gdn.py:177,199-209``). With ``round_before_activation`` the conv output is rounded
+    to ``x.dtype`` before the SiLU, the rounding point of the reference's unfused route
+    (``causal_conv1d_varlen`` then ``F.silu``, ``gdn.py:208-209``). Forward only.
     """
     name = "qkv_causal_conv1d"
     _no_grad_check(name, x, weight)
@@ -441,7 +453,7 @@ def qkv_causal_conv1d(x: Tensor, weight: Tensor, qk_dim: int, v_dim: int, head_d
     if tuple(weight.shape) != (2 * qk_dim + v_dim, 4):
         raise ValueError(f"{name}: weight must be [{2 * qk_dim + v_dim}, 4], got {tuple(weight.shape)}")
     if activation in ("silu", "swish"):
-        act = _lib.ACT_SILU
+        act = _lib.ACT_SILU_ROUNDED if round_before_activation else _lib.ACT_SILU
     elif activation is None:
         act = _lib.ACT_NONE
     else:

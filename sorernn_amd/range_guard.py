@@ -37,6 +37,9 @@ _mode = os.environ.get("SORERNN_RANGE_GUARD", "warn")
 if _mode not in MODES:
     raise ValueError(f"SORERNN_RANGE_GUARD={_mode!r}: expected one of {MODES}")
 _words: dict[int, tuple[torch.Tensor, np.ndarray]] = {}
+# Flag words unregistered by set_range_guard("off"). Kernels still in flight, and graphs captured
+# while a word was registered, keep its address, so a word is never freed before the process ends.
+_retired: list[torch.Tensor] = []
 _fallback_noted = False
 
 _EARLIER = ("chunk_gated_delta_rule: an earlier chunked forward on cuda:{dev} stored inf or NaN outputs (an fp16 "
@@ -53,7 +56,8 @@ def set_range_guard(mode: str) -> None:
     if mode == "off":
         for dev in list(_words):
             _lib.call("gdn_set_range_flag", dev, None)
-            del _words[dev]
+            # kept alive: launches in flight and captured graphs may still store into it
+            _retired.append(_words.pop(dev)[0])
 
 
 def range_guard() -> str:
@@ -93,8 +97,15 @@ def before_call(device: torch.device) -> np.ndarray | None:
 
 def call_overflowed(word: np.ndarray | None, device: torch.device) -> bool:
     """After a chunk launch in the "raise" and "fallback" modes: wait for the call's stream and
-    return True (clearing the word) when the call set the flag. False in the other modes."""
+    return True (clearing the word) when the call set the flag. False in the other modes, and during
+    HIP graph capture (a synchronisation would invalidate the capture): a captured call is then
+    reported as in "warn" mode, by the next eager call or ``check_chunk_range()``.
+
+    The word is per device, not per call or stream: a flag that a call on another stream of the
+    device set while this one ran is reported here as well."""
     if word is None or _mode not in ("raise", "fallback"):
+        return False
+    if torch.cuda.is_current_stream_capturing():
         return False
     torch.cuda.current_stream(device).synchronize()
     if not word[0]:

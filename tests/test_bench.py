@@ -23,10 +23,11 @@ def _fake_parts():
     pct = {"p10_ms": 0.16, "median_ms": 0.17, "p90_ms": 0.18}
     return {
         "prefill": {"B": 4, "T": 4096, "H": 16, "K": 128, "ms_step": 0.17, "ms_launch": 0.168, "wall_ms": 0.2,
-                    "pct": pct, "pct_rot": pct, "min_bytes": 278921216, "cold_ms_step": 0.2,
+                    "pct": pct, "ms_step_cache_resident": 0.15, "ms_launch_cache_resident": 0.148,
+                    "pct_cache_resident": pct, "input_sets": 2, "min_bytes": 278921216, "cold_ms_step": 0.2,
                     "settle": {"calls": 640, "ms": 100.2}},
         "decode": {"us_step": 25.0, "rot_us_step": 32.0, "eager_us_step": 40.0, "per_graph": 50},
-        "varlen": {"ms_step": 0.4, "ms_launch": 0.39, "pct": pct, "lens": [4096] * 8},
+        "varlen": {"ms_step": 0.4, "ms_launch": 0.39, "pct": pct, "lens": [4096] * 8, "input_sets": 2},
         "varlen_docs": {"ms_step": 0.5, "ms_launch": 0.49, "pct": pct, "lens": [100, 4000, 28668]},
         "train": {"fwd_ms": 0.28, "bwd_ms": 0.6},
         "block_pair": {"gdn_layer_ms": 1.0, "attn_layer_ms": 1.0},
@@ -50,6 +51,11 @@ def test_assembled_line_keeps_the_driver_contract():
     assert rf["achieved"] == pytest.approx(47_244_640_256 / 0.168e-3 / 1e12, rel=1e-3)
     assert rf["frac"] == pytest.approx(rf["achieved"] / bench.BF16_PEAK_TFLOPS, rel=1e-3)
     assert rf["flops_causal_halved"] == 36_507_222_016 and rf["flops_reference_flops_py"] == 17_179_869_184
+    # the headline rotates over two input sets (DRAM-served); the one-set rate is reported beside it
+    assert rf["input_sets"] == 2 and line["varlen"]["input_sets"] == 2
+    assert line["cache_resident_value"] == pytest.approx(4 * 4096 / 0.15e-3, rel=1e-6)
+    assert rf["cache_resident_frac"] == pytest.approx(47_244_640_256 / 0.148e-3 / 1e12 / bench.BF16_PEAK_TFLOPS,
+                                                      rel=1e-3)
     # the decode headline is the DRAM-served (rotating) step; the cache-resident one is reported beside it
     assert line["decode"]["us_per_step"] == 32.0
     assert line["decode"]["frac_hbm_peak"] == pytest.approx(bench.decode_bytes() / 32e-6 / 8e12, rel=1e-3)

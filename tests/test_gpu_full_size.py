@@ -54,7 +54,8 @@ def _gdn_layer_config4():
     from sorernn_amd.gdn_layer import GatedDeltaNet, GDNLayerConfig
 
     torch.manual_seed(4)
-    cfg = GDNLayerConfig(d_model=2048, gdn_qk_heads=16, gdn_v_heads=16, gdn_head_dim=128, gdn_kernel_gate=True)
+    cfg = GDNLayerConfig(d_model=2048, gdn_qk_heads=16, gdn_v_heads=16, gdn_head_dim=128, gdn_kernel_gate=True,
+                         gdn_fla_conv=True, fused_norm_gate=True)
     layer = GatedDeltaNet(cfg)
     with torch.no_grad():
         for name in ("q_proj", "k_proj", "v_proj", "g_proj", "a_proj", "b_proj", "o_proj"):

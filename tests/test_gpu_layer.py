@@ -8,7 +8,9 @@ control (``:165-193``), and the no-host-sync property of the packed path (``test
 import pytest
 import torch
 
-from oracle import causal_conv1d_silu, gate_and_beta, l2norm, recurrent_gated_delta_rule, rms_norm_gated
+import torch.nn.functional as F
+
+from oracle import causal_conv1d_silu, gate_and_beta, l2norm, recurrent_gated_delta_rule, rms_norm, rms_norm_gated
 from sorernn_amd.gdn_layer import GatedDeltaNet, GDNLayerConfig
 
 pytestmark = pytest.mark.gpu
@@ -16,26 +18,42 @@ DEV = "cuda"
 BF16 = torch.bfloat16
 
 
-def _layer(kernel_gate=True, rep=2, seed=0, d_model=256, head_dim=128):
+def _layer(kernel_gate=True, rep=2, seed=0, d_model=256, head_dim=128, fla_conv=True, fused_norm_gate=True):
+    """The layer with the caller flags of the reference's training presets (gdn_fla_conv and
+    fused_norm_gate on, sore/model/config.py:116,123) unless asked otherwise."""
     torch.manual_seed(seed)
     cfg = GDNLayerConfig(d_model=d_model, gdn_qk_heads=2, gdn_v_heads=2 * rep, gdn_head_dim=head_dim,
-                         gdn_kernel_gate=kernel_gate)
+                         gdn_kernel_gate=kernel_gate, gdn_fla_conv=fla_conv, fused_norm_gate=fused_norm_gate)
     return GatedDeltaNet(cfg)
 
 
 def _oracle_forward(layer, x, cu=None):
-    """The same layer computed with the CPU oracle in fp32 (bf16 rounding where the GPU path stores bf16)."""
+    """The same layer computed with the CPU oracle in fp32 (bf16 rounding where the GPU path stores bf16),
+    with the rounding points of the layer's caller flags: without gdn_fla_conv the conv weight is
+    rounded to bf16 and the conv output rounded before the SiLU (sore/model/gdn.py:208-209); without
+    fused_norm_gate RMSNorm(o) is rounded to bf16 before the product with silu(gate) (gdn.py:188)."""
     b, t, _ = x.shape
     hd, hq, hv = layer.head_dim, layer.qk_heads, layer.v_heads
     with torch.no_grad():
         xb = x.to(BF16).float()
         lin = lambda m: (xb @ m.weight.to(BF16).float().T).to(BF16)  # noqa: E731  bf16 GEMM, bf16 output
-        q = causal_conv1d_silu(lin(layer.q_proj), layer.conv_q.float(), cu).view(b, t, hq, hd)
-        k = causal_conv1d_silu(lin(layer.k_proj), layer.conv_k.float(), cu).view(b, t, hq, hd)
-        v = causal_conv1d_silu(lin(layer.v_proj), layer.conv_v.float(), cu).view(b, t, hv, hd)
+
+        def conv(h, w):
+            if layer.fla_conv:
+                return causal_conv1d_silu(h, w.float(), cu)
+            return F.silu(causal_conv1d_silu(h, w.to(BF16).float(), cu, activation=None).float()).to(BF16)
+
+        q = conv(lin(layer.q_proj), layer.conv_q).view(b, t, hq, hd)
+        k = conv(lin(layer.k_proj), layer.conv_k).view(b, t, hq, hd)
+        v = conv(lin(layer.v_proj), layer.conv_v).view(b, t, hv, hd)
         g, beta = gate_and_beta(lin(layer.a_proj), lin(layer.b_proj), layer.A_log, layer.dt_bias)
         o, _ = recurrent_gated_delta_rule(l2norm(q), l2norm(k), v, g, beta, hd**-0.5, cu_seqlens=cu)
-        o = rms_norm_gated(o, lin(layer.g_proj).view(b, t, hv, hd), layer.o_norm.weight, layer.o_norm.eps)
+        gate = lin(layer.g_proj).view(b, t, hv, hd)
+        if layer.fused_norm_gate:
+            o = rms_norm_gated(o, gate, layer.o_norm.weight, layer.o_norm.eps)
+        else:
+            o = (rms_norm(o, layer.o_norm.weight, layer.o_norm.eps).float() * F.silu(gate.float()).to(BF16).float())
+            o = o.to(BF16)
         return o.flatten(-2).float() @ layer.o_proj.weight.to(BF16).float().T
 
 
@@ -63,6 +81,32 @@ def test_layer_matches_oracle(kernel_gate, cu_case, rep):
     out = _run(layer.to(DEV), x, cu_t)
     err = (out - ref).abs().max().item()
     assert err <= 2e-2 * ref.abs().max().item() + 1e-3, f"max-abs error {err:.3e} (max|ref| {ref.abs().max():.3e})"
+
+
+@pytest.mark.parametrize("route", ["inference", "reference"])
+@pytest.mark.parametrize("cu_case", ["rows", "short_docs"])
+def test_layer_unfused_caller_flags_match_oracle(route, cu_case):
+    """gdn_fla_conv and fused_norm_gate off (the reference's ModelConfig defaults): the layer takes the
+    reference's rounding points (conv weight in bf16 and the conv output rounded before F.silu,
+    o_norm(o) rounded before the gate product), on both of its routes."""
+    cu = _CU_CASES[cu_case]
+    layer = _layer(True, rep=2, fla_conv=False, fused_norm_gate=False)
+    b = 2 if cu is None else 1
+    x = torch.randn(b, 512, 256, generator=torch.Generator().manual_seed(12))
+    cu_t = None if cu is None else torch.tensor(cu)
+    ref = _oracle_forward(layer, x, cu_t)
+    layer = layer.to(DEV)
+    if route == "inference":
+        out = _run(layer, x, cu_t)
+    else:
+        with torch.no_grad(), torch.autocast("cuda", dtype=BF16):
+            cu_dev = None if cu_t is None else cu_t.to(DEV)
+            out = layer._forward_reference(x.to(DEV), cu_seqlens=cu_dev, cu_seqlens_cpu=cu_t).float().cpu()
+    err = (out - ref).abs().max().item()
+    assert err <= 2e-2 * ref.abs().max().item() + 1e-3, f"max-abs error {err:.3e} (max|ref| {ref.abs().max():.3e})"
+    # negative control: the fused-flag oracle differs from the unfused one at these rounding points
+    layer.fla_conv = layer.fused_norm_gate = True
+    assert (_oracle_forward(layer.cpu(), x, cu_t) - ref).abs().max() > 0
 
 
 def test_layer_packed_equals_separate_and_no_host_sync():
@@ -142,7 +186,8 @@ def test_layer_extreme_inputs_stay_finite():
 
     sorernn_amd.check_chunk_range()
     torch.manual_seed(0)
-    cfg = GDNLayerConfig(d_model=128, gdn_qk_heads=2, gdn_v_heads=4, gdn_head_dim=64, gdn_kernel_gate=True)
+    cfg = GDNLayerConfig(d_model=128, gdn_qk_heads=2, gdn_v_heads=4, gdn_head_dim=64, gdn_kernel_gate=True,
+                         gdn_fla_conv=True, fused_norm_gate=True)
     layer = GatedDeltaNet(cfg).to(DEV)
     x = (torch.randn(1, 64, 128, generator=torch.Generator().manual_seed(6)) * 100).to(DEV).requires_grad_(True)
     cu = torch.tensor([0, 30, 64])
@@ -166,7 +211,8 @@ def test_layer_cu_seqlens_cpu_is_exact():
 
     def run(with_cpu):
         torch.manual_seed(0)
-        cfg = GDNLayerConfig(d_model=128, gdn_qk_heads=2, gdn_v_heads=4, gdn_head_dim=64, gdn_kernel_gate=True)
+        cfg = GDNLayerConfig(d_model=128, gdn_qk_heads=2, gdn_v_heads=4, gdn_head_dim=64, gdn_kernel_gate=True,
+                         gdn_fla_conv=True, fused_norm_gate=True)
         layer = GatedDeltaNet(cfg).to(DEV)
         xd = x.to(DEV).requires_grad_(True)
         with torch.autocast("cuda", dtype=BF16):

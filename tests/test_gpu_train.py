@@ -134,7 +134,8 @@ _CU_CASES = {"rows": None, "short_docs": [0, 1, 3, 4, 70, 200, 512], "one_doc": 
 def test_layer_backward_matches_oracle(rep, cu_case, kernel_gate):
     cu = _CU_CASES[cu_case]
     torch.manual_seed(0)
-    cfg = GDNLayerConfig(d_model=128, gdn_qk_heads=2, gdn_v_heads=2 * rep, gdn_head_dim=64, gdn_kernel_gate=kernel_gate)
+    cfg = GDNLayerConfig(d_model=128, gdn_qk_heads=2, gdn_v_heads=2 * rep, gdn_head_dim=64, gdn_kernel_gate=kernel_gate,
+                         gdn_fla_conv=True, fused_norm_gate=True)
     layer = GatedDeltaNet(cfg)
     gen = torch.Generator().manual_seed(2)
     b = 2 if cu is None else 1
@@ -162,7 +163,8 @@ def test_layer_step_compiles_without_graph_breaks(cu):
     """``torch.compile(fullgraph=True)`` of a layer's forward + backward (a graph break raises); the
     compiled step's gradients match the eager step's."""
     torch.manual_seed(0)
-    cfg = GDNLayerConfig(d_model=128, gdn_qk_heads=2, gdn_v_heads=4, gdn_head_dim=64, gdn_kernel_gate=True)
+    cfg = GDNLayerConfig(d_model=128, gdn_qk_heads=2, gdn_v_heads=4, gdn_head_dim=64, gdn_kernel_gate=True,
+                         gdn_fla_conv=True, fused_norm_gate=True)
     layer = GatedDeltaNet(cfg).to(DEV)
     b = 2 if cu is None else 1
     x = torch.randn(b, 256, 128, generator=torch.Generator().manual_seed(3)).to(DEV)
@@ -195,7 +197,8 @@ def test_selective_checkpoint_policy_sees_the_gdn_ops():
     from torch.utils.checkpoint import CheckpointPolicy, checkpoint, create_selective_checkpoint_contexts
 
     torch.manual_seed(0)
-    cfg = GDNLayerConfig(d_model=128, gdn_qk_heads=2, gdn_v_heads=4, gdn_head_dim=64, gdn_kernel_gate=True)
+    cfg = GDNLayerConfig(d_model=128, gdn_qk_heads=2, gdn_v_heads=4, gdn_head_dim=64, gdn_kernel_gate=True,
+                         gdn_fla_conv=True, fused_norm_gate=True)
     layer = GatedDeltaNet(cfg).to(DEV)
     x = torch.randn(2, 192, 128, generator=torch.Generator().manual_seed(4)).to(DEV)
     seen = set()

@@ -25,7 +25,8 @@ def test_size_formulas_match_the_library():
 
 def _trace_layer_forward(kernel_gate):
     torch.manual_seed(0)
-    cfg = GDNLayerConfig(d_model=128, gdn_qk_heads=2, gdn_v_heads=4, gdn_head_dim=64, gdn_kernel_gate=kernel_gate)
+    cfg = GDNLayerConfig(d_model=128, gdn_qk_heads=2, gdn_v_heads=4, gdn_head_dim=64, gdn_kernel_gate=kernel_gate,
+                         gdn_fla_conv=True, fused_norm_gate=True)
     layer = GatedDeltaNet(cfg).to(torch.bfloat16)
     params = dict(layer.named_parameters())
 

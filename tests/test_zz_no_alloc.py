@@ -56,7 +56,8 @@ def test_noalloc_matches_workspace_entry_varlen():
 def test_noalloc_rejects_sizes_beyond_its_array():
     cap = int(_lib.load().gdn_chunk_fwd_noalloc_max_workspace())
     tokens = cap // (16 * 128) + 64  # more token-heads than the array holds at HV = 16
-    p = 1 << 20  # never dereferenced: the size check fails before anything is launched
+    # null tensor pointers: the size check fails first; were it ever skipped, the entry point's
+    # null-pointer check would still stop the call on the host before any launch
     with pytest.raises(ValueError, match="scratch array"):
-        _lib.call("gdn_chunk_fwd_noalloc", p, p, p, p, p, None, p, None, None, 1, tokens, 16, 16, 128, 128, 1,
-                  _lib.DTYPE_BF16, _lib.DTYPE_F32, _lib.DTYPE_F32, 0.088, 0, None, None, None)
+        _lib.call("gdn_chunk_fwd_noalloc", None, None, None, None, None, None, None, None, None, 1, tokens, 16, 16,
+                  128, 128, 1, _lib.DTYPE_BF16, _lib.DTYPE_F32, _lib.DTYPE_F32, 0.088, 0, None, None, None)
