@@ -38,5 +38,34 @@ inline int64_t chunk_t_bytes(int64_t tokens, int64_t HV) { return align256(token
 
 // Launches the index kernel (with cu) and the prep kernel; returns a GDN status.
 int launch_chunk_prep(const ChunkPrepParams& p, int64_t B, int64_t K, hipStream_t s);
+// Launches the index kernel only (with cu): chunk_first and the longest-first order.
+int launch_chunk_index(const void* cu, int cu_i32, int64_t N, int* chunk_first, int* order, hipStream_t s);
+
+// The cooperative prefill (gdn_chunk_coop.hip): one launch for K = V = 128 inference calls. The
+// four 32-column slices of a (sequence, head) chain share the per-chunk P, T/A blocks and gate
+// terms through a ring in the workspace; the sync words must be zero at launch (the launcher
+// clears them with a fill kernel first).
+struct CoopArgs {
+  const void *q, *k, *v, *g, *beta;
+  const float* h0;
+  void* o;
+  float* ht;
+  const void* cu;
+  const int* order;
+  int cu_i32;
+  int64_t T, H, HV, N;
+  int dg, db;
+  float scale;
+  unsigned flags;
+  const float *A_log, *dt_bias;
+  char* ring;
+  unsigned* sync;
+  unsigned* range_flag;
+  unsigned* err;
+};
+int coop_ring_slots(int64_t T);                    // ring slots per chain for sequences of <= T tokens
+int64_t coop_ring_bytes(int64_t chains, int64_t T);
+int64_t coop_sync_bytes(int64_t chains);  // includes one error word after the chains' sync words
+int launch_chunk_coop(const CoopArgs& a, hipStream_t s);
 
 }  // namespace gdn

@@ -43,7 +43,10 @@
 //
 // LDS: K (3 slots), Q (2 slots), T - I, P, V and O (2 slots each), gate terms (3 slots).
 
+#include <algorithm>
 #include <atomic>
+#include <cstdlib>
+#include <cstring>
 #include <mutex>
 #include <type_traits>
 
@@ -679,11 +682,22 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
 
 using namespace gdn;
 
+// Workspace layouts: the two-kernel prefill (training forward, head dims other than 128) keeps the
+// T - I rows first, then the varlen index; the cooperative prefill keeps its package ring and sync
+// words first, then the varlen index. The size covers both.
+namespace {
+size_t index_bytes(int64_t N, int varlen) {
+  return varlen ? (size_t)(align256((N + 1) * 4) + align256(N * 4)) : 0;
+}
+size_t coop_front_bytes(int64_t T, int64_t HV, int64_t N) {
+  return (size_t)(coop_ring_bytes(N * HV, T) + coop_sync_bytes(N * HV));
+}
+}  // namespace
+
 extern "C" size_t gdn_chunk_workspace_size(int64_t B, int64_t T, int64_t HV, int64_t N, int varlen) {
   if (B <= 0 || T < 0 || HV <= 0 || N <= 0) return 0;
-  size_t bytes = (size_t)chunk_t_bytes(B * T, HV);
-  if (varlen) bytes += (size_t)(align256((N + 1) * 4) + align256(N * 4));
-  return bytes;
+  const size_t front = std::max((size_t)chunk_t_bytes(B * T, HV), coop_front_bytes(T, HV, N));
+  return front + index_bytes(N, varlen);
 }
 
 namespace {
@@ -740,13 +754,37 @@ int chunk_fwd_impl(const void* q, const void* k, const void* v, const void* g, c
     return GDN_ERR_INVALID;
   }
   if (T == 0) return GDN_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int cu_i32 = (flags & GDN_FLAG_CU_INT32) ? 1 : 0;
+  const int dev = stream_device(s);
+  unsigned* const range_flag = dev >= 0 && dev < kMaxDevices ? g_range_flag[dev].load(std::memory_order_acquire)
+                                                             : nullptr;
+  // The cooperative single-launch prefill for K = V = 128 inference calls, while it is being
+  // brought up selected with SORERNN_PREFILL=coop (the two-kernel prefill otherwise).
+  static const bool two_kernel = [] {
+    const char* e = getenv("SORERNN_PREFILL");
+    return !(e && !strcmp(e, "coop"));
+  }();
+  if (!chunk_states && K == 128 && V == 128 && !two_kernel) {
+    char* const ws = static_cast<char*>(workspace);
+    const int64_t chains = N * HV;
+    const size_t front = coop_front_bytes(T, HV, N);
+    int* const chunk_first = cu_seqlens ? reinterpret_cast<int*>(ws + front) : nullptr;
+    int* const order = cu_seqlens ? reinterpret_cast<int*>(ws + front + align256((N + 1) * 4)) : nullptr;
+    if (cu_seqlens) {
+      const int rc = launch_chunk_index(cu_seqlens, cu_i32, N, chunk_first, order, s);
+      if (rc != GDN_OK) return rc;
+    }
+    unsigned* const sync = reinterpret_cast<unsigned*>(ws + coop_ring_bytes(chains, T));
+    CoopArgs a{q, k, v, g, beta, initial_state, o, final_state, cu_seqlens, order, cu_i32, T, H, HV, N,
+               g_dtype, beta_dtype, scale, flags, A_log, dt_bias, ws, sync, range_flag, nullptr};
+    return launch_chunk_coop(a, s);
+  }
   const int64_t blocks = N * HV * (V / kVB);
   if (blocks > 0x7fffffff) {
     gdn_internal_set_error("gdn_chunk_fwd: grid too large");
     return GDN_ERR_UNSUPPORTED;
   }
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const int cu_i32 = (flags & GDN_FLAG_CU_INT32) ? 1 : 0;
   f16* tw = static_cast<f16*>(workspace);
   char* const ws = static_cast<char*>(workspace);
   const int* chunk_first = cu_seqlens ? reinterpret_cast<const int*>(ws + chunk_t_bytes(B * T, HV)) : nullptr;
@@ -756,9 +794,6 @@ int chunk_fwd_impl(const void* q, const void* k, const void* v, const void* g, c
                      A_log, dt_bias};
   const int rc = launch_chunk_prep(pp, B, K, s);
   if (rc != GDN_OK) return rc;
-  const int dev = stream_device(s);
-  unsigned* const range_flag = dev >= 0 && dev < kMaxDevices ? g_range_flag[dev].load(std::memory_order_acquire)
-                                                             : nullptr;
   ChunkParams p{q, k, v, g, beta, initial_state, o, final_state, tw, cu_seqlens, order, cu_i32, T, H, HV, N,
                 g_dtype, beta_dtype, scale, flags, A_log, dt_bias, static_cast<bf16*>(chunk_states), chunk_first,
                 range_flag};

@@ -403,6 +403,11 @@ int device_cus(hipStream_t s) {
 
 }  // namespace
 
+int launch_chunk_index(const void* cu, int cu_i32, int64_t N, int* chunk_first, int* order, hipStream_t s) {
+  hipLaunchKernelGGL(gated_delta_chunk_index_kernel, dim3(1), dim3(1024), 0, s, cu, cu_i32, N, chunk_first, order);
+  return gdn_internal_check_launch("gated_delta_chunk_index_kernel");
+}
+
 int launch_chunk_prep(const ChunkPrepParams& prm, int64_t B, int64_t K, hipStream_t s) {
   ChunkPrepParams p = prm;
   if (p.cu) {

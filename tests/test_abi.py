@@ -59,13 +59,27 @@ def test_unsupported_options_raise():
         chunk_gated_delta_rule(q, q, q, torch.zeros(1, 4, 1), torch.ones(1, 4, 1), allow_neg_eigval=True)
 
 
+def _align(b):
+    return (b + 255) // 256 * 256
+
+
+def _coop_front(t, hv, n):
+    """The cooperative prefill's package ring (16 KiB per slot, min(8, ceil(T / 64)) slots per
+    (sequence, head) chain) and its sync words (8 + 8 per slot per chain, 4 bytes each, plus one error word)."""
+    slots = min(8, max(1, -(-t // 64)))
+    return _align(n * hv * slots * 16384) + _align((n * hv * (8 + 8 * 8) + 1) * 4)
+
+
 def test_chunk_workspace_size_matches_layout():
-    """gdn_chunk_workspace_size: one 128-byte row of T - I per token-head, plus the varlen index
-    arrays (chunk_first[N + 1] and order[N], int32, 256-byte aligned each); 0 for invalid sizes."""
+    """gdn_chunk_workspace_size: the larger of the two-kernel prefill's T - I rows (one 128-byte row per
+    token-head) and the cooperative prefill's package ring + sync words, plus the varlen index arrays
+    (chunk_first[N + 1] and order[N], int32, 256-byte aligned each); 0 for invalid sizes."""
     from sorernn_amd.ops import chunk_workspace_bytes
+    assert chunk_workspace_bytes(4, 4096, 16, 4, False) == max(4 * 4096 * 16 * 128, _coop_front(4096, 16, 4))
     assert chunk_workspace_bytes(4, 4096, 16, 4, False) == 4 * 4096 * 16 * 128
-    assert chunk_workspace_bytes(1, 32768, 16, 8, True) == 32768 * 16 * 128 + 256 + 256
-    assert chunk_workspace_bytes(1, 100, 3, 300, True) == 100 * 3 * 128 + 1280 + 1280
+    assert chunk_workspace_bytes(1, 32768, 16, 8, True) == max(32768 * 16 * 128, _coop_front(32768, 16, 8)) + 512
+    assert chunk_workspace_bytes(1, 100, 3, 300, True) == max(_align(100 * 3 * 128), _coop_front(100, 3, 300)) + 2560
+    assert chunk_workspace_bytes(1, 100, 3, 300, True) == _coop_front(100, 3, 300) + 2560
     assert chunk_workspace_bytes(0, 100, 3, 1, False) == 0
 
 
