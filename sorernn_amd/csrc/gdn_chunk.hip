@@ -759,13 +759,11 @@ int chunk_fwd_impl(const void* q, const void* k, const void* v, const void* g, c
   const int dev = stream_device(s);
   unsigned* const range_flag = dev >= 0 && dev < kMaxDevices ? g_range_flag[dev].load(std::memory_order_acquire)
                                                              : nullptr;
-  // The cooperative single-launch prefill for K = V = 128 inference calls, while it is being
-  // brought up selected with SORERNN_PREFILL=coop (the two-kernel prefill otherwise).
-  static const bool two_kernel = [] {
-    const char* e = getenv("SORERNN_PREFILL");
-    return !(e && !strcmp(e, "coop"));
-  }();
-  if (!chunk_states && K == 128 && V == 128 && !two_kernel) {
+  // The cooperative single-launch prefill for K = V = 128 inference calls, selected per call with
+  // SORERNN_PREFILL=coop (the two-kernel prefill otherwise, which is faster at every measured size).
+  const char* const sel = getenv("SORERNN_PREFILL");
+  const bool coop = sel && !strcmp(sel, "coop");
+  if (!chunk_states && K == 128 && V == 128 && coop) {
     char* const ws = static_cast<char*>(workspace);
     const int64_t chains = N * HV;
     const size_t front = coop_front_bytes(T, HV, N);

@@ -64,10 +64,11 @@ def _align(b):
 
 
 def _coop_front(t, hv, n):
-    """The cooperative prefill's package ring (16 KiB per slot, min(8, ceil(T / 64)) slots per
-    (sequence, head) chain) and its sync words (8 + 8 per slot per chain, 4 bytes each, plus one error word)."""
+    """The cooperative prefill's package ring (47,360 bytes per slot: the fp16 K and Q rows, P, the T/A
+    blocks and the gate terms of a chunk; min(8, ceil(T / 64)) slots per (sequence, head) chain) and its
+    sync words (8 + 8 per slot of 8 per chain, 4 bytes each, plus one error word)."""
     slots = min(8, max(1, -(-t // 64)))
-    return _align(n * hv * slots * 16384) + _align((n * hv * (8 + 8 * 8) + 1) * 4)
+    return _align(n * hv * slots * 47360) + _align((n * hv * (8 + 8 * 8) + 1) * 4)
 
 
 def test_chunk_workspace_size_matches_layout():

@@ -219,3 +219,25 @@ def test_chunk_config0_full_precision_inputs(dtype):
     assert_output_close(o.cpu(), o_ref)
     assert_state_close(st.cpu(), st_ref)
 
+
+
+@pytest.mark.parametrize("case", ["T700_h0", "T640_gva2x", "varlen", "short"])
+def test_cooperative_prefill_matches_oracle(case, monkeypatch):
+    """The cooperative single-launch prefill (``SORERNN_PREFILL=coop``, K = V = 128 inference): more
+    chunks than the ring has slots (the slots are reused), grouped value heads, varlen documents that
+    end inside a chunk, and a sequence shorter than a chunk."""
+    monkeypatch.setenv("SORERNN_PREFILL", "coop")
+    print(f"cooperative prefill {case}", flush=True)
+    if case == "T700_h0":
+        inp = gdn_inputs(2, 700, 2, 128, dtype=torch.bfloat16, seed=21, h0=True)
+    elif case == "T640_gva2x":
+        inp = gdn_inputs(1, 640, 2, 128, HV=4, dtype=torch.bfloat16, seed=22, h0=False)
+    elif case == "varlen":
+        cu = torch.tensor([0, 5, 600, 601, 1000], dtype=torch.long)
+        inp = gdn_inputs(1, 1000, 2, 128, HV=2, dtype=torch.bfloat16, seed=23, h0=True, cu_seqlens=cu)
+    else:
+        inp = gdn_inputs(3, 37, 2, 128, dtype=torch.bfloat16, seed=24, h0=True)
+    o, st = _chunk(inp)
+    o_ref, st_ref = _oracle(inp)
+    assert_output_close(o.cpu(), o_ref)
+    assert_state_close(st.cpu(), st_ref)
