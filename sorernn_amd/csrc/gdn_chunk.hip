@@ -94,6 +94,112 @@ constexpr int kNT = 512;      // threads per workgroup (8 waves)
 // SAVE (training forward): the state waves also store the state entering every chunk, rounded to
 // bf16 and transposed ([V][K]: a lane's four consecutive keys are one 8-byte store), the input of
 // the backward's per-chunk gradient kernel, which uses it only as a bf16 MFMA operand.
+// The fp32 recurrence of one 32-column slice of a (sequence, value head), per token (the algebra of
+// gated_delta_recurrent_kernel, sore/model/gdn_ref.py:17-21):
+//   a = exp(g), delta = beta (v - a S^T k^), S' = a S + k^ delta^T, o = scale S'^T q^
+// with k^, q^ the fp32 L2-normalised k and q when asked. Wave w owns the columns 4w .. 4w + 3 of the
+// slice: lane (g, i) holds rows i * KD/16 .. +KD/16 of column 4w + g, and the column's dot products
+// are sums over its 16 lanes (DPP). Each chunk's q/k rows, V slice and gate values are staged in
+// LDS (the chunk kernel's tiles, no longer in use) by all 512 threads first.
+template <int KD, int VD, bool SAVE>
+__device__ __forceinline__ void recover_slice(const ChunkParams& p, int64_t n, int hv, int h, int vb, int64_t bos,
+                                           int64_t eos, int64_t cg_first, bf16* kl, bf16* ql, bf16* vl,
+                                           ChunkGates* gl) {
+  constexpr int KPL = KD / 16;
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6, g4 = lane >> 4, li = lane & 15;
+  const int col = vb * kVB + 4 * w + g4;  // value column within the head
+  const bool l2 = p.flags & GDN_FLAG_QK_L2NORM;
+  const int64_t sb0 = (n * p.HV + hv) * (int64_t)KD * VD;
+  float s[KPL];
+#pragma unroll
+  for (int e = 0; e < KPL; ++e) s[e] = p.h0 ? p.h0[sb0 + (int64_t)(li * KPL + e) * VD + col] : 0.f;
+  const bf16* qg = static_cast<const bf16*>(p.q);
+  const bf16* kg = static_cast<const bf16*>(p.k);
+  const bf16* vg = static_cast<const bf16*>(p.v);
+  bf16* og = static_cast<bf16*>(p.o);
+  u16x2 om = {0, 0};
+  const int nc = (int)((eos - bos + kC - 1) / kC);
+  for (int c = 0; c < nc; ++c) {
+    const int64_t c0 = bos + (int64_t)c * kC;
+    const int len = (int)((eos - c0) < kC ? (eos - c0) : kC);
+    if constexpr (SAVE) {
+      // the state entering chunk c, bf16, [V][K] (as the chunk kernel saves it)
+      bf16* hs = p.hs + ((cg_first + c) * p.HV + hv) * (int64_t)(KD * VD) + (int64_t)col * KD + li * KPL;
+#pragma unroll
+      for (int e = 0; e < KPL; ++e) hs[e] = static_cast<bf16>(s[e]);
+    }
+    __syncthreads();  // the previous chunk's tiles are consumed
+    for (int e = t; e < kC * KD; e += kNT) {
+      const int r = e / KD, x = e % KD;
+      const bool in = r < len;
+      kl[e] = in ? kg[((c0 + r) * p.H + h) * KD + x] : bf16{};
+      ql[e] = in ? qg[((c0 + r) * p.H + h) * KD + x] : bf16{};
+    }
+    for (int e = t; e < kC * kVB; e += kNT) {
+      const int r = e / kVB, x = e % kVB;
+      vl[e] = r < len ? vg[((c0 + r) * p.HV + hv) * VD + vb * kVB + x] : bf16{};
+    }
+    if (t < kC) {
+      float a = 1.f, b = 0.f;
+      if (t < len) {
+        const int64_t idx = (c0 + t) * p.HV + hv;
+        float gvv = load_as_f32(p.g, p.dg, idx);
+        if (p.flags & GDN_FLAG_GATE_IN_KERNEL) gvv = -expf(p.A_log[hv]) * softplus_f32(gvv + p.dt_bias[hv]);
+        a = expf(gvv);
+        const float bv = load_as_f32(p.beta, p.db, idx);
+        b = (p.flags & GDN_FLAG_BETA_SIGMOID) ? sigmoid_f32(bv) : bv;
+      }
+      gl->gam[t] = a;
+      gl->bet[t] = b;
+    }
+    __syncthreads();
+    for (int r = 0; r < len; ++r) {
+      float kr[KPL], qr[KPL];
+#pragma unroll
+      for (int e = 0; e < KPL; ++e) {
+        kr[e] = (float)kl[r * KD + li * KPL + e];
+        qr[e] = (float)ql[r * KD + li * KPL + e];
+      }
+      const float a = gl->gam[r], b = gl->bet[r], vv = (float)vl[r * kVB + 4 * w + g4];
+      float pk = 0.f, pq = 0.f, kq = 0.f, kk = 0.f, qq = 0.f;
+#pragma unroll
+      for (int e = 0; e < KPL; ++e) {
+        pk += s[e] * kr[e];
+        pq += s[e] * qr[e];
+        kq += kr[e] * qr[e];
+        kk += kr[e] * kr[e];
+        qq += qr[e] * qr[e];
+      }
+      pk = group_sum<16>(pk);
+      pq = group_sum<16>(pq);
+      kq = group_sum<16>(kq);
+      kk = group_sum<16>(kk);
+      qq = group_sum<16>(qq);
+      // F.normalize semantics: x / max(||x||, 1e-12)
+      const float ik = l2 ? 1.f / fmaxf(sqrtf(kk), 1e-12f) : 1.f;
+      const float iq = l2 ? 1.f / fmaxf(sqrtf(qq), 1e-12f) : 1.f;
+      const float d = b * (vv - a * pk * ik);
+      const float o = p.scale * (a * pq * iq + d * kq * ik * iq);
+#pragma unroll
+      for (int e = 0; e < KPL; ++e) s[e] = a * s[e] + kr[e] * ik * d;
+      if (li == 0) {
+        const bf16 ob = static_cast<bf16>(o);
+        og[(c0 + r) * p.HV * VD + (int64_t)hv * VD + col] = ob;
+        om = __builtin_elementwise_max(om, u16x2{(unsigned short)(__builtin_bit_cast(unsigned short, ob) & 0x7fff), 0});
+      }
+    }
+  }
+  uint32_t smax = 0;
+  if (p.ht) {
+#pragma unroll
+    for (int e = 0; e < KPL; ++e) {
+      p.ht[sb0 + (int64_t)(li * KPL + e) * VD + col] = s[e];
+      smax = max(smax, __float_as_uint(s[e]) & 0x7fffffffu);
+    }
+  }
+  if (p.range_flag) flag_nonfinite(p.range_flag, smax >= 0x7f800000u || om[0] >= 0x7f80);
+}
+
 template <int KD, int VD, bool SAVE>
 __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p) {
   constexpr int NVB = VD / kVB;
@@ -115,6 +221,7 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
   __shared__ __align__(16) bf16 Vc[2][kC * kVB];  // V slice of chunk c in slot c % 2 (vo_off)
   __shared__ __align__(16) bf16 Ob[2][kC * kVB];  // O of chunk c, stored to HBM during chunk c + 1 (vo_off)
   __shared__ __align__(16) ChunkGates gv[3];      // gate terms of chunk c in slot c % 3
+  __shared__ int bad;                              // an O or final-state element of this slice is inf / NaN
 
   // w is read back as a scalar: the compiler then treats the role branches as wave-uniform
   const int t = threadIdx.x, lane = t & 63, w = __builtin_amdgcn_readfirstlane(t >> 6), g4 = lane >> 4, li = lane & 15;
@@ -386,6 +493,7 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
   GateBits ngate{0, 0, 0, 0};  // wave 4: raw gate bits of the chunk two steps ahead, in flight
 
   // ------------------------------------------------------------------ prologue
+  if (t == 0) bad = 0;
   // P is causally lower: its tiles above the diagonal stay zero for the whole run
   for (int e = t; e < kC * kC / 8; e += kNT) {
     reinterpret_cast<f16x8*>(Pb[0])[e] = f16x8{};
@@ -617,7 +725,7 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
           smax = max(smax, __float_as_uint(S[a][r]) & 0x7fffffffu);
         }
       }
-      if (p.range_flag) flag_nonfinite(p.range_flag, smax >= 0x7f800000u);
+      if (smax >= 0x7f800000u) __hip_atomic_fetch_or(&bad, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
   } else if (qk_wave) {
     // K/Q of chunks 0 and 1 staged, chunk 2 in flight
@@ -674,8 +782,20 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
       __syncthreads();
     }
     if (nc > 0) store_o(nc - 1, thv, om);
-    if (p.range_flag) flag_nonfinite(p.range_flag, om[0] >= 0x7f80 || om[1] >= 0x7f80);
+    if (om[0] >= 0x7f80 || om[1] >= 0x7f80) __hip_atomic_fetch_or(&bad, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
+
+  // ------------------------------------------------------------------ recovery
+  // A slice whose fp16 matrix-core operands left the fp16 range (65504) -- for instance from inputs
+  // of a scale fp32 and bf16 hold but fp16 does not -- has stored an inf or NaN in O or the final
+  // state. The slice then computes its 32 columns again by the fp32 token-by-token recurrence
+  // (value columns of the state evolve independently), overwriting O, the final state and (SAVE)
+  // the saved chunk states, and flags the call only if that recomputation is non-finite as well
+  // (non-finite inputs). Slices that stored finite values skip it: the cost is this barrier.
+  __syncthreads();
+  if (__builtin_amdgcn_readfirstlane(bad)) recover_slice<KD, VD, SAVE>(p, n, hv, h, vb, bos, eos, cg_first,
+                                                                          (bf16*)&Kc[0][0], (bf16*)&Qc[0][0],
+                                                                          (bf16*)&Vc[0][0], &gv[0]);
 }
 
 }  // namespace gdn

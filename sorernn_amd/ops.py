@@ -188,8 +188,8 @@ def _gdn_call(entry, name, q, k, v, g, beta, scale, initial_state, output_final_
         if _range.call_overflowed(word, q.device):
             if _range.range_guard() == "raise" or needs_grad:
                 raise FloatingPointError(
-                    f"{name}: the chunked forward stored inf or NaN outputs (an fp16 operand of the chunk "
-                    "kernel past 65504, or non-finite inputs)"
+                    f"{name}: the chunked forward stored inf or NaN outputs (non-finite inputs, or an fp16 "
+                    "operand of the chunk kernel past 65504 that its fp32 recomputation did not bring back into range)"
                     + ("; no fallback with grad: the backward needs the chunk forward" if needs_grad else ""))
             _range.note_fallback(name)
             return _gdn_call("gdn_recurrent_fwd", name, q, k, v, g, beta, scale, initial_state, output_final_state,

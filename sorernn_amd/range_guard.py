@@ -1,12 +1,16 @@
-"""Range guard of the chunked forward's fp16 matrix-core operands.
+"""Range guard of the chunked forward: reports non-finite outputs.
 
 The chunk forward (``gdn_chunk.hip``) feeds the state S, X, Delta, T - I and scale * P to the
 matrix cores as fp16, whose largest finite value is 65504; FLA's kernels use bf16 operands, which
-keep fp32's exponent range. An operand past the fp16 range becomes inf, and every product that
-reads it carries the inf (or a NaN) into ``o`` and the final state. The kernels check what they
-store and set a flag word (``gdn_set_range_flag`` in ``include/gdn.h``) when an ``o`` or
-final-state element is inf or NaN. This module keeps one pinned host word per device, registered
-with the library on the first chunk call on that device, and decides what a set flag does:
+keep fp32's exponent range. A workgroup of the chunk kernel whose fp16 operands overflow (it stored
+an inf or NaN in ``o`` or the final state) computes its columns again by the fp32 token-by-token
+recurrence before it exits, so finite inputs whose fp32 results are finite give finite outputs.
+The kernel then sets a flag word (``gdn_set_range_flag`` in ``include/gdn.h``) only when that
+recomputation is non-finite too: non-finite inputs, for which FLA returns non-finite outputs as
+well. (The cooperative prefill, selected with ``SORERNN_PREFILL=coop``, has no such recomputation
+and sets the flag on its own non-finite outputs.) This module keeps one pinned host word per device,
+registered with the library on the first chunk call on that device, and decides what a set flag
+does:
 
 - ``"warn"`` (the default): no synchronisation. A flag that earlier calls set is cleared and
   reported with a ``RuntimeWarning`` by the next ``chunk_gated_delta_rule`` call on that device,
@@ -18,8 +22,7 @@ with the library on the first chunk call on that device, and decides what a set 
   chunk forward's saved states) and raises instead.
 - ``"off"``: no flag, no check.
 
-Non-finite inputs set the flag as well; FLA returns non-finite outputs for them too, and the
-fallback recomputation then returns them unchanged. ``SORERNN_RANGE_GUARD`` sets the initial mode.
+``SORERNN_RANGE_GUARD`` sets the initial mode.
 """
 from __future__ import annotations
 
@@ -42,9 +45,10 @@ _words: dict[int, tuple[torch.Tensor, np.ndarray]] = {}
 _retired: list[torch.Tensor] = []
 _fallback_noted = False
 
-_EARLIER = ("chunk_gated_delta_rule: an earlier chunked forward on cuda:{dev} stored inf or NaN outputs (an fp16 "
-            "operand of the chunk kernel past 65504, or non-finite inputs). Set sorernn_amd.set_range_guard("
-            "'fallback') to recompute such calls with the fp32 recurrent kernel, or 'raise' to stop at the call.")
+_EARLIER = ("chunk_gated_delta_rule: an earlier chunked forward on cuda:{dev} stored inf or NaN outputs (non-finite "
+            "inputs, or an fp16 operand of the chunk kernel past 65504 that its fp32 recomputation did not bring "
+            "back into range). Set sorernn_amd.set_range_guard('fallback') to recompute such calls with the fp32 "
+            "recurrent kernel, or 'raise' to stop at the call.")
 
 
 def set_range_guard(mode: str) -> None:
