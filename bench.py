@@ -173,8 +173,15 @@ def block_pair(torch, steps: int) -> dict:
         # gdn_layer: the inference route (fused projections and prologue); gdn_layer_reference_route:
         # the reference's call expressions (three convs, chunked rule with in-kernel q/k L2 norm),
         # the route the layer takes under autograd
+        def fused_epilogue():  # the norm applied inside the chunk kernel (not the layer's default)
+            gdn.fused_epilogue = True
+            try:
+                return gdn(x)
+            finally:
+                gdn.fused_epilogue = False
+
         for name, fn in (("gdn_layer", lambda: gdn(x)), ("gdn_layer_reference_route", lambda: gdn._forward_reference(x)),
-                         ("attn_layer", lambda: attn(x))):
+                         ("gdn_layer_fused_epilogue", fused_epilogue), ("attn_layer", lambda: attn(x))):
             for _ in range(2):
                 fn()
             settle(torch, fn)
@@ -387,7 +394,8 @@ def run_only(torch, args) -> int:
 
     if args.only == "block_pair":
         bp = block_pair(torch, args.steps)
-        print(f"ran block_pair: gdn {bp['gdn_layer_ms']} ms (reference route {bp['gdn_layer_reference_route_ms']} ms), attn {bp['attn_layer_ms']} ms, "
+        print(f"ran block_pair: gdn {bp['gdn_layer_ms']} ms (norm fused into the chunk kernel {bp['gdn_layer_fused_epilogue_ms']} ms, "
+              f"reference route {bp['gdn_layer_reference_route_ms']} ms), attn {bp['attn_layer_ms']} ms, "
               f"attention kernel {bp['attn_kernel_ms']} ms", flush=True)
         return 0
     if args.only == "train":

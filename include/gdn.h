@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define GDN_ABI_VERSION 6
+#define GDN_ABI_VERSION 7
 
 #if defined(__GNUC__) || defined(__clang__)
 #define GDN_API __attribute__((visibility("default")))
@@ -78,6 +78,30 @@ GDN_API int gdn_chunk_fwd(const void* q, const void* k, const void* v, const voi
                   int qkv_dtype, int g_dtype, int beta_dtype, float scale, unsigned flags,
                   const float* A_log, const float* dt_bias, void* workspace, size_t workspace_bytes,
                   void* stream);
+
+/*
+ * gdn_chunk_fwd with the layer's gated RMSNorm applied to o as it is stored (inference only):
+ * o = rmsnorm(o_rule) * norm_weight * silu(gate) per (token, value head) over the V values, with
+ * rmsnorm(x) = x / sqrt(mean(x^2) + norm_eps) of the rule's output rounded to bf16 -- what FLA
+ * rms_norm_gated(o, gate, weight, None, activation="swish", eps) computes from chunk_gated_delta_rule's
+ * o (sore/model/gdn.py:166-169 then 182-186), in fp32 with one rounding. norm_split != 0 rounds
+ * like the reference's unfused route instead, o_norm(o) * F.silu(gate) (gdn.py:188): the norm
+ * result and silu(gate) each rounded to bf16, then their product. gate [B, T, HV, V] bf16,
+ * norm_weight [V] fp32. The rule's own o is not returned. The V / 32 column slices of a (sequence,
+ * head) exchange their per-token sums of squares through the workspace (at least
+ * gdn_chunk_gated_norm_workspace_size bytes), so all of them must be able to run at once: they
+ * are dispatched next to each other, ahead of later sequences. A call whose outputs are not finite
+ * sets the range flag (no fp32 recomputation on this path).
+ */
+GDN_API int gdn_chunk_fwd_gated_norm(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                             const float* initial_state, void* o, float* final_state, const void* cu_seqlens,
+                             int64_t B, int64_t T, int64_t H, int64_t HV, int64_t K, int64_t V, int64_t N,
+                             int qkv_dtype, int g_dtype, int beta_dtype, float scale, unsigned flags,
+                             const float* A_log, const float* dt_bias, const void* gate, const float* norm_weight,
+                             float norm_eps, int norm_split, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace bytes gdn_chunk_fwd_gated_norm needs; 0 for invalid sizes. No counterpart in the reference. */
+GDN_API size_t gdn_chunk_gated_norm_workspace_size(int64_t B, int64_t T, int64_t HV, int64_t N, int64_t V, int varlen);
 
 /*
  * Workspace bytes gdn_chunk_fwd needs for these sizes (varlen != 0 when cu_seqlens is passed);

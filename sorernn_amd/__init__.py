@@ -7,6 +7,7 @@ and gated-norm modules used by ``sore/model/gdn.py``: Python host code calls the
 from sorernn_amd.ops import (  # noqa: F401
     causal_conv1d,
     chunk_gated_delta_rule,
+    chunk_gated_delta_rule_gated_norm,
     fused_recurrent_gated_delta_rule,
     gated_delta_decode_step,
     l2norm,

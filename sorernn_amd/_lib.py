@@ -21,7 +21,7 @@ FLAG_BETA_SIGMOID = 0x2
 FLAG_GATE_IN_KERNEL = 0x4
 FLAG_CU_INT32 = 0x8
 ACT_NONE, ACT_SILU, ACT_SILU_ROUNDED = 0, 1, 2
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -36,6 +36,8 @@ SIGNATURES = {
     "gdn_last_error": [],
     "gdn_chunk_fwd": [_P] * 9 + [_I64] * 7 + [_INT] * 3 + [_F, _U, _P, _P, _P, _SZ, _P],
     "gdn_chunk_workspace_size": [_I64] * 4 + [_INT],
+    "gdn_chunk_fwd_gated_norm": [_P] * 9 + [_I64] * 7 + [_INT] * 3 + [_F, _U, _P, _P, _P, _P, _F, _INT, _P, _SZ, _P],
+    "gdn_chunk_gated_norm_workspace_size": [_I64] * 5 + [_INT],
     "gdn_chunk_fwd_train": [_P] * 9 + [_I64] * 7 + [_INT] * 3 + [_F, _U, _P, _P, _P, _P, _SZ, _P],
     "gdn_chunk_fwd_noalloc": [_P] * 9 + [_I64] * 7 + [_INT] * 3 + [_F, _U, _P, _P, _P],
     "gdn_chunk_fwd_noalloc_max_workspace": [],
@@ -61,6 +63,7 @@ SIGNATURES = {
 RESTYPES = {
     "gdn_last_error": ctypes.c_char_p,
     "gdn_chunk_workspace_size": ctypes.c_size_t,
+    "gdn_chunk_gated_norm_workspace_size": ctypes.c_size_t,
     "gdn_chunk_states_size": ctypes.c_size_t,
     "gdn_chunk_fwd_noalloc_max_workspace": ctypes.c_size_t,
     "gdn_chunk_bwd_workspace_size": ctypes.c_size_t,

@@ -67,5 +67,7 @@ int coop_ring_slots(int64_t T);                    // ring slots per chain for s
 int64_t coop_ring_bytes(int64_t chains, int64_t T);
 int64_t coop_sync_bytes(int64_t chains);  // includes one error word after the chains' sync words
 int launch_chunk_coop(const CoopArgs& a, hipStream_t s);
+// Zeroes `words` 32-bit words with a fill kernel (captured graphs clear them on every replay).
+int launch_fill_zero(unsigned* w, int64_t words, hipStream_t s);
 
 }  // namespace gdn

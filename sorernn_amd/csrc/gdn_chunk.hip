@@ -71,7 +71,15 @@ struct ChunkParams {
   bf16* hs;                  // SAVE only: the state entering each chunk, bf16 [chunks][HV][V][K] (transposed)
   const int* chunk_first;    // SAVE with cu: chunks before each sequence
   unsigned* range_flag;      // set to 1 when a stored output is inf or NaN (null: no check)
+  // NORM only: the gated RMSNorm of O applied as it is stored (gdn_chunk_fwd_gated_norm)
+  const bf16* gate;          // [tokens][HV][V], the layer's output gate
+  const float* nw;           // [V] norm weight
+  float neps;
+  int nsplit;                // 1: the reference's separate rmsnorm and silu(gate) roundings
+  u32x2* npart;              // [chains][kNormSlots][V / 32][64] (sum of squares of a slice's columns, chunk + 1)
 };
+
+constexpr int kNormSlots = 8;  // chunks whose partial sums are in flight per chain
 
 // Running maximum, per 16-bit half, of the magnitude bits of the bf16 values in x: a half at or
 // above 0x7f80 (all-ones exponent) has seen an inf or a NaN.
@@ -200,8 +208,9 @@ __device__ __forceinline__ void recover_slice(const ChunkParams& p, int64_t n, i
   if (p.range_flag) flag_nonfinite(p.range_flag, smax >= 0x7f800000u || om[0] >= 0x7f80);
 }
 
-template <int KD, int VD, bool SAVE>
+template <int KD, int VD, bool SAVE, bool NORM = false>
 __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p) {
+  static_assert(!(SAVE && NORM), "the fused norm is an inference epilogue");
   constexpr int NVB = VD / kVB;
   // q/k tiles in LDS: at KD = 128 rows are unpadded (256 B) and the 16-byte chunk c of row r sits
   // at chunk c ^ kq_sw(r) = c ^ ((r & 7) << 1). Measured with SQ_LDS_BANK_CONFLICT on gfx950, the
@@ -219,7 +228,9 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
   __shared__ __align__(16) f16 Tb[2][kC * kC];    // T - I of chunk c in slot c % 2 (tok_col columns, tp_off)
   __shared__ __align__(16) f16 Pb[2][kC * kC];    // scale * P of chunk c in slot c % 2 (tok_col columns, tp_off)
   __shared__ __align__(16) bf16 Vc[2][kC * kVB];  // V slice of chunk c in slot c % 2 (vo_off)
-  __shared__ __align__(16) bf16 Ob[2][kC * kVB];  // O of chunk c, stored to HBM during chunk c + 1 (vo_off)
+  // O of chunk c, stored to HBM during chunk c + 1 (slot c % 2), or with NORM during chunk c + 4 (slot c % 6)
+  __shared__ __align__(16) bf16 Ob[NORM ? 6 : 2][kC * kVB];
+  __shared__ float psum[NORM ? 2 : 1][2][kC];     // NORM: per-token sums of squares of each state wave's O
   __shared__ __align__(16) ChunkGates gv[3];      // gate terms of chunk c in slot c % 3
   __shared__ int bad;                              // an O or final-state element of this slice is inf / NaN
 
@@ -389,6 +400,90 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
     }
   };
 
+  // NORM: the slice's per-token sums of squares of chunk c (its two state waves' halves, from psum)
+  // go to the chain's exchange slot during step c + 1 as 8-byte (sum, c + 1) pairs, one store per
+  // token (wave 5); every slice loads the pairs of its rows in step c + 3 and checks in step c + 4
+  // that each carries c + 1 (loading again, boundedly, where one does not yet), so no counter and no
+  // wait sit between the slices. The slices of a chain may sit on different XCDs: the pairs are
+  // written through to memory and read with device-scope loads.
+  const int64_t nslot0 = k_rank * kNormSlots;
+  const auto rnp = make_rsrc(p.npart + nslot0 * NVB * kC, (uint32_t)(kNormSlots * NVB * kC * 8));
+  auto publish_sums = [&](int c) {
+    const float v = psum[c & 1][0][lane] + psum[c & 1][1][lane];
+    const u32x2 pr = {__float_as_uint(v), (unsigned)(c + 1)};
+    __builtin_amdgcn_raw_buffer_store_b64(pr, rnp, (int)((((c % kNormSlots) * NVB + vb) * kC + lane) * 8), 0, 16);
+  };
+  // the pairs of rows tq / 4 and tq / 4 + 32 of chunk c from every slice (device-scope loads)
+  auto load_sums = [&](int c, int tq, u32x2 (&ps)[2][NVB]) {
+    const int row = tq >> 2;
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int sl = 0; sl < NVB; ++sl)
+        ps[u][sl] = __builtin_amdgcn_raw_buffer_load_b64(rnp, (int)((((c % kNormSlots) * NVB + sl) * kC + row + 32 * u) * 8),
+                                                        0, 16);
+  };
+  // NORM: the gate rows of chunk c this thread stores (rows tq / 4 and tq / 4 + 32, chunk tq % 4)
+  auto load_gate = [&](int c, int tq, bf16x8 (&pg)[2]) {
+    const int64_t c0 = bos + (int64_t)c * kC;
+    const auto rg = make_rsrc(p.gate + (c0 * p.HV + hv) * VD + vb * kVB, (uint32_t)chunk_len(c) * v_row);
+    const int row = tq >> 2, c8 = tq & 3;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) pg[u] = buf_load16(rg, (uint32_t)(row + 32 * u) * v_row + c8 * 16);
+  };
+  // NORM: O of chunk c normalised and gated as it is stored, once every slice of the chain has
+  // published its sums: y = o rstd w silu(gate), rstd = 1 / sqrt(mean(o^2) + eps) over the head's
+  // V columns of the rounded o, fp32 math and one rounding (FLA rms_norm_gated(o, gate, w, None,
+  // "swish", eps)); with nsplit, rmsnorm and the gate product rounded separately, as
+  // o_norm(o) * F.silu(gate) does. A wait that runs out marks the output with the range flag.
+  // the silu uses v_exp / v_rcp (silu_fast, relative error ~1e-7, far below the bf16 rounding that
+  // follows) and the weights of the thread's 8 columns are read once per call
+  auto store_o_norm = [&](int c, int tq, u16x2& om, const bf16x8 (&pg)[2], u32x2 (&ps)[2][NVB]) {
+    unsigned spins = 0;
+    while (true) {
+      bool ready = true;
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int sl = 0; sl < NVB; ++sl) ready = ready && ps[u][sl][1] == (unsigned)(c + 1);
+      if (__builtin_amdgcn_ballot_w64(!ready) == 0) break;
+      if (++spins >= (1u << 22)) {
+        if (p.range_flag) flag_nonfinite(p.range_flag, true);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+      load_sums(c, tq, ps);
+    }
+    const int64_t c0 = bos + (int64_t)c * kC;
+    const auto ro = make_rsrc(og + (c0 * p.HV + hv) * VD + vb * kVB, (uint32_t)chunk_len(c) * v_row);
+    const int row = tq >> 2, c8 = tq & 3;
+    float wv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) wv[e] = p.nw[vb * kVB + c8 * 8 + e];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int r = row + 32 * u;
+      float ssum = 0.f;
+#pragma unroll
+      for (int sl = 0; sl < NVB; ++sl) ssum += __uint_as_float(ps[u][sl][0]);
+      const float rstd = __builtin_amdgcn_rsqf(ssum * (1.f / (float)VD) + p.neps);
+      const bf16x8 x = *reinterpret_cast<const bf16x8*>(&Ob[c % 6][vo_off(r, c8 * 8)]);
+      bf16x8 y;
+      if (p.nsplit) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float y1 = (float)static_cast<bf16>((float)x[e] * rstd * wv[e]);
+          y[e] = static_cast<bf16>(y1 * (float)static_cast<bf16>(silu_fast((float)pg[u][e])));
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) y[e] = static_cast<bf16>((float)x[e] * rstd * wv[e] * silu_fast((float)pg[u][e]));
+      }
+      om = bf16_mag_max(om, y);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, y), ro, (int)((uint32_t)r * v_row + c8 * 16), 0, 2);
+    }
+  };
+
   // scale * P^T of chunk c for key-row tiles JA..JA+JN-1 and query-row tiles TA..TA+TN-1 (tiles
   // with jt <= tt only): element (j = 16jt + 4g + r, t = 16tt + i), stored at Pb[t][tok_col(j)].
   // Waves 2, 3, 6, 7 (SIMDs 2 and 3) take the 2x2, 2x2, 2x1 and 2x1 tile blocks of the lower triangle.
@@ -550,7 +645,7 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
       const f16* tp = Tb[PH & 1];
       const bf16* vp = Vc[PH & 1];
       const f16* pp = Pb[PH & 1];
-      bf16* op = Ob[PH & 1];
+      bf16* op = Ob[NORM ? PH : PH & 1];
       const ChunkGates& G = gv[PH % 3];
 
       // The chain S -> Y -> X -> Delta -> Delta~ -> S' runs through phases 6 (Y of the next chunk,
@@ -681,7 +776,20 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
         f32x4 o = Zt[tb] * eg[tb];
         o = mmah(db0, pf[tb], o);
         if (tb >= 2) o = mmah(db1, pf[tb + 2], o);
-        *reinterpret_cast<bf16x4*>(op + vo_off(16 * tb + li, 16 * sw + 4 * g4)) = to_bf16x4(o[0], o[1], o[2], o[3]);
+        const bf16x4 ob = to_bf16x4(o[0], o[1], o[2], o[3]);
+        *reinterpret_cast<bf16x4*>(op + vo_off(16 * tb + li, 16 * sw + 4 * g4)) = ob;
+        if constexpr (NORM) {
+          // the sum of squares of token 16 tb + i over the wave's 16 columns, from the rounded O the
+          // reference's norm reads: lanes i, i + 16, i + 32, i + 48 hold its four column groups
+          float ss = 0.f;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) ss += (float)ob[r] * (float)ob[r];
+          const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(ss), __float_as_uint(ss), false, false);
+          ss = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+          const auto b2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(ss), __float_as_uint(ss), false, false);
+          ss = __uint_as_float(b2[0]) + __uint_as_float(b2[1]);
+          if (g4 == 0) psum[PH & 1][sw][16 * tb + li] = ss;
+        }
       }
       f16x8 kfb[KS - KSH][4];
 #pragma unroll
@@ -770,18 +878,45 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
     }
     __syncthreads();
     __syncthreads();
+    bf16x8 pgt[2];      // NORM: gate rows of the chunk whose O goes out next step
+    u32x2 pss[2][NVB];  // NORM: (sum, chunk + 1) pairs of those rows from every slice
     for (int i = 0; i < nc; ++i) {  // gates of chunk i+2, O of chunk i-1 out, T/V of chunk i+1 into LDS, loads of chunk i+2
       const int tq = thv_of(opaque_int(lane));
       if (w == 4) {  // gates of chunk i+2 (loaded a step ago), then the loads for chunk i+3
         stage_gates(i + 2, ngate);
         fetch_gates(i + 3, ngate);
       }
-      if (i > 0) store_o(i - 1, tq, om);
+      if constexpr (NORM) {  // sums of chunk i-1 out, O of chunk i-4 out
+        if (w == 5 && i >= 1) publish_sums(i - 1);
+        if (i >= 4) store_o_norm(i - 4, tq, om, pgt, pss);
+      } else {
+        if (i > 0) store_o(i - 1, tq, om);
+      }
       stage_tv(pt, pv, (i + 1) & 1, tq);
       fetch_tv(pt, pv, i + 2, tq);
+      if constexpr (NORM) {
+        // gates and sums of chunk i-3, issued after the T/V loads: loads complete in order, and the
+        // next step's T/V staging then does not wait for these slower device-scope loads
+        if (i >= 3) {
+          load_gate(i - 3, tq, pgt);
+          load_sums(i - 3, tq, pss);
+        }
+      }
       __syncthreads();
     }
-    if (nc > 0) store_o(nc - 1, thv, om);
+    if constexpr (NORM) {
+      // the pipeline's last four steps, without the state waves (no barrier)
+      for (int i = nc; i < nc + 4; ++i) {
+        if (w == 5 && i >= 1 && i - 1 < nc) publish_sums(i - 1);
+        if (i >= 4 && i - 4 < nc) store_o_norm(i - 4, thv, om, pgt, pss);
+        if (i >= 3 && i - 3 < nc) {
+          load_gate(i - 3, thv, pgt);
+          load_sums(i - 3, thv, pss);
+        }
+      }
+    } else {
+      if (nc > 0) store_o(nc - 1, thv, om);
+    }
     if (om[0] >= 0x7f80 || om[1] >= 0x7f80) __hip_atomic_fetch_or(&bad, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
 
@@ -792,10 +927,17 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
   // (value columns of the state evolve independently), overwriting O, the final state and (SAVE)
   // the saved chunk states, and flags the call only if that recomputation is non-finite as well
   // (non-finite inputs). Slices that stored finite values skip it: the cost is this barrier.
+  // The fused-norm variant has no recomputation (the sums of every slice of the chain enter each
+  // slice's outputs): it reports the call through the range flag.
   __syncthreads();
-  if (__builtin_amdgcn_readfirstlane(bad)) recover_slice<KD, VD, SAVE>(p, n, hv, h, vb, bos, eos, cg_first,
-                                                                          (bf16*)&Kc[0][0], (bf16*)&Qc[0][0],
-                                                                          (bf16*)&Vc[0][0], &gv[0]);
+  if (__builtin_amdgcn_readfirstlane(bad)) {
+    if constexpr (NORM) {
+      if (t == 0 && p.range_flag) flag_nonfinite(p.range_flag, true);
+    } else {
+      recover_slice<KD, VD, SAVE>(p, n, hv, h, vb, bos, eos, cg_first, (bf16*)&Kc[0][0], (bf16*)&Qc[0][0],
+                                  (bf16*)&Vc[0][0], &gv[0]);
+    }
+  }
 }
 
 }  // namespace gdn
@@ -836,11 +978,16 @@ int stream_device(hipStream_t stream) {
   return dev;
 }
 
+// The fused-norm exchange area (after the chunk workspace): per chain, kNormSlots slots of the V / 32
+// slices' 64 per-token sums, then the slots' arrival counters.
+size_t norm_part_bytes(int64_t N, int64_t HV, int64_t V) { return (size_t)align256(N * HV * kNormSlots * (V / kVB) * kC * 8); }
+
 int chunk_fwd_impl(const void* q, const void* k, const void* v, const void* g, const void* beta,
                    const float* initial_state, void* o, float* final_state, const void* cu_seqlens, int64_t B,
                    int64_t T, int64_t H, int64_t HV, int64_t K, int64_t V, int64_t N, int qkv_dtype, int g_dtype,
                    int beta_dtype, float scale, unsigned flags, const float* A_log, const float* dt_bias,
-                   void* chunk_states, void* workspace, size_t workspace_bytes, void* stream) {
+                   void* chunk_states, void* workspace, size_t workspace_bytes, void* stream,
+                   const void* ngate = nullptr, const float* nweight = nullptr, float neps = 0.f, int nsplit = 0) {
   if (!q || !k || !v || !g || !beta || !o) {
     gdn_internal_set_error("gdn_chunk_fwd: null tensor pointer");
     return GDN_ERR_INVALID;
@@ -867,7 +1014,13 @@ int chunk_fwd_impl(const void* q, const void* k, const void* v, const void* g, c
     gdn_internal_set_error("gdn_chunk_fwd: q/k/v dtype %d unsupported by the chunk kernel (bf16 only)", qkv_dtype);
     return GDN_ERR_UNSUPPORTED;
   }
-  const size_t need = gdn_chunk_workspace_size(B, T, HV, N, cu_seqlens != nullptr);
+  const bool norm = ngate != nullptr;
+  if (norm && (!nweight || chunk_states)) {
+    gdn_internal_set_error("gdn_chunk_fwd_gated_norm: the norm weight is required (inference calls only)");
+    return GDN_ERR_INVALID;
+  }
+  const size_t base_need = gdn_chunk_workspace_size(B, T, HV, N, cu_seqlens != nullptr);
+  const size_t need = norm && base_need ? base_need + norm_part_bytes(N, HV, V) : base_need;
   if (need > 0 && (!workspace || workspace_bytes < need)) {
     gdn_internal_set_error("gdn_chunk_fwd: workspace of %zu bytes needed (got %zu)", need,
                            workspace ? workspace_bytes : (size_t)0);
@@ -883,7 +1036,7 @@ int chunk_fwd_impl(const void* q, const void* k, const void* v, const void* g, c
   // SORERNN_PREFILL=coop (the two-kernel prefill otherwise, which is faster at every measured size).
   const char* const sel = getenv("SORERNN_PREFILL");
   const bool coop = sel && !strcmp(sel, "coop");
-  if (!chunk_states && K == 128 && V == 128 && coop) {
+  if (!chunk_states && !norm && K == 128 && V == 128 && coop) {
     char* const ws = static_cast<char*>(workspace);
     const int64_t chains = N * HV;
     const size_t front = coop_front_bytes(T, HV, N);
@@ -914,9 +1067,19 @@ int chunk_fwd_impl(const void* q, const void* k, const void* v, const void* g, c
   if (rc != GDN_OK) return rc;
   ChunkParams p{q, k, v, g, beta, initial_state, o, final_state, tw, cu_seqlens, order, cu_i32, T, H, HV, N,
                 g_dtype, beta_dtype, scale, flags, A_log, dt_bias, static_cast<bf16*>(chunk_states), chunk_first,
-                range_flag};
+                range_flag, static_cast<const bf16*>(ngate), nweight, neps, nsplit, nullptr};
   dim3 grid((unsigned)blocks), block(kNT);
-  if (chunk_states) {
+  if (norm) {
+    // the pairs carry their chunk, and no chunk index is 0 (they store c + 1): zeroing the exchange
+    // area is enough for any earlier contents (a fill kernel, so that captured graphs clear it too)
+    p.npart = reinterpret_cast<u32x2*>(ws + base_need);
+    const int frc = launch_fill_zero(reinterpret_cast<unsigned*>(p.npart), (int64_t)(norm_part_bytes(N, HV, V) / 4), s);
+    if (frc != GDN_OK) return frc;
+    if (K == 128 && V == 128) hipLaunchKernelGGL((gated_delta_chunk_kernel<128, 128, false, true>), grid, block, 0, s, p);
+    else if (K == 64 && V == 64) hipLaunchKernelGGL((gated_delta_chunk_kernel<64, 64, false, true>), grid, block, 0, s, p);
+    else if (K == 128 && V == 64) hipLaunchKernelGGL((gated_delta_chunk_kernel<128, 64, false, true>), grid, block, 0, s, p);
+    else hipLaunchKernelGGL((gated_delta_chunk_kernel<64, 128, false, true>), grid, block, 0, s, p);
+  } else if (chunk_states) {
     if (K == 128 && V == 128) hipLaunchKernelGGL((gated_delta_chunk_kernel<128, 128, true>), grid, block, 0, s, p);
     else if (K == 64 && V == 64) hipLaunchKernelGGL((gated_delta_chunk_kernel<64, 64, true>), grid, block, 0, s, p);
     else if (K == 128 && V == 64) hipLaunchKernelGGL((gated_delta_chunk_kernel<128, 64, true>), grid, block, 0, s, p);
@@ -962,6 +1125,29 @@ extern "C" int gdn_chunk_fwd(const void* q, const void* k, const void* v, const 
                              void* stream) {
   return chunk_fwd_impl(q, k, v, g, beta, initial_state, o, final_state, cu_seqlens, B, T, H, HV, K, V, N, qkv_dtype,
                         g_dtype, beta_dtype, scale, flags, A_log, dt_bias, nullptr, workspace, workspace_bytes, stream);
+}
+
+extern "C" size_t gdn_chunk_gated_norm_workspace_size(int64_t B, int64_t T, int64_t HV, int64_t N, int64_t V,
+                                                      int varlen) {
+  const size_t base = gdn_chunk_workspace_size(B, T, HV, N, varlen);
+  if (!base || (V != 64 && V != 128)) return 0;
+  return base + norm_part_bytes(N, HV, V);
+}
+
+extern "C" int gdn_chunk_fwd_gated_norm(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                                        const float* initial_state, void* o, float* final_state, const void* cu_seqlens,
+                                        int64_t B, int64_t T, int64_t H, int64_t HV, int64_t K, int64_t V, int64_t N,
+                                        int qkv_dtype, int g_dtype, int beta_dtype, float scale, unsigned flags,
+                                        const float* A_log, const float* dt_bias, const void* gate,
+                                        const float* norm_weight, float norm_eps, int norm_split, void* workspace,
+                                        size_t workspace_bytes, void* stream) {
+  if (!gate) {
+    gdn_internal_set_error("gdn_chunk_fwd_gated_norm: gate is required");
+    return GDN_ERR_INVALID;
+  }
+  return chunk_fwd_impl(q, k, v, g, beta, initial_state, o, final_state, cu_seqlens, B, T, H, HV, K, V, N, qkv_dtype,
+                        g_dtype, beta_dtype, scale, flags, A_log, dt_bias, nullptr, workspace, workspace_bytes, stream,
+                        gate, norm_weight, norm_eps, norm_split);
 }
 
 extern "C" int gdn_chunk_fwd_train(const void* q, const void* k, const void* v, const void* g, const void* beta,

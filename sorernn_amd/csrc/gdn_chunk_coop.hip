@@ -912,6 +912,13 @@ __global__ __launch_bounds__(256) void gated_delta_chunk_sync_clear_kernel(unsig
   for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < words; e += (int64_t)gridDim.x * 256) w[e] = 0u;
 }
 
+int launch_fill_zero(unsigned* w, int64_t words, hipStream_t s) {
+  if (words <= 0) return GDN_OK;
+  const unsigned grid = (unsigned)std::min<int64_t>(256, (words + 255) / 256);
+  hipLaunchKernelGGL(gated_delta_chunk_sync_clear_kernel, dim3(grid), dim3(256), 0, s, w, words);
+  return gdn_internal_check_launch("gated_delta_chunk_sync_clear_kernel");
+}
+
 int coop_ring_slots(int64_t T) { return (int)std::min<int64_t>(kRing, std::max<int64_t>(1, (T + kC - 1) / kC)); }
 int64_t coop_ring_bytes(int64_t chains, int64_t T) { return align256(chains * (int64_t)coop_ring_slots(T) * kSlotBytes); }
 int64_t coop_sync_bytes(int64_t chains) { return align256((chains * (int64_t)(kHeadWords + kRing * kSyncWords) + 1) * 4); }

@@ -28,6 +28,7 @@ from __future__ import annotations
 import warnings
 
 import torch
+import torch.nn.functional as F
 from torch import Tensor
 
 from sorernn_amd import _lib
@@ -259,11 +260,14 @@ def chunk_gated_delta_rule(
 
     Range: the chunk kernel's matrix-core operands for the state, X, Delta, T - I and scale * P are
     fp16 (largest finite value 65504; FLA's bf16 operands reach fp32's range). L2-normalised q/k
-    with activation-scale v stay far inside it (|scale * P| <= scale, states of order |v|); an
-    operand past it turns o and the final state non-finite. The kernel flags every inf or NaN it
-    stores, and ``sorernn_amd.set_range_guard`` selects the response: a warning at the next call
-    (default, no synchronisation), ``FloatingPointError``, or a recomputation of the call by the
-    fp32 recurrent kernel. ``sorernn_amd.check_chunk_range()`` reports the flag on demand.
+    with activation-scale v stay far inside it (|scale * P| <= scale, states of order |v|). A
+    workgroup whose operands leave that range (it stored an inf or NaN) computes its columns again
+    by the fp32 token-by-token recurrence before the kernel ends, so finite inputs with finite fp32
+    results give finite outputs. The kernel flags the call only when that recomputation is
+    non-finite as well (non-finite inputs), and ``sorernn_amd.set_range_guard`` selects the
+    response: a warning at the next call (default, no synchronisation), ``FloatingPointError``, or a
+    recomputation of the call by the fp32 recurrent kernel. ``sorernn_amd.check_chunk_range()``
+    reports the flag on demand.
     fp32/fp16 q/k/v run on the recurrent kernel (a warning says so once per dtype).
     """
     if allow_neg_eigval or state_v_first or cp_context is not None:
@@ -271,6 +275,87 @@ def chunk_gated_delta_rule(
     return _gdn_call("gdn_chunk_fwd", "chunk_gated_delta_rule", q, k, v, g, beta, scale, initial_state,
                      output_final_state, cu_seqlens, cu_seqlens_cpu, use_qk_l2norm_in_kernel,
                      use_beta_sigmoid_in_kernel, use_gate_in_kernel, A_log, dt_bias)
+
+
+def chunk_gated_delta_rule_gated_norm(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    g: Tensor,
+    beta: Tensor,
+    gate: Tensor,
+    norm_weight: Tensor,
+    norm_eps: float = 1e-6,
+    norm_split: bool = False,
+    scale: float | None = None,
+    initial_state: Tensor | None = None,
+    output_final_state: bool = False,
+    use_qk_l2norm_in_kernel: bool = False,
+    use_beta_sigmoid_in_kernel: bool = False,
+    cu_seqlens: Tensor | None = None,
+    cu_seqlens_cpu: Tensor | None = None,
+    use_gate_in_kernel: bool = False,
+    A_log: Tensor | None = None,
+    dt_bias: Tensor | None = None,
+):
+    """``chunk_gated_delta_rule`` with the layer's gated RMSNorm applied as ``o`` is stored (inference).
+
+    Returns ``(rms_norm_gated(o, gate, norm_weight, None, "swish", norm_eps), final_state)`` for the
+    ``o`` chunk_gated_delta_rule would return: the call at ``sore/model/gdn.py:166-169`` followed by the
+    norm at ``gdn.py:182-186``, one kernel, ``o`` never written to HBM. ``norm_split=True`` rounds as the
+    reference's unfused route ``o_norm(o) * F.silu(gate)`` (``gdn.py:188``). ``gate`` has ``v``'s shape
+    and dtype (bf16); ``norm_weight [V]``. Inputs must not require grad (the backward of the norm
+    needs ``o``). A call whose outputs are not finite is handled by the range guard as in
+    ``chunk_gated_delta_rule``; its fallback recomputes the call as chunk_gated_delta_rule + the norm.
+    """
+    name = "chunk_gated_delta_rule_gated_norm"
+    _check_cuda(name, q, k, v, g, beta, initial_state, cu_seqlens, A_log, dt_bias, gate, norm_weight)
+    grad_inputs = [q, k, v, g, beta, initial_state, gate, norm_weight, A_log, dt_bias]
+    if torch.is_grad_enabled() and any(x is not None and x.requires_grad for x in grad_inputs):
+        raise NotImplementedError(f"{name}: inference only (inputs require grad); use chunk_gated_delta_rule and "
+                                  "rms_norm_gated for training")
+    if q.dtype != torch.bfloat16 or gate.dtype != v.dtype or gate.shape != v.shape:
+        raise ValueError(f"{name}: bf16 q/k/v and a gate of v's shape and dtype are required "
+                         f"(got q {q.dtype}, v {tuple(v.shape)} {v.dtype}, gate {tuple(gate.shape)} {gate.dtype})")
+    a_log_in, dt_bias_in = A_log, dt_bias
+    b, t, h, kd, hv, vd, n, flags, scale, A_log, dt_bias = _delta_rule_args(
+        name, q, k, v, g, beta, scale, initial_state, cu_seqlens, cu_seqlens_cpu,
+        use_qk_l2norm_in_kernel, use_beta_sigmoid_in_kernel, use_gate_in_kernel, A_log, dt_bias)
+    if norm_weight.shape != (vd,):
+        raise ValueError(f"{name}: norm_weight must be [{vd}] (got {tuple(norm_weight.shape)})")
+    word = _range.before_call(q.device)
+    q, k, v, g, beta, gate = (x.contiguous() for x in (q, k, v, g, beta, gate))
+    w = norm_weight.float().contiguous()
+    h0 = None if initial_state is None else initial_state.float().contiguous()
+    final = torch.empty(n, hv, kd, vd, device=q.device, dtype=torch.float32) if output_final_state else None
+    o = torch.empty(b, t, hv, vd, device=q.device, dtype=q.dtype)
+    if t > 0:
+        cu = cu_seqlens.contiguous() if cu_seqlens is not None else None
+        nbytes = int(_lib.load().gdn_chunk_gated_norm_workspace_size(b, t, hv, n, vd, int(cu is not None)))
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
+        _lib.call("gdn_chunk_fwd_gated_norm", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.ptr(beta),
+                  _lib.ptr(h0), _lib.ptr(o), _lib.ptr(final), _lib.ptr(cu), b, t, h, hv, kd, vd, n,
+                  _lib.dtype_code(q.dtype), _lib.dtype_code(g.dtype), _lib.dtype_code(beta.dtype), scale, flags,
+                  _lib.ptr(A_log), _lib.ptr(dt_bias), _lib.ptr(gate), _lib.ptr(w), float(norm_eps),
+                  int(bool(norm_split)), _lib.ptr(ws), nbytes, _lib.stream_of(q))
+    elif final is not None:
+        final.copy_(h0 if h0 is not None else torch.zeros_like(final))
+    if _range.call_overflowed(word, q.device):
+        if _range.range_guard() == "raise":
+            raise FloatingPointError(f"{name}: the fused chunked forward and norm stored inf or NaN outputs (non-finite "
+                                     "inputs, or an fp16 operand of the chunk kernel past 65504)")
+        _range.note_fallback(name)
+        o2, final = chunk_gated_delta_rule(q, k, v, g, beta, scale=scale, initial_state=initial_state,
+                                           output_final_state=output_final_state,
+                                           use_qk_l2norm_in_kernel=use_qk_l2norm_in_kernel,
+                                           use_beta_sigmoid_in_kernel=use_beta_sigmoid_in_kernel,
+                                           cu_seqlens=cu_seqlens, cu_seqlens_cpu=cu_seqlens_cpu,
+                                           use_gate_in_kernel=use_gate_in_kernel, A_log=a_log_in, dt_bias=dt_bias_in)
+        if norm_split:
+            o = rms_norm_gated(o2, None, norm_weight, None, eps=norm_eps) * F.silu(gate)
+        else:
+            o = rms_norm_gated(o2, gate, norm_weight, None, activation="swish", eps=norm_eps)
+    return o, final
 
 
 def fused_recurrent_gated_delta_rule(

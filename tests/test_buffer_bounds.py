@@ -229,11 +229,25 @@ def state_kernel(s: Shape, eg: int, eb: int, save: bool) -> int:
         done += check(f"fwd v slice {vb}", s.tokens * HV * V * 2, base_v, _col(ln) * v_row, _last(off_v.ravel()), 16)
     # gates of chunks c < nc + 3 (two steps ahead of the staging, one more in flight)
     done += gate_loads(s, eg, eb, extra=3)
-    # O stores of chunks c < nc (store_o: the V-slice layout)
+    # O stores of chunks c < nc (store_o: the V-slice layout); the fused-norm variant's gate loads
+    # (load_gate) and normalised O stores (store_o_norm) use the same layout on gate and o
     c0, ln, cg, nn = chunk_rows(s)
     for vb in range(V // 32):
         base_o = ((_col(c0) * HV + _mid(hv)) * V + vb * 32) * 2
         done += check(f"fwd o slice {vb}", s.tokens * HV * V * 2, base_o, _col(ln) * v_row, _last(off_v.ravel()), 16)
+        done += check(f"fwd norm gate slice {vb}", s.tokens * HV * V * 2, base_o, _col(ln) * v_row,
+                      _last(off_v.ravel()), 16)
+        done += check(f"fwd norm o slice {vb}", s.tokens * HV * V * 2, base_o, _col(ln) * v_row,
+                      _last(off_v.ravel()), 16)
+    # the fused norm's exchange area: per chain a resource over its 8 slots x NVB slices x 64 tokens of
+    # 8-byte (sum, chunk + 1) pairs; slice vb stores lane l's pair of slot c % 8, every slice loads the
+    # pairs of its rows from all NVB slices
+    nvb, chains = V // 32, s.N * HV
+    rec = 8 * nvb * 64 * 8
+    r_ = np.arange(chains)
+    slot_, vb_, l_ = np.meshgrid(np.arange(8), np.arange(nvb), np.arange(64), indexing="ij")
+    off_np = ((((slot_ * nvb + vb_) * 64) + l_) * 8).ravel()
+    done += check("fwd norm sum pairs", chains * rec, _col(r_ * rec), _col(np.full(chains, rec)), _last(off_np), 8)
     # h0 loads / ht stores (plain, fp32 [N][HV][K][V]) and, with SAVE, the state entering each chunk
     # (bf16 [chunks][HV][V][K], an 8-byte store per lane and state tile)
     rank, vbs = state_kernel_grid(s)
@@ -427,7 +441,7 @@ def test_checker_flags_the_old_gate_loads(shape):
 
 def test_model_covers_every_buffer_resource():
     """Each buffer resource a kernel file creates has a counterpart above; a new one must be modelled."""
-    expected = {"gdn_chunk.hip": 9, "gdn_chunk_bwd.hip": 9, "gdn_chunk_prep.hip": 0}
+    expected = {"gdn_chunk.hip": 12, "gdn_chunk_bwd.hip": 9, "gdn_chunk_prep.hip": 0}
     for fname, n in expected.items():
         with open(os.path.join(CSRC, fname)) as f:
             src = f.read()

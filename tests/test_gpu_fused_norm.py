@@ -1,0 +1,150 @@
+"""GPU: the chunked forward with the layer's gated RMSNorm fused into its O store
+(``chunk_gated_delta_rule_gated_norm``, ``gdn_chunk_fwd_gated_norm``) against the two-op route it
+replaces -- ``chunk_gated_delta_rule`` then ``rms_norm_gated`` (sore/model/gdn.py:166-169 then
+182-186), or ``o_norm(o) * F.silu(gate)`` with ``norm_split`` (gdn.py:188) -- and against the CPU
+oracle's rule followed by the oracle norm. The V / 32 column slices of every (sequence, head)
+exchange their per-token sums of squares, so the cases cover several slices per head (V = 128),
+two (V = 64), grouped value heads, varlen documents that end inside a chunk, the kernel's gate and
+beta options, the BASELINE config-4 layer size, and the layer's inference route with its
+``fused_epilogue`` switch on (off by default: measured slower than the two kernels).
+Tolerances: the two-op route within one bf16 rounding step of the output (the fused kernel sums the
+squares in another order); the oracle within max-abs 2e-2 of the normalised output's scale.
+"""
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import recurrent_gated_delta_rule, rms_norm, rms_norm_gated
+from sorernn_amd import chunk_gated_delta_rule, chunk_gated_delta_rule_gated_norm
+from sorernn_amd import rms_norm_gated as gpu_rms_norm_gated
+from sorernn_amd.synthetic import gdn_inputs
+from tests.parity import assert_output_close
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+EPS = 1e-6
+
+
+def _gate_weight(shape, vd, seed):
+    gen = torch.Generator().manual_seed(seed)
+    gate = torch.randn(*shape, generator=gen).to(torch.bfloat16)
+    w = 1.0 + 0.1 * torch.randn(vd, generator=gen)
+    return gate, w
+
+
+def _both(inp, gate, w, split, **kw):
+    d = inp.to(DEV)
+    gd, wd = gate.to(DEV), w.to(DEV)
+    common = dict(scale=inp.scale, initial_state=d.h0, output_final_state=True, cu_seqlens=d.cu_seqlens,
+                  cu_seqlens_cpu=inp.cu_seqlens, **kw)
+    y, st = chunk_gated_delta_rule_gated_norm(d.q, d.k, d.v, d.g, d.beta, gd, wd, EPS, norm_split=split, **common)
+    o, st2 = chunk_gated_delta_rule(d.q, d.k, d.v, d.g, d.beta, **common)
+    if split:
+        y2 = gpu_rms_norm_gated(o, None, wd, None, eps=EPS) * F.silu(gd)
+    else:
+        y2 = gpu_rms_norm_gated(o, gd, wd, None, activation="swish", eps=EPS)
+    torch.cuda.synchronize()
+    return y.cpu(), st.cpu(), y2.cpu(), st2.cpu()
+
+
+def _oracle(inp, gate, w, split):
+    cu = None if inp.cu_seqlens is None else inp.cu_seqlens.long()
+    o, _ = recurrent_gated_delta_rule(inp.q, inp.k, inp.v, inp.g, inp.beta, inp.scale, inp.h0, True, cu_seqlens=cu)
+    if split:
+        return (rms_norm(o, w, EPS).to(torch.bfloat16).float() * F.silu(gate.float()).to(torch.bfloat16).float())
+    return rms_norm_gated(o, gate, w, EPS)
+
+
+def _check(y, st, y2, st2, ref):
+    assert torch.isfinite(y).all()
+    assert torch.equal(st, st2), "the final state is the plain call's"
+    # one bf16 rounding step of the output: |y - y2| <= 2^-7 |y2| (+ a floor for values near 0)
+    diff = (y.float() - y2.float()).abs()
+    assert (diff <= y2.float().abs() * 2.0 ** -7 + 1e-3).all(), f"fused vs two-op max diff {diff.max().item():.3e}"
+    assert_output_close(y, ref, tol=2e-2 * float(ref.abs().max()))
+
+
+@pytest.mark.parametrize("split", [False, True], ids=["fused_round", "split_round"])
+@pytest.mark.parametrize("dims", [(128, 128, 2), (64, 64, 1), (128, 128, 1)], ids=["d128_gva2x", "d64", "d128"])
+def test_fused_norm_matches_two_op_route(split, dims):
+    kd, vd, rep = dims
+    print(f"fused norm K={kd} V={vd} rep={rep} split={split}", flush=True)
+    inp = gdn_inputs(2, 300, 2, kd, V=vd, HV=2 * rep, dtype=torch.bfloat16, seed=40 + kd + rep, h0=True)
+    gate, w = _gate_weight(inp.v.shape, vd, 5)
+    _check(*_both(inp, gate, w, split), _oracle(inp, gate, w, split))
+
+
+def test_fused_norm_varlen_documents():
+    cu = torch.tensor([0, 1, 63, 64, 200, 777], dtype=torch.long)
+    inp = gdn_inputs(1, 777, 2, 128, HV=4, dtype=torch.bfloat16, seed=48, h0=True, cu_seqlens=cu)
+    gate, w = _gate_weight(inp.v.shape, 128, 6)
+    _check(*_both(inp, gate, w, False), _oracle(inp, gate, w, False))
+
+
+def test_fused_norm_kernel_options():
+    """Unnormalised q/k, gate and beta logits as the layer passes them with gdn_kernel_gate."""
+    gen = torch.Generator().manual_seed(49)
+    t, h, hv, dd = 257, 2, 4, 128
+    q = (torch.randn(1, t, h, dd, generator=gen) * 2).to(torch.bfloat16)
+    k = (torch.randn(1, t, h, dd, generator=gen) * 2).to(torch.bfloat16)
+    v = torch.randn(1, t, hv, dd, generator=gen).to(torch.bfloat16)
+    a = torch.randn(1, t, hv, generator=gen).to(torch.bfloat16)
+    bl = torch.randn(1, t, hv, generator=gen).to(torch.bfloat16)
+    A_log = torch.rand(hv, generator=gen) * 2
+    dt_bias = torch.randn(hv, generator=gen) * 0.5
+    gate, w = _gate_weight(v.shape, dd, 7)
+    d = [x.to(DEV) for x in (q, k, v, a, bl, gate, w, A_log, dt_bias)]
+    kw = dict(scale=dd ** -0.5, use_qk_l2norm_in_kernel=True, use_beta_sigmoid_in_kernel=True,
+              use_gate_in_kernel=True, A_log=d[7], dt_bias=d[8])
+    y, _ = chunk_gated_delta_rule_gated_norm(d[0], d[1], d[2], d[3], d[4], d[5], d[6], EPS, **kw)
+    o, _ = chunk_gated_delta_rule(d[0], d[1], d[2], d[3], d[4], **kw)
+    y2 = gpu_rms_norm_gated(o, d[5], d[6], None, activation="swish", eps=EPS)
+    torch.cuda.synchronize()
+    diff = (y.float() - y2.float()).abs()
+    assert (diff <= y2.float().abs() * 2.0 ** -7 + 1e-3).all(), f"max diff {diff.max().item():.3e}"
+
+
+def test_fused_norm_config4_size():
+    """BASELINE config 4's GDN call (B=2, T=8192, H=16, d=128), against the two-op route in full."""
+    print("fused norm config-4 size", flush=True)
+    inp = gdn_inputs(2, 8192, 16, 128, dtype=torch.bfloat16, seed=50, h0=False)
+    gate, w = _gate_weight(inp.v.shape, 128, 8)
+    y, st, y2, st2 = _both(inp, gate, w, False)
+    assert torch.isfinite(y).all() and torch.equal(st, st2)
+    diff = (y.float() - y2.float()).abs()
+    assert (diff <= y2.float().abs() * 2.0 ** -7 + 1e-3).all(), f"max diff {diff.max().item():.3e}"
+
+
+def test_fused_norm_rejects_grad():
+    inp = gdn_inputs(1, 64, 2, 128, dtype=torch.bfloat16, seed=51)
+    d = inp.to(DEV)
+    gate, w = _gate_weight(inp.v.shape, 128, 9)
+    q = d.q.clone().requires_grad_(True)
+    with pytest.raises(NotImplementedError, match="inference only"):
+        chunk_gated_delta_rule_gated_norm(q, d.k, d.v, d.g, d.beta, gate.to(DEV), w.to(DEV), EPS)
+
+
+@pytest.mark.parametrize("fused_norm_gate", [True, False], ids=["fused_flag", "unfused_flag"])
+@pytest.mark.parametrize("cu_case", ["rows", "short_docs"])
+def test_layer_with_fused_epilogue_matches_oracle(fused_norm_gate, cu_case, monkeypatch):
+    """The layer's inference route with ``fused_epilogue`` on (the norm inside the chunk kernel, both
+    rounding routes of fused_norm_gate) against the layer oracle; the norm kernel is not called."""
+    from tests.test_gpu_layer import _CU_CASES, _layer, _oracle_forward, _run
+    import sorernn_amd.gdn_layer as gl
+
+    cu = _CU_CASES[cu_case]
+    layer = _layer(True, rep=2, fla_conv=True, fused_norm_gate=fused_norm_gate)
+    b = 2 if cu is None else 1
+    x = torch.randn(b, 512, 256, generator=torch.Generator().manual_seed(13))
+    cu_t = None if cu is None else torch.tensor(cu)
+    ref = _oracle_forward(layer, x, cu_t)
+    layer = layer.to(DEV)
+    layer.fused_epilogue = True
+
+    def no_norm_kernel(*a, **k):
+        raise AssertionError("the fused epilogue route called the separate norm kernel")
+
+    monkeypatch.setattr(gl, "rms_norm_gated", no_norm_kernel)
+    out = _run(layer, x, cu_t)
+    err = (out - ref).abs().max().item()
+    assert err <= 2e-2 * ref.abs().max().item() + 1e-3, f"max-abs error {err:.3e} (max|ref| {ref.abs().max():.3e})"
