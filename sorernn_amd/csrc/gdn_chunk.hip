@@ -102,6 +102,61 @@ constexpr int kNT = 512;      // threads per workgroup (8 waves)
 // SAVE (training forward): the state waves also store the state entering every chunk, rounded to
 // bf16 and transposed ([V][K]: a lane's four consecutive keys are one 8-byte store), the input of
 // the backward's per-chunk gradient kernel, which uses it only as a bf16 MFMA operand.
+// workgroup -> (chain rank k, slice vb) -> (sequence n, value head hv). Workgroups are dispatched
+// in blockIdx order and blockIdx b lands on XCD b % 8: XCD x takes chain ranks x, x + 8, ..., all
+// NVB slices of a chain on one XCD (its q/k tiles are then read from one L2). Chain ranks follow
+// the longest-first sequence order with cu_seqlens, so a grid larger than the machine starts the
+// longest recurrences first.
+struct SliceLoc {
+  int64_t k;            // chain rank
+  int64_t n, bos, eos;  // sequence and its token range
+  int hv, h, vb;        // value head, its q/k head, V slice
+};
+template <int NVB>
+__device__ __forceinline__ SliceLoc locate_slice(const ChunkParams& p) {
+  const int64_t chains = p.N * p.HV;
+  int64_t k_rank;
+  SliceLoc l;
+  if (chains % 8 == 0) {
+    const int64_t x = blockIdx.x % 8, j = blockIdx.x / 8;
+    k_rank = 8 * (j / NVB) + x;
+    l.vb = (int)(j % NVB);
+  } else {
+    k_rank = blockIdx.x / NVB;
+    l.vb = (int)(blockIdx.x % NVB);
+  }
+  l.k = k_rank;
+  l.hv = (int)(k_rank % p.HV);
+  l.n = p.order ? (int64_t)p.order[k_rank / p.HV] : k_rank / p.HV;
+  l.h = l.hv / (int)(p.HV / p.H);
+  if (p.cu) {
+    l.bos = load_index(p.cu, p.cu_i32, l.n);
+    l.eos = load_index(p.cu, p.cu_i32, l.n + 1);
+  } else {
+    l.bos = l.n * p.T;
+    l.eos = l.bos + p.T;
+  }
+  return l;
+}
+
+// The kernel's parameters read again from the kernarg segment (the chunk kernel's only argument sits
+// at offset 0), through an address the optimiser cannot see through: code that runs after the main
+// loops (the recovery) then loads them where it runs, instead of keeping them in scalar registers
+// through the loops.
+__device__ __forceinline__ ChunkParams reload_params() {
+  static_assert(sizeof(ChunkParams) % 8 == 0, "read as 8-byte words");
+  constexpr int kWords = sizeof(ChunkParams) / 8;
+  typedef const __attribute__((address_space(4))) uint64_t* kwords;
+  uint64_t a = reinterpret_cast<uint64_t>(__builtin_amdgcn_kernarg_segment_ptr());
+  asm volatile("" : "+s"(a));
+  struct Words {
+    uint64_t w[kWords];
+  } r;
+#pragma unroll
+  for (int i = 0; i < kWords; ++i) r.w[i] = reinterpret_cast<kwords>(a)[i];
+  return __builtin_bit_cast(ChunkParams, r);
+}
+
 // The fp32 recurrence of one 32-column slice of a (sequence, value head), per token (the algebra of
 // gated_delta_recurrent_kernel, sore/model/gdn_ref.py:17-21):
 //   a = exp(g), delta = beta (v - a S^T k^), S' = a S + k^ delta^T, o = scale S'^T q^
@@ -257,33 +312,9 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
     return __builtin_bit_cast(f16x8, bf16x8{x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]});
   };
 
-  // workgroup -> (chain rank k, slice vb) -> (sequence n, value head hv). Workgroups are dispatched
-  // in blockIdx order and blockIdx b lands on XCD b % 8: XCD x takes chain ranks x, x + 8, ..., all
-  // NVB slices of a chain on one XCD (its q/k tiles are then read from one L2). Chain ranks follow
-  // the longest-first sequence order with cu_seqlens, so a grid larger than the machine starts the
-  // longest recurrences first.
-  const int64_t chains = p.N * p.HV;
-  int64_t k_rank;
-  int vb;
-  if (chains % 8 == 0) {
-    const int64_t x = blockIdx.x % 8, j = blockIdx.x / 8;
-    k_rank = 8 * (j / NVB) + x;
-    vb = (int)(j % NVB);
-  } else {
-    k_rank = blockIdx.x / NVB;
-    vb = (int)(blockIdx.x % NVB);
-  }
-  const int hv = (int)(k_rank % p.HV);
-  const int64_t n = p.order ? (int64_t)p.order[k_rank / p.HV] : k_rank / p.HV;
-  const int h = hv / (int)(p.HV / p.H);
-  int64_t bos, eos;
-  if (p.cu) {
-    bos = load_index(p.cu, p.cu_i32, n);
-    eos = load_index(p.cu, p.cu_i32, n + 1);
-  } else {
-    bos = n * p.T;
-    eos = bos + p.T;
-  }
+  const SliceLoc loc = locate_slice<NVB>(p);
+  const int64_t k_rank = loc.k, n = loc.n, bos = loc.bos, eos = loc.eos;
+  const int hv = loc.hv, h = loc.h, vb = loc.vb;
   const int nc = (int)((eos - bos + kC - 1) / kC);
   const bool l2 = p.flags & GDN_FLAG_QK_L2NORM;
   const float a_log = p.A_log ? p.A_log[hv] : 0.f, dt_b = p.dt_bias ? p.dt_bias[hv] : 0.f;
@@ -932,10 +963,14 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
   __syncthreads();
   if (__builtin_amdgcn_readfirstlane(bad)) {
     if constexpr (NORM) {
-      if (t == 0 && p.range_flag) flag_nonfinite(p.range_flag, true);
+      const ChunkParams pr = reload_params();
+      if (t == 0 && pr.range_flag) flag_nonfinite(pr.range_flag, true);
     } else {
-      recover_slice<KD, VD, SAVE>(p, n, hv, h, vb, bos, eos, cg_first, (bf16*)&Kc[0][0], (bf16*)&Qc[0][0],
-                                  (bf16*)&Vc[0][0], &gv[0]);
+      const ChunkParams pr = reload_params();
+      const SliceLoc lr = locate_slice<NVB>(pr);
+      const int64_t cgr = SAVE ? (pr.cu ? (int64_t)pr.chunk_first[lr.n] : lr.n * ((pr.T + kC - 1) / kC)) : 0;
+      recover_slice<KD, VD, SAVE>(pr, lr.n, lr.hv, lr.h, lr.vb, lr.bos, lr.eos, cgr, (bf16*)&Kc[0][0],
+                                  (bf16*)&Qc[0][0], (bf16*)&Vc[0][0], &gv[0]);
     }
   }
 }
