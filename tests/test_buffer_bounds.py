@@ -285,14 +285,20 @@ def state_kernel(s: Shape, eg: int, eb: int, save: bool) -> int:
 
 
 def prep_kernel(s: Shape, eg: int, eb: int) -> int:
-    """gdn_chunk_prep.hip: k rows and gates are plain loads guarded by row < len; T - I rows are
-    plain 16-byte stores guarded the same way (one workgroup per (chunk, value head))."""
+    """gdn_chunk_prep.hip. The one-wave kernel loads the k rows of a chunk through a resource over
+    its valid rows of head h (lane offsets row * H * K * 2 + 16-byte piece, every row of the tile);
+    the workgroup kernel kept for comparison loads them plainly, guarded by row < len. Both load the
+    gates plainly (lane = token < len) and store the T - I rows as plain 16-byte stores guarded by
+    row < len."""
     c0, ln, _, _ = chunk_rows(s)
     K, H, HV = s.K, s.H, s.HV
     kch = K // 8
     e = np.arange(C * kch)
     row, c8 = e // kch, e % kch
     done = 0
+    off = row * H * K * 2 + c8 * 16
+    done += check("prep k (resource)", s.tokens * H * K * 2, (_col(c0) * H + _mid(np.arange(H))) * K * 2,
+                  _col(ln) * H * K * 2, _last(off), 16)
     for hv in range(HV):
         h = hv // (HV // H)
         idx = ((_col(c0)[:, :, 0] + row[None, :]) * H + h) * K + c8[None, :] * 8
@@ -441,7 +447,7 @@ def test_checker_flags_the_old_gate_loads(shape):
 
 def test_model_covers_every_buffer_resource():
     """Each buffer resource a kernel file creates has a counterpart above; a new one must be modelled."""
-    expected = {"gdn_chunk.hip": 12, "gdn_chunk_bwd.hip": 9, "gdn_chunk_prep.hip": 0}
+    expected = {"gdn_chunk.hip": 12, "gdn_chunk_bwd.hip": 9, "gdn_chunk_prep.hip": 1}
     for fname, n in expected.items():
         with open(os.path.join(CSRC, fname)) as f:
             src = f.read()
