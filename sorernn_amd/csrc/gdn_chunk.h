@@ -38,6 +38,10 @@ inline int64_t chunk_t_bytes(int64_t tokens, int64_t HV) { return align256(token
 
 // Launches the index kernel (with cu) and the prep kernel; returns a GDN status.
 int launch_chunk_prep(const ChunkPrepParams& p, int64_t B, int64_t K, hipStream_t s);
+// The index kernel sorts sequences longest first for up to kOrderMax of them (identity order above).
+constexpr int kOrderMax = 2048;
+// Compute units of the device that runs stream s (cached per device).
+int device_compute_units(hipStream_t s);
 // Launches the index kernel only (with cu): chunk_first and the longest-first order.
 int launch_chunk_index(const void* cu, int cu_i32, int64_t N, int* chunk_first, int* order, hipStream_t s);
 

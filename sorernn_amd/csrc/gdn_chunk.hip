@@ -77,9 +77,12 @@ struct ChunkParams {
   float neps;
   int nsplit;                // 1: the reference's separate rmsnorm and silu(gate) roundings
   u32x2* npart;              // [chains][kNormSlots][V / 32][64] (sum of squares of a slice's columns, chunk + 1)
+  int nq;                    // PERSIST only: groups of V / 32 workgroups
+  int pad_;
 };
 
 constexpr int kNormSlots = 8;  // chunks whose partial sums are in flight per chain
+constexpr int kJobTab = 512;   // PERSIST: jobs per group held in LDS (the grid is used when no group needs more)
 
 // Running maximum, per 16-bit half, of the magnitude bits of the bf16 values in x: a half at or
 // above 0x7f80 (all-ones exponent) has seen an inf or a NaN.
@@ -263,9 +266,125 @@ __device__ __forceinline__ void recover_slice(const ChunkParams& p, int64_t n, i
   if (p.range_flag) flag_nonfinite(p.range_flag, smax >= 0x7f800000u || om[0] >= 0x7f80);
 }
 
-template <int KD, int VD, bool SAVE, bool NORM = false>
+constexpr int kLptMax = 128;  // PERSIST: sequences scheduled by rows (LPT); more go in snake order
+struct SchedScratch {
+  int nch[kLptMax], bos[kLptMax], eos[kLptMax], seq[kLptMax];  // the sequence of rank d (longest first)
+  int ne;                                                        // non-empty sequences
+};
+
+// PERSIST: the job list of group gq, into jtab, by every thread of the workgroup (all groups compute
+// the same schedule from the index kernel's longest-first order, each keeping its own list):
+//   rows (HV divides the group count and at most kLptMax sequences): every value head of a
+//   sequence goes to one row of HV groups, head h to the row's h-th group, so the groups of a row
+//   carry equal loads, and wave 0 deals the sequences, longest first, each to the least-loaded row
+//   (LPT; over the reference's document lengths the busiest group gets 135 chunks against a mean
+//   of 134.5, against 157 in snake order);
+//   otherwise the chains of the non-empty sequences in snake order (rank r: sequence order[r / HV],
+//   head r % HV; job k of group q is rank k nq + q for even k, k nq + nq - 1 - q for odd k).
+// gjob = (jobs, chunks in all of them). Empty sequences (last in the order) are in no list.
+__device__ __forceinline__ void schedule_group(const ChunkParams& p, int gq, int4* jtab, int* gjob, SchedScratch& sc) {
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int N = (int)p.N, HV = (int)p.HV, nq = p.nq;
+  const bool by_rows = nq % HV == 0 && N <= kLptMax;
+  if (t == 0) {
+    sc.ne = 0;
+    gjob[0] = gjob[1] = 0;
+  }
+  __syncthreads();
+  for (int d = t; d < N; d += kNT) {
+    const int sq = p.order[d];
+    const int64_t b = load_index(p.cu, p.cu_i32, sq), e = load_index(p.cu, p.cu_i32, sq + 1);
+    if (by_rows) {
+      sc.seq[d] = sq;
+      sc.bos[d] = (int)b;
+      sc.eos[d] = (int)e;
+      sc.nch[d] = (int)((e - b + kC - 1) / kC);
+    }
+    if (e > b) atomicAdd(&sc.ne, 1);
+  }
+  __syncthreads();
+  const int ne = sc.ne;
+  if (by_rows) {
+    if (w == 0) {
+      // lane r < R holds row r's load; the least-loaded row is the minimum of (load << 6 | lane)
+      // (loads stay below 2^25 chunks, so the keys stay positive)
+      const int R = nq / HV, my_row = gq / HV, h = gq % HV;
+      int load = lane < R ? 0 : 0x1ffffff, nj = 0, steps = 0, blk = 0;
+      if (R <= 8) {
+        // up to 8 rows: their loads in scalar registers (uniform code, no cross-lane steps)
+        int ld[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        for (int d = 0; d < ne; ++d) {
+          if ((d & 63) == 0) blk = d + lane < ne ? sc.nch[d + lane] : 0;
+          const int ncd = __builtin_amdgcn_readlane(blk, d & 63);
+          int row = 0, best = ld[0];
+#pragma unroll
+          for (int r = 1; r < 8; ++r)
+            if (r < R && ld[r] < best) {
+              best = ld[r];
+              row = r;
+            }
+#pragma unroll
+          for (int r = 0; r < 8; ++r) ld[r] += r == row ? ncd : 0;
+          if (row == my_row) {
+            if (lane == 0) jtab[nj] = make_int4(sc.bos[d], sc.eos[d], sc.seq[d], h);
+            ++nj;
+            steps += ncd;
+          }
+        }
+        if (lane == 0) {
+          gjob[0] = nj;
+          gjob[1] = steps;
+        }
+      }
+      for (int d = 0; R > 8 && d < ne; ++d) {
+        if ((d & 63) == 0) blk = d + lane < ne ? sc.nch[d + lane] : 0;
+        const int ncd = __builtin_amdgcn_readlane(blk, d & 63);
+        int key = (load << 6) | lane;
+        key = min(key, __builtin_amdgcn_mov_dpp(key, 0xb1, 0xf, 0xf, false));   // quad_perm [1,0,3,2]
+        key = min(key, __builtin_amdgcn_mov_dpp(key, 0x4e, 0xf, 0xf, false));   // quad_perm [2,3,0,1]
+        key = min(key, __builtin_amdgcn_mov_dpp(key, 0x141, 0xf, 0xf, false));  // row_half_mirror
+        key = min(key, __builtin_amdgcn_mov_dpp(key, 0x140, 0xf, 0xf, false));  // row_mirror
+        const int m = min(min(__builtin_amdgcn_readlane(key, 0), __builtin_amdgcn_readlane(key, 16)),
+                          min(__builtin_amdgcn_readlane(key, 32), __builtin_amdgcn_readlane(key, 48)));
+        const int row = m & 63;
+        if (row == my_row) {
+          if (lane == 0) jtab[nj] = make_int4(sc.bos[d], sc.eos[d], sc.seq[d], h);
+          ++nj;
+          steps += ncd;
+        }
+        if (lane == row) load += ncd;
+      }
+      if (R > 8 && lane == 0) {
+        gjob[0] = nj;
+        gjob[1] = steps;
+      }
+    }
+  } else {
+    const int64_t chains = (int64_t)ne * HV;
+    for (int k = t; k < kJobTab; k += kNT) {
+      const int64_t r = (int64_t)k * nq + ((k & 1) ? nq - 1 - gq : gq);
+      if (r >= chains) break;
+      const int sq = p.order[r / HV];
+      const int64_t b = load_index(p.cu, p.cu_i32, sq), e = load_index(p.cu, p.cu_i32, sq + 1);
+      jtab[k] = make_int4((int)b, (int)e, sq, (int)(r % HV));
+      atomicAdd(&gjob[1], (int)((e - b + kC - 1) / kC));
+      atomicMax(&gjob[0], k + 1);
+    }
+  }
+  __syncthreads();
+}
+
+// PERSIST (inference with cu_seqlens and many chains, no initial or final state: the reference
+// model's call): one workgroup per CU; the V / 32 workgroups of a group (on one XCD) walk the group's
+// job list, a sequence of (sequence, value head) chains of their V-slice, back to back: every role
+// treats the jobs' chunks as one stream of steps, so a short sequence does not pay a workgroup's
+// pipeline fill and drain. At the last step of a job the state waves zero the state. (Storing and
+// loading states there, in each of the six unrolled steps, made the kernel's code larger than the
+// instruction cache two CUs share; calls with states keep one workgroup per slice.)
+template <int KD, int VD, bool SAVE, bool NORM = false, bool PERSIST = false>
 __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p) {
   static_assert(!(SAVE && NORM), "the fused norm is an inference epilogue");
+  static_assert(!(PERSIST && (SAVE || NORM)), "the persistent grid runs plain inference calls");
   constexpr int NVB = VD / kVB;
   // q/k tiles in LDS: at KD = 128 rows are unpadded (256 B) and the 16-byte chunk c of row r sits
   // at chunk c ^ kq_sw(r) = c ^ ((r & 7) << 1). Measured with SQ_LDS_BANK_CONFLICT on gfx950, the
@@ -288,6 +407,8 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
   __shared__ float psum[NORM ? 2 : 1][2][kC];     // NORM: per-token sums of squares of each state wave's O
   __shared__ __align__(16) ChunkGates gv[3];      // gate terms of chunk c in slot c % 3
   __shared__ int bad;                              // an O or final-state element of this slice is inf / NaN
+  __shared__ int4 jtab[PERSIST ? kJobTab : 1];     // PERSIST: the group's job list (bos, eos, sequence, head)
+  __shared__ SchedScratch sched;                   // PERSIST: the scheduler's per-sequence arrays
 
   // w is read back as a scalar: the compiler then treats the role branches as wave-uniform
   const int t = threadIdx.x, lane = t & 63, w = __builtin_amdgcn_readfirstlane(t >> 6), g4 = lane >> 4, li = lane & 15;
@@ -312,10 +433,56 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
     return __builtin_bit_cast(f16x8, bf16x8{x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]});
   };
 
-  const SliceLoc loc = locate_slice<NVB>(p);
+  // A_log and dt_bias are read per job (PERSIST) through the constant address space, as scalar loads:
+  // as vector loads, the compiler follows each with a wait for every vector load in flight, which
+  // drains the helpers' prefetched tiles.
+  typedef const __attribute__((address_space(4))) float* const_f32p;
+  // PERSIST: group gq of workgroups (blockIdx b on XCD b % 8 when the group count is a multiple of 8,
+  // all NVB of a group on one XCD), its jobs and the chunks in all of them
+  int gq = 0, gvb = 0;
+  if constexpr (PERSIST) {
+    if (p.nq % 8 == 0) {
+      const int x = blockIdx.x % 8, j = blockIdx.x / 8;
+      gq = 8 * (j / NVB) + x;
+      gvb = j % NVB;
+    } else {
+      gq = blockIdx.x / NVB;
+      gvb = blockIdx.x % NVB;
+    }
+  }
+  // PERSIST: the group's job count and chunks in all its jobs (set by the prologue's scheduling)
+  __shared__ int gjob[2];
+  int njobs = 0, gsteps = 0;
+  // a role's position in its chunk stream: chunk c of job j (PERSIST), with the job's tokens and heads
+  struct Cursor {
+    int j, c, nc, bos, eos, n, hv, h;
+  };
+  auto cur_job = [&](Cursor& u, int j) {
+    u.j = j;
+    u.c = 0;
+    if (j < njobs) {
+      // from the LDS copy (a scalar load here, whose result the role needs at once, stalled each
+      // role for its latency at every job switch)
+      const int4 e = jtab[j];
+      u.bos = __builtin_amdgcn_readfirstlane(e.x);
+      u.eos = __builtin_amdgcn_readfirstlane(e.y);
+      u.n = __builtin_amdgcn_readfirstlane(e.z);
+      u.hv = __builtin_amdgcn_readfirstlane(e.w);
+      u.h = u.hv / (int)(p.HV / p.H);
+      u.nc = (int)((u.eos - u.bos + kC - 1) / kC);
+    } else {
+      u.bos = u.eos = u.n = 0;
+      u.hv = u.h = 0;
+      u.nc = 0;
+    }
+  };
+  auto cur_next = [&](Cursor& u) {
+    if (++u.c >= u.nc && u.j < njobs) cur_job(u, u.j + 1);
+  };
+  const SliceLoc loc = PERSIST ? SliceLoc{gq, 0, 0, 0, 0, 0, gvb} : locate_slice<NVB>(p);
   const int64_t k_rank = loc.k, n = loc.n, bos = loc.bos, eos = loc.eos;
   const int hv = loc.hv, h = loc.h, vb = loc.vb;
-  const int nc = (int)((eos - bos + kC - 1) / kC);
+  int nc = PERSIST ? 0 : (int)((eos - bos + kC - 1) / kC);
   const bool l2 = p.flags & GDN_FLAG_QK_L2NORM;
   const float a_log = p.A_log ? p.A_log[hv] : 0.f, dt_b = p.dt_bias ? p.dt_bias[hv] : 0.f;
   const bf16* __restrict__ qg = static_cast<const bf16*>(p.q);
@@ -326,6 +493,17 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
   auto chunk_len = [&](int c) {
     const int64_t c0 = bos + (int64_t)c * kC;
     return c < nc ? (int)((eos - c0) < kC ? (eos - c0) : kC) : 0;
+  };
+  // a chunk's first token, valid rows and heads: chunk c of the workgroup's sequence, or a cursor's chunk
+  struct ChunkAt {
+    int64_t c0;
+    uint32_t len;
+    int h, hv;
+  };
+  auto at = [&](int c) { return ChunkAt{bos + (int64_t)c * kC, (uint32_t)chunk_len(c), h, hv}; };
+  auto cur_at = [&](const Cursor& u) {
+    const int64_t c0 = u.bos + (int64_t)u.c * kC;
+    return ChunkAt{c0, u.c < u.nc ? (uint32_t)((u.eos - c0) < kC ? (u.eos - c0) : kC) : 0u, u.h, u.hv};
   };
 
   // ------------------------------------------------------------------ helper-side staging
@@ -346,9 +524,8 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
   // being hoisted out of the loop into registers that would stay live through the state waves' code.
   // Thread tq of the q/k waves handles the 16-byte chunks tq + 256u of a q/k tile: row tq / KCH + u (256
   // / KCH), chunk tq % KCH.
-  auto fetch_rows = [&](bf16x8 (&dst)[QKPT], const bf16* src, int c, int tq) {
-    const int64_t c0 = bos + (int64_t)c * kC;
-    const auto rs = make_rsrc(src + (c0 * p.H + h) * KD, (uint32_t)chunk_len(c) * qk_row);
+  auto fetch_rows = [&](bf16x8 (&dst)[QKPT], const bf16* src, const ChunkAt& a, int tq) {
+    const auto rs = make_rsrc(src + (a.c0 * p.H + a.h) * KD, a.len * qk_row);
     const uint32_t base = (uint32_t)(tq / KCH) * qk_row + (uint32_t)(tq % KCH) * 16;
 #pragma unroll
     for (int u = 0; u < QKPT; ++u) dst[u] = buf_load16(rs, base + (uint32_t)(u * (256 / KCH)) * qk_row);
@@ -361,9 +538,10 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
   };
   // Thread tq of waves 4-5: T - I chunks tq + 128u (row tq / 8 + 16u, 8 chunks of 16 B per row)
   // and V-slice chunks tq + 128u (row tq / 4 + 32u, 4 chunks per row).
-  auto fetch_tv = [&](bf16x8 (&pt)[4], bf16x8 (&pv)[2], int c, int tq) {
-    const int64_t c0 = bos + (int64_t)c * kC;
-    const uint32_t len = (uint32_t)chunk_len(c);
+  auto fetch_tv = [&](bf16x8 (&pt)[4], bf16x8 (&pv)[2], const ChunkAt& a, int tq) {
+    const int64_t c0 = a.c0;
+    const uint32_t len = a.len;
+    const int hv = a.hv;
     const auto rt = make_rsrc(p.tw + (c0 * p.HV + hv) * kC, len * t_row);
     const uint32_t bt = (uint32_t)(tq >> 3) * t_row + (uint32_t)(tq & 7) * 16;
 #pragma unroll
@@ -393,11 +571,12 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
   struct GateBits {
     uint32_t g32, g16, b32, b16;
   };
-  auto fetch_gates = [&](int c, GateBits& r) {  // wave 4, lane = token
-    const int64_t c0 = bos + (int64_t)c * kC;
+  auto fetch_gates = [&](const ChunkAt& a, GateBits& r) {  // wave 4, lane = token
+    const int64_t c0 = a.c0;
+    const int hv = a.hv;
     const uint32_t eg = (uint32_t)dtype_bytes(p.dg), eb = (uint32_t)dtype_bytes(p.db);
     const uint32_t gb = (uint32_t)p.HV * eg, bb = (uint32_t)p.HV * eb;
-    const uint32_t len = (uint32_t)chunk_len(c);
+    const uint32_t len = a.len;
     const uint32_t gext = len ? (len - 1) * gb + eg : 0u, bext = len ? (len - 1) * bb + eb : 0u;
     const char* gsrc = static_cast<const char*>(p.g) + (c0 * p.HV + hv) * eg;
     const char* bsrc = static_cast<const char*>(p.beta) + (c0 * p.HV + hv) * eb;
@@ -408,23 +587,29 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
     r.b32 = __builtin_amdgcn_raw_buffer_load_b32(rb32, (int)(lane * bb), 0, 0);
     r.b16 = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rb16, (int)(lane * bb), 0, 0);
   };
-  auto stage_gates = [&](int c, const GateBits& r) {
+  auto stage_gates = [&](int slot, const ChunkAt& a, const GateBits& r) {
     // (A_log through opaque_int: its exp is recomputed here, not held in a register)
-    const float al = __int_as_float(opaque_int(__float_as_int(a_log)));
+    float al, db;
+    if constexpr (PERSIST) {  // the job's head (scalar loads: read-only parameters)
+      al = p.A_log ? reinterpret_cast<const_f32p>(reinterpret_cast<uint64_t>(p.A_log))[a.hv] : 0.f;
+      db = p.dt_bias ? reinterpret_cast<const_f32p>(reinterpret_cast<uint64_t>(p.dt_bias))[a.hv] : 0.f;
+    } else {
+      al = __int_as_float(opaque_int(__float_as_int(a_log)));
+      db = dt_b;
+    }
     const uint32_t graw = p.dg == GDN_DTYPE_F32 ? r.g32 : r.g16, braw = p.db == GDN_DTYPE_F32 ? r.b32 : r.b16;
-    chunk_gates_from_raw(gv[c % 3], graw, braw, p.dg, p.db, chunk_len(c), p.flags, al, dt_b, lane);
+    chunk_gates_from_raw(gv[slot], graw, braw, p.dg, p.db, (int)a.len, p.flags, al, db, lane);
   };
   // waves 4-5: O of chunk c from Ob to HBM, rows tq / 4 + 32u; om keeps the stored values' magnitude maximum
   // O rows go out as non-temporal stores in the inference kernel: streamed past the caches, they
   // leave L2 to the q/k/T/V tiles that the slices of a chain share (config-1 call 130.3 -> 125.2 us,
   // same-box A/B). The training kernel keeps cached stores (non-temporal ones measured slower there).
-  auto store_o = [&](int c, int tq, u16x2& om) {
-    const int64_t c0 = bos + (int64_t)c * kC;
-    const auto ro = make_rsrc(og + (c0 * p.HV + hv) * VD + vb * kVB, (uint32_t)chunk_len(c) * v_row);
+  auto store_o = [&](int slot, const ChunkAt& a, int tq, u16x2& om) {
+    const auto ro = make_rsrc(og + (a.c0 * p.HV + a.hv) * VD + vb * kVB, a.len * v_row);
     const int row = tq >> 2, c8 = tq & 3;
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      const bf16x8 x = *reinterpret_cast<const bf16x8*>(&Ob[c & 1][vo_off(row + 32 * u, c8 * 8)]);
+      const bf16x8 x = *reinterpret_cast<const bf16x8*>(&Ob[slot][vo_off(row + 32 * u, c8 * 8)]);
       om = bf16_mag_max(om, x);
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), ro,
                                              (int)((uint32_t)(row + 32 * u) * v_row + c8 * 16), 0, SAVE ? 0 : 2);
@@ -620,6 +805,12 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
 
   // ------------------------------------------------------------------ prologue
   if (t == 0) bad = 0;
+  if constexpr (PERSIST) {
+    schedule_group(p, gq, jtab, gjob, sched);
+    njobs = gjob[0];
+    gsteps = gjob[1];
+    nc = gsteps;
+  }
   // P is causally lower: its tiles above the diagonal stay zero for the whole run
   for (int e = t; e < kC * kC / 8; e += kNT) {
     reinterpret_cast<f16x8*>(Pb[0])[e] = f16x8{};
@@ -630,11 +821,14 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
   // others' register allocation: the helpers hold the global loads of the next step's tiles across
   // the barrier, a full step of latency hiding.
   if (w < 2) {
+    // PERSIST: the job of the current step (no initial state: every job starts from zero)
+    Cursor sc{};
+    if constexpr (PERSIST) cur_job(sc, 0);
 #pragma unroll
     for (int a = 0; a < KT; ++a) {
       const int kd0 = 32 * (a >> 1) + 8 * g4 + 4 * (a & 1);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) S[a][r] = p.h0 ? p.h0[sbase + (int64_t)(kd0 + r) * VD + li] : 0.f;
+      for (int r = 0; r < 4; ++r) S[a][r] = !PERSIST && p.h0 ? p.h0[sbase + (int64_t)(kd0 + r) * VD + li] : 0.f;
     }
     make_sb();
     if constexpr (SAVE) {
@@ -773,6 +967,14 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
 #pragma unroll
         for (int u = 0; u < 2; ++u) S[a] = mmah(ktf[a][u], dt[u], S[a]);
       phase();
+      if constexpr (PERSIST) {
+        // the last chunk of a job: the next job starts from the zero state
+        if (sc.c + 1 >= sc.nc) {
+#pragma unroll
+          for (int a = 0; a < KT; ++a) S[a] = f32x4{};
+        }
+        cur_next(sc);
+      }
       // ---- 5: Q reads and the first half of the K reads of the next chunk; S in fp16
       const f16* kn = Kc[(PH + 1) % 3];
       f16x8 kfa[KSH][4];
@@ -853,7 +1055,7 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
       if (i + 4 < nc) step(std::integral_constant<int, 4>{}, i + 4);
       if (i + 5 < nc) step(std::integral_constant<int, 5>{}, i + 5);
     }
-    if (p.ht) {
+    if (!PERSIST && p.ht) {  // (PERSIST: stored at each job's last chunk)
       uint32_t smax = 0;  // magnitude bits: at or above 0x7f800000 for inf and NaN
 #pragma unroll
       for (int a = 0; a < KT; ++a) {
@@ -867,16 +1069,32 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
       if (smax >= 0x7f800000u) __hip_atomic_fetch_or(&bad, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
   } else if (qk_wave) {
+    // the chunk stream's q/k loads in order: chunk c of the sequence, or the cursor's next chunk
+    Cursor fq{};
+    if constexpr (PERSIST) cur_job(fq, 0);
+    auto qk_src = [&](int c) {
+      if constexpr (PERSIST) {
+        const ChunkAt a = cur_at(fq);
+        cur_next(fq);
+        return a;
+      } else {
+        return at(c);
+      }
+    };
     // K/Q of chunks 0 and 1 staged, chunk 2 in flight
     bf16x8 pk[QKPT], pq[QKPT];
     for (int c = 0; c < 2; ++c) {
-      fetch_rows(pk, kg, c, thq);
-      fetch_rows(pq, qg, c, thq);
+      const ChunkAt a = qk_src(c);
+      fetch_rows(pk, kg, a, thq);
+      fetch_rows(pq, qg, a, thq);
       stage_rows(pk, Kc[c], thq);
       stage_rows(pq, Qc[c], thq);
     }
-    fetch_rows(pk, kg, 2, thq);
-    fetch_rows(pq, qg, 2, thq);
+    {
+      const ChunkAt a = qk_src(2);
+      fetch_rows(pk, kg, a, thq);
+      fetch_rows(pq, qg, a, thq);
+    }
     __syncthreads();
     if (nc > 0) run_p_side(0, lane);
     __syncthreads();
@@ -887,25 +1105,44 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
       const int tq = thq_of(opaque_int(lane));
       stage_rows(pk, Kc[(i + 2) % 3], tq);
       stage_rows(pq, Qc[i & 1], tq);
-      fetch_rows(pk, kg, i + 3, tq);
-      fetch_rows(pq, qg, i + 3, tq);
+      const ChunkAt a = qk_src(i + 3);
+      fetch_rows(pk, kg, a, tq);
+      fetch_rows(pq, qg, a, tq);
       if (i + 1 < nc) run_p_side(i + 1, opaque_int(lane));
       __syncthreads();
     }
   } else {
+    // the chunk streams of this role, each walked in order: T/V loads and gate staging (the same
+    // chunks), gate loads (wave 4), O stores
+    Cursor ct{}, cgf{}, co{};
+    if constexpr (PERSIST) {
+      cur_job(ct, 0);
+      cur_job(cgf, 0);
+      cur_job(co, 0);
+    }
+    auto src = [&](Cursor& u, int c) {
+      if constexpr (PERSIST) {
+        const ChunkAt a = cur_at(u);
+        cur_next(u);
+        return a;
+      } else {
+        return at(c);
+      }
+    };
     // T/V of chunk 0 staged and chunk 1 in flight; gates of chunks 0 and 1 staged, chunk 2 in flight
     bf16x8 pt[4], pv[2];
     u16x2 om = {0, 0};
-    fetch_tv(pt, pv, 0, thv);
+    const ChunkAt a0 = src(ct, 0), a1 = src(ct, 1);
+    fetch_tv(pt, pv, a0, thv);
     stage_tv(pt, pv, 0, thv);
-    fetch_tv(pt, pv, 1, thv);
+    fetch_tv(pt, pv, a1, thv);
     if (w == 4) {
       for (int c = 0; c < 2; ++c) {
         GateBits gb0;
-        fetch_gates(c, gb0);
-        stage_gates(c, gb0);
+        fetch_gates(src(cgf, c), gb0);
+        stage_gates(c, c ? a1 : a0, gb0);
       }
-      fetch_gates(2, ngate);
+      fetch_gates(src(cgf, 2), ngate);
     }
     __syncthreads();
     __syncthreads();
@@ -913,18 +1150,19 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
     u32x2 pss[2][NVB];  // NORM: (sum, chunk + 1) pairs of those rows from every slice
     for (int i = 0; i < nc; ++i) {  // gates of chunk i+2, O of chunk i-1 out, T/V of chunk i+1 into LDS, loads of chunk i+2
       const int tq = thv_of(opaque_int(lane));
+      const ChunkAt a2 = src(ct, i + 2);  // the chunk whose gates are staged and T/V loaded this step
       if (w == 4) {  // gates of chunk i+2 (loaded a step ago), then the loads for chunk i+3
-        stage_gates(i + 2, ngate);
-        fetch_gates(i + 3, ngate);
+        stage_gates((i + 2) % 3, a2, ngate);
+        fetch_gates(src(cgf, i + 3), ngate);
       }
       if constexpr (NORM) {  // sums of chunk i-1 out, O of chunk i-4 out
         if (w == 5 && i >= 1) publish_sums(i - 1);
         if (i >= 4) store_o_norm(i - 4, tq, om, pgt, pss);
       } else {
-        if (i > 0) store_o(i - 1, tq, om);
+        if (i > 0) store_o((i - 1) & 1, src(co, i - 1), tq, om);
       }
       stage_tv(pt, pv, (i + 1) & 1, tq);
-      fetch_tv(pt, pv, i + 2, tq);
+      fetch_tv(pt, pv, a2, tq);
       if constexpr (NORM) {
         // gates and sums of chunk i-3, issued after the T/V loads: loads complete in order, and the
         // next step's T/V staging then does not wait for these slower device-scope loads
@@ -946,7 +1184,7 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
         }
       }
     } else {
-      if (nc > 0) store_o(nc - 1, thv, om);
+      if (nc > 0) store_o((nc - 1) & 1, src(co, nc - 1), thv, om);
     }
     if (om[0] >= 0x7f80 || om[1] >= 0x7f80) __hip_atomic_fetch_or(&bad, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
@@ -967,10 +1205,23 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
       if (t == 0 && pr.range_flag) flag_nonfinite(pr.range_flag, true);
     } else {
       const ChunkParams pr = reload_params();
-      const SliceLoc lr = locate_slice<NVB>(pr);
-      const int64_t cgr = SAVE ? (pr.cu ? (int64_t)pr.chunk_first[lr.n] : lr.n * ((pr.T + kC - 1) / kC)) : 0;
-      recover_slice<KD, VD, SAVE>(pr, lr.n, lr.hv, lr.h, lr.vb, lr.bos, lr.eos, cgr, (bf16*)&Kc[0][0],
-                                  (bf16*)&Qc[0][0], (bf16*)&Vc[0][0], &gv[0]);
+      if constexpr (PERSIST) {
+        // every job of the group, in turn (the workgroup's V-slice of each)
+        // (the job list is still in LDS: the recomputation stages its tiles in the chunk slots)
+        const int rvb = pr.nq % 8 == 0 ? (int)((blockIdx.x / 8) % NVB) : (int)(blockIdx.x % NVB);
+        const int rjobs = gjob[0];
+        for (int j = 0; j < rjobs; ++j) {
+          const int4 e = jtab[j];
+          recover_slice<KD, VD, SAVE>(pr, e.z, e.w, e.w / (int)(pr.HV / pr.H), rvb, e.x, e.y, 0, (bf16*)&Kc[0][0],
+                                      (bf16*)&Qc[0][0], (bf16*)&Vc[0][0], &gv[0]);
+          __syncthreads();  // the next job's staging reuses the tiles
+        }
+      } else {
+        const SliceLoc lr = locate_slice<NVB>(pr);
+        const int64_t cgr = SAVE ? (pr.cu ? (int64_t)pr.chunk_first[lr.n] : lr.n * ((pr.T + kC - 1) / kC)) : 0;
+        recover_slice<KD, VD, SAVE>(pr, lr.n, lr.hv, lr.h, lr.vb, lr.bos, lr.eos, cgr, (bf16*)&Kc[0][0],
+                                    (bf16*)&Qc[0][0], (bf16*)&Vc[0][0], &gv[0]);
+      }
     }
   }
 }
@@ -1086,11 +1337,21 @@ int chunk_fwd_impl(const void* q, const void* k, const void* v, const void* g, c
                g_dtype, beta_dtype, scale, flags, A_log, dt_bias, ws, sync, range_flag, nullptr};
     return launch_chunk_coop(a, s);
   }
-  const int64_t blocks = N * HV * (V / kVB);
+  const int64_t nvb = V / kVB;
+  int64_t blocks = N * HV * nvb;
   if (blocks > 0x7fffffff) {
     gdn_internal_set_error("gdn_chunk_fwd: grid too large");
     return GDN_ERR_UNSUPPORTED;
   }
+  // The persistent grid for inference calls with cu_seqlens and no initial or final state whose
+  // chains (sequence, value head) are many against the machine: one workgroup per CU, in groups of V / 32 (one per V-slice), each
+  // group walking a job list of at least four chains on average (snake order over the chains sorted
+  // longest first, so the lists' lengths come out even). Fewer, longer chains keep one workgroup per
+  // slice, dispatched longest first: there the longest sequence sets the time.
+  const int64_t cus = device_compute_units(s);
+  const int64_t nq = cus / nvb;
+  const bool persist = cu_seqlens && !chunk_states && !norm && !initial_state && !final_state && N <= kOrderMax &&
+                       nq >= 1 && N * HV >= 4 * nq && (N * HV + nq - 1) / nq <= kJobTab;
   f16* tw = static_cast<f16*>(workspace);
   char* const ws = static_cast<char*>(workspace);
   const int* chunk_first = cu_seqlens ? reinterpret_cast<const int*>(ws + chunk_t_bytes(B * T, HV)) : nullptr;
@@ -1103,8 +1364,17 @@ int chunk_fwd_impl(const void* q, const void* k, const void* v, const void* g, c
   ChunkParams p{q, k, v, g, beta, initial_state, o, final_state, tw, cu_seqlens, order, cu_i32, T, H, HV, N,
                 g_dtype, beta_dtype, scale, flags, A_log, dt_bias, static_cast<bf16*>(chunk_states), chunk_first,
                 range_flag, static_cast<const bf16*>(ngate), nweight, neps, nsplit, nullptr};
+  if (persist) {
+    p.nq = (int)nq;
+    blocks = nq * nvb;
+  }
   dim3 grid((unsigned)blocks), block(kNT);
-  if (norm) {
+  if (persist) {
+    if (K == 128 && V == 128) hipLaunchKernelGGL((gated_delta_chunk_kernel<128, 128, false, false, true>), grid, block, 0, s, p);
+    else if (K == 64 && V == 64) hipLaunchKernelGGL((gated_delta_chunk_kernel<64, 64, false, false, true>), grid, block, 0, s, p);
+    else if (K == 128 && V == 64) hipLaunchKernelGGL((gated_delta_chunk_kernel<128, 64, false, false, true>), grid, block, 0, s, p);
+    else hipLaunchKernelGGL((gated_delta_chunk_kernel<64, 128, false, false, true>), grid, block, 0, s, p);
+  } else if (norm) {
     // the pairs carry their chunk, and no chunk index is 0 (they store c + 1): zeroing the exchange
     // area is enough for any earlier contents (a fill kernel, so that captured graphs clear it too)
     p.npart = reinterpret_cast<u32x2*>(ws + base_need);

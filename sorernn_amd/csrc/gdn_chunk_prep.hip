@@ -313,7 +313,6 @@ __global__ __attribute__((amdgpu_waves_per_eu(3))) __launch_bounds__(kWave) void
 //   order[k] = the sequence of rank k by length, longest first (ties by index), for N <= kOrderMax
 //   (a bitonic sort in LDS; identity above that): the state kernel starts the longest recurrences
 //   first, so a grid larger than the machine finishes near the longest sequence's own time.
-constexpr int kOrderMax = 2048;
 __global__ __launch_bounds__(1024) void gated_delta_chunk_index_kernel(const void* cu, int cu_i32, int64_t N,
                                                                         int* chunk_first, int* order) {
   __shared__ int wsum[16];
@@ -397,6 +396,8 @@ int device_cus(hipStream_t s) {
 }
 
 }  // namespace
+
+int device_compute_units(hipStream_t s) { return device_cus(s); }
 
 int launch_chunk_index(const void* cu, int cu_i32, int64_t N, int* chunk_first, int* order, hipStream_t s) {
   hipLaunchKernelGGL(gated_delta_chunk_index_kernel, dim3(1), dim3(1024), 0, s, cu, cu_i32, N, chunk_first, order);
