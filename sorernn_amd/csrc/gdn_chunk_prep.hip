@@ -307,9 +307,10 @@ __global__ __attribute__((amdgpu_waves_per_eu(3))) __launch_bounds__(kWave) void
   }
 }
 
-// One block, with cu_seqlens:
+// One block of nt = 64..1024 threads (a multiple of 64, sized to N by the launcher: one wave for up
+// to 64 sequences, whose barriers are then nearly free), with cu_seqlens:
 //   chunk_first[0] = 0, chunk_first[n + 1] = chunk_first[n] + ceil(len_n / 64) (a running block-wide
-//   scan over tiles of 1024 sequences): the prep kernel's chunk -> sequence map;
+//   scan over tiles of nt sequences): the prep kernel's chunk -> sequence map;
 //   order[k] = the sequence of rank k by length, longest first (ties by index), for N <= kOrderMax
 //   (a bitonic sort in LDS; identity above that): the state kernel starts the longest recurrences
 //   first, so a grid larger than the machine finishes near the longest sequence's own time.
@@ -318,13 +319,13 @@ __global__ __launch_bounds__(1024) void gated_delta_chunk_index_kernel(const voi
   __shared__ int wsum[16];
   __shared__ int carry;
   __shared__ unsigned long long keys[kOrderMax];
-  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6, nt = (int)blockDim.x;
   if (t == 0) {
     carry = 0;
     chunk_first[0] = 0;
   }
   __syncthreads();
-  for (int64_t base = 0; base < N; base += 1024) {
+  for (int64_t base = 0; base < N; base += nt) {
     const int64_t n = base + t;
     int v = 0;
     if (n < N) v = (int)((load_index(cu, cu_i32, n + 1) - load_index(cu, cu_i32, n) + kC - 1) / kC);
@@ -340,17 +341,17 @@ __global__ __launch_bounds__(1024) void gated_delta_chunk_index_kernel(const voi
     for (int j = 0; j < w; ++j) before += wsum[j];
     if (n < N) chunk_first[n + 1] = before + incl;
     __syncthreads();
-    if (t == 1023) carry = before + incl;
+    if (t == nt - 1) carry = before + incl;
     __syncthreads();
   }
   if (N > kOrderMax) {
-    for (int64_t n = t; n < N; n += 1024) order[n] = (int)n;
+    for (int64_t n = t; n < N; n += nt) order[n] = (int)n;
     return;
   }
   // key = (chunks descending, index ascending); padding sorts last
   int m = 1;
   while (m < N) m <<= 1;
-  for (int n = t; n < m; n += 1024) {
+  for (int n = t; n < m; n += nt) {
     unsigned long long key = ~0ull;
     if (n < N) {
       const unsigned nch = (unsigned)((load_index(cu, cu_i32, n + 1) - load_index(cu, cu_i32, n) + kC - 1) / kC);
@@ -361,7 +362,7 @@ __global__ __launch_bounds__(1024) void gated_delta_chunk_index_kernel(const voi
   __syncthreads();
   for (int size = 2; size <= m; size <<= 1) {
     for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      for (int n = t; n < m; n += 1024) {
+      for (int n = t; n < m; n += nt) {
         const int partner = n ^ stride;
         if (partner > n) {
           const bool up = (n & size) == 0;
@@ -375,7 +376,7 @@ __global__ __launch_bounds__(1024) void gated_delta_chunk_index_kernel(const voi
       __syncthreads();
     }
   }
-  for (int n = t; n < N; n += 1024) order[n] = (int)(keys[n] & 0xffffffffu);
+  for (int n = t; n < N; n += nt) order[n] = (int)(keys[n] & 0xffffffffu);
 }
 
 namespace {
@@ -399,15 +400,19 @@ int device_cus(hipStream_t s) {
 
 int device_compute_units(hipStream_t s) { return device_cus(s); }
 
+// Threads of the index kernel's block for N sequences: N rounded up to a wave, at most 1024.
+static unsigned index_threads(int64_t N) { return (unsigned)std::min<int64_t>(1024, std::max<int64_t>(1, (N + 63) / 64) * 64); }
+
 int launch_chunk_index(const void* cu, int cu_i32, int64_t N, int* chunk_first, int* order, hipStream_t s) {
-  hipLaunchKernelGGL(gated_delta_chunk_index_kernel, dim3(1), dim3(1024), 0, s, cu, cu_i32, N, chunk_first, order);
+  hipLaunchKernelGGL(gated_delta_chunk_index_kernel, dim3(1), dim3(index_threads(N)), 0, s, cu, cu_i32, N, chunk_first,
+                     order);
   return gdn_internal_check_launch("gated_delta_chunk_index_kernel");
 }
 
 int launch_chunk_prep(const ChunkPrepParams& prm, int64_t B, int64_t K, hipStream_t s) {
   ChunkPrepParams p = prm;
   if (p.cu) {
-    hipLaunchKernelGGL(gated_delta_chunk_index_kernel, dim3(1), dim3(1024), 0, s, p.cu, p.cu_i32, p.N,
+    hipLaunchKernelGGL(gated_delta_chunk_index_kernel, dim3(1), dim3(index_threads(p.N)), 0, s, p.cu, p.cu_i32, p.N,
                        const_cast<int*>(p.chunk_first), const_cast<int*>(p.order));
     p.items = (p.T + kC - 1) / kC + p.N;  // upper bound on the number of chunks
   } else {
@@ -418,8 +423,6 @@ int launch_chunk_prep(const ChunkPrepParams& prm, int64_t B, int64_t K, hipStrea
                            (long long)p.HV);
     return GDN_ERR_UNSUPPORTED;
   }
-  // About four workgroups per CU (the LDS holds four), each walking an equal share of its value
-  // head's chunks with stride gridDim.x.
   // One wave per workgroup, about kPrepWavesPerCU per CU, each walking an equal share of its value
   // head's chunks with stride gridDim.x (waves past the last chunk return at once).
   static const int64_t wpc = [] {
