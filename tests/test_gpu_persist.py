@@ -5,9 +5,11 @@ sore/model/gdn.py:166-169) has at least four (sequence, value head) chains per g
 (groups = CUs / (V / 32); 64 on MI355X at V = 128), the state kernel runs one workgroup per CU and
 each group walks a job list of chains, its pipeline continuing from one chain into the next. These
 tests check it against the oracle (one-token documents, GVA, K/V 64 and 128, the in-kernel gate
-options, empty sequences through the C ABI) and, per document, bitwise against the same document run
-alone (one chain per workgroup: the non-persistent grid), since each chain's arithmetic is the same
-on both. A many-chain call with states takes the non-persistent grid and is checked against the
+options, empty sequences through the C ABI, fp16 overflow recovery, the reference's document lengths
+at full size, and both schedulers: LPT by rows of HV groups, and snake order for more than 128
+sequences or a head count that does not divide the group count) and, per document, bitwise against
+the same document run alone (one chain per workgroup: the non-persistent grid), since each chain's
+arithmetic is the same on both. A many-chain call with states takes the non-persistent grid and is checked against the
 oracle too. Tolerances: max-abs 2e-2 on bf16 outputs, relative L2 1e-3 on fp32 final states.
 """
 import pytest
@@ -159,3 +161,42 @@ def test_persistent_grid_recomputes_fp16_overflow():
     o_ref, _ = recurrent_gated_delta_rule(inp.q, inp.k, inp.v, inp.g, inp.beta, inp.scale, None, False, cu_seqlens=cu)
     assert_output_close((o.float().cpu() / big).to(torch.bfloat16), o_ref.float() / big, what="o / 1e5")
     assert not sorernn_amd.check_chunk_range()
+
+
+def test_persistent_grid_reference_document_lengths_full_size():
+    """The bench's real-distribution workload at full size (53 documents of the reference's corpus
+    lengths in 32,768 tokens, HV = 16: rows of 16 groups, scheduled with the row loads in scalar
+    registers), checked on the longest, a mid-length and the shortest document, two value heads each."""
+    import json
+    import os
+
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "doc_lengths_pt.json")
+    with open(path) as f:
+        lens = [n for w in json.load(f)["windows"] for n in w]
+    cu = _cu(lens)
+    print(f"persistent reference lengths: {len(lens)} docs, {int(cu[-1])} tokens", flush=True)
+    inp = gdn_inputs(1, int(cu[-1]), 16, 128, dtype=torch.bfloat16, seed=57, cu_seqlens=cu)
+    o, _ = _run(inp)
+    o = o.cpu()
+    heads = [0, 13]
+    srt = sorted(range(len(lens)), key=lambda i: lens[i])
+    for n in (srt[-1], srt[len(srt) // 2], srt[0]):
+        a, e = int(cu[n]), int(cu[n + 1])
+        sl = lambda x: x[:, a:e, heads]  # noqa: E731
+        o_ref, _ = recurrent_gated_delta_rule(sl(inp.q), sl(inp.k), sl(inp.v), sl(inp.g), sl(inp.beta), inp.scale,
+                                              None, False)
+        assert_output_close(o[:, a:e, heads], o_ref, what=f"o of document {n} ({lens[n]} tokens)")
+
+
+@pytest.mark.parametrize("shape", [(200, 1, 4), (100, 1, 3)], ids=["over_128_sequences", "hv3_snake"])
+def test_persistent_grid_snake_order(shape):
+    """Job lists in snake order: more sequences than the LPT scheduler takes (200 > 128), or a head
+    count that does not divide the group count (HV = 3, 64 groups); short documents, GVA."""
+    docs, h, hv = shape
+    lens = _lengths(docs, 1, 90, seed=docs + hv, extra=(1, 64, 65))
+    cu = _cu(lens)
+    print(f"persistent snake order: {docs} docs, HV={hv}, {int(cu[-1])} tokens", flush=True)
+    inp = gdn_inputs(1, int(cu[-1]), h, 128, HV=hv, dtype=torch.bfloat16, seed=58, cu_seqlens=cu)
+    o, _ = _run(inp)
+    o_ref, _ = recurrent_gated_delta_rule(inp.q, inp.k, inp.v, inp.g, inp.beta, inp.scale, None, False, cu_seqlens=cu)
+    assert_output_close(o.cpu(), o_ref)
