@@ -173,6 +173,11 @@ def _gdn_call(entry, name, q, k, v, g, beta, scale, initial_state, output_final_
             f"{name}: the backward exists for chunk_gated_delta_rule with bf16 q/k/v only (inputs "
             "require grad); run under torch.no_grad() or detach the inputs"
         )
+    q_raw, k_raw = q, k
+    if (entry == "gdn_chunk_fwd" and (flags & _lib.FLAG_QK_L2NORM) and not needs_grad
+            and _l2norm_first(q, n, hv, vd, b * t)):
+        q, k = (_l2norm_rows(x) for x in (q, k))
+        flags &= ~_lib.FLAG_QK_L2NORM
     if entry == "gdn_chunk_fwd":
         # the torch.library op (sorernn::chunk_gated_delta_rule_fwd): traceable by torch.compile, with
         # the backward registered on it; with grad it also keeps the per-chunk states for the backward.
@@ -193,9 +198,9 @@ def _gdn_call(entry, name, q, k, v, g, beta, scale, initial_state, output_final_
                     "operand of the chunk kernel past 65504 that its fp32 recomputation did not bring back into range)"
                     + ("; no fallback with grad: the backward needs the chunk forward" if needs_grad else ""))
             _range.note_fallback(name)
-            return _gdn_call("gdn_recurrent_fwd", name, q, k, v, g, beta, scale, initial_state, output_final_state,
-                             cu_seqlens, cu_seqlens_cpu, use_qk_l2norm_in_kernel, use_beta_sigmoid_in_kernel,
-                             use_gate_in_kernel, a_log_in, dt_bias_in)
+            return _gdn_call("gdn_recurrent_fwd", name, q_raw, k_raw, v, g, beta, scale, initial_state,
+                             output_final_state, cu_seqlens, cu_seqlens_cpu, use_qk_l2norm_in_kernel,
+                             use_beta_sigmoid_in_kernel, use_gate_in_kernel, a_log_in, dt_bias_in)
         return o, (final if output_final_state else None)
     q, k, v, g, beta = (x.contiguous() for x in (q, k, v, g, beta))
     h0 = None
@@ -324,6 +329,10 @@ def chunk_gated_delta_rule_gated_norm(
     if norm_weight.shape != (vd,):
         raise ValueError(f"{name}: norm_weight must be [{vd}] (got {tuple(norm_weight.shape)})")
     word = _range.before_call(q.device)
+    q_raw, k_raw = q, k
+    if (flags & _lib.FLAG_QK_L2NORM) and _l2norm_first(q, n, hv, vd, b * t):
+        q, k = (_l2norm_rows(x) for x in (q, k))
+        flags &= ~_lib.FLAG_QK_L2NORM
     q, k, v, g, beta, gate = (x.contiguous() for x in (q, k, v, g, beta, gate))
     w = norm_weight.float().contiguous()
     h0 = None if initial_state is None else initial_state.float().contiguous()
@@ -345,7 +354,7 @@ def chunk_gated_delta_rule_gated_norm(
             raise FloatingPointError(f"{name}: the fused chunked forward and norm stored inf or NaN outputs (non-finite "
                                      "inputs, or an fp16 operand of the chunk kernel past 65504)")
         _range.note_fallback(name)
-        o2, final = chunk_gated_delta_rule(q, k, v, g, beta, scale=scale, initial_state=initial_state,
+        o2, final = chunk_gated_delta_rule(q_raw, k_raw, v, g, beta, scale=scale, initial_state=initial_state,
                                            output_final_state=output_final_state,
                                            use_qk_l2norm_in_kernel=use_qk_l2norm_in_kernel,
                                            use_beta_sigmoid_in_kernel=use_beta_sigmoid_in_kernel,
@@ -555,6 +564,39 @@ def qkv_causal_conv1d(x: Tensor, weight: Tensor, qk_dim: int, v_dim: int, head_d
     _lib.call("gdn_qkv_conv_fwd", x.data_ptr(), stride, w.data_ptr(), None, q.data_ptr(), k.data_ptr(), v.data_ptr(),
               _lib.ptr(cu), b, t, qk_dim, v_dim, head_dim, n, _lib.dtype_code(x.dtype), act, flags, _lib.stream_of(x))
     return q, k, v
+
+
+_cu_count: dict = {}
+
+
+def _l2norm_first(q: Tensor, n: int, hv: int, vd: int, tokens: int) -> bool:
+    """Whether an inference call with use_qk_l2norm_in_kernel normalises q and k by the row kernel
+    before the chunk kernels (which then run without the flag) instead of inside them.
+
+    Inside, each of a chain's V/32 state-kernel workgroups normalises the chain's q/k rows on the
+    helper waves that set the step time, ~0.9 us more per chunk step. The row kernel instead costs a
+    pass over q and k (read and write) on the whole chip. That pays when the state kernel leaves
+    half the CUs or more idle and its chains are long. Measured per call (HIP events): B=2, T=8192,
+    16 heads of 128 (32 chains, 128 workgroups): 243 us against 310 us; B=4, T=4096 (256
+    workgroups): 180 us against 170 us, so the flag stays in the kernels there."""
+    dev = q.get_device()
+    cus = _cu_count.get(dev)
+    if cus is None:
+        cus = _cu_count[dev] = torch.cuda.get_device_properties(dev).multi_processor_count
+    return 2 * n * hv * max(1, vd // 32) <= cus and tokens >= 2048 * n
+
+
+def _l2norm_rows(x: Tensor, eps: float = 1e-12) -> Tensor:
+    """``l2norm`` without grad: plain eager calls go to the kernel directly (no dispatcher round trip)."""
+    if not _plain_eager(x):
+        return _library.l2norm_fwd(x, float(eps))
+    xc = x.contiguous()
+    y = torch.empty_like(xc)
+    d = xc.shape[-1]
+    if xc.numel():
+        _lib.call("gdn_l2norm_fwd", _lib.ptr(xc), _lib.ptr(y), xc.numel() // d, d, _lib.dtype_code(xc.dtype), float(eps),
+                  _lib.stream_of(xc))
+    return y
 
 
 def l2norm(x: Tensor, eps: float = 1e-12) -> Tensor:

@@ -10,7 +10,7 @@ import torch
 import torch.nn.functional as F
 
 from oracle import recurrent_gated_delta_rule
-from sorernn_amd import chunk_gated_delta_rule, fused_recurrent_gated_delta_rule
+from sorernn_amd import _lib, chunk_gated_delta_rule, fused_recurrent_gated_delta_rule
 from sorernn_amd.synthetic import config_inputs, gdn_inputs, varlen_cu_seqlens
 from tests.parity import assert_output_close, assert_state_close
 
@@ -90,6 +90,47 @@ def test_chunk_kernel_options_match_oracle():
     o_ref, st_ref = recurrent_gated_delta_rule(qn, kn, v, g_ref, b.float().sigmoid(), d**-0.5, None, True, cu_seqlens=cu)
     assert_output_close(o.cpu(), o_ref)
     assert_state_close(st.cpu(), st_ref)
+
+
+def test_chunk_kernel_in_kernel_l2norm_through_the_abi():
+    """The two q/k L2-norm routes of an inference call: inside the chunk kernels
+    (GDN_FLAG_QK_L2NORM through gdn_chunk_fwd, as C callers, the training forward and calls that
+    fill the chip use it), and the row kernel first with the flag cleared (the Python op's route for
+    few, long chains: here one 4096-token sequence, 16 workgroups). Both against the oracle, and
+    against each other within half the output bar (the routes sum the squares in a different order,
+    so a normalised element can differ by one bf16 step)."""
+    from sorernn_amd.ops import _l2norm_first, chunk_workspace_bytes
+
+    gen = torch.Generator().manual_seed(33)
+    t, h, hv, d = 4096, 2, 4, 128
+    q = (torch.randn(1, t, h, d, generator=gen) * 3).to(torch.bfloat16)
+    k = (torch.randn(1, t, h, d, generator=gen) * 3).to(torch.bfloat16)
+    v = torch.randn(1, t, hv, d, generator=gen).to(torch.bfloat16)
+    g = -F.softplus(torch.randn(1, t, hv, generator=gen))
+    beta = torch.rand(1, t, hv, generator=gen)
+    h0 = 0.02 * torch.randn(1, hv, d, d, generator=gen)
+    qd, kd_, vd_, gd, bd, h0d = (x.to(DEV) for x in (q, k, v, g, beta, h0))
+    assert _l2norm_first(qd, 1, hv, d, t), "this shape takes the row-kernel route"
+    assert not _l2norm_first(qd, 4, 16, 128, 4 * 4096), "config 1 keeps the flag in the kernels"
+    o = torch.empty(1, t, hv, d, device=DEV, dtype=torch.bfloat16)
+    st = torch.empty(1, hv, d, d, device=DEV)
+    nbytes = chunk_workspace_bytes(1, t, hv, 1, False)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
+    _lib.call("gdn_chunk_fwd", _lib.ptr(qd), _lib.ptr(kd_), _lib.ptr(vd_), _lib.ptr(gd), _lib.ptr(bd), _lib.ptr(h0d),
+              _lib.ptr(o), _lib.ptr(st), None, 1, t, h, hv, d, d, 1, _lib.DTYPE_BF16, _lib.DTYPE_F32, _lib.DTYPE_F32,
+              d**-0.5, _lib.FLAG_QK_L2NORM, None, None, _lib.ptr(ws), nbytes, _lib.stream_of(qd))
+    o_op, st_op = chunk_gated_delta_rule(qd, kd_, vd_, gd, bd, initial_state=h0d, output_final_state=True,
+                                         use_qk_l2norm_in_kernel=True)
+    torch.cuda.synchronize()
+    qn = F.normalize(q.float(), dim=-1).to(torch.bfloat16)
+    kn = F.normalize(k.float(), dim=-1).to(torch.bfloat16)
+    o_ref, st_ref = recurrent_gated_delta_rule(qn, kn, v, g, beta, d**-0.5, h0, True)
+    assert_output_close(o.cpu(), o_ref, what="o (in-kernel L2 norm)")
+    assert_state_close(st.cpu(), st_ref, what="final state (in-kernel L2 norm)")
+    assert_output_close(o_op.cpu(), o_ref, what="o (row-kernel L2 norm)")
+    assert_state_close(st_op.cpu(), st_ref, what="final state (row-kernel L2 norm)")
+    diff = (o.float() - o_op.float()).abs().max().item()
+    assert diff <= 1e-2, f"the two L2-norm routes differ by {diff:.3e}"
 
 
 def test_chunk_in_kernel_gate_bf16_config1_size():
