@@ -97,7 +97,12 @@ def chunk_bwd_flops(lengths, heads: int, d: int) -> int:
 
 
 def train_step_times(torch, inp, steps: int):
-    """(training forward ms, backward ms) of chunk_gated_delta_rule under autograd, HIP events per step."""
+    """(training forward ms, backward ms) of chunk_gated_delta_rule under autograd, HIP events per step.
+
+    The steps run back to back, one synchronisation after the last. The host then runs ahead of
+    the GPU, as in a training loop, and each event span is the GPU time of that forward or backward.
+    A synchronisation after every step would put the host's launch latency for the next forward
+    (the GPU idle until the first kernel arrives) into the forward's span."""
     from sorernn_amd import chunk_gated_delta_rule
 
     leaves = [x.detach().clone().requires_grad_(True) for x in (inp.q, inp.k, inp.v, inp.g, inp.beta, inp.h0)]
@@ -114,17 +119,17 @@ def train_step_times(torch, inp, steps: int):
     for _ in range(2):
         bwd(*fwd())
     settle(torch, lambda: bwd(*fwd()))
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
-    tf = tb = 0.0
-    for _ in range(steps):
-        ev[0].record()
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    for e in ev:
+        e[0].record()
         o, st = fwd()
-        ev[1].record()
+        e[1].record()
         bwd(o, st)
-        ev[2].record()
-        torch.cuda.synchronize()
-        tf += ev[0].elapsed_time(ev[1])
-        tb += ev[1].elapsed_time(ev[2])
+        e[2].record()
+    torch.cuda.synchronize()
+    tf = sum(e[0].elapsed_time(e[1]) for e in ev)
+    tb = sum(e[1].elapsed_time(e[2]) for e in ev)
     return tf / steps, tb / steps
 
 
