@@ -115,6 +115,36 @@ def test_fused_norm_config4_size():
     assert (diff <= y2.float().abs() * 2.0 ** -7 + 1e-3).all(), f"max diff {diff.max().item():.3e}"
 
 
+def test_fused_norm_l2norm_on_few_long_chains():
+    """use_qk_l2norm_in_kernel on a few-chain call (one 4096-token sequence, 4 value heads): the op
+    normalises q and k with the row kernel first and runs the fused kernel without the flag. Against
+    the oracle (F.normalize then the rule and the norm) and the two-op route on the same raw q/k."""
+    from sorernn_amd.ops import _l2norm_first
+
+    gen = torch.Generator().manual_seed(41)
+    t, h, hv, dd = 4096, 2, 4, 128
+    q = (torch.randn(1, t, h, dd, generator=gen) * 3).to(torch.bfloat16)
+    k = (torch.randn(1, t, h, dd, generator=gen) * 3).to(torch.bfloat16)
+    v = torch.randn(1, t, hv, dd, generator=gen).to(torch.bfloat16)
+    g = -F.softplus(torch.randn(1, t, hv, generator=gen))
+    beta = torch.rand(1, t, hv, generator=gen)
+    gate, w = _gate_weight(v.shape, dd, 42)
+    d = [x.to(DEV) for x in (q, k, v, g, beta, gate, w)]
+    assert _l2norm_first(d[0], 1, hv, dd, t)
+    y, _ = chunk_gated_delta_rule_gated_norm(d[0], d[1], d[2], d[3], d[4], d[5], d[6], EPS, scale=dd**-0.5,
+                                             use_qk_l2norm_in_kernel=True)
+    o, _ = chunk_gated_delta_rule(d[0], d[1], d[2], d[3], d[4], scale=dd**-0.5, use_qk_l2norm_in_kernel=True)
+    y2 = gpu_rms_norm_gated(o, d[5], d[6], None, activation="swish", eps=EPS)
+    torch.cuda.synchronize()
+    diff = (y.float() - y2.float()).abs()
+    assert (diff <= y2.float().abs() * 2.0 ** -7 + 1e-3).all(), f"fused vs two-op max diff {diff.max().item():.3e}"
+    qn = F.normalize(q.float(), dim=-1).to(torch.bfloat16)
+    kn = F.normalize(k.float(), dim=-1).to(torch.bfloat16)
+    o_ref, _ = recurrent_gated_delta_rule(qn, kn, v, g, beta, dd**-0.5, None, False)
+    ref = rms_norm_gated(o_ref, gate, w, EPS)
+    assert_output_close(y.cpu(), ref, tol=2e-2 * float(ref.abs().max()))
+
+
 def test_fused_norm_rejects_grad():
     inp = gdn_inputs(1, 64, 2, 128, dtype=torch.bfloat16, seed=51)
     d = inp.to(DEV)
