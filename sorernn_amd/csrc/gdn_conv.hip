@@ -6,6 +6,8 @@
 // One thread per channel walks TT consecutive tokens with the last W-1 inputs in registers; a
 // wave covers 64 consecutive channels, so every load and store of a token row is coalesced.
 
+#include <type_traits>
+
 #include "gdn_common.h"
 
 namespace gdn {
@@ -201,11 +203,13 @@ __global__ __launch_bounds__(256) void gated_delta_conv1d_v8_kernel(ConvParams p
 // The GDN layer's whole q/k/v prologue in one pass (inference): the packed projection output
 // x [B, T, >= 2*Cqk + Cv] (row stride x_stride, e.g. the q|k|v columns of one fused GEMM output)
 // -> depthwise causal conv (width 4) + SiLU, rounded to the activation dtype as the separate conv
-// stores it, then, with l2, each q and k head of D channels L2-normalised (F.normalize, eps 1e-12,
-// fp32 math, rounded again) -> contiguous q, k [B, T, Cqk] and v [B, T, Cv]. The normalised q/k
-// follow the same formulas as the separate conv followed by the chunk kernels' in-kernel norm.
+// stores it, then, with l2, each q and k head of D channels L2-normalised (x / max(|x|, 1e-12) as
+// v_rsq_f32 of max(|x|^2, 1e-24), the chunk kernels' in-kernel formula; fp32 math, rounded again)
+// -> contiguous q, k [B, T, Cqk] and v [B, T, Cv].
 // Thread = 8 channels as in gated_delta_conv1d_v8_kernel; a head of D channels is D/8 consecutive
 // lanes, so its sum of squares is a DPP group sum. No conv caches (the layer's forward uses none).
+// The activation and the varlen document walk are template parameters, so the unrolled row loop has
+// no branches on them (with the reciprocal square root: 110 -> 104 us at config 4's shape).
 struct QkvConvParams {
   const void* x;
   int64_t x_stride;
@@ -218,7 +222,7 @@ struct QkvConvParams {
   int act, l2;
 };
 
-template <typename E, int D>
+template <typename E, int D, int ACT, bool VARLEN>
 __global__ __launch_bounds__(256) void gated_delta_qkv_conv1d_kernel(QkvConvParams p) {
   constexpr int W = 4;
   typedef E V8 __attribute__((ext_vector_type(8)));
@@ -253,7 +257,7 @@ __global__ __launch_bounds__(256) void gated_delta_qkv_conv1d_kernel(QkvConvPara
     bias[e] = p.bias ? p.bias[cc + e] : 0.f;
   }
   int64_t d = 0, ds = 0, de = p.T;
-  if (p.cu) {
+  if (VARLEN) {
     int64_t lo = 0, hi = p.N - 1;  // largest d with cu[d] <= t0
     while (lo < hi) {
       const int64_t mid = (lo + hi + 1) / 2;
@@ -288,7 +292,7 @@ __global__ __launch_bounds__(256) void gated_delta_qkv_conv1d_kernel(QkvConvPara
     for (int g = 0; g < 8; ++g) {
       const int64_t t = tg + g;
       if (t >= t1) break;  // uniform: t1 is the same for the whole block
-      while (t >= de) {  // next document: the window restarts from zeros
+      while (VARLEN && t >= de) {  // next document: the window restarts from zeros
         ++d;
         ds = de;
         de = load_index(p.cu, p.cu_i32, d + 1);
@@ -304,10 +308,10 @@ __global__ __launch_bounds__(256) void gated_delta_qkv_conv1d_kernel(QkvConvPara
         float acc = bias[e] + w[e][W - 1] * xt;
 #pragma unroll
         for (int i = 0; i < W - 1; ++i) acc += w[e][i] * win[i][e];
-        if (p.act == GDN_ACT_SILU) acc = silu_fast(acc);
+        if (ACT == GDN_ACT_SILU) acc = silu_fast(acc);
         // the reference's unfused route (sore/model/gdn.py:208-209): the conv output is rounded to the
         // activation dtype before F.silu
-        else if (p.act == GDN_ACT_SILU_ROUNDED) acc = silu_fast((float)(E)acc);
+        else if (ACT == GDN_ACT_SILU_ROUNDED) acc = silu_fast((float)(E)acc);
         y[e] = (float)(E)acc;  // the separate conv's stored value
         ss += y[e] * y[e];
 #pragma unroll
@@ -315,7 +319,7 @@ __global__ __launch_bounds__(256) void gated_delta_qkv_conv1d_kernel(QkvConvPara
         win[W - 2][e] = xt;
       }
       ss = group_sum<D / 8>(ss);
-      const float inv = norm ? 1.f / fmaxf(sqrtf(ss), 1e-12f) : 1.f;
+      const float inv = norm ? __builtin_amdgcn_rsqf(fmaxf(ss, 1e-24f)) : 1.f;
       V8 yv;
 #pragma unroll
       for (int e = 0; e < 8; ++e) yv[e] = (E)(norm ? y[e] * inv : y[e]);
@@ -628,12 +632,26 @@ extern "C" int gdn_qkv_conv_fwd(const void* x, int64_t x_row_stride, const float
   const int64_t threads = (2 * Cqk + Cv) / 8;
   const dim3 grid((unsigned)((threads + 255) / 256), (unsigned)tb, (unsigned)B), block(256);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (x_dtype == GDN_DTYPE_BF16) {
-    if (head_dim == 128) hipLaunchKernelGGL((gated_delta_qkv_conv1d_kernel<bf16, 128>), grid, block, 0, s, p);
-    else hipLaunchKernelGGL((gated_delta_qkv_conv1d_kernel<bf16, 64>), grid, block, 0, s, p);
-  } else {
-    if (head_dim == 128) hipLaunchKernelGGL((gated_delta_qkv_conv1d_kernel<f16, 128>), grid, block, 0, s, p);
-    else hipLaunchKernelGGL((gated_delta_qkv_conv1d_kernel<f16, 64>), grid, block, 0, s, p);
-  }
+  // dtype, head dim, activation and varlen as template arguments
+  auto go = [&](auto e_tag, auto d_c, auto a_c, auto v_c) {
+    using E = decltype(e_tag);
+    hipLaunchKernelGGL((gated_delta_qkv_conv1d_kernel<E, decltype(d_c)::value, decltype(a_c)::value, decltype(v_c)::value>),
+                       grid, block, 0, s, p);
+  };
+  auto by_act = [&](auto e_tag, auto d_c, auto v_c) {
+    if (activation == GDN_ACT_SILU) go(e_tag, d_c, std::integral_constant<int, GDN_ACT_SILU>{}, v_c);
+    else if (activation == GDN_ACT_SILU_ROUNDED) go(e_tag, d_c, std::integral_constant<int, GDN_ACT_SILU_ROUNDED>{}, v_c);
+    else go(e_tag, d_c, std::integral_constant<int, GDN_ACT_NONE>{}, v_c);
+  };
+  auto by_var = [&](auto e_tag, auto d_c) {
+    if (cu_seqlens) by_act(e_tag, d_c, std::true_type{});
+    else by_act(e_tag, d_c, std::false_type{});
+  };
+  auto by_d = [&](auto e_tag) {
+    if (head_dim == 128) by_var(e_tag, std::integral_constant<int, 128>{});
+    else by_var(e_tag, std::integral_constant<int, 64>{});
+  };
+  if (x_dtype == GDN_DTYPE_BF16) by_d(bf16{});
+  else by_d(f16{});
   return gdn_internal_check_launch("gated_delta_qkv_conv1d_kernel");
 }

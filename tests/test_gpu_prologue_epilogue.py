@@ -112,8 +112,10 @@ def test_rms_norm_gated_matches_oracle(dtype, d):
 @pytest.mark.parametrize("cu", [None, [0, 1, 3, 40, 41, 200]], ids=["rows", "varlen"])
 def test_qkv_conv_equals_three_convs_and_l2norm(dtype, head_dim, cu):
     """The fused prologue (one launch over q | k | v read from a wider projection row) equals three
-    causal_conv1d calls followed by l2norm of every q/k head: the same fp32 formulas (the two kernels
-    may contract a multiply-add differently), so within two ulps and almost always equal."""
+    causal_conv1d calls followed by l2norm of every q/k head up to fp32 rounding: the conv and SiLU
+    are the same formulas (the kernels may contract a multiply-add differently), and the norm is
+    v_rsq_f32 of max(|x|^2, 1e-24) against the row kernel's 1 / max(sqrt(|x|^2), 1e-12). So the
+    outputs are within two ulps and almost always equal."""
     gen = torch.Generator().manual_seed(5)
     b = 2 if cu is None else 1
     t, cqk, cv = 200, 2 * head_dim, 4 * head_dim
