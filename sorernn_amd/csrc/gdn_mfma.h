@@ -135,14 +135,6 @@ __device__ __forceinline__ f16x4 to_f16x4(float a, float b, float c, float d) {
   return f16x4{static_cast<f16>(a), static_cast<f16>(b), static_cast<f16>(c), static_cast<f16>(d)};
 }
 
-// fp32 product step for a 16x16x16 tile, acc += A B, with lane (i, g) holding A[i][4g..4g+3] and
-// B[4g..4g+3][i]: four v_mfma_f32_16x16x4_f32, the m-th contracting the indices 4g + m.
-__device__ __forceinline__ f32x4 mma16f(const float (&a)[4], const float (&b)[4], f32x4 acc) {
-#pragma unroll
-  for (int m = 0; m < 4; ++m) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[m], b[m], acc, 0, 0, 0);
-  return acc;
-}
-
 // Per-token gate terms of one chunk: gam = in-chunk cumsum of g, egam = exp(gam), bet = beta,
 // begam = beta exp(gam), dlast = exp(gam_last - gam). Padding rows carry g = 0 and beta = 0.
 struct ChunkGates {
