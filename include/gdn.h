@@ -105,7 +105,11 @@ GDN_API size_t gdn_chunk_gated_norm_workspace_size(int64_t B, int64_t T, int64_t
 
 /*
  * Workspace bytes gdn_chunk_fwd needs for these sizes (varlen != 0 when cu_seqlens is passed);
- * 0 for invalid sizes. No counterpart in the reference: FLA allocates its intermediates itself.
+ * 0 for invalid sizes: 128 bytes per token-head, plus 8 bytes per sequence with cu_seqlens. While
+ * the environment variable SORERNN_PREFILL=coop selects the cooperative prefill, the size also
+ * covers its package ring (up to 8 x 47,360 bytes per sequence and value head); gdn_chunk_fwd reads
+ * the variable again, so size and call must see the same value. No counterpart in the reference:
+ * FLA allocates its intermediates itself.
  */
 GDN_API size_t gdn_chunk_workspace_size(int64_t B, int64_t T, int64_t HV, int64_t N, int varlen);
 
@@ -130,7 +134,8 @@ GDN_API int gdn_chunk_fwd_train(const void* q, const void* k, const void* v, con
  * it is for callers that cannot allocate device memory (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc). The workspace is a fixed array in the library's device
  * memory of gdn_chunk_fwd_noalloc_max_workspace() bytes (64 MiB + 64 KiB: up to 524,288 token-heads,
- * e.g. BASELINE config 1 or 3), held on every device the library runs on until the process ends.
+ * e.g. 4 x 4,096 or 32,768 tokens at 16 value heads, with the default prefill), held on every device
+ * the library runs on until the process ends.
  * Sizes needing more return GDN_ERR_INVALID. The stream's device must be the current device. Calls
  * on one device share the array: calls that overlap on one device race.
  */

@@ -1230,9 +1230,11 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
 
 using namespace gdn;
 
-// Workspace layouts: the two-kernel prefill (training forward, head dims other than 128) keeps the
-// T - I rows first, then the varlen index; the cooperative prefill keeps its package ring and sync
-// words first, then the varlen index. The size covers both.
+// Workspace layouts: the two-kernel prefill keeps the T - I rows first, then the varlen index; the
+// cooperative prefill keeps its package ring and sync words first, then the varlen index. The size
+// covers the ring only while SORERNN_PREFILL=coop selects that route: the ring is 8 slots of 47 KB per
+// (sequence, value head), which for many short sequences dwarfs the two-kernel prefill's 128 bytes per
+// token-head (6 GB against 0.2 GB for 1,000 sequences of 100 tokens at 16 heads).
 namespace {
 size_t index_bytes(int64_t N, int varlen) {
   return varlen ? (size_t)(align256((N + 1) * 4) + align256(N * 4)) : 0;
@@ -1240,11 +1242,17 @@ size_t index_bytes(int64_t N, int varlen) {
 size_t coop_front_bytes(int64_t T, int64_t HV, int64_t N) {
   return (size_t)(coop_ring_bytes(N * HV, T) + coop_sync_bytes(N * HV));
 }
+// The cooperative single-launch prefill, selected per call with SORERNN_PREFILL=coop.
+bool coop_selected() {
+  const char* const sel = getenv("SORERNN_PREFILL");
+  return sel && !strcmp(sel, "coop");
+}
 }  // namespace
 
 extern "C" size_t gdn_chunk_workspace_size(int64_t B, int64_t T, int64_t HV, int64_t N, int varlen) {
   if (B <= 0 || T < 0 || HV <= 0 || N <= 0) return 0;
-  const size_t front = std::max((size_t)chunk_t_bytes(B * T, HV), coop_front_bytes(T, HV, N));
+  size_t front = (size_t)chunk_t_bytes(B * T, HV);
+  if (coop_selected()) front = std::max(front, coop_front_bytes(T, HV, N));
   return front + index_bytes(N, varlen);
 }
 
@@ -1320,9 +1328,8 @@ int chunk_fwd_impl(const void* q, const void* k, const void* v, const void* g, c
                                                              : nullptr;
   // The cooperative single-launch prefill for K = V = 128 inference calls, selected per call with
   // SORERNN_PREFILL=coop (the two-kernel prefill otherwise, which is faster at every measured size).
-  const char* const sel = getenv("SORERNN_PREFILL");
-  const bool coop = sel && !strcmp(sel, "coop");
-  if (!chunk_states && !norm && K == 128 && V == 128 && coop) {
+  // The workspace check above used the size that includes its ring when it is selected.
+  if (!chunk_states && !norm && K == 128 && V == 128 && coop_selected()) {
     char* const ws = static_cast<char*>(workspace);
     const int64_t chains = N * HV;
     const size_t front = coop_front_bytes(T, HV, N);

@@ -14,6 +14,7 @@ without a graph break and ``make_fx`` records it as one node. The reference's pe
 ``sore/train/trainer.py:99-103``). Absent optional outputs are empty tensors; the public wrapper
 in ``ops.py`` turns them back into ``None``.
 """
+import os
 from typing import Optional
 
 import torch
@@ -30,12 +31,14 @@ def _align256(x):
 
 def fwd_workspace_bytes(b, t, hv, n, varlen: bool):
     """``gdn_chunk_workspace_size`` in Python arithmetic (symbolic sizes allowed under tracing): the
-    larger of the two-kernel prefill's T - I rows and the cooperative prefill's package ring (47,360
-    bytes per slot, min(8, ceil(T / 64)) slots per chain) with its sync words (72 per chain + 1), then
-    the varlen index arrays."""
-    slots = torch.sym_min(8, torch.sym_max(1, (t + C - 1) // C))
-    coop = _align256(n * hv * slots * 47360) + _align256((n * hv * 72 + 1) * 4)
-    nb = torch.sym_max(_align256(b * t * hv * C * 2), coop)
+    two-kernel prefill's T - I rows (the larger of those and the cooperative prefill's package ring,
+    47,360 bytes per slot, min(8, ceil(T / 64)) slots per chain, with its sync words, 72 per chain + 1,
+    while SORERNN_PREFILL=coop selects that route), then the varlen index arrays."""
+    nb = _align256(b * t * hv * C * 2)
+    if os.environ.get("SORERNN_PREFILL") == "coop":
+        slots = torch.sym_min(8, torch.sym_max(1, (t + C - 1) // C))
+        coop = _align256(n * hv * slots * 47360) + _align256((n * hv * 72 + 1) * 4)
+        nb = torch.sym_max(nb, coop)
     if varlen:
         nb = nb + _align256((n + 1) * 4) + _align256(n * 4)
     return nb

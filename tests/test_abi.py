@@ -71,15 +71,22 @@ def _coop_front(t, hv, n):
     return _align(n * hv * slots * 47360) + _align((n * hv * (8 + 8 * 8) + 1) * 4)
 
 
-def test_chunk_workspace_size_matches_layout():
-    """gdn_chunk_workspace_size: the larger of the two-kernel prefill's T - I rows (one 128-byte row per
-    token-head) and the cooperative prefill's package ring + sync words, plus the varlen index arrays
-    (chunk_first[N + 1] and order[N], int32, 256-byte aligned each); 0 for invalid sizes."""
+def test_chunk_workspace_size_matches_layout(monkeypatch):
+    """gdn_chunk_workspace_size: the two-kernel prefill's T - I rows (one 128-byte row per token-head),
+    or, while SORERNN_PREFILL=coop selects the cooperative prefill, the larger of those and its package
+    ring + sync words; plus the varlen index arrays (chunk_first[N + 1] and order[N], int32, 256-byte
+    aligned each); 0 for invalid sizes."""
     from sorernn_amd.ops import chunk_workspace_bytes
+    monkeypatch.delenv("SORERNN_PREFILL", raising=False)
+    assert chunk_workspace_bytes(4, 4096, 16, 4, False) == 4 * 4096 * 16 * 128
+    assert chunk_workspace_bytes(1, 32768, 16, 8, True) == 32768 * 16 * 128 + 512
+    # Many short documents: the ring would need 300 x 3 x 2 slots of 47,360 bytes, the rows only 38 KB.
+    assert chunk_workspace_bytes(1, 100, 3, 300, True) == _align(100 * 3 * 128) + 2560
+    assert chunk_workspace_bytes(0, 100, 3, 1, False) == 0
+    monkeypatch.setenv("SORERNN_PREFILL", "coop")
     assert chunk_workspace_bytes(4, 4096, 16, 4, False) == max(4 * 4096 * 16 * 128, _coop_front(4096, 16, 4))
     assert chunk_workspace_bytes(4, 4096, 16, 4, False) == 4 * 4096 * 16 * 128
     assert chunk_workspace_bytes(1, 32768, 16, 8, True) == max(32768 * 16 * 128, _coop_front(32768, 16, 8)) + 512
-    assert chunk_workspace_bytes(1, 100, 3, 300, True) == max(_align(100 * 3 * 128), _coop_front(100, 3, 300)) + 2560
     assert chunk_workspace_bytes(1, 100, 3, 300, True) == _coop_front(100, 3, 300) + 2560
     assert chunk_workspace_bytes(0, 100, 3, 1, False) == 0
 

@@ -6,6 +6,7 @@ registered autograd formulas, so a trace of the layer's forward and backward wit
 (no GPU needed: nothing runs) records them as ``sorernn::*`` nodes. The Python size formulas used
 by the fake implementations must equal the library's size functions.
 """
+import pytest
 import torch
 from torch.fx.experimental.proxy_tensor import make_fx
 
@@ -13,10 +14,18 @@ from sorernn_amd import _lib, library
 from sorernn_amd.gdn_layer import GatedDeltaNet, GDNLayerConfig
 
 
-def test_size_formulas_match_the_library():
+@pytest.mark.parametrize("prefill", [None, "coop"])
+def test_size_formulas_match_the_library(prefill, monkeypatch):
+    """Both with the default two-kernel prefill and with the cooperative prefill selected, whose ring
+    the forward workspace covers only then."""
+    if prefill is None:
+        monkeypatch.delenv("SORERNN_PREFILL", raising=False)
+    else:
+        monkeypatch.setenv("SORERNN_PREFILL", prefill)
     lib = _lib.load()
     for (b, t, hv, kd, vd, n, varlen) in [(4, 4096, 16, 128, 128, 4, False), (1, 100, 3, 64, 64, 5, True),
-                                          (2, 65, 2, 128, 64, 2, False), (1, 32768, 16, 128, 128, 8, True)]:
+                                          (2, 65, 2, 128, 64, 2, False), (1, 32768, 16, 128, 128, 8, True),
+                                          (1, 100, 3, 128, 128, 300, True)]:
         assert library.states_bytes(b, t, hv, kd, vd, n, varlen) == lib.gdn_chunk_states_size(b, t, hv, kd, vd, n, int(varlen))
         assert library.fwd_workspace_bytes(b, t, hv, n, varlen) == lib.gdn_chunk_workspace_size(b, t, hv, n, int(varlen))
         assert library.bwd_workspace_bytes(b, t, hv, kd, vd, n, varlen) == lib.gdn_chunk_bwd_workspace_size(

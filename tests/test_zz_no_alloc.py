@@ -54,18 +54,21 @@ def test_noalloc_matches_workspace_entry_varlen():
     _same(gdn_inputs(1, 1024, 2, 128, HV=4, dtype=torch.bfloat16, seed=9, h0=True, cu_seqlens=cu))
 
 
-def test_noalloc_matches_workspace_entry_persistent_grid():
+def test_noalloc_matches_workspace_entry_persistent_grid(monkeypatch):
     """Many documents, no initial or final state: both entries run the persistent state grid (the
     index kernel's order and chunk map in the scratch array); then the varlen call with states again.
-    64 documents of 1-7 tokens (256 in all, 256 chains at HV = 4): the workspace, which also sizes
-    the cooperative prefill's ring per (sequence, head), then fits the built-in array."""
+    1,000 documents of 1-100 tokens at HV = 8 (8,000 chains, ~400k token-heads): the default
+    prefill's workspace fits the built-in array, where the cooperative prefill's ring (counted only
+    when SORERNN_PREFILL=coop selects it) would not."""
     print("noalloc: persistent grid", flush=True)
+    monkeypatch.delenv("SORERNN_PREFILL", raising=False)
     gen = torch.Generator().manual_seed(12)
-    lens = torch.randint(1, 8, (64,), generator=gen).tolist()
+    lens = torch.randint(1, 101, (1000,), generator=gen).tolist()
     cu = torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist())
-    need = int(_lib.load().gdn_chunk_workspace_size(1, int(cu[-1]), 4, 64, 1))
-    assert need <= int(_lib.load().gdn_chunk_fwd_noalloc_max_workspace()), need
-    _same(gdn_inputs(1, int(cu[-1]), 2, 128, HV=4, dtype=torch.bfloat16, seed=13, cu_seqlens=cu), final_state=False)
+    lib = _lib.load()
+    need = int(lib.gdn_chunk_workspace_size(1, int(cu[-1]), 8, 1000, 1))
+    assert need <= int(lib.gdn_chunk_fwd_noalloc_max_workspace()), need
+    _same(gdn_inputs(1, int(cu[-1]), 2, 128, HV=8, dtype=torch.bfloat16, seed=13, cu_seqlens=cu), final_state=False)
     cu2 = torch.tensor([0, 1, 70, 200, 777, 1024])
     _same(gdn_inputs(1, 1024, 2, 128, HV=4, dtype=torch.bfloat16, seed=9, h0=True, cu_seqlens=cu2))
 
