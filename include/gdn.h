@@ -80,18 +80,20 @@ GDN_API int gdn_chunk_fwd(const void* q, const void* k, const void* v, const voi
                   void* stream);
 
 /*
- * gdn_chunk_fwd with the layer's gated RMSNorm applied to o as it is stored (inference only):
+ * gdn_chunk_fwd with the layer's gated RMSNorm applied to o in the same call (inference only):
  * o = rmsnorm(o_rule) * norm_weight * silu(gate) per (token, value head) over the V values, with
  * rmsnorm(x) = x / sqrt(mean(x^2) + norm_eps) of the rule's output rounded to bf16 -- what FLA
  * rms_norm_gated(o, gate, weight, None, activation="swish", eps) computes from chunk_gated_delta_rule's
- * o (sore/model/gdn.py:166-169 then 182-186), in fp32 with one rounding. norm_split != 0 rounds
- * like the reference's unfused route instead, o_norm(o) * F.silu(gate) (gdn.py:188): the norm
- * result and silu(gate) each rounded to bf16, then their product. gate [B, T, HV, V] bf16,
- * norm_weight [V] fp32. The rule's own o is not returned. The V / 32 column slices of a (sequence,
- * head) exchange their per-token sums of squares through the workspace (at least
- * gdn_chunk_gated_norm_workspace_size bytes), so all of them must be able to run at once: they
- * are dispatched next to each other, ahead of later sequences. A call whose outputs are not finite
- * sets the range flag (no fp32 recomputation on this path).
+ * o (sore/model/gdn.py:166-169 then 182-186), in fp32 with one rounding, with the arithmetic of
+ * gdn_rms_norm_gated_fwd. norm_split != 0 rounds like the reference's unfused route instead,
+ * o_norm(o) * F.silu(gate) (gdn.py:188): the norm result and silu(gate) each rounded to bf16, then
+ * their product. gate [B, T, HV, V] bf16, norm_weight [V] fp32. The rule's own o is not returned:
+ * the result is written over it in o. When the chunk kernel's V / 32 column slices leave at least two
+ * CUs per (sequence, head) free, workgroups of the same launch apply the norm to each 64-token
+ * tile once all its slices have stored it (progress words in the workspace, which must hold
+ * gdn_chunk_gated_norm_workspace_size bytes); a call whose outputs are not finite then sets the
+ * range flag (no fp32 recomputation on that route). Otherwise the norm kernel runs in place after
+ * the chunk kernel.
  */
 GDN_API int gdn_chunk_fwd_gated_norm(const void* q, const void* k, const void* v, const void* g, const void* beta,
                              const float* initial_state, void* o, float* final_state, const void* cu_seqlens,

@@ -73,5 +73,9 @@ int64_t coop_sync_bytes(int64_t chains);  // includes one error word after the c
 int launch_chunk_coop(const CoopArgs& a, hipStream_t s);
 // Zeroes `words` 32-bit words with a fill kernel (captured graphs clear them on every replay).
 int launch_fill_zero(unsigned* w, int64_t words, hipStream_t s);
+// Gated RMSNorm of bf16 rows (gdn_norm.hip): y = x rstd w silu(gate), or with split the norm and
+// silu(gate) rounded separately (o_norm(o) * F.silu(gate)); y may be x. Returns a GDN status.
+int gdn_internal_rms_norm_gated(const void* x, const void* gate, const float* w, void* y, int64_t rows, int64_t D,
+                                float eps, int split, hipStream_t s);
 
 }  // namespace gdn

@@ -71,17 +71,25 @@ struct ChunkParams {
   bf16* hs;                  // SAVE only: the state entering each chunk, bf16 [chunks][HV][V][K] (transposed)
   const int* chunk_first;    // SAVE with cu: chunks before each sequence
   unsigned* range_flag;      // set to 1 when a stored output is inf or NaN (null: no check)
-  // NORM only: the gated RMSNorm of O applied as it is stored (gdn_chunk_fwd_gated_norm)
+  // NORM only: the gated RMSNorm of O, applied by epilogue workgroups of the same launch
+  // (gdn_chunk_fwd_gated_norm)
   const bf16* gate;          // [tokens][HV][V], the layer's output gate
   const float* nw;           // [V] norm weight
   float neps;
   int nsplit;                // 1: the reference's separate rmsnorm and silu(gate) roundings
-  u32x2* npart;              // [chains][kNormSlots][V / 32][64] (sum of squares of a slice's columns, chunk + 1)
+  unsigned* prog;            // [chains][kProgStride]: chunks whose O each V / 32 slice has stored (zero at launch)
   int nq;                    // PERSIST only: groups of V / 32 workgroups
-  int pad_;
+  int nprod;                 // NORM only: workgroups that run the chains' slices (the rest: epilogue)
 };
 
-constexpr int kNormSlots = 8;  // chunks whose partial sums are in flight per chain
+// Cache policy bits of the buffer instructions (gfx950): sc1 = device scope, nt = non-temporal.
+constexpr int kPolSC1 = 16, kPolNT = 2;
+// s_waitcnt vmcnt(0) (gfx9 encoding, the other counters left at their maxima)
+constexpr int kWaitVm0 = 0x0F70;
+constexpr unsigned kEpiSpinMax = 1u << 21;  // NORM: polls of an epilogue workgroup before it gives up
+// NORM: 32-bit words between the progress words of consecutive chains (each chain's NVB words in a
+// 256-byte block of its own, so the epilogue workgroups' polls spread over memory channels)
+constexpr int kProgStride = 64;
 constexpr int kJobTab = 512;   // PERSIST: jobs per group held in LDS (the grid is used when no group needs more)
 
 // Running maximum, per 16-bit half, of the magnitude bits of the bf16 values in x: a half at or
@@ -381,6 +389,104 @@ __device__ __forceinline__ void schedule_group(const ChunkParams& p, int gq, int
 // pipeline fill and drain. At the last step of a job the state waves zero the state. (Storing and
 // loading states there, in each of the six unrolled steps, made the kernel's code larger than the
 // instruction cache two CUs share; calls with states keep one workgroup per slice.)
+// NORM: epilogue workgroup j of nw (placed after the chains' slices in the grid, on CUs the slices
+// leave free) applies the gated RMSNorm to O tiles of 64 tokens x V columns, in place:
+// y = o rstd w silu(gate), rstd = 1 / sqrt(mean(o^2) + eps) over the head's V values of the rounded
+// o, fp32 math and one rounding (FLA rms_norm_gated(o, gate, w, None, "swish", eps)); with nsplit
+// the norm and silu(gate) are each rounded to bf16 before their product, as o_norm(o) * F.silu(gate)
+// does. The arithmetic is the norm kernel's (gated_delta_norm_v8_kernel: a lane's 8 values, then
+// the row's lane group), so the outputs equal those of the chunk kernel followed by that kernel.
+// The host gives at least two epilogue workgroups per chain: R = nw / chains of them share a chain,
+// workgroup j taking the chunks j / chains, + R, + 2R, ... of chain j % chains (in the order the
+// slices store them). Wave 0 polls the chain's V / 32 progress words (device-scope loads, a sleep
+// of ~2k cycles between polls) until they pass the chunk, and a barrier releases the workgroup's
+// eight waves, each of which handles its own rows of the tile. The polls are what the slices feel
+// of the epilogue: at config 4, one polling wave per workgroup and a few polls per chunk keep the
+// call at 206 us against 186 us for the chunk kernel alone (559 us with every wave polling every
+// ~100 cycles, the polls queueing on the memory channel that held the words). The gate loads and
+// y stores are non-temporal, leaving L2 to the slices' tiles. A wait that runs out sets the range
+// flag, and the workgroup stops waiting.
+template <int VD>
+__device__ void norm_epilogue(const ChunkParams& p, int j, int nw) {
+  constexpr int NVB = VD / kVB, LPR = VD / 8, RPW = kWave / LPR, NWV = kNT / kWave, U = kC / (RPW * NWV);
+  static_assert(U * RPW * NWV == kC, "a tile's rows divide among the waves");
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, sub = lane / LPR, li = lane % LPR;
+  const int64_t chains = p.N * p.HV, R = nw / chains;
+  if (R < 1 || j >= R * chains) return;
+  const int64_t ch = j % chains, n = ch / p.HV, hv = ch % p.HV;
+  int64_t bos, eos;
+  if (p.cu) {
+    bos = load_index(p.cu, p.cu_i32, n);
+    eos = load_index(p.cu, p.cu_i32, n + 1);
+  } else {
+    bos = n * p.T;
+    eos = bos + p.T;
+  }
+  float wv[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) wv[e] = p.nw[li * 8 + e];
+  const uint32_t vrow = (uint32_t)(p.HV * VD * 2);
+  bf16* const og = static_cast<bf16*>(p.o);
+  // lanes 0..NVB-1 of wave 0 read the slices' words; the other lanes' offsets are past the resource
+  const auto rp = make_rsrc(p.prog + ch * kProgStride, NVB * 4);
+  bool dead = false;  // wave 0: a wait ran out
+  for (int64_t c = j / chains; bos + c * kC < eos; c += R) {
+    const int64_t c0 = bos + c * kC;
+    const uint32_t len = (uint32_t)min<int64_t>(kC, eos - c0);
+    if (w == 0) {
+      unsigned spins = 0;
+      while (!dead) {
+        const unsigned got = __builtin_amdgcn_raw_buffer_load_b32(rp, lane * 4, 0, kPolSC1);
+        if (__builtin_amdgcn_ballot_w64(lane < NVB && got < (unsigned)(c + 1)) == 0) break;
+        if (++spins >= kEpiSpinMax) {
+          dead = true;
+          if (lane == 0 && p.range_flag) flag_nonfinite(p.range_flag, true);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(32);
+      }
+    }
+    __syncthreads();  // the tile is stored (or wave 0 gave up)
+    // O rows through device-scope loads (written through by the slices on any XCD); rows past
+    // len read as zeros and their stores are dropped (buffer range)
+    const auto ro = make_rsrc(og + (c0 * p.HV + hv) * VD, len * vrow);
+    const auto rg = make_rsrc(p.gate + (c0 * p.HV + hv) * VD, len * vrow);
+    u32x4 xo[U], xg[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int row = (u * NWV + w) * RPW + sub;
+      xo[u] = __builtin_amdgcn_raw_buffer_load_b128(ro, (int)((uint32_t)row * vrow + li * 16), 0, kPolSC1);
+      xg[u] = __builtin_amdgcn_raw_buffer_load_b128(rg, (int)((uint32_t)row * vrow + li * 16), 0, kPolNT);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int row = (u * NWV + w) * RPW + sub;
+      const bf16x8 xv = __builtin_bit_cast(bf16x8, xo[u]), gvv = __builtin_bit_cast(bf16x8, xg[u]);
+      float xf[8], ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        xf[e] = (float)xv[e];
+        ss += xf[e] * xf[e];
+      }
+      ss = group_sum<LPR>(ss);
+      const float scale = __builtin_amdgcn_rsqf(ss / (float)VD + p.neps);
+      bf16x8 y;
+      if (p.nsplit) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float y1 = (float)static_cast<bf16>(xf[e] * scale * wv[e]);
+          y[e] = static_cast<bf16>(y1 * (float)static_cast<bf16>(silu_fast((float)gvv[e])));
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) y[e] = static_cast<bf16>(xf[e] * scale * wv[e] * silu_fast((float)gvv[e]));
+      }
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, y), ro, (int)((uint32_t)row * vrow + li * 16), 0,
+                                             kPolNT);
+    }
+  }
+}
+
 template <int KD, int VD, bool SAVE, bool NORM = false, bool PERSIST = false>
 __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p) {
   static_assert(!(SAVE && NORM), "the fused norm is an inference epilogue");
@@ -402,9 +508,8 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
   __shared__ __align__(16) f16 Tb[2][kC * kC];    // T - I of chunk c in slot c % 2 (tok_col columns, tp_off)
   __shared__ __align__(16) f16 Pb[2][kC * kC];    // scale * P of chunk c in slot c % 2 (tok_col columns, tp_off)
   __shared__ __align__(16) bf16 Vc[2][kC * kVB];  // V slice of chunk c in slot c % 2 (vo_off)
-  // O of chunk c, stored to HBM during chunk c + 1 (slot c % 2), or with NORM during chunk c + 4 (slot c % 6)
-  __shared__ __align__(16) bf16 Ob[NORM ? 6 : 2][kC * kVB];
-  __shared__ float psum[NORM ? 2 : 1][2][kC];     // NORM: per-token sums of squares of each state wave's O
+  // O of chunk c, stored to HBM during chunk c + 1 (slot c % 2)
+  __shared__ __align__(16) bf16 Ob[2][kC * kVB];
   __shared__ __align__(16) ChunkGates gv[3];      // gate terms of chunk c in slot c % 3
   __shared__ int bad;                              // an O or final-state element of this slice is inf / NaN
   __shared__ int4 jtab[PERSIST ? kJobTab : 1];     // PERSIST: the group's job list (bos, eos, sequence, head)
@@ -412,6 +517,12 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
 
   // w is read back as a scalar: the compiler then treats the role branches as wave-uniform
   const int t = threadIdx.x, lane = t & 63, w = __builtin_amdgcn_readfirstlane(t >> 6), g4 = lane >> 4, li = lane & 15;
+  if constexpr (NORM) {
+    if ((int)blockIdx.x >= p.nprod) {
+      norm_epilogue<VD>(p, (int)blockIdx.x - p.nprod, (int)gridDim.x - p.nprod);
+      return;
+    }
+  }
 
   // q/k tile addressing (element offsets): the swizzle of row r, the column of the row fragment for
   // key step s (lane row li, lane group g: keys 32s + 8g..+7), and the transposed K^T fragment of
@@ -604,6 +715,8 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
   // O rows go out as non-temporal stores in the inference kernel: streamed past the caches, they
   // leave L2 to the q/k/T/V tiles that the slices of a chain share (config-1 call 130.3 -> 125.2 us,
   // same-box A/B). The training kernel keeps cached stores (non-temporal ones measured slower there).
+  // With NORM they are also written through to memory (device scope), where the epilogue
+  // workgroups, on any XCD, read them.
   auto store_o = [&](int slot, const ChunkAt& a, int tq, u16x2& om) {
     const auto ro = make_rsrc(og + (a.c0 * p.HV + a.hv) * VD + vb * kVB, a.len * v_row);
     const int row = tq >> 2, c8 = tq & 3;
@@ -612,92 +725,17 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
       const bf16x8 x = *reinterpret_cast<const bf16x8*>(&Ob[slot][vo_off(row + 32 * u, c8 * 8)]);
       om = bf16_mag_max(om, x);
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), ro,
-                                             (int)((uint32_t)(row + 32 * u) * v_row + c8 * 16), 0, SAVE ? 0 : 2);
+                                             (int)((uint32_t)(row + 32 * u) * v_row + c8 * 16), 0,
+                                             SAVE ? 0 : NORM ? kPolSC1 | kPolNT : kPolNT);
     }
   };
 
-  // NORM: the slice's per-token sums of squares of chunk c (its two state waves' halves, from psum)
-  // go to the chain's exchange slot during step c + 1 as 8-byte (sum, c + 1) pairs, one store per
-  // token (wave 5); every slice loads the pairs of its rows in step c + 3 and checks in step c + 4
-  // that each carries c + 1 (loading again, boundedly, where one does not yet), so no counter and no
-  // wait sit between the slices. The slices of a chain may sit on different XCDs: the pairs are
-  // written through to memory and read with device-scope loads.
-  const int64_t nslot0 = k_rank * kNormSlots;
-  const auto rnp = make_rsrc(p.npart + nslot0 * NVB * kC, (uint32_t)(kNormSlots * NVB * kC * 8));
-  auto publish_sums = [&](int c) {
-    const float v = psum[c & 1][0][lane] + psum[c & 1][1][lane];
-    const u32x2 pr = {__float_as_uint(v), (unsigned)(c + 1)};
-    __builtin_amdgcn_raw_buffer_store_b64(pr, rnp, (int)((((c % kNormSlots) * NVB + vb) * kC + lane) * 8), 0, 16);
-  };
-  // the pairs of rows tq / 4 and tq / 4 + 32 of chunk c from every slice (device-scope loads)
-  auto load_sums = [&](int c, int tq, u32x2 (&ps)[2][NVB]) {
-    const int row = tq >> 2;
-#pragma unroll
-    for (int u = 0; u < 2; ++u)
-#pragma unroll
-      for (int sl = 0; sl < NVB; ++sl)
-        ps[u][sl] = __builtin_amdgcn_raw_buffer_load_b64(rnp, (int)((((c % kNormSlots) * NVB + sl) * kC + row + 32 * u) * 8),
-                                                        0, 16);
-  };
-  // NORM: the gate rows of chunk c this thread stores (rows tq / 4 and tq / 4 + 32, chunk tq % 4)
-  auto load_gate = [&](int c, int tq, bf16x8 (&pg)[2]) {
-    const int64_t c0 = bos + (int64_t)c * kC;
-    const auto rg = make_rsrc(p.gate + (c0 * p.HV + hv) * VD + vb * kVB, (uint32_t)chunk_len(c) * v_row);
-    const int row = tq >> 2, c8 = tq & 3;
-#pragma unroll
-    for (int u = 0; u < 2; ++u) pg[u] = buf_load16(rg, (uint32_t)(row + 32 * u) * v_row + c8 * 16);
-  };
-  // NORM: O of chunk c normalised and gated as it is stored, once every slice of the chain has
-  // published its sums: y = o rstd w silu(gate), rstd = 1 / sqrt(mean(o^2) + eps) over the head's
-  // V columns of the rounded o, fp32 math and one rounding (FLA rms_norm_gated(o, gate, w, None,
-  // "swish", eps)); with nsplit, rmsnorm and the gate product rounded separately, as
-  // o_norm(o) * F.silu(gate) does. A wait that runs out marks the output with the range flag.
-  // the silu uses v_exp / v_rcp (silu_fast, relative error ~1e-7, far below the bf16 rounding that
-  // follows) and the weights of the thread's 8 columns are read once per call
-  auto store_o_norm = [&](int c, int tq, u16x2& om, const bf16x8 (&pg)[2], u32x2 (&ps)[2][NVB]) {
-    unsigned spins = 0;
-    while (true) {
-      bool ready = true;
-#pragma unroll
-      for (int u = 0; u < 2; ++u)
-#pragma unroll
-        for (int sl = 0; sl < NVB; ++sl) ready = ready && ps[u][sl][1] == (unsigned)(c + 1);
-      if (__builtin_amdgcn_ballot_w64(!ready) == 0) break;
-      if (++spins >= (1u << 22)) {
-        if (p.range_flag) flag_nonfinite(p.range_flag, true);
-        break;
-      }
-      __builtin_amdgcn_s_sleep(2);
-      load_sums(c, tq, ps);
-    }
-    const int64_t c0 = bos + (int64_t)c * kC;
-    const auto ro = make_rsrc(og + (c0 * p.HV + hv) * VD + vb * kVB, (uint32_t)chunk_len(c) * v_row);
-    const int row = tq >> 2, c8 = tq & 3;
-    float wv[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) wv[e] = p.nw[vb * kVB + c8 * 8 + e];
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int r = row + 32 * u;
-      float ssum = 0.f;
-#pragma unroll
-      for (int sl = 0; sl < NVB; ++sl) ssum += __uint_as_float(ps[u][sl][0]);
-      const float rstd = __builtin_amdgcn_rsqf(ssum * (1.f / (float)VD) + p.neps);
-      const bf16x8 x = *reinterpret_cast<const bf16x8*>(&Ob[c % 6][vo_off(r, c8 * 8)]);
-      bf16x8 y;
-      if (p.nsplit) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float y1 = (float)static_cast<bf16>((float)x[e] * rstd * wv[e]);
-          y[e] = static_cast<bf16>(y1 * (float)static_cast<bf16>(silu_fast((float)pg[u][e])));
-        }
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) y[e] = static_cast<bf16>((float)x[e] * rstd * wv[e] * silu_fast((float)pg[u][e]));
-      }
-      om = bf16_mag_max(om, y);
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, y), ro, (int)((uint32_t)r * v_row + c8 * 16), 0, 2);
-    }
+  // NORM: the slice's progress word, the number of chunks whose O rows it has stored, written
+  // through to memory once every storing thread has waited for those stores (s_waitcnt before a
+  // barrier): an epilogue workgroup that reads the word with a device-scope load then sees the rows.
+  auto publish_o = [&](int count) {
+    const auto rp = make_rsrc(p.prog + (n * p.HV + hv) * kProgStride, NVB * 4);
+    __builtin_amdgcn_raw_buffer_store_b32((unsigned)count, rp, vb * 4, 0, kPolSC1);
   };
 
   // scale * P^T of chunk c for key-row tiles JA..JA+JN-1 and query-row tiles TA..TA+TN-1 (tiles
@@ -870,7 +908,7 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
       const f16* tp = Tb[PH & 1];
       const bf16* vp = Vc[PH & 1];
       const f16* pp = Pb[PH & 1];
-      bf16* op = Ob[NORM ? PH : PH & 1];
+      bf16* op = Ob[PH & 1];
       const ChunkGates& G = gv[PH % 3];
 
       // The chain S -> Y -> X -> Delta -> Delta~ -> S' runs through phases 6 (Y of the next chunk,
@@ -1011,18 +1049,6 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
         if (tb >= 2) o = mmah(db1, pf[tb + 2], o);
         const bf16x4 ob = to_bf16x4(o[0], o[1], o[2], o[3]);
         *reinterpret_cast<bf16x4*>(op + vo_off(16 * tb + li, 16 * sw + 4 * g4)) = ob;
-        if constexpr (NORM) {
-          // the sum of squares of token 16 tb + i over the wave's 16 columns, from the rounded O the
-          // reference's norm reads: lanes i, i + 16, i + 32, i + 48 hold its four column groups
-          float ss = 0.f;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) ss += (float)ob[r] * (float)ob[r];
-          const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(ss), __float_as_uint(ss), false, false);
-          ss = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-          const auto b2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(ss), __float_as_uint(ss), false, false);
-          ss = __uint_as_float(b2[0]) + __uint_as_float(b2[1]);
-          if (g4 == 0) psum[PH & 1][sw][16 * tb + li] = ss;
-        }
       }
       f16x8 kfb[KS - KSH][4];
 #pragma unroll
@@ -1146,46 +1172,27 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
     }
     __syncthreads();
     __syncthreads();
-    bf16x8 pgt[2];      // NORM: gate rows of the chunk whose O goes out next step
-    u32x2 pss[2][NVB];  // NORM: (sum, chunk + 1) pairs of those rows from every slice
     for (int i = 0; i < nc; ++i) {  // gates of chunk i+2, O of chunk i-1 out, T/V of chunk i+1 into LDS, loads of chunk i+2
+      if constexpr (NORM) {
+        // this thread's O stores of chunk i - 2 (issued last step, with the loads this step stages)
+        // have completed; every storing thread's stores of chunk i - 3 completed before the
+        // previous step's barrier, so chunks 0 .. i - 3 are published
+        __builtin_amdgcn_s_waitcnt(kWaitVm0);
+        if (w == 5 && lane == 0 && i >= 3) publish_o(i - 2);
+      }
       const int tq = thv_of(opaque_int(lane));
       const ChunkAt a2 = src(ct, i + 2);  // the chunk whose gates are staged and T/V loaded this step
       if (w == 4) {  // gates of chunk i+2 (loaded a step ago), then the loads for chunk i+3
         stage_gates((i + 2) % 3, a2, ngate);
         fetch_gates(src(cgf, i + 3), ngate);
       }
-      if constexpr (NORM) {  // sums of chunk i-1 out, O of chunk i-4 out
-        if (w == 5 && i >= 1) publish_sums(i - 1);
-        if (i >= 4) store_o_norm(i - 4, tq, om, pgt, pss);
-      } else {
-        if (i > 0) store_o((i - 1) & 1, src(co, i - 1), tq, om);
-      }
+      if (i > 0) store_o((i - 1) & 1, src(co, i - 1), tq, om);
       stage_tv(pt, pv, (i + 1) & 1, tq);
       fetch_tv(pt, pv, a2, tq);
-      if constexpr (NORM) {
-        // gates and sums of chunk i-3, issued after the T/V loads: loads complete in order, and the
-        // next step's T/V staging then does not wait for these slower device-scope loads
-        if (i >= 3) {
-          load_gate(i - 3, tq, pgt);
-          load_sums(i - 3, tq, pss);
-        }
-      }
       __syncthreads();
     }
-    if constexpr (NORM) {
-      // the pipeline's last four steps, without the state waves (no barrier)
-      for (int i = nc; i < nc + 4; ++i) {
-        if (w == 5 && i >= 1 && i - 1 < nc) publish_sums(i - 1);
-        if (i >= 4 && i - 4 < nc) store_o_norm(i - 4, thv, om, pgt, pss);
-        if (i >= 3 && i - 3 < nc) {
-          load_gate(i - 3, thv, pgt);
-          load_sums(i - 3, thv, pss);
-        }
-      }
-    } else {
-      if (nc > 0) store_o((nc - 1) & 1, src(co, nc - 1), thv, om);
-    }
+    if (nc > 0) store_o((nc - 1) & 1, src(co, nc - 1), thv, om);
+    if constexpr (NORM) __builtin_amdgcn_s_waitcnt(kWaitVm0);  // before the barrier ahead of the last word
     if (om[0] >= 0x7f80 || om[1] >= 0x7f80) __hip_atomic_fetch_or(&bad, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
 
@@ -1196,9 +1203,12 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
   // (value columns of the state evolve independently), overwriting O, the final state and (SAVE)
   // the saved chunk states, and flags the call only if that recomputation is non-finite as well
   // (non-finite inputs). Slices that stored finite values skip it: the cost is this barrier.
-  // The fused-norm variant has no recomputation (the sums of every slice of the chain enter each
-  // slice's outputs): it reports the call through the range flag.
+  // The fused-norm variant has no recomputation (the epilogue workgroups may already have read the
+  // slice's O): it publishes its last chunks and reports the call through the range flag.
   __syncthreads();
+  if constexpr (NORM) {
+    if (t == 5 * kWave) publish_o(nc);
+  }
   if (__builtin_amdgcn_readfirstlane(bad)) {
     if constexpr (NORM) {
       const ChunkParams pr = reload_params();
@@ -1272,9 +1282,13 @@ int stream_device(hipStream_t stream) {
   return dev;
 }
 
-// The fused-norm exchange area (after the chunk workspace): per chain, kNormSlots slots of the V / 32
-// slices' 64 per-token sums, then the slots' arrival counters.
-size_t norm_part_bytes(int64_t N, int64_t HV, int64_t V) { return (size_t)align256(N * HV * kNormSlots * (V / kVB) * kC * 8); }
+// The fused norm's progress words (after the chunk workspace): one per chain and V / 32 slice, in a
+// 256-byte block per chain.
+size_t norm_prog_bytes(int64_t N, int64_t HV, int64_t V) {
+  static_assert(128 / kVB <= kProgStride, "a chain's words fit its block");
+  (void)V;
+  return (size_t)align256(N * HV * kProgStride * 4);
+}
 
 int chunk_fwd_impl(const void* q, const void* k, const void* v, const void* g, const void* beta,
                    const float* initial_state, void* o, float* final_state, const void* cu_seqlens, int64_t B,
@@ -1314,7 +1328,7 @@ int chunk_fwd_impl(const void* q, const void* k, const void* v, const void* g, c
     return GDN_ERR_INVALID;
   }
   const size_t base_need = gdn_chunk_workspace_size(B, T, HV, N, cu_seqlens != nullptr);
-  const size_t need = norm && base_need ? base_need + norm_part_bytes(N, HV, V) : base_need;
+  const size_t need = norm && base_need ? base_need + norm_prog_bytes(N, HV, V) : base_need;
   if (need > 0 && (!workspace || workspace_bytes < need)) {
     gdn_internal_set_error("gdn_chunk_fwd: workspace of %zu bytes needed (got %zu)", need,
                            workspace ? workspace_bytes : (size_t)0);
@@ -1357,7 +1371,12 @@ int chunk_fwd_impl(const void* q, const void* k, const void* v, const void* g, c
   // slice, dispatched longest first: there the longest sequence sets the time.
   const int64_t cus = device_compute_units(s);
   const int64_t nq = cus / nvb;
-  const bool persist = cu_seqlens && !chunk_states && !norm && !initial_state && !final_state && N <= kOrderMax &&
+  // The fused norm runs in epilogue workgroups of the same launch when the chains' slices leave at
+  // least two CUs per chain free (one workgroup per CU, so the whole grid is resident at once;
+  // config 4's 32 chains have 128 slices and 128 epilogue workgroups on 256 CUs). Otherwise the
+  // chunk kernel stores O into the output and the norm kernel follows in place.
+  const bool epi = norm && blocks + 2 * N * HV <= cus;
+  const bool persist = cu_seqlens && !chunk_states && !epi && !initial_state && !final_state && N <= kOrderMax &&
                        nq >= 1 && N * HV >= 4 * nq && (N * HV + nq - 1) / nq <= kJobTab;
   f16* tw = static_cast<f16*>(workspace);
   char* const ws = static_cast<char*>(workspace);
@@ -1375,17 +1394,20 @@ int chunk_fwd_impl(const void* q, const void* k, const void* v, const void* g, c
     p.nq = (int)nq;
     blocks = nq * nvb;
   }
+  if (epi) {
+    p.nprod = (int)blocks;
+    blocks = cus;
+  }
   dim3 grid((unsigned)blocks), block(kNT);
   if (persist) {
     if (K == 128 && V == 128) hipLaunchKernelGGL((gated_delta_chunk_kernel<128, 128, false, false, true>), grid, block, 0, s, p);
     else if (K == 64 && V == 64) hipLaunchKernelGGL((gated_delta_chunk_kernel<64, 64, false, false, true>), grid, block, 0, s, p);
     else if (K == 128 && V == 64) hipLaunchKernelGGL((gated_delta_chunk_kernel<128, 64, false, false, true>), grid, block, 0, s, p);
     else hipLaunchKernelGGL((gated_delta_chunk_kernel<64, 128, false, false, true>), grid, block, 0, s, p);
-  } else if (norm) {
-    // the pairs carry their chunk, and no chunk index is 0 (they store c + 1): zeroing the exchange
-    // area is enough for any earlier contents (a fill kernel, so that captured graphs clear it too)
-    p.npart = reinterpret_cast<u32x2*>(ws + base_need);
-    const int frc = launch_fill_zero(reinterpret_cast<unsigned*>(p.npart), (int64_t)(norm_part_bytes(N, HV, V) / 4), s);
+  } else if (epi) {
+    // progress words from zero (a fill kernel, so that captured graphs clear them too)
+    p.prog = reinterpret_cast<unsigned*>(ws + base_need);
+    const int frc = launch_fill_zero(p.prog, (int64_t)(norm_prog_bytes(N, HV, V) / 4), s);
     if (frc != GDN_OK) return frc;
     if (K == 128 && V == 128) hipLaunchKernelGGL((gated_delta_chunk_kernel<128, 128, false, true>), grid, block, 0, s, p);
     else if (K == 64 && V == 64) hipLaunchKernelGGL((gated_delta_chunk_kernel<64, 64, false, true>), grid, block, 0, s, p);
@@ -1402,7 +1424,10 @@ int chunk_fwd_impl(const void* q, const void* k, const void* v, const void* g, c
     else if (K == 128 && V == 64) hipLaunchKernelGGL((gated_delta_chunk_kernel<128, 64, false>), grid, block, 0, s, p);
     else hipLaunchKernelGGL((gated_delta_chunk_kernel<64, 128, false>), grid, block, 0, s, p);
   }
-  return gdn_internal_check_launch("gated_delta_chunk_kernel");
+  const int lrc = gdn_internal_check_launch("gated_delta_chunk_kernel");
+  if (lrc != GDN_OK || !norm || epi) return lrc;
+  // the norm over the rows just stored, in place (each wave reads its rows before it writes them)
+  return gdn_internal_rms_norm_gated(o, ngate, nweight, o, B * T * HV, V, neps, nsplit, s);
 }
 
 }  // namespace
@@ -1443,7 +1468,7 @@ extern "C" size_t gdn_chunk_gated_norm_workspace_size(int64_t B, int64_t T, int6
                                                       int varlen) {
   const size_t base = gdn_chunk_workspace_size(B, T, HV, N, varlen);
   if (!base || (V != 64 && V != 128)) return 0;
-  return base + norm_part_bytes(N, HV, V);
+  return base + norm_prog_bytes(N, HV, V);
 }
 
 extern "C" int gdn_chunk_fwd_gated_norm(const void* q, const void* k, const void* v, const void* g, const void* beta,

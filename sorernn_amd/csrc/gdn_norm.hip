@@ -4,7 +4,7 @@
 // D/64 elements, the sum of squares is reduced across the wave, and the row is written once with
 // fp32 math and a single rounding. Both kernels are HBM-bound elementwise passes.
 
-#include "gdn_common.h"
+#include "gdn_chunk.h"
 
 namespace gdn {
 
@@ -17,7 +17,8 @@ struct NormParams {
   int64_t rows, D;
   int dt, act;
   float eps;
-  int mode;  // 0 = L2 norm, 1 = (gated) RMSNorm
+  int mode;   // 0 = L2 norm, 1 = (gated) RMSNorm
+  int split;  // RMSNorm with a gate: the norm (w, bias) and act(gate) each rounded before their product
 };
 
 constexpr int kNormMaxPerLane = 16;  // D <= 1024
@@ -50,7 +51,8 @@ __global__ __launch_bounds__(256) void gated_delta_norm_kernel(NormParams p) {
         if (p.bias) out += p.bias[e];
         if (p.gate) {
           const float gv = load_as_f32(p.gate, p.dt, base + e);
-          out *= (p.act == GDN_ACT_SILU) ? silu_f32(gv) : gv;
+          const float a = (p.act == GDN_ACT_SILU) ? silu_f32(gv) : gv;
+          out = p.split ? round_to(p.dt, out) * round_to(p.dt, a) : out * a;
         }
       }
       store_from_f32(p.y, p.dt, base + e, out);
@@ -108,7 +110,8 @@ __global__ __launch_bounds__(256) void gated_delta_norm_v8_kernel(NormParams p) 
           out = out * wv[e] + bv[e];
           if (gated) {
             const float g = (float)gv[u][e];
-            out *= (p.act == GDN_ACT_SILU) ? silu_fast(g) : g;
+            const float a = (p.act == GDN_ACT_SILU) ? silu_fast(g) : g;
+            out = p.split ? (float)(E)out * (float)(E)a : out * a;
           }
         }
         yv[e] = (E)out;
@@ -259,6 +262,12 @@ static int launch_norm(const NormParams& p, void* stream, const char* what) {
 }  // namespace gdn
 
 using namespace gdn;
+
+int gdn::gdn_internal_rms_norm_gated(const void* x, const void* gate, const float* w, void* y, int64_t rows, int64_t D,
+                                     float eps, int split, hipStream_t s) {
+  NormParams p{x, gate, w, nullptr, y, rows, D, GDN_DTYPE_BF16, GDN_ACT_SILU, eps, 1, split};
+  return launch_norm(p, s, "gated_delta_norm_kernel(rms)");
+}
 
 extern "C" int gdn_l2norm_fwd(const void* x, void* y, int64_t rows, int64_t D, int dtype, float eps, void* stream) {
   if (!x || !y || rows < 0 || D <= 0) {

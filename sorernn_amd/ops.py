@@ -303,15 +303,18 @@ def chunk_gated_delta_rule_gated_norm(
     A_log: Tensor | None = None,
     dt_bias: Tensor | None = None,
 ):
-    """``chunk_gated_delta_rule`` with the layer's gated RMSNorm applied as ``o`` is stored (inference).
+    """``chunk_gated_delta_rule`` with the layer's gated RMSNorm in the same call (inference).
 
     Returns ``(rms_norm_gated(o, gate, norm_weight, None, "swish", norm_eps), final_state)`` for the
     ``o`` chunk_gated_delta_rule would return: the call at ``sore/model/gdn.py:166-169`` followed by the
-    norm at ``gdn.py:182-186``, one kernel, ``o`` never written to HBM. ``norm_split=True`` rounds as the
-    reference's unfused route ``o_norm(o) * F.silu(gate)`` (``gdn.py:188``). ``gate`` has ``v``'s shape
-    and dtype (bf16); ``norm_weight [V]``. Inputs must not require grad (the backward of the norm
-    needs ``o``). A call whose outputs are not finite is handled by the range guard as in
-    ``chunk_gated_delta_rule``; its fallback recomputes the call as chunk_gated_delta_rule + the norm.
+    norm at ``gdn.py:182-186``, equal bit for bit to those two calls here. ``norm_split=True`` rounds
+    as the reference's unfused route ``o_norm(o) * F.silu(gate)`` (``gdn.py:188``). ``gate`` has
+    ``v``'s shape and dtype (bf16); ``norm_weight [V]``. Inputs must not require grad (the backward of
+    the norm needs ``o``). When the chains leave CUs free (two per (sequence, head) at least), the
+    norm runs in epilogue workgroups of the chunk kernel's own launch, over each O tile as soon as
+    it is stored; otherwise the norm kernel follows in place. A call whose outputs are not finite is
+    handled by the range guard as in ``chunk_gated_delta_rule``; its fallback recomputes the call as
+    chunk_gated_delta_rule + the norm.
     """
     name = "chunk_gated_delta_rule_gated_norm"
     _check_cuda(name, q, k, v, g, beta, initial_state, cu_seqlens, A_log, dt_bias, gate, norm_weight)

@@ -229,25 +229,26 @@ def state_kernel(s: Shape, eg: int, eb: int, save: bool) -> int:
         done += check(f"fwd v slice {vb}", s.tokens * HV * V * 2, base_v, _col(ln) * v_row, _last(off_v.ravel()), 16)
     # gates of chunks c < nc + 3 (two steps ahead of the staging, one more in flight)
     done += gate_loads(s, eg, eb, extra=3)
-    # O stores of chunks c < nc (store_o: the V-slice layout); the fused-norm variant's gate loads
-    # (load_gate) and normalised O stores (store_o_norm) use the same layout on gate and o
+    # O stores of chunks c < nc (store_o: the V-slice layout)
     c0, ln, cg, nn = chunk_rows(s)
     for vb in range(V // 32):
         base_o = ((_col(c0) * HV + _mid(hv)) * V + vb * 32) * 2
         done += check(f"fwd o slice {vb}", s.tokens * HV * V * 2, base_o, _col(ln) * v_row, _last(off_v.ravel()), 16)
-        done += check(f"fwd norm gate slice {vb}", s.tokens * HV * V * 2, base_o, _col(ln) * v_row,
-                      _last(off_v.ravel()), 16)
-        done += check(f"fwd norm o slice {vb}", s.tokens * HV * V * 2, base_o, _col(ln) * v_row,
-                      _last(off_v.ravel()), 16)
-    # the fused norm's exchange area: per chain a resource over its 8 slots x NVB slices x 64 tokens of
-    # 8-byte (sum, chunk + 1) pairs; slice vb stores lane l's pair of slot c % 8, every slice loads the
-    # pairs of its rows from all NVB slices
-    nvb, chains = V // 32, s.N * HV
-    rec = 8 * nvb * 64 * 8
-    r_ = np.arange(chains)
-    slot_, vb_, l_ = np.meshgrid(np.arange(8), np.arange(nvb), np.arange(64), indexing="ij")
-    off_np = ((((slot_ * nvb + vb_) * 64) + l_) * 8).ravel()
-    done += check("fwd norm sum pairs", chains * rec, _col(r_ * rec), _col(np.full(chains, rec)), _last(off_np), 8)
+    # the fused norm's progress words, NVB per chain (4 bytes each) at the start of the chain's
+    # 64-word block: a slice stores its own word through a resource over its chain's words
+    # (publish_o); an epilogue wave polls them with lane l reading word l (lanes l >= NVB fall
+    # outside the resource)
+    nvb, chains, stride = V // 32, s.N * HV, 64
+    base_w, nrec_w = _col(np.arange(chains) * stride * 4), _col(np.full(chains, nvb * 4))
+    done += check("fwd norm progress store", chains * stride * 4, base_w, nrec_w, _last(np.arange(nvb) * 4), 4)
+    done += check("fwd norm progress poll", chains * stride * 4, base_w, nrec_w, _last(np.arange(64) * 4), 4)
+    # the epilogue's O loads, gate loads and y stores (norm_epilogue): per (chunk, head) a resource
+    # over the chunk's valid rows of the head, offsets row * HV * V * 2 + 16-byte piece for the
+    # 64 rows of the tile and V / 8 pieces per row
+    off_e = (np.arange(C)[:, None] * v_row + (np.arange(V // 8) * 16)[None, :]).ravel()
+    base_e = (_col(c0) * HV + _mid(hv)) * V * 2
+    for name in ("o", "gate"):
+        done += check(f"fwd norm epilogue {name}", s.tokens * HV * V * 2, base_e, _col(ln) * v_row, _last(off_e), 16)
     # h0 loads / ht stores (plain, fp32 [N][HV][K][V]) and, with SAVE, the state entering each chunk
     # (bf16 [chunks][HV][V][K], an 8-byte store per lane and state tile)
     rank, vbs = state_kernel_grid(s)
@@ -447,7 +448,7 @@ def test_checker_flags_the_old_gate_loads(shape):
 
 def test_model_covers_every_buffer_resource():
     """Each buffer resource a kernel file creates has a counterpart above; a new one must be modelled."""
-    expected = {"gdn_chunk.hip": 12, "gdn_chunk_bwd.hip": 9, "gdn_chunk_prep.hip": 1}
+    expected = {"gdn_chunk.hip": 13, "gdn_chunk_bwd.hip": 9, "gdn_chunk_prep.hip": 1}
     for fname, n in expected.items():
         with open(os.path.join(CSRC, fname)) as f:
             src = f.read()
