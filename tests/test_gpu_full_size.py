@@ -4,6 +4,9 @@ in seconds.
 - Config 3 (8 packed documents, 32768 tokens): the whole op runs once; its outputs and final states
   for the 1,112-token and the 9,480-token documents (two value heads each) are compared with the
   oracle's recurrence over those documents from their own initial states.
+- Config 4's chunked op alone (B=2, T=8192, H=16, d=128, config 1's input distributions, initial
+  states): every output and final state against the oracle's recurrence, at BASELINE's absolute
+  bars (128-chunk chains, twice config 1's).
 - Config 4's GDN layer (B=2, T=8192, hidden 2048, 16 heads of 128, in-kernel gate): the full layer
   runs on both routes (the fused inference route and the reference-expression route); the input of
   its o_proj (the gated RMSNorm of the delta rule's output) is captured and compared, for batch row
@@ -48,6 +51,21 @@ def test_config3_documents_match_oracle():
                                                    inp.scale, inp.h0[n:n + 1, heads], True)
         assert_output_close(o[:, a:e, heads], o_ref, what=f"o of document {n} ({length} tokens)")
         assert_state_close(st[n:n + 1, heads], st_ref, what=f"final state of document {n}")
+
+
+def test_config4_chunk_op_matches_oracle():
+    from sorernn_amd.synthetic import gdn_inputs
+
+    inp = gdn_inputs(2, 8192, 16, 128, dtype=BF16, seed=1004, h0=True)
+    print("config-4 chunk op: B=2, T=8192, H=16, d=128", flush=True)
+    d = inp.to(DEV)
+    o, st = chunk_gated_delta_rule(d.q, d.k, d.v, d.g, d.beta, scale=inp.scale, initial_state=d.h0,
+                                   output_final_state=True)
+    torch.cuda.synchronize()
+    o_ref, st_ref = recurrent_gated_delta_rule(inp.q, inp.k, inp.v, inp.g, inp.beta, inp.scale, inp.h0, True)
+    err = assert_output_close(o.cpu(), o_ref)
+    rel = assert_state_close(st.cpu(), st_ref)
+    print(f"  max-abs {err:.3e} (max|ref| {o_ref.abs().max().item():.2f}), state relative L2 {rel:.2e}", flush=True)
 
 
 def _gdn_layer_config4():
