@@ -245,3 +245,46 @@ def test_layer_with_fused_epilogue_matches_oracle(fused_norm_gate, cu_case, monk
     out = _run(layer, x, cu_t)
     err = (out - ref).abs().max().item()
     assert err <= 2e-2 * ref.abs().max().item() + 1e-3, f"max-abs error {err:.3e} (max|ref| {ref.abs().max():.3e})"
+
+
+@pytest.mark.parametrize("n_docs", [10, 100], ids=["epilogue_route", "in_place_route"])
+def test_fused_norm_empty_sequences_through_the_abi(n_docs):
+    """Empty sequences (allowed by the C ABI, rejected by the Python op as the reference's cu_seqlens
+    contract does) on both routes, with initial and final states: the outputs equal the plain entry
+    point's O normalised by the norm kernel, bit for bit, and the final states are the plain call's
+    (an empty sequence's final state is its initial state)."""
+    from sorernn_amd import _lib
+
+    gen = torch.Generator().manual_seed(57 + n_docs)
+    lens = torch.randint(1, 150, (n_docs,), generator=gen).tolist()
+    for i in (0, n_docs // 2, n_docs - 1):
+        lens[i] = 0
+    cu = torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist())
+    t, n, hv = int(cu[-1]), n_docs, 4
+    assert _epilogue_route(n, hv, 128) == (n_docs == 10)
+    print(f"fused norm, empty sequences through the ABI: {n} docs, {t} tokens", flush=True)
+    inp = gdn_inputs(1, t, 2, 128, HV=hv, dtype=torch.bfloat16, seed=58, h0=True, cu_seqlens=cu)
+    gate, w = _gate_weight(inp.v.shape, 128, 12)
+    d = inp.to(DEV)
+    gd, wd = gate.to(DEV), w.to(DEV)
+    lib = _lib.load()
+    common = [_lib.ptr(d.q), _lib.ptr(d.k), _lib.ptr(d.v), _lib.ptr(d.g), _lib.ptr(d.beta), _lib.ptr(d.h0)]
+    sizes = [1, t, 2, hv, 128, 128, n, _lib.DTYPE_BF16, _lib.DTYPE_F32, _lib.DTYPE_F32, inp.scale, 0, None, None]
+    y = torch.empty(1, t, hv, 128, device=DEV, dtype=torch.bfloat16)
+    st = torch.empty(n, hv, 128, 128, device=DEV, dtype=torch.float32)
+    nb = int(lib.gdn_chunk_gated_norm_workspace_size(1, t, hv, n, 128, 1))
+    ws = torch.empty(nb, dtype=torch.uint8, device=DEV)
+    _lib.call("gdn_chunk_fwd_gated_norm", *common, _lib.ptr(y), _lib.ptr(st), _lib.ptr(d.cu_seqlens), *sizes,
+              _lib.ptr(gd), _lib.ptr(wd), EPS, 0, _lib.ptr(ws), nb, _lib.stream_of(d.q))
+    o = torch.empty_like(y)
+    st2 = torch.empty_like(st)
+    nb2 = int(lib.gdn_chunk_workspace_size(1, t, hv, n, 1))
+    ws2 = torch.empty(nb2, dtype=torch.uint8, device=DEV)
+    _lib.call("gdn_chunk_fwd", *common, _lib.ptr(o), _lib.ptr(st2), _lib.ptr(d.cu_seqlens), *sizes, _lib.ptr(ws2), nb2,
+              _lib.stream_of(d.q))
+    y2 = gpu_rms_norm_gated(o, gd, wd, None, activation="swish", eps=EPS)
+    torch.cuda.synchronize()
+    _same_as_two_op(y.cpu(), y2.cpu(), False)
+    assert torch.equal(st.cpu(), st2.cpu())
+    for i in (0, n_docs // 2, n_docs - 1):
+        assert torch.equal(st[i].cpu(), inp.h0[i]), f"empty sequence {i}: final state is not its initial state"
