@@ -91,9 +91,10 @@ GDN_API int gdn_chunk_fwd(const void* q, const void* k, const void* v, const voi
  * the result is written over it in o. When the chunk kernel's V / 32 column slices leave at least two
  * CUs per (sequence, head) free, workgroups of the same launch apply the norm to each 64-token
  * tile once all its slices have stored it (progress words in the workspace, which must hold
- * gdn_chunk_gated_norm_workspace_size bytes); a call whose outputs are not finite then sets the
- * range flag (no fp32 recomputation on that route). Otherwise the norm kernel runs in place after
- * the chunk kernel.
+ * gdn_chunk_gated_norm_workspace_size bytes). Otherwise the norm kernel runs in place after the
+ * chunk kernel. On both routes a slice whose fp16 operands overflowed recomputes its columns in
+ * fp32 (on the first route from its first non-finite chunk, before that chunk is normalised), as
+ * gdn_chunk_fwd does.
  */
 GDN_API int gdn_chunk_fwd_gated_norm(const void* q, const void* k, const void* v, const void* g, const void* beta,
                              const float* initial_state, void* o, float* final_state, const void* cu_seqlens,

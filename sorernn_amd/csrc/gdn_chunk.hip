@@ -178,7 +178,7 @@ __device__ __forceinline__ ChunkParams reload_params() {
 template <int KD, int VD, bool SAVE>
 __device__ __forceinline__ void recover_slice(const ChunkParams& p, int64_t n, int hv, int h, int vb, int64_t bos,
                                            int64_t eos, int64_t cg_first, bf16* kl, bf16* ql, bf16* vl,
-                                           ChunkGates* gl) {
+                                           ChunkGates* gl, int c_out_from = 0) {
   constexpr int KPL = KD / 16;
   const int t = threadIdx.x, lane = t & 63, w = t >> 6, g4 = lane >> 4, li = lane & 15;
   const int col = vb * kVB + 4 * w + g4;  // value column within the head
@@ -256,7 +256,7 @@ __device__ __forceinline__ void recover_slice(const ChunkParams& p, int64_t n, i
       const float o = p.scale * (a * pq * iq + d * kq * ik * iq);
 #pragma unroll
       for (int e = 0; e < KPL; ++e) s[e] = a * s[e] + kr[e] * ik * d;
-      if (li == 0) {
+      if (li == 0 && c >= c_out_from) {
         const bf16 ob = static_cast<bf16>(o);
         og[(c0 + r) * p.HV * VD + (int64_t)hv * VD + col] = ob;
         om = __builtin_elementwise_max(om, u16x2{(unsigned short)(__builtin_bit_cast(unsigned short, ob) & 0x7fff), 0});
@@ -512,6 +512,7 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
   __shared__ __align__(16) bf16 Ob[2][kC * kVB];
   __shared__ __align__(16) ChunkGates gv[3];      // gate terms of chunk c in slot c % 3
   __shared__ int bad;                              // an O or final-state element of this slice is inf / NaN
+  __shared__ int first_bad;                        // NORM: the first chunk whose stored O holds an inf or NaN
   __shared__ int4 jtab[PERSIST ? kJobTab : 1];     // PERSIST: the group's job list (bos, eos, sequence, head)
   __shared__ SchedScratch sched;                   // PERSIST: the scheduler's per-sequence arrays
 
@@ -842,7 +843,10 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
   GateBits ngate{0, 0, 0, 0};  // wave 4: raw gate bits of the chunk two steps ahead, in flight
 
   // ------------------------------------------------------------------ prologue
-  if (t == 0) bad = 0;
+  if (t == 0) {
+    bad = 0;
+    first_bad = 0x7fffffff;
+  }
   if constexpr (PERSIST) {
     schedule_group(p, gq, jtab, gjob, sched);
     njobs = gjob[0];
@@ -1177,8 +1181,9 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
         // this thread's O stores of chunk i - 2 (issued last step, with the loads this step stages)
         // have completed; every storing thread's stores of chunk i - 3 completed before the
         // previous step's barrier, so chunks 0 .. i - 3 are published
+        // (never past a chunk whose O held an inf or NaN: the recomputation below rewrites those)
         __builtin_amdgcn_s_waitcnt(kWaitVm0);
-        if (w == 5 && lane == 0 && i >= 3) publish_o(i - 2);
+        if (w == 5 && lane == 0 && i >= 3) publish_o(min(i - 2, first_bad));
       }
       const int tq = thv_of(opaque_int(lane));
       const ChunkAt a2 = src(ct, i + 2);  // the chunk whose gates are staged and T/V loaded this step
@@ -1186,13 +1191,21 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
         stage_gates((i + 2) % 3, a2, ngate);
         fetch_gates(src(cgf, i + 3), ngate);
       }
-      if (i > 0) store_o((i - 1) & 1, src(co, i - 1), tq, om);
+      if (i > 0) {
+        store_o((i - 1) & 1, src(co, i - 1), tq, om);
+        if constexpr (NORM) {
+          if (om[0] >= 0x7f80 || om[1] >= 0x7f80) atomicMin(&first_bad, i - 1);
+        }
+      }
       stage_tv(pt, pv, (i + 1) & 1, tq);
       fetch_tv(pt, pv, a2, tq);
       __syncthreads();
     }
     if (nc > 0) store_o((nc - 1) & 1, src(co, nc - 1), thv, om);
-    if constexpr (NORM) __builtin_amdgcn_s_waitcnt(kWaitVm0);  // before the barrier ahead of the last word
+    if constexpr (NORM) {
+      if (om[0] >= 0x7f80 || om[1] >= 0x7f80) atomicMin(&first_bad, nc - 1);
+      __builtin_amdgcn_s_waitcnt(kWaitVm0);  // before the barrier ahead of the last word
+    }
     if (om[0] >= 0x7f80 || om[1] >= 0x7f80) __hip_atomic_fetch_or(&bad, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
 
@@ -1203,16 +1216,20 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
   // (value columns of the state evolve independently), overwriting O, the final state and (SAVE)
   // the saved chunk states, and flags the call only if that recomputation is non-finite as well
   // (non-finite inputs). Slices that stored finite values skip it: the cost is this barrier.
-  // The fused-norm variant has no recomputation (the epilogue workgroups may already have read the
-  // slice's O): it publishes its last chunks and reports the call through the range flag.
+  // With NORM the slice has published no chunk from the first one whose O was not finite: the
+  // recomputation rewrites O from that chunk on (the epilogue workgroups may already have
+  // normalised the chunks before it in place), writes it back to memory (an agent-scope release)
+  // and then publishes every chunk.
   __syncthreads();
-  if constexpr (NORM) {
-    if (t == 5 * kWave) publish_o(nc);
-  }
   if (__builtin_amdgcn_readfirstlane(bad)) {
     if constexpr (NORM) {
+      const int fb = first_bad;
       const ChunkParams pr = reload_params();
-      if (t == 0 && pr.range_flag) flag_nonfinite(pr.range_flag, true);
+      const SliceLoc lr = locate_slice<NVB>(pr);
+      recover_slice<KD, VD, false>(pr, lr.n, lr.hv, lr.h, lr.vb, lr.bos, lr.eos, 0, (bf16*)&Kc[0][0],
+                                   (bf16*)&Qc[0][0], (bf16*)&Vc[0][0], &gv[0], fb);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+      __syncthreads();
     } else {
       const ChunkParams pr = reload_params();
       if constexpr (PERSIST) {
@@ -1233,6 +1250,9 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
                                     (bf16*)&Qc[0][0], (bf16*)&Vc[0][0], &gv[0]);
       }
     }
+  }
+  if constexpr (NORM) {
+    if (t == 5 * kWave) publish_o(nc);
   }
 }
 

@@ -288,3 +288,36 @@ def test_fused_norm_empty_sequences_through_the_abi(n_docs):
     assert torch.equal(st.cpu(), st2.cpu())
     for i in (0, n_docs // 2, n_docs - 1):
         assert torch.equal(st[i].cpu(), inp.h0[i]), f"empty sequence {i}: final state is not its initial state"
+
+
+@pytest.mark.parametrize("varlen", [False, True], ids=["fixed", "varlen"])
+def test_fused_norm_fp16_overflow_is_recomputed(varlen):
+    """v x 1e5 on the epilogue route: the chunk kernel's fp16 operands overflow while the fp32
+    results stay finite (tests/test_gpu_range.py). A slice that stored a non-finite O publishes no
+    chunk from that one on, recomputes its columns in fp32, and publishes them afterwards: y is
+    finite and meets the oracle's bar (the RMS norm removes the input's scale), the final states
+    equal the plain call's, and the range flag stays clear."""
+    import sorernn_amd
+
+    sorernn_amd.set_range_guard("warn")
+    sorernn_amd.check_chunk_range()
+    big = 1.0e5
+    if varlen:
+        cu = torch.tensor([0, 40, 41, 300], dtype=torch.long)
+        inp = gdn_inputs(1, 300, 2, 128, HV=4, dtype=torch.bfloat16, seed=72, h0=True, cu_seqlens=cu)
+        n, hv = 3, 4
+    else:
+        inp = gdn_inputs(1, 130, 2, 128, dtype=torch.bfloat16, seed=70, h0=True)
+        n, hv = 1, 2
+    inp.v = (inp.v.float() * big).to(torch.bfloat16)
+    assert _epilogue_route(n, hv, 128)
+    print(f"fused norm, v x {big:g}, varlen={varlen}", flush=True)
+    gate, w = _gate_weight(inp.v.shape, 128, 13)
+    y, st, y2, st2 = _both(inp, gate, w, False)
+    assert torch.isfinite(y).all() and torch.isfinite(st).all()
+    assert torch.equal(st, st2), "the final state is the plain call's (both recomputed in fp32)"
+    ref = _oracle(inp, gate, w, False)
+    scale = float(ref.abs().max())
+    assert_output_close(y, ref, tol=2e-2 * scale)
+    assert (y.float() - y2.float()).abs().max().item() <= 2e-2 * scale
+    assert not sorernn_amd.check_chunk_range(), "the recomputation was finite: the flag must stay clear"
