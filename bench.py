@@ -205,6 +205,26 @@ def block_pair(torch, steps: int) -> dict:
         settle(torch, fa)
         _, fa_ms = time_launches(torch, fa, steps)
         fl = attn_flops(B, T, H, Dh)
+        # the layer's GDN call alone at this shape (synthetic config-1 distributions, bf16 gate):
+        # the chunked op, the op followed by the norm kernel, and the op with the norm in the call
+        from sorernn_amd import chunk_gated_delta_rule, rms_norm_gated
+        from sorernn_amd.ops import chunk_gated_delta_rule_gated_norm
+        from sorernn_amd.synthetic import gdn_inputs
+        gi = gdn_inputs(B, T, H, Dh, dtype=torch.bfloat16, seed=1004).to("cuda")
+        og = torch.randn(B, T, H, Dh, device="cuda").to(torch.bfloat16)
+        ow = torch.rand(Dh, device="cuda") + 0.5
+        op = lambda: chunk_gated_delta_rule(gi.q, gi.k, gi.v, gi.g, gi.beta, scale=gi.scale)[0]  # noqa: E731
+        ops_ = {
+            "gdn_op": op,
+            "gdn_op_then_norm": lambda: rms_norm_gated(op(), og, ow, eps=1e-6),
+            "gdn_op_norm_in_call": lambda: chunk_gated_delta_rule_gated_norm(gi.q, gi.k, gi.v, gi.g, gi.beta, og, ow,
+                                                                              1e-6, scale=gi.scale)[0],
+        }
+        for name, fn in ops_.items():
+            fn()
+            settle(torch, fn)
+            ms, _ = time_launches(torch, fn, steps)
+            out[f"{name}_ms"] = round(ms, 4)
     pair_ms = out["gdn_layer_ms"] + out["attn_layer_ms"]
     out.update({
         "pair_ms": round(pair_ms, 4),
@@ -403,7 +423,8 @@ def run_only(torch, args) -> int:
         bp = block_pair(torch, args.steps)
         print(f"ran block_pair: gdn {bp['gdn_layer_ms']} ms (chunk op and norm as two calls {bp['gdn_layer_unfused_epilogue_ms']} ms, "
               f"reference route {bp['gdn_layer_reference_route_ms']} ms), attn {bp['attn_layer_ms']} ms, "
-              f"attention kernel {bp['attn_kernel_ms']} ms", flush=True)
+              f"attention kernel {bp['attn_kernel_ms']} ms; GDN call {bp['gdn_op_ms']} ms, then the norm kernel "
+              f"{bp['gdn_op_then_norm_ms']} ms, norm in the call {bp['gdn_op_norm_in_call_ms']} ms", flush=True)
         return 0
     if args.only == "train":
         tf, tb = train_step_times(torch, config_inputs(1).to("cuda"), args.steps)
