@@ -91,6 +91,20 @@ def test_chunk_workspace_size_matches_layout(monkeypatch):
     assert chunk_workspace_bytes(0, 100, 3, 1, False) == 0
 
 
+def test_gated_norm_workspace_size_matches_layout(monkeypatch):
+    """gdn_chunk_gated_norm_workspace_size: gdn_chunk_fwd's workspace, then the epilogue's progress
+    words (a 256-byte block per (sequence, value head)); 0 for invalid sizes or head dims."""
+    from sorernn_amd import _lib
+    from sorernn_amd.ops import chunk_workspace_bytes
+    monkeypatch.delenv("SORERNN_PREFILL", raising=False)
+    lib = _lib.load()
+    for (b, t, hv, n, v, varlen) in [(2, 8192, 16, 2, 128, 0), (1, 777, 4, 5, 128, 1), (2, 300, 2, 2, 64, 0)]:
+        assert lib.gdn_chunk_gated_norm_workspace_size(b, t, hv, n, v, varlen) == (
+            chunk_workspace_bytes(b, t, hv, n, bool(varlen)) + _align(n * hv * 256))
+    assert lib.gdn_chunk_gated_norm_workspace_size(2, 300, 2, 2, 96, 0) == 0
+    assert lib.gdn_chunk_gated_norm_workspace_size(0, 300, 2, 2, 128, 0) == 0
+
+
 def test_chunk_backward_buffer_sizes_match_layout():
     """gdn_chunk_states_size: one bf16 K x V state per chunk and value head (chunk count bounded by
     ceil(T/64) + N with cu_seqlens). gdn_chunk_bwd_workspace_size: bf16 (T - I)^T rows [tokens][HV][64],
