@@ -426,6 +426,24 @@ def run_only(torch, args) -> int:
               f"attention kernel {bp['attn_kernel_ms']} ms; GDN call {bp['gdn_op_ms']} ms, then the norm kernel "
               f"{bp['gdn_op_then_norm_ms']} ms, norm in the call {bp['gdn_op_norm_in_call_ms']} ms", flush=True)
         return 0
+    if args.only in ("gdn_norm_call", "gdn_norm_two_calls"):
+        # config 4's GDN call with the layer's gated RMSNorm: in the call (the layer's route), or the
+        # op followed by the norm kernel; synthetic config-1 distributions, bf16 gate, --steps calls
+        from sorernn_amd import rms_norm_gated
+        from sorernn_amd.ops import chunk_gated_delta_rule_gated_norm
+        from sorernn_amd.synthetic import gdn_inputs
+        gi = gdn_inputs(2, 8192, 16, 128, dtype=torch.bfloat16, seed=1004).to("cuda")
+        og = torch.randn(2, 8192, 16, 128, device="cuda").to(torch.bfloat16)
+        ow = torch.rand(128, device="cuda") + 0.5
+        for _ in range(args.steps):
+            if args.only == "gdn_norm_call":
+                chunk_gated_delta_rule_gated_norm(gi.q, gi.k, gi.v, gi.g, gi.beta, og, ow, 1e-6, scale=gi.scale)
+            else:
+                o, _ = chunk_gated_delta_rule(gi.q, gi.k, gi.v, gi.g, gi.beta, scale=gi.scale)
+                rms_norm_gated(o, og, ow, eps=1e-6)
+        torch.cuda.synchronize()
+        print(f"ran {args.only}: {args.steps} calls", flush=True)
+        return 0
     if args.only == "train":
         tf, tb = train_step_times(torch, config_inputs(1).to("cuda"), args.steps)
         print(f"ran train: {args.steps} steps, forward {tf:.3f} ms, backward {tb:.3f} ms", flush=True)
@@ -835,7 +853,7 @@ def main() -> int:
                     help="only run a plain 256 MiB device copy (the reference kernel for PMC byte counters)")
     ap.add_argument("--settle-ms", type=float, default=SETTLE_MS,
                     help="untimed run of each workload's own step before its warmup steps (0: none)")
-    ap.add_argument("--only", choices=list(PARTS) + ["decode_rot"], default=None,
+    ap.add_argument("--only", choices=list(PARTS) + ["decode_rot", "gdn_norm_call", "gdn_norm_two_calls"], default=None,
                     help="run one workload only (for profiler runs); prints no JSON line")
     ap.add_argument("--part", choices=PARTS, default=None,
                     help="(internal) run one workload and print its raw measurements as JSON")

@@ -90,6 +90,11 @@ constexpr unsigned kEpiSpinMax = 1u << 21;  // NORM: polls of an epilogue workgr
 // NORM: 32-bit words between the progress words of consecutive chains (each chain's NVB words in a
 // 256-byte block of its own, so the epilogue workgroups' polls spread over memory channels)
 constexpr int kProgStride = 64;
+// NORM: words 16 .. 16 + kEpiPostMax - 1 of a chain's block hold the XCC ids (+ 1) its epilogue
+// workgroups post at start-up
+constexpr int kEpiPostBase = 16, kEpiPostMax = 48;
+// The XCC (XCD) the wave runs on (hardware register XCC_ID).
+__device__ __forceinline__ unsigned wave_xcc() { return __builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20); }
 constexpr int kJobTab = 512;   // PERSIST: jobs per group held in LDS (the grid is used when no group needs more)
 
 // Running maximum, per 16-bit half, of the magnitude bits of the bf16 values in x: a half at or
@@ -397,8 +402,11 @@ __device__ __forceinline__ void schedule_group(const ChunkParams& p, int gq, int
 // does. The arithmetic is the norm kernel's (gated_delta_norm_v8_kernel: a lane's 8 values, then
 // the row's lane group), so the outputs equal those of the chunk kernel followed by that kernel.
 // The host gives at least two epilogue workgroups per chain: R = nw / chains of them share a chain,
-// workgroup j taking the chunks j / chains, + R, + 2R, ... of chain j % chains (in the order the
-// slices store them). Wave 0 polls the chain's V / 32 progress words (device-scope loads, a sleep
+// workgroup j taking the chunks j / chains, + R, + 2R, ... of the chain with dispatch rank j % chains
+// (in the order the slices store them). With the chain count a multiple of 8 the workgroup then runs
+// on the XCD of its chain's slices (blockIdx b on XCD b % 8); it posts its XCC id at start-up, and a
+// slice whose epilogue workgroups all share its XCD stores O to L2 only (the workgroups' device-scope
+// loads are served there), otherwise written through to memory. Wave 0 polls the chain's V / 32 progress words (device-scope loads, a sleep
 // of ~2k cycles between polls) until they pass the chunk, and a barrier releases the workgroup's
 // eight waves, each of which handles its own rows of the tile. The polls are what the slices feel
 // of the epilogue: at config 4, one polling wave per workgroup and a few polls per chunk keep the
@@ -413,7 +421,12 @@ __device__ void norm_epilogue(const ChunkParams& p, int j, int nw) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, sub = lane / LPR, li = lane % LPR;
   const int64_t chains = p.N * p.HV, R = nw / chains;
   if (R < 1 || j >= R * chains) return;
-  const int64_t ch = j % chains, n = ch / p.HV, hv = ch % p.HV;
+  const int64_t kr = j % chains, n = p.order ? (int64_t)p.order[kr / p.HV] : kr / p.HV, hv = kr % p.HV;
+  const int64_t ch = n * p.HV + hv;
+  if (threadIdx.x == 0 && j / chains < kEpiPostMax) {
+    const auto rb = make_rsrc(p.prog + ch * kProgStride, kProgStride * 4);
+    __builtin_amdgcn_raw_buffer_store_b32(wave_xcc() + 1, rb, (int)((kEpiPostBase + j / chains) * 4), 0, kPolSC1);
+  }
   int64_t bos, eos;
   if (p.cu) {
     bos = load_index(p.cu, p.cu_i32, n);
@@ -717,7 +730,9 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
   // leave L2 to the q/k/T/V tiles that the slices of a chain share (config-1 call 130.3 -> 125.2 us,
   // same-box A/B). The training kernel keeps cached stores (non-temporal ones measured slower there).
   // With NORM they are also written through to memory (device scope), where the epilogue
-  // workgroups, on any XCD, read them.
+  // workgroups, on any XCD, read them; or, when every epilogue workgroup of the chain runs on this
+  // wave's XCD (o_local), they stay in that XCD's L2, where the workgroups read them.
+  bool o_local = false;
   auto store_o = [&](int slot, const ChunkAt& a, int tq, u16x2& om) {
     const auto ro = make_rsrc(og + (a.c0 * p.HV + a.hv) * VD + vb * kVB, a.len * v_row);
     const int row = tq >> 2, c8 = tq & 3;
@@ -725,9 +740,14 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
     for (int u = 0; u < 2; ++u) {
       const bf16x8 x = *reinterpret_cast<const bf16x8*>(&Ob[slot][vo_off(row + 32 * u, c8 * 8)]);
       om = bf16_mag_max(om, x);
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), ro,
-                                             (int)((uint32_t)(row + 32 * u) * v_row + c8 * 16), 0,
-                                             SAVE ? 0 : NORM ? kPolSC1 | kPolNT : kPolNT);
+      if (NORM && !o_local)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), ro,
+                                               (int)((uint32_t)(row + 32 * u) * v_row + c8 * 16), 0,
+                                               kPolSC1 | kPolNT);
+      else
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), ro,
+                                               (int)((uint32_t)(row + 32 * u) * v_row + c8 * 16), 0,
+                                               SAVE ? 0 : NORM ? 0 : kPolNT);
     }
   };
 
@@ -1176,8 +1196,21 @@ __global__ __launch_bounds__(kNT, 1) void gated_delta_chunk_kernel(ChunkParams p
     }
     __syncthreads();
     __syncthreads();
+    unsigned posted = 0;  // NORM: lane l, the XCC id (+ 1) epilogue workgroup l of the chain posted
     for (int i = 0; i < nc; ++i) {  // gates of chunk i+2, O of chunk i-1 out, T/V of chunk i+1 into LDS, loads of chunk i+2
       if constexpr (NORM) {
+        // the epilogue workgroups' posts, read in step 0 and checked in step 1, before the first O
+        // store (each wave decides for its own stores)
+        if (i <= 1) {
+          const auto rb = make_rsrc(p.prog + (n * p.HV + hv) * kProgStride, kProgStride * 4);
+          if (i == 0) {
+            posted = __builtin_amdgcn_raw_buffer_load_b32(rb, (kEpiPostBase + lane) * 4, 0, kPolSC1);
+          } else {
+            const int64_t nr = ((int64_t)gridDim.x - p.nprod) / (p.N * p.HV);
+            __builtin_amdgcn_s_waitcnt(kWaitVm0);
+            o_local = nr <= kEpiPostMax && __builtin_amdgcn_ballot_w64(lane < nr && posted != wave_xcc() + 1) == 0;
+          }
+        }
         // this thread's O stores of chunk i - 2 (issued last step, with the loads this step stages)
         // have completed; every storing thread's stores of chunk i - 3 completed before the
         // previous step's barrier, so chunks 0 .. i - 3 are published

@@ -242,6 +242,11 @@ def state_kernel(s: Shape, eg: int, eb: int, save: bool) -> int:
     base_w, nrec_w = _col(np.arange(chains) * stride * 4), _col(np.full(chains, nvb * 4))
     done += check("fwd norm progress store", chains * stride * 4, base_w, nrec_w, _last(np.arange(nvb) * 4), 4)
     done += check("fwd norm progress poll", chains * stride * 4, base_w, nrec_w, _last(np.arange(64) * 4), 4)
+    # the epilogue workgroups' XCC posts (word 16 + r of the chain's whole 64-word block, r < 48) and
+    # the slices' reads of them (lane l reads word 16 + l; lanes past the block read nothing)
+    nrec_b = _col(np.full(chains, stride * 4))
+    done += check("fwd norm epilogue post", chains * stride * 4, base_w, nrec_b, _last((16 + np.arange(48)) * 4), 4)
+    done += check("fwd norm post read", chains * stride * 4, base_w, nrec_b, _last((16 + np.arange(64)) * 4), 4)
     # the epilogue's O loads, gate loads and y stores (norm_epilogue): per (chunk, head) a resource
     # over the chunk's valid rows of the head, offsets row * HV * V * 2 + 16-byte piece for the
     # 64 rows of the tile and V / 8 pieces per row
@@ -448,7 +453,7 @@ def test_checker_flags_the_old_gate_loads(shape):
 
 def test_model_covers_every_buffer_resource():
     """Each buffer resource a kernel file creates has a counterpart above; a new one must be modelled."""
-    expected = {"gdn_chunk.hip": 13, "gdn_chunk_bwd.hip": 9, "gdn_chunk_prep.hip": 1}
+    expected = {"gdn_chunk.hip": 15, "gdn_chunk_bwd.hip": 9, "gdn_chunk_prep.hip": 1}
     for fname, n in expected.items():
         with open(os.path.join(CSRC, fname)) as f:
             src = f.read()
