@@ -1,7 +1,8 @@
 """GPU: the kernels inside captured HIP graphs (torch.cuda.CUDAGraph) give the eager results on every replay.
 
 A serving loop replays one captured decode step per token, and a training step may capture the
-varlen prefill. The chunk kernel's grid depends only on the number of sequences (not on their
+varlen prefill; the fused-norm call clears its progress words with a fill kernel that the graph
+holds. The chunk kernel's grid depends only on the number of sequences (not on their
 lengths), so a graph captured for one ``cu_seqlens`` stays valid when the lengths change: the
 failure documented for FLA's varlen kernels in the reference (``docs/perf/cuda-graphs.md:79-91``,
 grid frozen at capture) cannot happen. Each test replays several times with eager work and
@@ -74,3 +75,35 @@ def test_varlen_prefill_graph_survives_new_lengths():
         torch.cuda.synchronize()
         assert torch.equal(o_buf["o"], o_e), f"replay {rep}: output differs for {bounds}"
         assert torch.equal(o_buf["st"], st_e), f"replay {rep}: final state differs for {bounds}"
+
+
+def test_fused_norm_graph_replays_match_eager():
+    """chunk_gated_delta_rule_gated_norm on its epilogue route (8 chains, so epilogue workgroups on
+    the free CUs): the progress words are cleared by a fill kernel inside the graph, so every replay,
+    with new q, v and gate written in place between replays, equals the eager call bit for bit."""
+    from sorernn_amd.ops import chunk_gated_delta_rule_gated_norm
+
+    inp = gdn_inputs(2, 512, 4, 128, dtype=torch.bfloat16, seed=11, h0=True)
+    d = inp.to(DEV)
+    gen = torch.Generator().manual_seed(12)
+    gate = torch.randn(d.v.shape, generator=gen).to(torch.bfloat16).to(DEV)
+    w = (1.0 + 0.1 * torch.randn(128, generator=gen)).to(DEV)
+    buf = {}
+
+    def run():
+        buf["y"], buf["st"] = chunk_gated_delta_rule_gated_norm(d.q, d.k, d.v, d.g, d.beta, gate, w, 1e-6,
+                                                                scale=inp.scale, initial_state=d.h0,
+                                                                output_final_state=True)
+
+    graph = _capture(run)
+    for rep in range(4):
+        d.q.copy_(torch.randn(d.q.shape, generator=gen).to(torch.bfloat16))
+        d.v.copy_(torch.randn(d.v.shape, generator=gen).to(torch.bfloat16))
+        gate.copy_(torch.randn(gate.shape, generator=gen).to(torch.bfloat16))
+        graph.replay()
+        y_e, st_e = chunk_gated_delta_rule_gated_norm(d.q, d.k, d.v, d.g, d.beta, gate, w, 1e-6, scale=inp.scale,
+                                                      initial_state=d.h0, output_final_state=True)
+        torch.cuda.synchronize()
+        assert torch.equal(buf["y"], y_e), f"replay {rep}: output differs"
+        assert torch.equal(buf["st"], st_e), f"replay {rep}: final state differs"
+        _ = (st_e * 2).sum().item()  # unrelated eager work between replays
