@@ -321,3 +321,38 @@ def test_fused_norm_fp16_overflow_is_recomputed(varlen):
     assert_output_close(y, ref, tol=2e-2 * scale)
     assert (y.float() - y2.float()).abs().max().item() <= 2e-2 * scale
     assert not sorernn_amd.check_chunk_range(), "the recomputation was finite: the flag must stay clear"
+
+
+def test_fused_norm_two_streams_at_once():
+    """Two calls on the epilogue route issued on two streams at once, each grid as large as the
+    machine: the slices never wait for the epilogue workgroups, and each launch dispatches its
+    slices first, so both complete; each output equals the same call run alone."""
+    import sorernn_amd
+
+    sorernn_amd.set_range_guard("warn")
+    sorernn_amd.check_chunk_range()
+    runs = []
+    for seed in (60, 61):
+        inp = gdn_inputs(2, 1024, 4, 128, dtype=torch.bfloat16, seed=seed, h0=True)
+        gate, w = _gate_weight(inp.v.shape, 128, seed)
+        runs.append((inp.to(DEV), gate.to(DEV), w.to(DEV), inp.scale))
+    assert _epilogue_route(2, 4, 128)
+
+    def call(r):
+        d, gd, wd, sc = r
+        return chunk_gated_delta_rule_gated_norm(d.q, d.k, d.v, d.g, d.beta, gd, wd, EPS, scale=sc,
+                                                 initial_state=d.h0, output_final_state=True)
+
+    alone = [call(r) for r in runs]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream())
+    outs = []
+    for s, r in zip(streams, runs):
+        with torch.cuda.stream(s):
+            outs.append(call(r))
+    torch.cuda.synchronize()
+    for (y, st), (y0, st0) in zip(outs, alone):
+        assert torch.equal(y, y0) and torch.equal(st, st0)
+    assert not sorernn_amd.check_chunk_range(), "a wait ran out"
